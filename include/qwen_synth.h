@@ -1,0 +1,72 @@
+/*
+ * qwen_synth.h -- deterministic random-init weights for the hybrid model and
+ * for standalone GEMV workloads (no counterpart in the reference, which only
+ * loads real checkpoints; real weights are not available to this build).
+ *
+ * Every byte is a pure function of (seed, tensor id, block index): a
+ * splitmix64 counter stream, Irwin-Hall normals built from exact integer sums,
+ * correctly rounded float->half.  The same seed yields the same bytes on any
+ * host, so a GGUF written here and the tensors generated straight into GPU
+ * memory are identical.
+ */
+#ifndef QWEN_SYNTH_H
+#define QWEN_SYNTH_H
+
+#include "gguf.h"
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    uint32_t n_embd, n_ff, n_layer;          /* n_layer = backbone layers (MTP layer extra) */
+    uint32_t n_head, n_kv_head, head_dim;
+    uint32_t n_k_heads, n_v_heads, state;    /* GDN: group_count, dt_rank, head_k = head_v */
+    uint32_t vocab, rope_dim, full_attn_interval, context_len;
+    float    rope_theta, eps;
+    int32_t  type_default;                   /* ggml type of every 2-D weight ...         */
+    int32_t  type_embd, type_output, type_qkv, type_eh_proj;   /* ... unless overridden (<0 = default) */
+    float    gain_output;                    /* output-RMS gain of the lm_head            */
+    uint64_t seed;
+} qwen_synth_spec_t;
+
+/* The 27B hybrid: 48 GDN + 16 GQA layers + MTP, H=5120, F=17408, V=248320, all IQ4_XS. */
+void qwen_synth_spec_27b(qwen_synth_spec_t *s, uint64_t seed);
+/* Small hybrid of the same structure for parity tests (dims in the body). */
+void qwen_synth_spec_tiny(qwen_synth_spec_t *s, uint64_t seed, int mixed_types);
+
+typedef struct {
+    char     name[GGUF_MAX_NAME];
+    uint32_t n_dims;
+    uint64_t ne[2];
+    int32_t  type;
+    uint64_t nbytes;
+    float    mu, sigma;                      /* F32 tensors: value = mu + sigma*z          */
+    int32_t  neg_abs;                        /* F32: value = -(mu + sigma*|z|)             */
+} qwen_synth_tensor_t;
+
+/* Number of tensors of the model and the i-th descriptor (canonical order). */
+uint32_t qwen_synth_count(const qwen_synth_spec_t *s);
+int      qwen_synth_describe(const qwen_synth_spec_t *s, uint32_t i, qwen_synth_tensor_t *out);
+/* Bytes of tensor i (out must hold nbytes). */
+int      qwen_synth_fill(const qwen_synth_spec_t *s, uint32_t i, void *out);
+/* Writes the whole model as a GGUF v3 file readable by gguf_open/model_init. */
+int      qwen_synth_write_gguf(const qwen_synth_spec_t *s, const char *path);
+
+/* Standalone matrix: ne1 rows of ne0 elements in ggml format `type`, with the
+ * IQ4_XS/K-quant super-block scale d ~ fp16(|N(0,1)| * sigma_d); `id` keys
+ * the stream.  Threads: 0 = auto. */
+int qwen_synth_matrix(int32_t type, uint64_t ne0, uint64_t ne1, uint64_t seed, uint64_t id,
+                      float sigma_d, void *out, int n_threads);
+/* fp32 values mu + sigma*z, z ~ Irwin-Hall(12) normal, keyed by (seed, id). */
+void qwen_synth_normal(float *out, uint64_t n, uint64_t seed, uint64_t id, float mu, float sigma);
+
+/* correctly rounded (nearest-even) float -> IEEE half, subnormals included */
+uint16_t qwen_f32_to_f16(float f);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,159 @@
+"""Regenerates the golden fixtures in this directory from the compiled
+reference engine (oracle/_ref/libqwenref.so, built by `make -C oracle` from
+the reference sources).  Run here, where the reference checkout exists:
+
+    python tests/golden/make_golden.py
+
+Inputs are produced with the package's deterministic generator (same seed ->
+same bytes on any host), so the fixtures store the generator seeds/ids next
+to the inputs and the reference outputs:
+
+  gemv_<FMT>_<ne0>x<ne1>.npz : W bytes, x [8][ne0], out_batch [8][ne1]
+                               (gemv_batch n=8), out_single [8][ne1] (8 x gemv),
+                               deq [ne1][ne0] (dequant_row of every row)
+  ops.npz                    : test_ops.c:171-240 random-dimension cases
+  model_<variant>.npz        : tiny hybrid model scenarios (ref_harness.c)
+"""
+import ctypes
+import hashlib
+import os
+import subprocess
+import sys
+import tempfile
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+REF_INC = "/root/reference/include"
+REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libqwenref.so")
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+import qwen_pkg  # noqa: E402  (loads the package's ctypes bindings)
+
+FMT = {"F32": 0, "Q8_0": 8, "Q4_K": 12, "Q5_K": 13, "Q6_K": 14, "IQ4_XS": 23}
+
+
+class TensorInfo(ctypes.Structure):
+    """Layout of gguf_tensor_info_t (GGUF descriptor)."""
+    _fields_ = [("name", ctypes.c_char * 64), ("n_dims", ctypes.c_uint32),
+                ("ne", ctypes.c_uint64 * 4), ("type", ctypes.c_int),
+                ("offset", ctypes.c_uint64), ("data", ctypes.c_void_p)]
+
+
+def fptr(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def gemv_fixtures(ref, host):
+    ref.gemv_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(TensorInfo), ctypes.POINTER(ctypes.c_float),
+                               ctypes.c_uint64, ctypes.c_int, ctypes.POINTER(ctypes.c_float), ctypes.c_uint64]
+    ref.gemv.argtypes = [ctypes.c_void_p, ctypes.POINTER(TensorInfo), ctypes.POINTER(ctypes.c_float),
+                         ctypes.POINTER(ctypes.c_float)]
+    ref.dequant_row.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_float)]
+    ref.quant_row_bytes.restype = ctypes.c_size_t
+    ref.quant_row_bytes.argtypes = [ctypes.c_int, ctypes.c_uint64]
+    for fmt, t in FMT.items():
+        for ne0, ne1, seed in ((512, 64, 11), (5120, 32, 12)):
+            rb = ref.quant_row_bytes(t, ne0)
+            sigma = 0.02 if t != 0 else 1.0
+            W = host.synth_matrix(t, ne0, ne1, seed, 100 + t, sigma)
+            assert W.nbytes == rb * ne1
+            x = host.synth_normal(8 * ne0, seed, 7, 0.0, 1.0).reshape(8, ne0)
+            ti = TensorInfo(name=b"W", n_dims=2, type=t, offset=0,
+                            data=W.ctypes.data_as(ctypes.c_void_p))
+            ti.ne[0], ti.ne[1], ti.ne[2], ti.ne[3] = ne0, ne1, 1, 1
+            ob = np.zeros((8, ne1), np.float32)
+            ref.gemv_batch(None, ctypes.byref(ti), fptr(x), ne0, 8, fptr(ob), ne1)
+            os_ = np.zeros((8, ne1), np.float32)
+            for k in range(8):
+                row = np.ascontiguousarray(x[k])
+                o = np.zeros(ne1, np.float32)
+                ref.gemv(None, ctypes.byref(ti), fptr(row), fptr(o))
+                os_[k] = o
+            deq = np.zeros((ne1, ne0), np.float32)
+            for r in range(ne1 if ne0 * ne1 <= 512 * 64 else 0):
+                ref.dequant_row(t, ctypes.c_void_p(W.ctypes.data + r * rb), ne0, fptr(deq[r]))
+            extra = {"deq": deq} if ne0 * ne1 <= 512 * 64 else {}
+            np.savez(os.path.join(HERE, f"gemv_{fmt}_{ne0}x{ne1}.npz"), W=W, x=x, out_batch=ob,
+                     out_single=os_, seed=np.uint64(seed), type=np.int32(t), sigma=np.float32(sigma), **extra)
+            print(fmt, ne0, ne1, "batch==single:", np.array_equal(ob, os_))
+
+
+def lcg_inputs(n, seed):
+    """test_ops.c:184-189 input generator (LCG, returns new seed)."""
+    x = np.zeros(n, np.float32)
+    w = np.zeros(n, np.float32)
+    for i in range(n):
+        seed = (seed * 1664525 + 1013904223) & 0xFFFFFFFF
+        x[i] = np.float32(((seed >> 16) - 32768)) / np.float32(3276.8)
+        seed = (seed * 1664525 + 1013904223) & 0xFFFFFFFF
+        w[i] = np.float32(0.5) + np.float32((seed >> 16) & 0xFFF) / np.float32(4096.0)
+    return x, w, seed
+
+
+def ops_fixtures(ref):
+    P = ctypes.POINTER(ctypes.c_float)
+    ref.rmsnorm.argtypes = [P, P, P, ctypes.c_uint64, ctypes.c_float]
+    ref.l2norm.argtypes = [P, P, ctypes.c_uint64, ctypes.c_float]
+    for f in ("silu_inplace", "sigmoid_inplace", "softplus_inplace", "softmax_inplace"):
+        getattr(ref, f).argtypes = [P, ctypes.c_uint64]
+    dims = [1, 3, 7, 8, 15, 16, 32, 64, 128, 256, 512, 5120]
+    seed = 12345
+    out = {}
+    for n in dims:
+        x, w, seed = lcg_inputs(n, seed)
+        out[f"x_{n}"] = x
+        out[f"w_{n}"] = w
+        o = np.zeros(n, np.float32)
+        ref.rmsnorm(fptr(o), fptr(x), fptr(w), n, 1e-6)
+        out[f"rmsnorm_{n}"] = o.copy()
+        ref.l2norm(fptr(o), fptr(x), n, 1e-6)
+        out[f"l2norm_{n}"] = o.copy()
+        for f in ("softmax", "silu", "sigmoid", "softplus"):
+            y = x.copy()
+            getattr(ref, f + "_inplace")(fptr(y), n)
+            out[f"{f}_{n}"] = y
+    # wide-range activations: exercise the +-88 clamp, the +-20 tails and the exp bit trick
+    xr = np.linspace(-100, 100, 4099).astype(np.float32)
+    out["x_range"] = xr
+    for f in ("silu", "sigmoid", "softplus", "softmax"):
+        y = xr.copy()
+        getattr(ref, f + "_inplace")(fptr(y), xr.size)
+        out[f"{f}_range"] = y
+    np.savez(os.path.join(HERE, "ops.npz"), dims=np.array(dims, np.int64), **out)
+    print("ops fixtures", len(out))
+
+
+def model_fixtures(host):
+    with tempfile.TemporaryDirectory() as td:
+        exe = os.path.join(td, "ref_harness")
+        subprocess.check_call(["gcc", "-O2", "-std=c11", f"-I{REF_INC}", os.path.join(HERE, "ref_harness.c"),
+                               REF_LIB, f"-Wl,-rpath,{os.path.dirname(REF_LIB)}", "-lm", "-lpthread", "-o", exe])
+        for variant, mixed, seed in (("tiny", 0, 1234), ("tiny_mixed", 1, 4321)):
+            path = os.path.join(td, variant + ".gguf")
+            host.write_tiny_gguf(path, seed, mixed)
+            sha = hashlib.sha256(open(path, "rb").read()).hexdigest()
+            outd = os.path.join(td, variant)
+            os.makedirs(outd)
+            subprocess.check_call([exe, path, outd, "256"])
+            arrs = {}
+            for fn in sorted(os.listdir(outd)):
+                base, ext = fn.rsplit(".", 1)
+                arrs[base] = np.fromfile(os.path.join(outd, fn), np.float32 if ext == "f32" else np.uint32)
+            np.savez(os.path.join(HERE, f"model_{variant}.npz"), gguf_sha256=np.array(sha), seed=np.uint64(seed),
+                     mixed=np.int32(mixed), n_ctx=np.int32(256), **arrs)
+            print(variant, sha[:16], {k: v.shape for k, v in arrs.items()})
+
+
+def main():
+    if not os.path.exists(REF_LIB):
+        sys.exit("build the reference first: make -C oracle")
+    ref = ctypes.CDLL(REF_LIB)
+    host = qwen_pkg.host_lib()
+    gemv_fixtures(ref, host)
+    ops_fixtures(ref)
+    model_fixtures(host)
+
+
+if __name__ == "__main__":
+    main()

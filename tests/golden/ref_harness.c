@@ -1,0 +1,200 @@
+/*
+ * ref_harness.c -- drives the compiled reference engine (oracle/_ref) through
+ * its public API to produce golden vectors.  Built and run only where the
+ * reference checkout exists (by make_golden.py); its outputs are committed
+ * as fixtures next to this file.
+ *
+ * usage: ref_harness <model.gguf> <out_dir> <n_ctx>
+ * Writes raw little-endian arrays (see make_golden.py for the manifest):
+ *   seq_logits.f32      sequential model_forward logits for prompt[0..7]
+ *   batch_logits.f32    model_forward_batch(prompt[0..7], pos 0, B=8) logits_b
+ *   batch_hsave.f32     matching h_save
+ *   mtp_logits.f32      mtp_forward(prompt[8], pos 8, 1) after an 8-token prefill + MTP prefill
+ *   rollback_logits.f32 debug_rollback.c pattern: batch(3) -> rollback_to(1) -> batch(3)
+ *   spec_k{K}.u32       greedy spec streams (main.c:158-231 loop, batched verify, K=1,2)
+ *   spec_seq_k{K}.u32   same streams with sequential verification (any K)
+ *   spec_j_k{K}.u32     accepted index j per cycle
+ *   greedy.u32          plain greedy stream (argmax of model_forward)
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "model.h"
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static void dump(const char *dir, const char *name, const void *p, size_t bytes)
+{
+    char path[512];
+    snprintf(path, sizeof path, "%s/%s", dir, name);
+    FILE *f = fopen(path, "wb");
+    if (!f || fwrite(p, 1, bytes, f) != bytes) { perror(path); exit(2); }
+    fclose(f);
+}
+
+static uint32_t prompt_tok(uint32_t i, uint32_t V) { return (uint32_t)((i * 2654435761u + 12345u) % V); }
+
+/* prefill exactly as main.c:133-152 */
+static void prefill(qwen_model_t *m, const uint32_t *p, uint32_t n, int mtp)
+{
+    uint32_t pos = 0, last = 0;
+    while (pos < n) {
+        uint32_t B = n - pos > PREFILL_MAX_B ? PREFILL_MAX_B : n - pos;
+        model_forward_batch(m, NULL, p + pos, pos, B, 0);
+        if (mtp) mtp_forward_batch(m, NULL, p + pos, pos, B, 0);
+        pos += B;
+        last = B;
+    }
+    memcpy(m->logits, m->logits_b + (size_t)(last - 1) * m->cfg.vocab_size,
+           (size_t)m->cfg.vocab_size * sizeof(float));
+}
+
+/* the spec loop of main.c:166-225 (k <= SPEC_MAX_B-1) */
+static uint32_t spec_batch(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n_predict,
+                           uint32_t *out, uint32_t *js, uint32_t *ncyc)
+{
+    const uint32_t V = m->cfg.vocab_size;
+    const float *last = m->logits;
+    uint32_t gen = 0, cyc = 0;
+    while (gen < n_predict) {
+        const uint32_t P = m->pos - 1, room = n_ctx - 1 - P;
+        if (room < 1) break;
+        const uint32_t kk = k < room - 1 ? k : room - 1;
+        uint32_t cand[SPEC_MAX_B];
+        cand[0] = model_sample_greedy(last, V);
+        for (uint32_t s = 1; s <= kk; s++) {
+            mtp_forward(m, NULL, cand[s - 1], P + s, 1);
+            cand[s] = model_sample_greedy(m->logits, V);
+        }
+        model_forward_batch(m, NULL, cand, P + 1, kk + 1, 1);
+        uint32_t j = kk;
+        for (uint32_t i = 0; i < kk; i++)
+            if (model_sample_greedy(m->logits_b + (size_t)i * V, V) != cand[i + 1]) { j = i; break; }
+        for (uint32_t i = 0; i <= j && gen < n_predict; i++) out[gen++] = cand[i];
+        js[cyc] = j;
+        if (m->pos >= n_ctx) { cyc++; break; }
+        if (j < kk) { model_rollback_to(m, j); m->pos = P + j + 2; }
+        memcpy(m->mtp_h, m->h_save + (size_t)j * m->dims.n_embd, m->dims.n_embd * sizeof(float));
+        mtp_forward(m, NULL, cand[j], P + j + 1, 0);
+        last = m->logits_b + (size_t)j * V;
+        cyc++;
+    }
+    *ncyc = cyc;
+    return gen;
+}
+
+/* Same stream for any k: drafts as main.c:182-185, verification by single-token
+ * forwards that stop at the first mismatch (no rollback needed), MTP anchored on
+ * the backbone hidden state after the last accepted token (debug_spec.c:26). */
+static uint32_t spec_seq(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n_predict,
+                         uint32_t *out, uint32_t *js, uint32_t *ncyc)
+{
+    const uint32_t V = m->cfg.vocab_size, E = m->dims.n_embd;
+    float *last = malloc(V * sizeof(float)), *h = malloc(E * sizeof(float));
+    memcpy(last, m->logits, V * sizeof(float));
+    uint32_t gen = 0, cyc = 0, cand[16];
+    while (gen < n_predict) {
+        const uint32_t P = m->pos - 1, room = n_ctx - 1 - P;
+        if (room < 1) break;
+        const uint32_t kk = k < room - 1 ? k : room - 1;
+        cand[0] = model_sample_greedy(last, V);
+        for (uint32_t s = 1; s <= kk; s++) {
+            mtp_forward(m, NULL, cand[s - 1], P + s, 1);
+            cand[s] = model_sample_greedy(m->logits, V);
+        }
+        uint32_t j = kk;
+        for (uint32_t i = 0; i <= kk; i++) {
+            model_forward(m, NULL, cand[i], P + 1 + i);
+            memcpy(last, m->logits, V * sizeof(float));
+            memcpy(h, m->x, E * sizeof(float));
+            if (i < kk && model_sample_greedy(last, V) != cand[i + 1]) { j = i; break; }
+        }
+        for (uint32_t i = 0; i <= j && gen < n_predict; i++) out[gen++] = cand[i];
+        js[cyc] = j;
+        if (m->pos >= n_ctx) { cyc++; break; }
+        memcpy(m->mtp_h, h, E * sizeof(float));
+        mtp_forward(m, NULL, cand[j], P + j + 1, 0);
+        cyc++;
+    }
+    free(last); free(h);
+    *ncyc = cyc;
+    return gen;
+}
+
+int main(int argc, char **argv)
+{
+    if (argc < 4) { fprintf(stderr, "usage: %s model.gguf outdir n_ctx\n", argv[0]); return 1; }
+    const char *path = argv[1], *dir = argv[2];
+    const uint32_t n_ctx = (uint32_t)atoi(argv[3]);
+    qwen_model_t *m = calloc(1, sizeof *m);
+    if (model_init(m, path, n_ctx)) return 1;
+    const uint32_t V = m->cfg.vocab_size, E = m->dims.n_embd;
+    uint32_t prompt[64];
+    for (uint32_t i = 0; i < 64; i++) prompt[i] = prompt_tok(i, V);
+    dump(dir, "prompt.u32", prompt, sizeof prompt);
+
+    /* sequential vs batched forward of prompt[0..7] */
+    float *seq = malloc((size_t)8 * V * sizeof(float));
+    for (uint32_t i = 0; i < 8; i++) {
+        model_forward(m, NULL, prompt[i], i);
+        memcpy(seq + (size_t)i * V, m->logits, V * sizeof(float));
+    }
+    dump(dir, "seq_logits.f32", seq, (size_t)8 * V * sizeof(float));
+    model_free(m);
+    if (model_init(m, path, n_ctx)) return 1;
+    model_forward_batch(m, NULL, prompt, 0, 8, 0);
+    dump(dir, "batch_logits.f32", m->logits_b, (size_t)8 * V * sizeof(float));
+    dump(dir, "batch_hsave.f32", m->h_save, (size_t)8 * E * sizeof(float));
+    /* MTP: prefill the MTP KV for prompt[0..7] then one draft with logits */
+    mtp_forward_batch(m, NULL, prompt, 0, 8, 0);
+    mtp_forward(m, NULL, prompt[8], 8, 1);
+    dump(dir, "mtp_logits.f32", m->logits, V * sizeof(float));
+    dump(dir, "mtp_h.f32", m->mtp_h, E * sizeof(float));
+    model_free(m);
+
+    /* rollback (debug_rollback.c:25-57 pattern) on prompt[0..4] */
+    if (model_init(m, path, n_ctx)) return 1;
+    for (uint32_t i = 0; i < 5; i++) model_forward(m, NULL, prompt[i], i);
+    uint32_t c1[3] = { prompt[10], prompt[11], prompt[12] }, c2[3] = { prompt[13], prompt[14], prompt[15] };
+    model_forward_batch(m, NULL, c1, 5, 3, 1);
+    model_rollback_to(m, 1);
+    m->pos = 5 + 1 + 2;
+    model_forward_batch(m, NULL, c2, 7, 3, 1);
+    dump(dir, "rollback_logits.f32", m->logits_b, (size_t)3 * V * sizeof(float));
+    model_free(m);
+
+    const uint32_t n_prompt = 20, n_predict = 40;
+    uint32_t out[256], js[256], nc, ng;
+    char name[64];
+    for (uint32_t k = 1; k <= 2; k++) {
+        if (model_init(m, path, n_ctx)) return 1;
+        prefill(m, prompt, n_prompt, 1);
+        memset(out, 0, sizeof out); memset(js, 0, sizeof js);
+        ng = spec_batch(m, k, n_ctx, n_predict, out, js, &nc);
+        snprintf(name, sizeof name, "spec_k%u.u32", k); dump(dir, name, out, ng * 4);
+        snprintf(name, sizeof name, "spec_j_k%u.u32", k); dump(dir, name, js, nc * 4);
+        model_free(m);
+    }
+    for (uint32_t k = 1; k <= 7; k++) {
+        if (model_init(m, path, n_ctx)) return 1;
+        prefill(m, prompt, n_prompt, 1);
+        memset(out, 0, sizeof out); memset(js, 0, sizeof js);
+        ng = spec_seq(m, k, n_ctx, n_predict, out, js, &nc);
+        snprintf(name, sizeof name, "spec_seq_k%u.u32", k); dump(dir, name, out, ng * 4);
+        snprintf(name, sizeof name, "spec_seq_j_k%u.u32", k); dump(dir, name, js, nc * 4);
+        model_free(m);
+    }
+    /* plain greedy stream */
+    if (model_init(m, path, n_ctx)) return 1;
+    prefill(m, prompt, n_prompt, 0);
+    uint32_t cur = model_sample_greedy(m->logits, V);
+    out[0] = cur;
+    for (uint32_t i = 1; i < n_predict; i++) {
+        model_forward(m, NULL, cur, m->pos);
+        cur = model_sample_greedy(m->logits, V);
+        out[i] = cur;
+    }
+    dump(dir, "greedy.u32", out, n_predict * 4);
+    model_free(m);
+    free(m); free(seq);
+    return 0;
+}
