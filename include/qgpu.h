@@ -1,0 +1,119 @@
+/*
+ * qgpu.h -- C-ABI of the MI355X (gfx950) HIP layer.
+ *
+ * Plain C types only.  Every compute entry point takes DEVICE pointers, is
+ * enqueued on the library's stream and returns immediately (stream order);
+ * qgpu_sync() waits.  Return value: QGPU_OK (0), a negative QGPU_E* for a
+ * rejected argument, or a positive hipError_t from the runtime.
+ *
+ * Each entry point names the reference function it replaces (file:line
+ * relative to the reference checkout).  The C11 host library (host/ sources)
+ * implements the reference's own API (include/kernels.h, include/model.h)
+ * on top of these.
+ */
+#ifndef QGPU_H
+#define QGPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QGPU_OK          0
+#define QGPU_E_ARG      -1    /* bad pointer / size / shape */
+#define QGPU_E_TYPE     -2    /* unsupported ggml type */
+#define QGPU_E_INIT     -3    /* qgpu_init not called / no device */
+#define QGPU_E_RANGE    -4    /* size beyond a documented maximum */
+
+#define QGPU_MAX_B       8    /* columns per batched GEMV (reference GEMV_MAX_B, kernels.h:19) */
+#define QGPU_MAX_MULTI   8    /* matrices per grouped GEMV (reference GEMV_MULTI_MAX, kernels.c:657) */
+
+/* ------------------------------------------------------------ runtime */
+/* Selects the device, creates the stream and the GEMV workspace. Idempotent. */
+int  qgpu_init(int device);
+/* Device name, compute-unit count and HBM bytes of the current device. */
+int  qgpu_device_info(char *name, int name_cap, int *n_cu, uint64_t *hbm_bytes);
+const char *qgpu_strerror(int status);
+int  qgpu_sync(void);
+int  qgpu_malloc(void **ptr, size_t bytes);
+int  qgpu_free(void *ptr);
+int  qgpu_memcpy_h2d(void *dst, const void *src, size_t bytes);     /* synchronous */
+int  qgpu_memcpy_d2h(void *dst, const void *src, size_t bytes);     /* synchronous */
+int  qgpu_memcpy_d2d(void *dst, const void *src, size_t bytes);     /* stream-ordered */
+int  qgpu_memset(void *dst, int value, size_t bytes);               /* stream-ordered */
+/* Timing on the library stream (HIP events). */
+int  qgpu_event_create(void **ev);
+int  qgpu_event_destroy(void *ev);
+int  qgpu_event_record(void *ev);
+int  qgpu_event_elapsed_ms(void *start, void *stop, float *ms);     /* waits for stop */
+/* HIP graph capture of the library stream. */
+int  qgpu_graph_begin(void);
+int  qgpu_graph_end(void **graph_exec);
+int  qgpu_graph_launch(void *graph_exec);
+int  qgpu_graph_destroy(void *graph_exec);
+
+/* ------------------------------------------------------------ weights */
+typedef struct qgpu_tensor qgpu_tensor;   /* device-resident weight matrix */
+
+/* Uploads ne1 rows of ne0 elements in ggml format `type` (F32, Q8_0, Q4_K,
+ * Q5_K, Q6_K, IQ4_XS; host bytes in GGUF row-major layout).  IQ4_XS is
+ * repacked losslessly into 16-row tiles for the matrix-core kernel; the other
+ * formats keep the GGUF layout.  Replaces binding gguf_tensor_info_t.data
+ * (reference gguf.h:63-70) for GPU use. */
+int  qgpu_tensor_upload(const void *host, int type, uint64_t ne0, uint64_t ne1, qgpu_tensor **out);
+/* Same from bytes already in device memory (GGUF layout). */
+int  qgpu_tensor_from_device(const void *dev, int type, uint64_t ne0, uint64_t ne1, qgpu_tensor **out);
+int  qgpu_tensor_free(qgpu_tensor *t);
+/* Rebuilds the GGUF-layout bytes (inverse of the repack) into host memory. */
+int  qgpu_tensor_download(const qgpu_tensor *t, void *host);
+int  qgpu_tensor_shape(const qgpu_tensor *t, int *type, uint64_t *ne0, uint64_t *ne1);
+/* Bytes of the matrix in its format (algorithmic bytes, = GGUF size). */
+uint64_t qgpu_tensor_bytes(const qgpu_tensor *t);
+
+/* ------------------------------------------------------------ GEMV */
+#define QGPU_GEMV_ACCUM  1    /* out += W x  instead of out = W x (fused residual add) */
+
+/* out[t*ldo + r] (+)= sum_i W[r,i] * x[t*ldx + i] for t < n <= 8, r < ne1.
+ * Replaces gemv_batch / gemv_rows_batch (reference kernels.c:570-648) and,
+ * with n = 1, gemv (kernels.c:615-621). */
+int  qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
+                     float *out, uint64_t ldo, int flags);
+/* Several matrices sharing x, one launch per format group.
+ * Replaces gemv_multi_batch / gemv_multi (reference kernels.c:666-736). */
+int  qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx,
+                           int n, float *const *outs, const uint64_t *ldos, int flags);
+/* Rows [r0, r1) only (reference gemv_rows, kernels.c:298-321). */
+int  qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
+                          float *out, uint64_t ldo, uint64_t r0, uint64_t r1);
+
+/* ------------------------------------------------------------ dequant */
+/* out[b*ldo + i] = dequant(row rows[b])[i] for b < n, rows in DEVICE memory.
+ * Bit-exact with the reference scalar decoder (quant.c:86-208); replaces the
+ * embedding fetch dequant_row(tok_embd, quant_row_ptr(tok_embd, token))
+ * (reference model.c:721,982,1045,1079). */
+int  qgpu_dequant_rows(const qgpu_tensor *W, const uint32_t *rows, int n, float *out, uint64_t ldo);
+
+/* ------------------------------------------------------------ ops (reference kernels.c:741-939) */
+/* rows x n: out[r*ldo+i] = x[r*ldx+i] / sqrt(mean(x^2)+eps) * w[i]   (w may be NULL) */
+int  qgpu_rmsnorm(float *out, uint64_t ldo, const float *x, uint64_t ldx, const float *w,
+                  uint64_t n, int rows, float eps);
+/* rows x n: out = x / max(||x||, eps) */
+int  qgpu_l2norm(float *out, uint64_t ldo, const float *x, uint64_t ldx, uint64_t n, int rows, float eps);
+int  qgpu_silu(float *x, uint64_t n);
+int  qgpu_sigmoid(float *x, uint64_t n);
+int  qgpu_softplus(float *x, uint64_t n);
+/* rows x n, in place */
+int  qgpu_softmax(float *x, uint64_t ld, uint64_t n, int rows);
+/* rows x n: a[r*lda+i] = silu(a[r*lda+i]) * b[r*ldb+i]   (FFN gate, model.c:477-480) */
+int  qgpu_silu_mul(float *a, uint64_t lda, const float *b, uint64_t ldb, uint64_t n, int rows);
+/* rows x n: y[r*ldy+i] += x[r*ldx+i]  (residual add) */
+int  qgpu_add(float *y, uint64_t ldy, const float *x, uint64_t ldx, uint64_t n, int rows);
+/* argmax of each of `rows` rows (lowest index wins ties; model.c:746-756) into out[r] */
+int  qgpu_argmax(const float *logits, uint64_t ld, uint32_t n, int rows, uint32_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,564 @@
+// Batched dequant-GEMV for the ggml formats of the model (gfx950).
+//
+// IQ4_XS (the bulk of the weights) runs on the matrix cores:
+//   * weights are repacked once into 16-row tiles; per (tile, 256-element
+//     super-block) a 2176-byte record holds the 16 row headers (d, scales_h,
+//     scales_l: 8 B each) and the 2048 nibble bytes arranged so that lane l of
+//     a wave loads its MFMA B operand for 4 sub-blocks with one 16-byte load;
+//   * a nibble dword decodes to 8 int8 codebook values with 6 v_perm_b32;
+//   * the activations are turned once per call into 4 balanced int8 "digits"
+//     of a 30-bit fixed-point value per (token, super-block):
+//       x = 2^-s * (d0 + 2^8 d1 + 2^16 d2 + 2^24 d3),  |x| 2^s < 2^30,
+//     so v_mfma_i32_16x16x32_i8 computes exact integer sub-block dot products
+//     for 4 tokens x 4 digits (rows of the A tile) against 16 weight rows;
+//   * the 6-bit sub-block scale (ls - 32) is applied in int32 (exact: |acc| <
+//     2^27 per super-block), then (d * 2^(8 dgt - s)) once per super-block in
+//     fp32.  The only roundings are the x quantisation (2^-31 of the block max)
+//     and the fp32 super-block accumulation, below the fp32 FMA rounding of the
+//     reference's own accumulation.
+// Other formats (Q4_K/Q5_K/Q6_K/Q8_0/F32: embeddings, lm_head, eh_proj of the
+// real checkpoint) use a VALU kernel on the GGUF layout.
+#include "qgpu_internal.h"
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+#define MAX_K       65536
+#define MAX_NSB     (MAX_K / 256)
+#define PLANE_BYTES ((size_t)MAX_NSB * 4096)
+#define XS_FLOATS   ((size_t)MAX_NSB * 16)
+
+size_t qg_gemv_workspace_bytes() { return 2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float); }
+
+static __device__ __forceinline__ float h2f(uint32_t h16) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h16); }
+
+// ---------------------------------------------------------------- repack
+// raw (GGUF rows of nsb 136-byte super-blocks) <-> tile records.
+// packed dword (row n, lane group g, sub-block ib) of record (T, s) at
+//   128 + ((ib/4)*64 + g*16 + n)*16 + (ib%4)*4  and holds qs bytes 4g..4g+3 of sub-block ib.
+__global__ void k_repack_iq4(const uint8_t *__restrict__ raw, uint8_t *__restrict__ pk, uint64_t ne1,
+                             uint32_t nsb, uint64_t rows_pad, int unpack)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows_pad * nsb) return;
+    const uint64_t r = i / nsb;
+    const uint32_t s = (uint32_t)(i % nsb);
+    const uint64_t T = r / IQ4_TILE_ROWS;
+    const uint32_t n = (uint32_t)(r % IQ4_TILE_ROWS);
+    uint8_t *rec = pk + (T * nsb + s) * IQ4_REC_BYTES;
+    const uint64_t rb = (uint64_t)nsb * 136;
+    if (unpack) {
+        if (r >= ne1) return;
+        uint8_t *blk = (uint8_t *)raw + r * rb + (uint64_t)s * 136;
+        *(uint2 *)blk = *(const uint2 *)(rec + n * 8);
+        for (int ib = 0; ib < 8; ib++)
+            for (int g = 0; g < 4; g++)
+                *(uint32_t *)(blk + 8 + 16 * ib + 4 * g) =
+                    *(const uint32_t *)(rec + IQ4_HDR_BYTES + ((ib / 4) * 64 + g * 16 + n) * 16 + (ib % 4) * 4);
+        return;
+    }
+    const uint8_t *blk = raw + r * rb + (uint64_t)s * 136;
+    const bool live = r < ne1;
+    *(uint2 *)(rec + n * 8) = live ? *(const uint2 *)blk : make_uint2(0, 0);
+    for (int ib = 0; ib < 8; ib++)
+        for (int g = 0; g < 4; g++)
+            *(uint32_t *)(rec + IQ4_HDR_BYTES + ((ib / 4) * 64 + g * 16 + n) * 16 + (ib % 4) * 4) =
+                live ? *(const uint32_t *)(blk + 8 + 16 * ib + 4 * g) : 0u;
+}
+
+int qg_repack_iq4xs(const void *raw, uint64_t ne0, uint64_t ne1, void *packed, int unpack)
+{
+    const uint32_t nsb = (uint32_t)(ne0 / 256);
+    const uint64_t rows_pad = (ne1 + IQ4_TILE_ROWS - 1) / IQ4_TILE_ROWS * IQ4_TILE_ROWS;
+    const uint64_t n = rows_pad * nsb;
+    hipLaunchKernelGGL(k_repack_iq4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, qg::stream,
+                       (const uint8_t *)raw, (uint8_t *)packed, ne1, nsb, rows_pad, unpack);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+// ---------------------------------------------------------------- activation prep
+// A operand of K-step (sb, ib) for plane a (tokens 4a..4a+3): 64 lanes x 8 bytes;
+// lane l = g*16 + m holds, for A row m = dgt*4 + t, the digit dgt of token t at
+// the 8 elements of sub-block ib that K-slots 8g..8g+7 stand for:
+//   slot 8g+c, c<4  -> element 4g+c        (low nibble of qs byte 4g+c)
+//   slot 8g+4+c     -> element 16+4g+c     (high nibble of qs byte 4g+c)
+// Two consecutive sub-blocks are interleaved so a lane fetches 16 bytes:
+//   byte offset ((sb*4 + ib/2)*64 + l)*16 + (ib%2)*8 + (slot%8).
+// xs[sb*16 + m] = 2^(8*dgt - s_t) converts the integer result of row m.
+__global__ __launch_bounds__(256) void k_prep_digits(const float *__restrict__ x, uint64_t ldx, int ntok,
+                                                     uint8_t *__restrict__ A, float *__restrict__ xs)
+{
+    __shared__ uint8_t stage[4096];
+    __shared__ float red[4][8];
+    __shared__ int shift[4];
+    const int e = threadIdx.x, sb = blockIdx.x, a = blockIdx.y;
+    const int lane = e & 63, wv = e >> 6;
+    float v[4], m[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int t = 4 * a + i;
+        v[i] = t < ntok ? x[(uint64_t)t * ldx + (uint64_t)sb * 256 + e] : 0.0f;
+        m[i] = fabsf(v[i]);
+#pragma unroll
+        for (int o = 32; o; o >>= 1) m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
+    }
+    if (lane == 0)
+        for (int i = 0; i < 4; i++) red[i][wv] = m[i];
+    __syncthreads();
+    if (e < 4) {
+        const float mx = fmaxf(fmaxf(red[e][0], red[e][1]), fmaxf(red[e][2], red[e][3]));
+        int E = 0;
+        if (mx > 0.0f && isfinite(mx)) { frexpf(mx, &E); shift[e] = 30 - E; }
+        else shift[e] = 0;
+    }
+    __syncthreads();
+    const int ib = e >> 5, w = e & 31, up = w >> 4, jj = w & 15, gg = jj >> 2, c = jj & 3;
+    const int boff = ((ib >> 1) * 64) * 16 + (ib & 1) * 8 + up * 4 + c;   // + lane*16
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float sv = ldexpf(v[i], shift[i]);
+        int X = isfinite(sv) ? (int)rintf(sv) : 0;
+#pragma unroll
+        for (int dg = 0; dg < 4; dg++) {
+            const int d = (dg < 3) ? (int)(int8_t)(X & 0xFF) : X;     // balanced base-256 digit
+            X = (X - d) >> 8;
+            stage[boff + (gg * 16 + dg * 4 + i) * 16] = (uint8_t)d;
+        }
+    }
+    __syncthreads();
+    uint8_t *dst = A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * 4096;
+    ((uint4 *)dst)[e] = ((const uint4 *)stage)[e];
+    if (e < 16) {
+        const int dg = e >> 2, t = e & 3;
+        xs[(uint64_t)a * XS_FLOATS + (uint64_t)sb * 16 + e] = ldexpf(1.0f, 8 * dg - shift[t]);
+    }
+}
+
+// ---------------------------------------------------------------- IQ4_XS MFMA GEMV
+struct GemvMat {
+    const uint8_t *W;
+    float *out;
+    uint64_t ldo;
+    uint32_t rows, tile0, row_lo, row_hi;   // flat tile start; rows written: [row_lo, row_hi)
+    uint32_t tile_first;                    // first tile of this matrix that is launched
+};
+struct GemvArgs {
+    GemvMat m[QGPU_MAX_MULTI];
+    int n_mat, nsb, ntok, flags;
+    const uint8_t *A;
+    const float *xs;
+    const float *x;        // VALU path: fp32 activations
+    uint64_t ldx, ne0;
+};
+
+static __device__ __forceinline__ void iq4_decode8(uint32_t q, uint32_t &lo, uint32_t &hi)
+{
+    // IQ4_NL codebook as int8 bytes {-127,-104,-83,-65 | -49,-35,-22,-10 | 1,13,25,38 | 53,69,89,113}
+    const uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
+    uint32_t s = q & 0x07070707u;
+    uint32_t a = __builtin_amdgcn_perm(T1, T0, s), b = __builtin_amdgcn_perm(T3, T2, s);
+    lo = __builtin_amdgcn_perm(b, a, ((q >> 1) & 0x04040404u) | 0x03020100u);
+    const uint32_t q4 = q >> 4;
+    s = q4 & 0x07070707u;
+    a = __builtin_amdgcn_perm(T1, T0, s);
+    b = __builtin_amdgcn_perm(T3, T2, s);
+    hi = __builtin_amdgcn_perm(b, a, ((q4 >> 1) & 0x04040404u) | 0x03020100u);
+}
+
+template <int NA, int NW>
+__global__ __launch_bounds__(NW * 64) void k_gemv_iq4(const GemvArgs args)
+{
+    __shared__ float red[NW][NA][4][16];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
+    const uint32_t tile = blockIdx.x;
+    int k = 0;
+    while (k + 1 < args.n_mat && tile >= args.m[k + 1].tile0) k++;
+    const GemvMat &M = args.m[k];
+    const uint32_t T = tile - M.tile0 + M.tile_first;
+    const int nsb = args.nsb;
+    const uint8_t *rec0 = M.W + (uint64_t)T * nsb * IQ4_REC_BYTES;
+    const int sb0 = wv * nsb / NW, sb1 = (wv + 1) * nsb / NW;
+
+    float accf[NA][4];
+#pragma unroll
+    for (int a = 0; a < NA; a++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) accf[a][i] = 0.0f;
+
+    for (int sb = sb0; sb < sb1; sb++) {
+        const uint8_t *rec = rec0 + (uint64_t)sb * IQ4_REC_BYTES;
+        const uint2 hdr = *(const uint2 *)(rec + n * 8);
+        const uint4 qa = *(const uint4 *)(rec + IQ4_HDR_BYTES + lane * 16);
+        const uint4 qb = *(const uint4 *)(rec + IQ4_HDR_BYTES + (64 + lane) * 16);
+        uint4 av[NA][4];
+        float4 xv[NA];
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            const uint8_t *Ab = args.A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * 4096 + lane * 16;
+#pragma unroll
+            for (int p = 0; p < 4; p++) av[a][p] = *(const uint4 *)(Ab + p * 1024);
+            xv[a] = *(const float4 *)(args.xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16 + 4 * g);
+        }
+        const uint32_t qd[8] = { qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w };
+        const uint32_t sh = hdr.x >> 16, sl = hdr.y;
+        v4i acci[NA];
+#pragma unroll
+        for (int a = 0; a < NA; a++) acci[a] = (v4i){0, 0, 0, 0};
+#pragma unroll
+        for (int ib = 0; ib < 8; ib++) {
+            uint32_t lo, hi;
+            iq4_decode8(qd[ib], lo, hi);
+            const long bop = (long)(((uint64_t)hi << 32) | lo);
+            const int wsc = (int)(((sl >> (4 * ib)) & 15u) | (((sh >> (2 * ib)) & 3u) << 4)) - 32;
+#pragma unroll
+            for (int a = 0; a < NA; a++) {
+                const uint4 q4 = av[a][ib >> 1];
+                const long aop = (ib & 1) ? (long)(((uint64_t)q4.w << 32) | q4.z)
+                                          : (long)(((uint64_t)q4.y << 32) | q4.x);
+                const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, (v4i){0, 0, 0, 0}, 0, 0, 0);
+                acci[a] += D * wsc;
+            }
+        }
+        const float d = h2f(hdr.x & 0xFFFFu);
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            accf[a][0] += (float)acci[a][0] * (d * xv[a].x);
+            accf[a][1] += (float)acci[a][1] * (d * xv[a].y);
+            accf[a][2] += (float)acci[a][2] * (d * xv[a].z);
+            accf[a][3] += (float)acci[a][3] * (d * xv[a].w);
+        }
+    }
+    // lanes n, n+16, n+32, n+48 hold digits 0..3 of the same (token, row): sum them
+#pragma unroll
+    for (int a = 0; a < NA; a++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float v = accf[a][i];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (g == 0) red[wv][a][i][n] = v;
+        }
+    __syncthreads();
+    if (tid < NA * 64) {
+        const int a = tid >> 6, i = (tid >> 4) & 3, nn = tid & 15;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) s += red[w][a][i][nn];
+        const int t = 4 * a + i;
+        const uint32_t r = T * IQ4_TILE_ROWS + nn;
+        if (t < args.ntok && r >= M.row_lo && r < M.row_hi) {
+            float *o = M.out + (uint64_t)t * M.ldo + r;
+            *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + s : s;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- VALU GEMV (GGUF layout)
+// Decoders of one 32-element chunk to the dequantised fp32 values (bit-exact
+// with the scalar reference: explicit round-to-nearest products, no FMA).
+static __device__ __forceinline__ uint32_t ld8(const uint8_t *p) { return *p; }
+
+template <int FMT>
+static __device__ __forceinline__ void decode_chunk(const uint8_t *__restrict__ row, uint32_t c, float w[32])
+{
+    if (FMT == T_F32) {
+        const float4 *p = (const float4 *)(row + (uint64_t)c * 128);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 v = p[j];
+            w[4 * j] = v.x; w[4 * j + 1] = v.y; w[4 * j + 2] = v.z; w[4 * j + 3] = v.w;
+        }
+    } else if (FMT == T_Q8_0) {
+        const uint8_t *b = row + (uint64_t)c * 34;
+        const float d = h2f(ld8(b) | (ld8(b + 1) << 8));
+#pragma unroll
+        for (int j = 0; j < 32; j++) w[j] = __fmul_rn(d, (float)(int8_t)b[2 + j]);
+    } else if (FMT == T_Q4_K || FMT == T_Q5_K) {
+        const uint32_t sbi = c >> 3, j = c & 7, g = j >> 1, half = j & 1;
+        const uint8_t *b = row + (uint64_t)sbi * (FMT == T_Q5_K ? 176 : 144);
+        const float d = h2f(*(const uint16_t *)b), dmin = h2f(*(const uint16_t *)(b + 2));
+        const uint8_t *sc = b + 4;
+        uint32_t s, m;
+        if (j < 4) { s = sc[j] & 63; m = sc[j + 4] & 63; }
+        else { s = (sc[j + 4] & 15) | ((sc[j - 4] >> 6) << 4); m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4); }
+        const float d1 = __fmul_rn(d, (float)s), m1 = __fmul_rn(dmin, (float)m);
+        const uint8_t *qs = b + (FMT == T_Q5_K ? 48 : 16) + 32 * g;
+        const uint4 q0 = ((const uint4 *)qs)[0], q1 = ((const uint4 *)qs)[1];
+        const uint32_t qw[8] = { q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w };
+        uint32_t hw[8];
+        if (FMT == T_Q5_K) {
+            const uint4 h0 = ((const uint4 *)(b + 16))[0], h1 = ((const uint4 *)(b + 16))[1];
+            hw[0] = h0.x; hw[1] = h0.y; hw[2] = h0.z; hw[3] = h0.w; hw[4] = h1.x; hw[5] = h1.y; hw[6] = h1.z; hw[7] = h1.w;
+        }
+        const uint32_t hb = 2 * g + half;
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const uint32_t byte = (qw[l >> 2] >> (8 * (l & 3))) & 0xFF;
+            uint32_t q = half ? (byte >> 4) : (byte & 15);
+            if (FMT == T_Q5_K) q += ((((hw[l >> 2] >> (8 * (l & 3))) & 0xFF) >> hb) & 1) << 4;
+            w[l] = __fsub_rn(__fmul_rn(d1, (float)q), m1);
+        }
+    } else if (FMT == T_Q6_K) {
+        const uint32_t sbi = c >> 3, j = c & 7, nh = j >> 2, quad = j & 3;
+        const uint8_t *b = row + (uint64_t)sbi * 210;
+        const float d = h2f(ld8(b + 208) | (ld8(b + 209) << 8));
+        const uint8_t *ql = b + 64 * nh + ((quad & 1) ? 32 : 0), *qh = b + 128 + 32 * nh;
+        const int8_t *sc = (const int8_t *)(b + 192 + 8 * nh);
+        const float ds0 = __fmul_rn(d, (float)sc[2 * quad]), ds1 = __fmul_rn(d, (float)sc[2 * quad + 1]);
+#pragma unroll
+        for (int l = 0; l < 32; l++) {
+            const uint32_t lo = ql[l];
+            const uint32_t nib = (quad & 2) ? (lo >> 4) : (lo & 15);
+            const int q = (int)(nib | (((qh[l] >> (2 * quad)) & 3) << 4)) - 32;
+            w[l] = __fmul_rn(l < 16 ? ds0 : ds1, (float)q);
+        }
+    }
+}
+
+// one wave per 2 rows, lanes stride over 32-element chunks (F32: over elements); 4 waves per block
+template <int FMT, int NT>
+__global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
+{
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint32_t grp = blockIdx.x;                  // flat row-group (8 rows) index
+    int k = 0;
+    while (k + 1 < args.n_mat && grp >= args.m[k + 1].tile0) k++;
+    const GemvMat &M = args.m[k];
+    const uint32_t r0 = (grp - M.tile0 + M.tile_first) * 8 + wv * 2;
+    const uint64_t rb = (FMT == T_F32) ? args.ne0 * 4 : (FMT == T_Q8_0 ? args.ne0 / 32 * 34 :
+                        args.ne0 / 256 * (FMT == T_Q4_K ? 144 : FMT == T_Q5_K ? 176 : 210));
+    const int nr = (r0 >= M.row_hi) ? 0 : (r0 + 1 >= M.row_hi ? 1 : 2);
+    float acc[2][NT];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[r][t] = 0.0f;
+    if (FMT == T_F32) {
+        for (uint64_t i = lane; i < args.ne0; i += 64) {
+            float w[2];
+            for (int r = 0; r < 2; r++) w[r] = r < nr ? ((const float *)(M.W + (uint64_t)(r0 + r) * rb))[i] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const float xv = t < args.ntok ? args.x[(uint64_t)t * args.ldx + i] : 0.0f;
+                acc[0][t] = fmaf(w[0], xv, acc[0][t]);
+                acc[1][t] = fmaf(w[1], xv, acc[1][t]);
+            }
+        }
+    } else {
+        const uint32_t nchunk = (uint32_t)(args.ne0 / 32);
+        for (uint32_t c = lane; c < nchunk; c += 64) {
+            float w[2][32];
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                if (r < nr) decode_chunk<FMT>(M.W + (uint64_t)(r0 + r) * rb, c, w[r]);
+                else {
+#pragma unroll
+                    for (int j = 0; j < 32; j++) w[r][j] = 0.0f;
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                if (t >= args.ntok) break;
+                const float4 *xp = (const float4 *)(args.x + (uint64_t)t * args.ldx + (uint64_t)c * 32);
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float4 v = xp[j];
+                    s0 = fmaf(w[0][4 * j], v.x, s0); s0 = fmaf(w[0][4 * j + 1], v.y, s0);
+                    s0 = fmaf(w[0][4 * j + 2], v.z, s0); s0 = fmaf(w[0][4 * j + 3], v.w, s0);
+                    s1 = fmaf(w[1][4 * j], v.x, s1); s1 = fmaf(w[1][4 * j + 1], v.y, s1);
+                    s1 = fmaf(w[1][4 * j + 2], v.z, s1); s1 = fmaf(w[1][4 * j + 3], v.w, s1);
+                }
+                acc[0][t] += s0;
+                acc[1][t] += s1;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            float v = acc[r][t];
+#pragma unroll
+            for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+            acc[r][t] = v;
+        }
+    if (lane == 0)
+        for (int r = 0; r < nr; r++) {
+            const uint32_t row = r0 + r;
+            if (row < M.row_lo) continue;
+            for (int t = 0; t < NT && t < args.ntok; t++) {
+                float *o = M.out + (uint64_t)t * M.ldo + row;
+                *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + acc[r][t] : acc[r][t];
+            }
+        }
+}
+
+// ---------------------------------------------------------------- launchers
+static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x, uint64_t ldx,
+                        int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
+                        const uint64_t *r1s)
+{
+    const qgpu_tensor *W0 = Ws[idx[0]];
+    GemvArgs A = {};
+    A.n_mat = cnt; A.ntok = n; A.flags = flags; A.x = x; A.ldx = ldx; A.ne0 = W0->ne0;
+    A.nsb = (int)(W0->ne0 / 256);
+    const bool iq4 = W0->type == T_IQ4_XS;
+    const uint32_t per = iq4 ? IQ4_TILE_ROWS : 8;
+    uint32_t tiles = 0;
+    for (int j = 0; j < cnt; j++) {
+        const qgpu_tensor *W = Ws[idx[j]];
+        const uint64_t lo = r0s ? r0s[idx[j]] : 0, hi = r1s ? r1s[idx[j]] : W->ne1;
+        GemvMat &M = A.m[j];
+        M.W = (const uint8_t *)W->data;
+        M.out = outs[idx[j]];
+        M.ldo = ldos[idx[j]];
+        M.rows = (uint32_t)W->ne1;
+        M.row_lo = (uint32_t)lo;
+        M.row_hi = (uint32_t)hi;
+        M.tile_first = (uint32_t)(lo / per);
+        M.tile0 = tiles;
+        tiles += (uint32_t)((hi + per - 1) / per - lo / per);
+    }
+    if (!tiles) return QGPU_OK;
+    if (iq4) {
+        if (W0->ne0 > MAX_K) return QGPU_E_RANGE;
+        const int na = n > 4 ? 2 : 1;
+        A.A = (const uint8_t *)qg::ws;
+        A.xs = (const float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES);
+        hipLaunchKernelGGL(k_prep_digits, dim3((unsigned)A.nsb, (unsigned)na), dim3(256), 0, qg::stream,
+                           x, ldx, n, (uint8_t *)qg::ws, (float *)A.xs);
+        QG_LAUNCH_CHECK();
+        if (na == 1) hipLaunchKernelGGL((k_gemv_iq4<1, 4>), dim3(tiles), dim3(256), 0, qg::stream, A);
+        else hipLaunchKernelGGL((k_gemv_iq4<2, 4>), dim3(tiles), dim3(256), 0, qg::stream, A);
+        QG_LAUNCH_CHECK();
+        return QGPU_OK;
+    }
+#define VALU_CASE(F)                                                                                              \
+    case F:                                                                                                       \
+        switch (n) {                                                                                              \
+        case 1: hipLaunchKernelGGL((k_gemv_valu<F, 1>), dim3(tiles), dim3(256), 0, qg::stream, A); break;        \
+        case 2: hipLaunchKernelGGL((k_gemv_valu<F, 2>), dim3(tiles), dim3(256), 0, qg::stream, A); break;        \
+        case 3: case 4: hipLaunchKernelGGL((k_gemv_valu<F, 4>), dim3(tiles), dim3(256), 0, qg::stream, A); break; \
+        default: hipLaunchKernelGGL((k_gemv_valu<F, 8>), dim3(tiles), dim3(256), 0, qg::stream, A); break;      \
+        }                                                                                                         \
+        break;
+    switch (W0->type) {
+        VALU_CASE(T_F32)
+        VALU_CASE(T_Q8_0)
+        VALU_CASE(T_Q4_K)
+        VALU_CASE(T_Q5_K)
+        VALU_CASE(T_Q6_K)
+    default: return QGPU_E_TYPE;
+    }
+#undef VALU_CASE
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx, int n,
+                      float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!Ws || !x || !outs || !ldos || n_mat < 1 || n_mat > QGPU_MAX_MULTI || n < 1 || n > QGPU_MAX_B)
+        return QGPU_E_ARG;
+    for (int j = 0; j < n_mat; j++) {
+        if (!Ws[j] || !outs[j] || Ws[j]->ne0 != Ws[0]->ne0 || ldx < Ws[j]->ne0) return QGPU_E_ARG;
+        if (n > 1 && ldos[j] < (r1s ? r1s[j] : Ws[j]->ne1)) return QGPU_E_ARG;
+        if (r0s && (r0s[j] > r1s[j] || r1s[j] > Ws[j]->ne1)) return QGPU_E_ARG;
+    }
+    if (Ws[0]->type != T_F32 && (ldx % 4 || ((uintptr_t)x & 15))) return QGPU_E_ARG;   // float4 activation loads
+    // group matrices of the same format (one launch per group)
+    int done[QGPU_MAX_MULTI] = {0};
+    for (int j = 0; j < n_mat; j++) {
+        if (done[j]) continue;
+        int idx[QGPU_MAX_MULTI], cnt = 0;
+        for (int i = j; i < n_mat; i++)
+            if (!done[i] && Ws[i]->type == Ws[j]->type) { idx[cnt++] = i; done[i] = 1; }
+        rc = launch_group(Ws, idx, cnt, x, ldx, n, outs, ldos, flags, r0s, r1s);
+        if (rc) return rc;
+    }
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
+                               uint64_t ldo, int flags)
+{
+    return gemv_multi(&W, 1, x, ldx, n, &out, &ldo, flags, nullptr, nullptr);
+}
+
+extern "C" int qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx, int n,
+                                     float *const *outs, const uint64_t *ldos, int flags)
+{
+    return gemv_multi(Ws, n_mat, x, ldx, n, outs, ldos, flags, nullptr, nullptr);
+}
+
+extern "C" int qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
+                                    uint64_t ldo, uint64_t r0, uint64_t r1)
+{
+    return gemv_multi(&W, 1, x, ldx, n, &out, &ldo, 0, &r0, &r1);
+}
+
+// ---------------------------------------------------------------- dequant rows (embedding)
+template <int FMT>
+__global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t *__restrict__ W, uint64_t ne0, uint64_t ne1,
+                                                      const uint32_t *__restrict__ rows, float *__restrict__ out,
+                                                      uint64_t ldo)
+{
+    const uint32_t r = rows[blockIdx.x];
+    float *o = out + (uint64_t)blockIdx.x * ldo;
+    const uint32_t nchunk = (uint32_t)(ne0 / 32);
+    if (r >= ne1) {                                   // out-of-range id: zeros, never a wild read
+        for (uint32_t i = threadIdx.x; i < ne0; i += blockDim.x) o[i] = 0.0f;
+        return;
+    }
+    for (uint32_t c = threadIdx.x; c < nchunk; c += blockDim.x) {
+        float w[32];
+        if (FMT == T_IQ4_XS) {
+            const uint32_t nsb = (uint32_t)(ne0 / 256), sb = c >> 3, ib = c & 7;
+            const uint8_t *rec = W + ((uint64_t)(r / IQ4_TILE_ROWS) * nsb + sb) * IQ4_REC_BYTES;
+            const uint32_t n = r % IQ4_TILE_ROWS;
+            const uint2 hdr = *(const uint2 *)(rec + n * 8);
+            const int ls = (int)(((hdr.y >> (4 * ib)) & 15u) | (((hdr.x >> 16 >> (2 * ib)) & 3u) << 4));
+            const float dl = __fmul_rn(h2f(hdr.x & 0xFFFFu), (float)(ls - 32));
+            const int8_t kv[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const uint32_t q = *(const uint32_t *)(rec + IQ4_HDR_BYTES + ((ib / 4) * 64 + g * 16 + n) * 16 + (ib % 4) * 4);
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    const uint32_t byte = (q >> (8 * cc)) & 0xFF;
+                    w[4 * g + cc] = __fmul_rn(dl, (float)kv[byte & 15]);
+                    w[16 + 4 * g + cc] = __fmul_rn(dl, (float)kv[byte >> 4]);
+                }
+            }
+        } else {
+            const uint64_t rb = (FMT == T_F32) ? ne0 * 4 : (FMT == T_Q8_0 ? ne0 / 32 * 34 :
+                                ne0 / 256 * (FMT == T_Q4_K ? 144 : FMT == T_Q5_K ? 176 : 210));
+            decode_chunk<FMT>(W + (uint64_t)r * rb, c, w);
+        }
+#pragma unroll
+        for (int j = 0; j < 32; j++) o[(uint64_t)c * 32 + j] = w[j];
+    }
+}
+
+extern "C" int qgpu_dequant_rows(const qgpu_tensor *W, const uint32_t *rows, int n, float *out, uint64_t ldo)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!W || !rows || !out || n < 0 || (n > 1 && ldo < W->ne0) || W->ne0 % 32) return QGPU_E_ARG;
+    if (!n) return QGPU_OK;
+    const dim3 grid((unsigned)n), blk(256);
+    switch (W->type) {
+    case T_IQ4_XS: hipLaunchKernelGGL(k_dequant_rows<T_IQ4_XS>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
+    case T_F32: hipLaunchKernelGGL(k_dequant_rows<T_F32>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
+    case T_Q8_0: hipLaunchKernelGGL(k_dequant_rows<T_Q8_0>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
+    case T_Q4_K: hipLaunchKernelGGL(k_dequant_rows<T_Q4_K>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
+    case T_Q5_K: hipLaunchKernelGGL(k_dequant_rows<T_Q5_K>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
+    case T_Q6_K: hipLaunchKernelGGL(k_dequant_rows<T_Q6_K>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
+    default: return QGPU_E_TYPE;
+    }
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}

@@ -1,0 +1,249 @@
+// Norms, activations, residual add and greedy argmax (gfx950).
+// Row-parallel kernels: one 256-thread block per row, fp32 throughout.
+// The reference's own results differ from these only by fp32 rounding
+// (its AVX2 exp is a degree-7 Taylor polynomial, kernels.c:807-822; here the
+// device libm expf is used).
+#include "qgpu_internal.h"
+
+namespace qg {
+void *ws_small = nullptr;     // 64 KiB: argmax partials
+}
+
+static __device__ __forceinline__ float block_sum(float v, float *sh)
+{
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) sh[w] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += sh[i];
+    return s;
+}
+
+static __device__ __forceinline__ float block_max(float v, float *sh)
+{
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) sh[w] = v;
+    __syncthreads();
+    float s = sh[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) s = fmaxf(s, sh[i]);
+    return s;
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm(float *out, uint64_t ldo, const float *x, uint64_t ldx,
+                                                 const float *w, uint64_t n, float eps)
+{
+    __shared__ float sh[4];
+    const float *xr = x + (uint64_t)blockIdx.x * ldx;
+    float *orow = out + (uint64_t)blockIdx.x * ldo;
+    float s = 0.0f;
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(xr[i], xr[i], s);
+    s = block_sum(s, sh);
+    const float scale = 1.0f / sqrtf(s / (float)n + eps);
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) orow[i] = w ? (xr[i] * scale) * w[i] : xr[i] * scale;
+}
+
+__global__ __launch_bounds__(256) void k_l2norm(float *out, uint64_t ldo, const float *x, uint64_t ldx,
+                                                uint64_t n, float eps)
+{
+    __shared__ float sh[4];
+    const float *xr = x + (uint64_t)blockIdx.x * ldx;
+    float *orow = out + (uint64_t)blockIdx.x * ldo;
+    float s = 0.0f;
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(xr[i], xr[i], s);
+    s = block_sum(s, sh);
+    const float nr = sqrtf(s);
+    const float scale = 1.0f / (nr > eps ? nr : eps);
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) orow[i] = xr[i] * scale;
+}
+
+__global__ void k_unary(float *x, uint64_t n, int op)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    float r;
+    if (op == 0) r = v / (1.0f + expf(-v));                              // silu
+    else if (op == 1) r = 1.0f / (1.0f + expf(-v));                      // sigmoid
+    else r = v > 30.0f ? v : (v < -30.0f ? expf(v) : log1pf(expf(v)));   // softplus (kernels.c:874-885)
+    x[i] = r;
+}
+
+__global__ __launch_bounds__(256) void k_softmax(float *x, uint64_t ld, uint64_t n)
+{
+    __shared__ float sh[4];
+    float *r = x + (uint64_t)blockIdx.x * ld;
+    float m = -INFINITY;
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, r[i]);
+    m = block_max(m, sh);
+    float s = 0.0f;
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float e = expf(r[i] - m);
+        r[i] = e;
+        s += e;
+    }
+    s = block_sum(s, sh);
+    const float inv = 1.0f / s;
+    for (uint64_t i = threadIdx.x; i < n; i += blockDim.x) r[i] *= inv;
+}
+
+__global__ void k_silu_mul(float *a, uint64_t lda, const float *b, uint64_t ldb, uint64_t n)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float *ar = a + (uint64_t)blockIdx.y * lda;
+    const float v = ar[i];
+    ar[i] = (v / (1.0f + expf(-v))) * b[(uint64_t)blockIdx.y * ldb + i];
+}
+
+__global__ void k_add(float *y, uint64_t ldy, const float *x, uint64_t ldx, uint64_t n)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    y[(uint64_t)blockIdx.y * ldy + i] += x[(uint64_t)blockIdx.y * ldx + i];
+}
+
+// ---------------------------------------------------------------- argmax
+// key = order-preserving float bits << 32 | ~index : the max key is the max
+// value with the lowest index (model.c:750 strict '>').
+static __device__ __forceinline__ uint64_t akey(float v, uint32_t i)
+{
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (0xFFFFFFFFu - i);
+}
+
+#define AMAX_CHUNKS 64
+__global__ __launch_bounds__(256) void k_argmax_part(const float *logits, uint64_t ld, uint32_t n, uint64_t *part)
+{
+    __shared__ uint64_t sh[4];
+    const float *r = logits + (uint64_t)blockIdx.y * ld;
+    const uint32_t per = (n + AMAX_CHUNKS - 1) / AMAX_CHUNKS;
+    const uint32_t lo = blockIdx.x * per, hi = min(n, lo + per);
+    uint64_t best = 0;
+    for (uint32_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+        const uint64_t k = akey(r[i], i);
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int o = 32; o; o >>= 1) {
+        const uint64_t k = __shfl_xor(best, o);
+        best = k > best ? k : best;
+    }
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = sh[0];
+        for (int i = 1; i < 4; i++) b = sh[i] > b ? sh[i] : b;
+        part[(uint64_t)blockIdx.y * AMAX_CHUNKS + blockIdx.x] = b;
+    }
+}
+
+__global__ void k_argmax_final(const uint64_t *part, uint32_t *out)
+{
+    uint64_t b = part[(uint64_t)blockIdx.x * AMAX_CHUNKS + threadIdx.x];
+#pragma unroll
+    for (int o = 32; o; o >>= 1) {
+        const uint64_t k = __shfl_xor(b, o);
+        b = k > b ? k : b;
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = 0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu);
+}
+
+// ---------------------------------------------------------------- C-ABI
+static int ensure_small()
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!qg::ws_small) QG_CHECK(hipMalloc(&qg::ws_small, 65536));
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_rmsnorm(float *out, uint64_t ldo, const float *x, uint64_t ldx, const float *w, uint64_t n,
+                            int rows, float eps)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!out || !x || !n || rows < 0) return QGPU_E_ARG;
+    if (!rows) return QGPU_OK;
+    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(256), 0, qg::stream, out, ldo, x, ldx, w, n, eps);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_l2norm(float *out, uint64_t ldo, const float *x, uint64_t ldx, uint64_t n, int rows, float eps)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!out || !x || !n || rows < 0) return QGPU_E_ARG;
+    if (!rows) return QGPU_OK;
+    hipLaunchKernelGGL(k_l2norm, dim3(rows), dim3(256), 0, qg::stream, out, ldo, x, ldx, n, eps);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+static int unary(float *x, uint64_t n, int op)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!x) return QGPU_E_ARG;
+    if (!n) return QGPU_OK;
+    hipLaunchKernelGGL(k_unary, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, qg::stream, x, n, op);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+extern "C" int qgpu_silu(float *x, uint64_t n) { return unary(x, n, 0); }
+extern "C" int qgpu_sigmoid(float *x, uint64_t n) { return unary(x, n, 1); }
+extern "C" int qgpu_softplus(float *x, uint64_t n) { return unary(x, n, 2); }
+
+extern "C" int qgpu_softmax(float *x, uint64_t ld, uint64_t n, int rows)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!x || rows < 0) return QGPU_E_ARG;
+    if (!rows || !n) return QGPU_OK;
+    hipLaunchKernelGGL(k_softmax, dim3(rows), dim3(256), 0, qg::stream, x, ld, n);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_silu_mul(float *a, uint64_t lda, const float *b, uint64_t ldb, uint64_t n, int rows)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!a || !b || rows < 0) return QGPU_E_ARG;
+    if (!rows || !n) return QGPU_OK;
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256), rows), dim3(256), 0, qg::stream, a, lda, b, ldb, n);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_add(float *y, uint64_t ldy, const float *x, uint64_t ldx, uint64_t n, int rows)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!y || !x || rows < 0) return QGPU_E_ARG;
+    if (!rows || !n) return QGPU_OK;
+    hipLaunchKernelGGL(k_add, dim3((unsigned)((n + 255) / 256), rows), dim3(256), 0, qg::stream, y, ldy, x, ldx, n);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_argmax(const float *logits, uint64_t ld, uint32_t n, int rows, uint32_t *out)
+{
+    int rc = ensure_small();
+    if (rc) return rc;
+    if (!logits || !out || !n || rows < 0 || rows > 64) return rows > 64 ? QGPU_E_RANGE : QGPU_E_ARG;
+    if (!rows) return QGPU_OK;
+    uint64_t *part = (uint64_t *)qg::ws_small;
+    hipLaunchKernelGGL(k_argmax_part, dim3(AMAX_CHUNKS, rows), dim3(256), 0, qg::stream, logits, ld, n, part);
+    QG_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_argmax_final, dim3(rows), dim3(64), 0, qg::stream, (const uint64_t *)part, out);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
