@@ -84,6 +84,11 @@ int  qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
  * Replaces gemv_multi_batch / gemv_multi (reference kernels.c:666-736). */
 int  qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx,
                            int n, float *const *outs, const uint64_t *ldos, int flags);
+/* Split form of the IQ4_XS path: qgpu_gemv_prepare converts the activations
+ * once (x: n rows of ne0 floats) and qgpu_gemv_prepared runs an IQ4_XS matrix
+ * with ne0 columns on them; several matrices may follow one prepare. */
+int  qgpu_gemv_prepare(const float *x, uint64_t ldx, int n, uint64_t ne0);
+int  qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, int flags);
 /* Rows [r0, r1) only (reference gemv_rows, kernels.c:298-321). */
 int  qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
                           float *out, uint64_t ldo, uint64_t r0, uint64_t r1);
@@ -110,6 +115,8 @@ int  qgpu_softmax(float *x, uint64_t ld, uint64_t n, int rows);
 int  qgpu_silu_mul(float *a, uint64_t lda, const float *b, uint64_t ldb, uint64_t n, int rows);
 /* rows x n: y[r*ldy+i] += x[r*ldx+i]  (residual add) */
 int  qgpu_add(float *y, uint64_t ldy, const float *x, uint64_t ldx, uint64_t n, int rows);
+/* device copy kernel (16-byte aligned, multiple of 16 bytes); graph-capturable */
+int  qgpu_copy(void *dst, const void *src, size_t bytes);
 /* argmax of each of `rows` rows (lowest index wins ties; model.c:746-756) into out[r] */
 int  qgpu_argmax(const float *logits, uint64_t ld, uint32_t n, int rows, uint32_t *out);
 

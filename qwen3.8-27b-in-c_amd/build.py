@@ -27,6 +27,8 @@ ARCH = "gfx950"
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{INC}", f"-I{os.path.join(PKG, 'csrc')}",
              # packed-FP32 VALU ops stay off: scalar/float2 code only
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             # matrix-core results in VGPRs (no v_accvgpr_read per result)
+             "-mllvm", "-amdgpu-mfma-vgpr-form",
              "-Wall", "-Wno-unused-function", "-Wno-unused-variable"]
 CC_FLAGS = ["-O2", "-std=c11", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter", f"-I{INC}"]
 

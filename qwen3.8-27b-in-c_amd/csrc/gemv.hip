@@ -19,6 +19,7 @@
 // Other formats (Q4_K/Q5_K/Q6_K/Q8_0/F32: embeddings, lm_head, eh_proj of the
 // real checkpoint) use a VALU kernel on the GGUF layout.
 #include "qgpu_internal.h"
+#include <stdlib.h>
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -32,6 +33,46 @@ size_t qg_gemv_workspace_bytes() { return 2 * PLANE_BYTES + 2 * XS_FLOATS * size
 static __device__ __forceinline__ float h2f(uint32_t h16) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h16); }
 
 // ---------------------------------------------------------------- repack
+// Row header re-arrangement (lossless, same 8 bytes).  GGUF: d | scales_h | scales_l[4]
+// with ls_ib = nibble ib of scales_l | 2 bits ib of scales_h << 4.  Packed: the
+// six-bit two's-complement value s_ib = ls_ib ^ 32 (= ls_ib - 32 mod 64) of
+// every sub-block at a fixed bit offset, so one signed bit-field extract yields
+// (ls - 32):
+//   x = d | s5 << 16 | s6 << 22 | (s7 & 15) << 28
+//   y = s0 | s1 << 6 | s2 << 12 | s3 << 18 | s4 << 24 | (s7 >> 4) << 30
+static __device__ __forceinline__ uint2 hdr_pack(uint2 raw)
+{
+    const uint32_t sh = raw.x >> 16, sl = raw.y;
+    uint32_t sv[8];
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) sv[ib] = ((((sl >> (4 * ib)) & 15u) | (((sh >> (2 * ib)) & 3u) << 4)) ^ 32u);
+    uint2 o;
+    o.x = (raw.x & 0xFFFFu) | (sv[5] << 16) | (sv[6] << 22) | ((sv[7] & 15u) << 28);
+    o.y = sv[0] | (sv[1] << 6) | (sv[2] << 12) | (sv[3] << 18) | (sv[4] << 24) | ((sv[7] >> 4) << 30);
+    return o;
+}
+static __device__ __forceinline__ uint32_t hdr_s6(uint2 h, int ib)   // unsigned 6-bit s_ib
+{
+    if (ib < 5) return (h.y >> (6 * ib)) & 63u;
+    if (ib < 7) return (h.x >> (16 + 6 * (ib - 5))) & 63u;
+    return (h.x >> 28) | ((h.y >> 30) << 4);
+}
+static __device__ __forceinline__ int hdr_scale(uint2 h, int ib)     // ls_ib - 32
+{
+    return ((int)(hdr_s6(h, ib) << 26)) >> 26;
+}
+static __device__ __forceinline__ uint2 hdr_unpack(uint2 h)
+{
+    uint32_t sh = 0, sl = 0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) {
+        const uint32_t ls = hdr_s6(h, ib) ^ 32u;
+        sl |= (ls & 15u) << (4 * ib);
+        sh |= (ls >> 4) << (2 * ib);
+    }
+    return make_uint2((h.x & 0xFFFFu) | (sh << 16), sl);
+}
+
 // raw (GGUF rows of nsb 136-byte super-blocks) <-> tile records.
 // packed dword (row n, lane group g, sub-block ib) of record (T, s) at
 //   128 + ((ib/4)*64 + g*16 + n)*16 + (ib%4)*4  and holds qs bytes 4g..4g+3 of sub-block ib.
@@ -49,7 +90,7 @@ __global__ void k_repack_iq4(const uint8_t *__restrict__ raw, uint8_t *__restric
     if (unpack) {
         if (r >= ne1) return;
         uint8_t *blk = (uint8_t *)raw + r * rb + (uint64_t)s * 136;
-        *(uint2 *)blk = *(const uint2 *)(rec + n * 8);
+        *(uint2 *)blk = hdr_unpack(*(const uint2 *)(rec + n * 8));
         for (int ib = 0; ib < 8; ib++)
             for (int g = 0; g < 4; g++)
                 *(uint32_t *)(blk + 8 + 16 * ib + 4 * g) =
@@ -58,7 +99,7 @@ __global__ void k_repack_iq4(const uint8_t *__restrict__ raw, uint8_t *__restric
     }
     const uint8_t *blk = raw + r * rb + (uint64_t)s * 136;
     const bool live = r < ne1;
-    *(uint2 *)(rec + n * 8) = live ? *(const uint2 *)blk : make_uint2(0, 0);
+    *(uint2 *)(rec + n * 8) = live ? hdr_pack(*(const uint2 *)blk) : make_uint2(0, 0);
     for (int ib = 0; ib < 8; ib++)
         for (int g = 0; g < 4; g++)
             *(uint32_t *)(rec + IQ4_HDR_BYTES + ((ib / 4) * 64 + g * 16 + n) * 16 + (ib % 4) * 4) =
@@ -165,6 +206,66 @@ static __device__ __forceinline__ void iq4_decode8(uint32_t q, uint32_t &lo, uin
     hi = __builtin_amdgcn_perm(b, a, ((q4 >> 1) & 0x04040404u) | 0x03020100u);
 }
 
+template <int NA>
+struct IQ4Stage {
+    uint2 hdr;
+    uint4 qa, qb;
+    uint4 av[NA][4];
+    float4 xv[NA];
+};
+
+template <int NA>
+static __device__ __forceinline__ void iq4_load(IQ4Stage<NA> &st, const uint8_t *rec, const uint8_t *Aall,
+                                                const float *xs, int sb, int lane, int n, int g)
+{
+    st.hdr = *(const uint2 *)(rec + n * 8);
+    st.qa = *(const uint4 *)(rec + IQ4_HDR_BYTES + lane * 16);
+    st.qb = *(const uint4 *)(rec + IQ4_HDR_BYTES + (64 + lane) * 16);
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+        const uint8_t *Ab = Aall + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * 4096 + lane * 16;
+#pragma unroll
+        for (int p = 0; p < 4; p++) st.av[a][p] = *(const uint4 *)(Ab + p * 1024);
+        st.xv[a] = *(const float4 *)(xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16 + 4 * g);
+    }
+}
+
+template <int NA>
+static __device__ __forceinline__ void iq4_compute(const IQ4Stage<NA> &st, float (&accf)[NA][4])
+{
+    const uint32_t qd[8] = { st.qa.x, st.qa.y, st.qa.z, st.qa.w, st.qb.x, st.qb.y, st.qb.z, st.qb.w };
+    v4i acci[NA];
+#pragma unroll
+    for (int a = 0; a < NA; a++) acci[a] = (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) {
+        uint32_t lo, hi;
+        iq4_decode8(qd[ib], lo, hi);
+        const long bop = (long)(((uint64_t)hi << 32) | lo);
+        const int wsc = hdr_scale(st.hdr, ib);
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            const uint4 q4 = st.av[a][ib >> 1];
+            const long aop = (ib & 1) ? (long)(((uint64_t)q4.w << 32) | q4.z)
+                                      : (long)(((uint64_t)q4.y << 32) | q4.x);
+            const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            // |D| < 2^19, |wsc| <= 32: exact 24-bit multiply-add
+#pragma unroll
+            for (int i = 0; i < 4; i++) acci[a][i] = __mul24(D[i], wsc) + acci[a][i];
+        }
+    }
+    const float d = h2f(st.hdr.x & 0xFFFFu);
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+        accf[a][0] += (float)acci[a][0] * (d * st.xv[a].x);
+        accf[a][1] += (float)acci[a][1] * (d * st.xv[a].y);
+        accf[a][2] += (float)acci[a][2] * (d * st.xv[a].z);
+        accf[a][3] += (float)acci[a][3] * (d * st.xv[a].w);
+    }
+}
+
+#define IQ4_DEPTH 3     // super-blocks in flight per wave
+
 template <int NA, int NW>
 __global__ __launch_bounds__(NW * 64) void k_gemv_iq4(const GemvArgs args)
 {
@@ -185,47 +286,23 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_iq4(const GemvArgs args)
 #pragma unroll
         for (int i = 0; i < 4; i++) accf[a][i] = 0.0f;
 
-    for (int sb = sb0; sb < sb1; sb++) {
-        const uint8_t *rec = rec0 + (uint64_t)sb * IQ4_REC_BYTES;
-        const uint2 hdr = *(const uint2 *)(rec + n * 8);
-        const uint4 qa = *(const uint4 *)(rec + IQ4_HDR_BYTES + lane * 16);
-        const uint4 qb = *(const uint4 *)(rec + IQ4_HDR_BYTES + (64 + lane) * 16);
-        uint4 av[NA][4];
-        float4 xv[NA];
+    // ring of IQ4_DEPTH register stages: super-block sb+IQ4_DEPTH-1 is loading
+    // while sb is decoded and multiplied (indices are compile-time after unrolling)
+    IQ4Stage<NA> st[IQ4_DEPTH];
 #pragma unroll
-        for (int a = 0; a < NA; a++) {
-            const uint8_t *Ab = args.A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * 4096 + lane * 16;
+    for (int d = 0; d < IQ4_DEPTH - 1; d++)
+        if (sb0 + d < sb1)
+            iq4_load<NA>(st[d], rec0 + (uint64_t)(sb0 + d) * IQ4_REC_BYTES, args.A, args.xs, sb0 + d, lane, n, g);
+    for (int sb = sb0; sb < sb1; sb += IQ4_DEPTH) {
 #pragma unroll
-            for (int p = 0; p < 4; p++) av[a][p] = *(const uint4 *)(Ab + p * 1024);
-            xv[a] = *(const float4 *)(args.xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16 + 4 * g);
-        }
-        const uint32_t qd[8] = { qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w };
-        const uint32_t sh = hdr.x >> 16, sl = hdr.y;
-        v4i acci[NA];
-#pragma unroll
-        for (int a = 0; a < NA; a++) acci[a] = (v4i){0, 0, 0, 0};
-#pragma unroll
-        for (int ib = 0; ib < 8; ib++) {
-            uint32_t lo, hi;
-            iq4_decode8(qd[ib], lo, hi);
-            const long bop = (long)(((uint64_t)hi << 32) | lo);
-            const int wsc = (int)(((sl >> (4 * ib)) & 15u) | (((sh >> (2 * ib)) & 3u) << 4)) - 32;
-#pragma unroll
-            for (int a = 0; a < NA; a++) {
-                const uint4 q4 = av[a][ib >> 1];
-                const long aop = (ib & 1) ? (long)(((uint64_t)q4.w << 32) | q4.z)
-                                          : (long)(((uint64_t)q4.y << 32) | q4.x);
-                const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, (v4i){0, 0, 0, 0}, 0, 0, 0);
-                acci[a] += D * wsc;
+        for (int d = 0; d < IQ4_DEPTH; d++) {
+            if (sb + d < sb1) {
+                const int pf = sb + d + IQ4_DEPTH - 1;
+                if (pf < sb1)
+                    iq4_load<NA>(st[(d + IQ4_DEPTH - 1) % IQ4_DEPTH], rec0 + (uint64_t)pf * IQ4_REC_BYTES, args.A,
+                                 args.xs, pf, lane, n, g);
+                iq4_compute<NA>(st[d], accf);
             }
-        }
-        const float d = h2f(hdr.x & 0xFFFFu);
-#pragma unroll
-        for (int a = 0; a < NA; a++) {
-            accf[a][0] += (float)acci[a][0] * (d * xv[a].x);
-            accf[a][1] += (float)acci[a][1] * (d * xv[a].y);
-            accf[a][2] += (float)acci[a][2] * (d * xv[a].z);
-            accf[a][3] += (float)acci[a][3] * (d * xv[a].w);
         }
     }
     // lanes n, n+16, n+32, n+48 hold digits 0..3 of the same (token, row): sum them
@@ -239,8 +316,8 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_iq4(const GemvArgs args)
             if (g == 0) red[wv][a][i][n] = v;
         }
     __syncthreads();
-    if (tid < NA * 64) {
-        const int a = tid >> 6, i = (tid >> 4) & 3, nn = tid & 15;
+    for (int e = tid; e < NA * 64; e += NW * 64) {     // (plane, token, row) entries of the tile
+        const int a = e >> 6, i = (e >> 4) & 3, nn = e & 15;
         float s = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; w++) s += red[w][a][i][nn];
@@ -395,9 +472,19 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
 }
 
 // ---------------------------------------------------------------- launchers
+static int prep_x(const float *x, uint64_t ldx, int n, uint64_t ne0)
+{
+    if (ne0 > MAX_K || ne0 % 256) return QGPU_E_RANGE;
+    const int na = n > 4 ? 2 : 1;
+    hipLaunchKernelGGL(k_prep_digits, dim3((unsigned)(ne0 / 256), (unsigned)na), dim3(256), 0, qg::stream,
+                       x, ldx, n, (uint8_t *)qg::ws, (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES));
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
 static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x, uint64_t ldx,
                         int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
-                        const uint64_t *r1s)
+                        const uint64_t *r1s, int prepared)
 {
     const qgpu_tensor *W0 = Ws[idx[0]];
     GemvArgs A = {};
@@ -426,11 +513,29 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
         const int na = n > 4 ? 2 : 1;
         A.A = (const uint8_t *)qg::ws;
         A.xs = (const float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES);
-        hipLaunchKernelGGL(k_prep_digits, dim3((unsigned)A.nsb, (unsigned)na), dim3(256), 0, qg::stream,
-                           x, ldx, n, (uint8_t *)qg::ws, (float *)A.xs);
-        QG_LAUNCH_CHECK();
-        if (na == 1) hipLaunchKernelGGL((k_gemv_iq4<1, 4>), dim3(tiles), dim3(256), 0, qg::stream, A);
-        else hipLaunchKernelGGL((k_gemv_iq4<2, 4>), dim3(tiles), dim3(256), 0, qg::stream, A);
+        if (!prepared) {
+            const int rc = prep_x(x, ldx, n, W0->ne0);
+            if (rc) return rc;
+        }
+        // waves per tile (K split inside the block).  Measured on MI355X over the
+        // model's shapes (K = 5120..17408, 5120..248320 rows, B = 1..8): 4 waves is
+        // best or within 1% everywhere except very tall matrices (lm_head), where
+        // 2 is marginally better.  QGPU_GEMV_NW=1|2|4|8 forces the split.
+        static int force_nw = -1;
+        if (force_nw < 0) {
+            const char *e = getenv("QGPU_GEMV_NW");
+            force_nw = e ? atoi(e) : 0;
+        }
+        int nw = tiles >= 8192 ? 2 : 4;
+        if (force_nw == 1 || force_nw == 2 || force_nw == 4 || force_nw == 8) nw = force_nw;
+        while (nw > 1 && A.nsb < nw) nw >>= 1;              // no idle waves on short K
+#define IQ4_GO(NA_, NW_) hipLaunchKernelGGL((k_gemv_iq4<NA_, NW_>), dim3(tiles), dim3(64 * NW_), 0, qg::stream, A)
+        if (na == 1) {
+            if (nw == 1) IQ4_GO(1, 1); else if (nw == 2) IQ4_GO(1, 2); else if (nw == 4) IQ4_GO(1, 4); else IQ4_GO(1, 8);
+        } else {
+            if (nw == 1) IQ4_GO(2, 1); else if (nw == 2) IQ4_GO(2, 2); else if (nw == 4) IQ4_GO(2, 4); else IQ4_GO(2, 8);
+        }
+#undef IQ4_GO
         QG_LAUNCH_CHECK();
         return QGPU_OK;
     }
@@ -457,10 +562,12 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
 }
 
 static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx, int n,
-                      float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s)
+                      float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s,
+                      int prepared = 0)
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
+    if (prepared && !x) x = (const float *)qg::ws;           // activations already in the workspace
     if (!Ws || !x || !outs || !ldos || n_mat < 1 || n_mat > QGPU_MAX_MULTI || n < 1 || n > QGPU_MAX_B)
         return QGPU_E_ARG;
     for (int j = 0; j < n_mat; j++) {
@@ -476,7 +583,7 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const float *x, u
         int idx[QGPU_MAX_MULTI], cnt = 0;
         for (int i = j; i < n_mat; i++)
             if (!done[i] && Ws[i]->type == Ws[j]->type) { idx[cnt++] = i; done[i] = 1; }
-        rc = launch_group(Ws, idx, cnt, x, ldx, n, outs, ldos, flags, r0s, r1s);
+        rc = launch_group(Ws, idx, cnt, x, ldx, n, outs, ldos, flags, r0s, r1s, prepared && Ws[j]->type == T_IQ4_XS);
         if (rc) return rc;
     }
     return QGPU_OK;
@@ -492,6 +599,20 @@ extern "C" int qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, co
                                      float *const *outs, const uint64_t *ldos, int flags)
 {
     return gemv_multi(Ws, n_mat, x, ldx, n, outs, ldos, flags, nullptr, nullptr);
+}
+
+extern "C" int qgpu_gemv_prepare(const float *x, uint64_t ldx, int n, uint64_t ne0)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!x || n < 1 || n > QGPU_MAX_B || ldx < ne0 || ldx % 4 || ((uintptr_t)x & 15)) return QGPU_E_ARG;
+    return prep_x(x, ldx, n, ne0);
+}
+
+extern "C" int qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, int flags)
+{
+    if (!W || W->type != T_IQ4_XS) return QGPU_E_TYPE;
+    return gemv_multi(&W, 1, nullptr, W->ne0, n, &out, &ldo, flags, nullptr, nullptr, 1);
 }
 
 extern "C" int qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
@@ -520,8 +641,7 @@ __global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t *__restrict_
             const uint8_t *rec = W + ((uint64_t)(r / IQ4_TILE_ROWS) * nsb + sb) * IQ4_REC_BYTES;
             const uint32_t n = r % IQ4_TILE_ROWS;
             const uint2 hdr = *(const uint2 *)(rec + n * 8);
-            const int ls = (int)(((hdr.y >> (4 * ib)) & 15u) | (((hdr.x >> 16 >> (2 * ib)) & 3u) << 4));
-            const float dl = __fmul_rn(h2f(hdr.x & 0xFFFFu), (float)(ls - 32));
+            const float dl = __fmul_rn(h2f(hdr.x & 0xFFFFu), (float)hdr_scale(hdr, (int)ib));
             const int8_t kv[16] = { -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113 };
 #pragma unroll
             for (int g = 0; g < 4; g++) {

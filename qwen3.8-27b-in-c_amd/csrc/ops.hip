@@ -155,7 +155,26 @@ __global__ void k_argmax_final(const uint64_t *part, uint32_t *out)
     if (threadIdx.x == 0) out[blockIdx.x] = 0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFu);
 }
 
+__global__ void k_copy(uint4 *__restrict__ d, const uint4 *__restrict__ s, uint64_t n16)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * blockDim.x)
+        d[i] = s[i];
+}
+
 // ---------------------------------------------------------------- C-ABI
+extern "C" int qgpu_copy(void *dst, const void *src, size_t bytes)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!dst || !src || bytes % 16 || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15)) return QGPU_E_ARG;
+    if (!bytes) return QGPU_OK;
+    const uint64_t n16 = bytes / 16;
+    const unsigned grid = (unsigned)(n16 / 256 < 8192 ? (n16 + 255) / 256 : 8192);
+    hipLaunchKernelGGL(k_copy, dim3(grid), dim3(256), 0, qg::stream, (uint4 *)dst, (const uint4 *)src, n16);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
 static int ensure_small()
 {
     int rc = qg::ensure_init();

@@ -238,6 +238,8 @@ class GpuLib:
             "qgpu_silu_mul": [F32P, u64, F32P, u64, u64, i32],
             "qgpu_add": [F32P, u64, F32P, u64, u64, i32],
             "qgpu_argmax": [F32P, u64, ctypes.c_uint32, i32, U32P],
+            "qgpu_gemv_prepare": [F32P, u64, i32, u64], "qgpu_gemv_prepared": [vp, i32, F32P, u64, i32],
+            "qgpu_copy": [vp, vp, ctypes.c_size_t],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)
