@@ -120,6 +120,52 @@ int  qgpu_copy(void *dst, const void *src, size_t bytes);
 /* argmax of each of `rows` rows (lowest index wins ties; model.c:746-756) into out[r] */
 int  qgpu_argmax(const float *logits, uint64_t ld, uint32_t n, int rows, uint32_t *out);
 
+/* ------------------------------------------------------------ Gated DeltaNet (model.c:494-615,845-941) */
+/* Recurrent state is kept in a ring of `nslot` slots of `slot_stride` floats:
+ * the current state is slot *cur (device int); the state after token b of a
+ * batch goes to slot (*cur + 1 + b) % nslot.  Rolling back to the state after
+ * token j (reference model_rollback_to, model.c:1015-1031) is *cur = (*cur+1+j) % nslot. */
+/* causal conv1d (4 taps) + SiLU of B <= 8 tokens: y[b] = silu(conv(state, x[b])) (model.c:891-909) */
+int  qgpu_gdn_conv(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w, float *ring,
+                   uint64_t slot_stride, int nslot, const int *cur, float *y, uint64_t ldy);
+/* per-k-head L2 norm of q,k and the delta-rule recurrence over B tokens for all
+ * n_v v-heads (v-head h reads k-head h % n_k), head_dim 128 (model.c:494-595) */
+int  qgpu_gdn_recurrence(const float *xq, uint64_t ldq, const float *beta_raw, const float *alpha_raw,
+                         uint64_t ldba, const float *dt_bias, const float *ssm_a, float *ring,
+                         uint64_t slot_stride, int nslot, const int *cur, int B, int n_k, int n_v,
+                         int head_dim, float eps, float *out, uint64_t ldo);
+/* rows x n: out = rmsnorm(x, w) * silu(z)  (per-head gated norm, model.c:928-941) */
+int  qgpu_rmsnorm_gated(float *out, const float *x, const float *z, const float *w, int n, int rows,
+                        uint64_t ld, float eps);
+
+/* ------------------------------------------------------------ attention (model.c:318-406,760-810) */
+/* q: [B][n_head*2*head_dim] (q | gate per head) normed + RoPE'd in place; k, v:
+ * [B][n_kv*head_dim]; k normed + RoPE'd and v written to the caches at row
+ * *pos_dev + b.  RoPE tables [n_ctx][rope_dim/2] (cos, sin). head_dim 256. */
+int  qgpu_attn_prep(float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                    const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                    const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev, int B,
+                    int n_head, int n_kv, int head_dim, float eps);
+/* out[b][h*hd+d] = (softmax_{t <= pos+b}(q_bh . k_t / sqrt(hd)) V)[d] * sigmoid(gate_bh[d]);
+ * ctx_bound >= pos + B bounds the positions read (chunks beyond *pos_dev+B-1 exit). */
+int  qgpu_attn_decode(const float *q, uint64_t ldq, const float *kcache, const float *vcache,
+                      const int *pos_dev, int ctx_bound, int B, int n_head, int n_kv, int head_dim,
+                      float *out, uint64_t ldo);
+/* allocates the attention workspace for ctx_bound positions now (no allocation later) */
+int  qgpu_attn_reserve(int ctx_bound, int n_kv);
+
+/* ------------------------------------------------------------ driver helpers */
+/* *dst = value, stream-ordered (graph-capturable) */
+int  qgpu_set_i32(int *dst, int value);
+/* Greedy acceptance of one speculative cycle (main.c:191-217) on the device:
+ *   j = first i < k with vtok[i] != cand[i+1], else k  (force_j >= 0: j = min(force_j, k),
+ *   the benchmark's fixed-acceptance modes; -1 for greedy acceptance);
+ *   out[0] = j; out[1 .. j+1] = cand[0 .. j] (emitted tokens); out[j+2] = vtok[j] (next cand[0]);
+ *   *cur = (*cur + 1 + j) % nslot (GDN rollback);  *pos += j + 1 (next position).
+ * `vtok` are the argmax tokens of the B = k+1 verify rows (qgpu_argmax). */
+int  qgpu_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int *pos, int *cur,
+                      int nslot, uint32_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -720,10 +720,12 @@ static void prefill(or_model_t *m, const uint32_t *prompt, uint32_t n, int with_
                (size_t)m->cfg.vocab_size * sizeof(float));
 }
 
-/* main.c:158-231 greedy MTP speculative decode */
-uint32_t or_generate_spec(or_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
-                          uint32_t k_req, uint32_t eos, uint32_t *out, or_spec_stats_t *stt,
-                          uint32_t *cycle_j)
+/* main.c:158-231 greedy MTP speculative decode.  force_accept (not in the
+ * reference) fixes j: 1 = k every cycle (all drafts accepted), 2 = cycle index
+ * mod (k + 1) (every rollback depth in turn). */
+uint32_t or_generate_spec_ex(or_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                             uint32_t k_req, uint32_t eos, int force_accept, uint32_t *out, or_spec_stats_t *stt,
+                             uint32_t *cycle_j)
 {
     const uint32_t V = m->cfg.vocab_size, ne = m->n_embd;
     if (k_req > m->k_max) k_req = m->k_max;
@@ -746,8 +748,11 @@ uint32_t or_generate_spec(or_model_t *m, const uint32_t *prompt, uint32_t n_prom
         const uint32_t B = k + 1;
         or_model_forward_batch(m, cand, P + 1, B, 1);
         uint32_t j = k;
-        for (uint32_t i = 0; i < k; i++)
-            if (or_argmax(m->logits_b + (size_t)i * V, V) != cand[i + 1]) { j = i; break; }
+        if (force_accept == 2)
+            j = (uint32_t)(s.n_cycles % (k + 1));
+        else
+            for (uint32_t i = 0; i < k && !force_accept; i++)
+                if (or_argmax(m->logits_b + (size_t)i * V, V) != cand[i + 1]) { j = i; break; }
         for (uint32_t i = 0; i <= j && gen < n_predict; i++) out[gen++] = cand[i];
         if (cycle_j) cycle_j[s.n_cycles] = j;
         s.n_accepted += j;
@@ -764,6 +769,12 @@ uint32_t or_generate_spec(or_model_t *m, const uint32_t *prompt, uint32_t n_prom
     }
     if (stt) *stt = s;
     return gen;
+}
+
+uint32_t or_generate_spec(or_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                          uint32_t k, uint32_t eos, uint32_t *out, or_spec_stats_t *st, uint32_t *cycle_j)
+{
+    return or_generate_spec_ex(m, prompt, n_prompt, n_predict, k, eos, 0, out, st, cycle_j);
 }
 
 /* Plain greedy stream used as the lossless-spec oracle: argmax of model_forward

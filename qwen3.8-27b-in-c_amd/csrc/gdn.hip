@@ -1,0 +1,182 @@
+// Gated DeltaNet verify block (gfx950): causal conv1d + SiLU, per-k-head L2
+// norm and the delta-rule recurrence over B tokens, with one state snapshot
+// per token (reference model.c:494-615, 845-941).
+//
+// Recurrent state lives in a ring of `nslot` slots per layer: the current
+// state is slot *cur, and the state after token b of a batch is written to
+// slot (*cur + 1 + b) % nslot, never over the current one.  Rolling back to
+// "state after token j" (reference model_rollback_to, model.c:1015-1031, a
+// 152 MB copy) is setting *cur to (*cur + 1 + j) % nslot.
+#include "qgpu_internal.h"
+
+#define GDN_MAXB 8
+#define GDN_HK   128          // head_k_dim = head_v_dim (= ssm state size)
+#define GDN_RB   16           // state rows per block
+
+static __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+
+// one thread per channel: 4-tap causal conv over the sliding window, SiLU, snapshots
+__global__ __launch_bounds__(256) void k_gdn_conv(const float *__restrict__ x, uint64_t ldx, int B, int conv_dim,
+                                                  const float *__restrict__ w, float *__restrict__ ring,
+                                                  uint64_t stride, int nslot, const int *__restrict__ cur_dev,
+                                                  float *__restrict__ y, uint64_t ldy)
+{
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= conv_dim) return;
+    const int cur = *cur_dev;
+    const float4 s0 = *(const float4 *)(ring + (uint64_t)cur * stride + (uint64_t)c * 4);
+    const float4 wc = *(const float4 *)(w + (uint64_t)c * 4);
+    float win[4 + GDN_MAXB];
+    win[0] = s0.x; win[1] = s0.y; win[2] = s0.z; win[3] = s0.w;
+#pragma unroll
+    for (int b = 0; b < GDN_MAXB; b++) {
+        if (b >= B) break;
+        win[4 + b] = x[(uint64_t)b * ldx + c];
+        const float a0 = win[b + 1], a1 = win[b + 2], a2 = win[b + 3], a3 = win[b + 4];
+        const float acc = ((a0 * wc.x + a1 * wc.y) + a2 * wc.z) + a3 * wc.w;
+        y[(uint64_t)b * ldy + c] = silu_f(acc);
+        const int slot = (cur + 1 + b) % nslot;
+        *(float4 *)(ring + (uint64_t)slot * stride + (uint64_t)c * 4) = make_float4(a0, a1, a2, a3);
+    }
+}
+
+// sum over the 16 lanes of a row group (lanes 16r .. 16r+15 of the wave)
+static __device__ __forceinline__ float sum16(float v)
+{
+#pragma unroll
+    for (int o = 8; o; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// block = 16 state rows of one v-head; thread (row r = tid/16, column chunk cc = tid%16, 8 columns)
+__global__ __launch_bounds__(256) void k_gdn_recur(const float *__restrict__ xq, uint64_t ldq,
+                                                   const float *__restrict__ beta_raw,
+                                                   const float *__restrict__ alpha_raw, uint64_t ldba,
+                                                   const float *__restrict__ dt_bias, const float *__restrict__ ssm_a,
+                                                   float *__restrict__ ring, uint64_t stride, int nslot,
+                                                   const int *__restrict__ cur_dev, int B, int n_k, int n_v,
+                                                   float eps, float *__restrict__ out, uint64_t ldo)
+{
+    const int h = blockIdx.x / (GDN_HK / GDN_RB);
+    const int rb = blockIdx.x % (GDN_HK / GDN_RB);
+    const int tid = threadIdx.x, r = tid >> 4, cc = tid & 15;
+    const int j = rb * GDN_RB + r;                   // state row (v index)
+    const int kh = h % n_k;                          // tiled v-head -> k-head map (model.c:565)
+    const int cur = *cur_dev;
+    const uint64_t hoff = (uint64_t)h * GDN_HK * GDN_HK + (uint64_t)j * GDN_HK + cc * 8;
+    const float *S0 = ring + (uint64_t)cur * stride + hoff;
+    float S[8];
+    {
+        const float4 a = *(const float4 *)S0, b = *(const float4 *)(S0 + 4);
+        S[0] = a.x; S[1] = a.y; S[2] = a.z; S[3] = a.w; S[4] = b.x; S[5] = b.y; S[6] = b.z; S[7] = b.w;
+    }
+    const float qscale = 1.0f / sqrtf((float)GDN_HK);
+    const float ah = ssm_a[h], dtb = dt_bias[h];
+    for (int b = 0; b < B; b++) {
+        const float *xb = xq + (uint64_t)b * ldq;
+        const float *qp = xb + kh * GDN_HK + cc * 8;
+        const float *kp = xb + n_k * GDN_HK + kh * GDN_HK + cc * 8;
+        float q[8], k[8];
+        {
+            const float4 q0 = *(const float4 *)qp, q1 = *(const float4 *)(qp + 4);
+            const float4 k0 = *(const float4 *)kp, k1 = *(const float4 *)(kp + 4);
+            q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w; q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
+            k[0] = k0.x; k[1] = k0.y; k[2] = k0.z; k[3] = k0.w; k[4] = k1.x; k[5] = k1.y; k[6] = k1.z; k[7] = k1.w;
+        }
+        float qq = 0.0f, kk = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) { qq = fmaf(q[i], q[i], qq); kk = fmaf(k[i], k[i], kk); }
+        qq = sum16(qq);
+        kk = sum16(kk);
+        const float qn = sqrtf(qq), kn = sqrtf(kk);
+        const float qs = 1.0f / (qn > eps ? qn : eps), ks = 1.0f / (kn > eps ? kn : eps);   // l2norm (kernels.c:780-805)
+        float kq = 0.0f, sk = 0.0f, sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            q[i] *= qs;
+            k[i] *= ks;
+            kq = fmaf(k[i], q[i], kq);
+            sk = fmaf(S[i], k[i], sk);
+            sq = fmaf(S[i], q[i], sq);
+        }
+        kq = sum16(kq);
+        sk = sum16(sk);
+        sq = sum16(sq);
+        const float beta = 1.0f / (1.0f + expf(-beta_raw[(uint64_t)b * ldba + h]));
+        const float araw = alpha_raw[(uint64_t)b * ldba + h] + dtb;
+        const float sp = araw > 30.0f ? araw : log1pf(expf(araw));
+        const float decay = expf(ah * sp);
+        const float vj = xb[2 * n_k * GDN_HK + (uint64_t)h * GDN_HK + j];
+        const float dj = (vj - decay * sk) * beta;
+        if (cc == 0) out[(uint64_t)b * ldo + (uint64_t)h * GDN_HK + j] = (decay * sq + dj * kq) * qscale;
+#pragma unroll
+        for (int i = 0; i < 8; i++) S[i] = fmaf(dj, k[i], decay * S[i]);
+        float *Sn = ring + (uint64_t)((cur + 1 + b) % nslot) * stride + hoff;
+        *(float4 *)Sn = make_float4(S[0], S[1], S[2], S[3]);
+        *(float4 *)(Sn + 4) = make_float4(S[4], S[5], S[6], S[7]);
+    }
+}
+
+// out[r] = rmsnorm(x[r], w) * silu(z[r]) for rows of n (per-head gated norm, model.c:928-941)
+__global__ __launch_bounds__(128) void k_rmsnorm_gated(float *out, const float *x, const float *z, const float *w,
+                                                       int n, uint64_t ld, float eps)
+{
+    __shared__ float sh[4];
+    const float *xr = x + (uint64_t)blockIdx.x * ld;
+    const float *zr = z + (uint64_t)blockIdx.x * ld;
+    float *orow = out + (uint64_t)blockIdx.x * ld;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(xr[i], xr[i], s);
+#pragma unroll
+    for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+    __syncthreads();
+    s = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += sh[i];
+    const float scale = 1.0f / sqrtf(s / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = ((xr[i] * scale) * w[i]) * silu_f(zr[i]);
+}
+
+extern "C" int qgpu_gdn_conv(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w, float *ring,
+                             uint64_t slot_stride, int nslot, const int *cur, float *y, uint64_t ldy)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!x || !conv_w || !ring || !cur || !y || B < 1 || B > GDN_MAXB || nslot < B + 1 || conv_dim < 1 ||
+        slot_stride < (uint64_t)conv_dim * 4 || ldx < (uint64_t)conv_dim || ldy < (uint64_t)conv_dim)
+        return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_gdn_conv, dim3((conv_dim + 255) / 256), dim3(256), 0, qg::stream, x, ldx, B, conv_dim,
+                       conv_w, ring, slot_stride, nslot, cur, y, ldy);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_gdn_recurrence(const float *xq, uint64_t ldq, const float *beta_raw, const float *alpha_raw,
+                                   uint64_t ldba, const float *dt_bias, const float *ssm_a, float *ring,
+                                   uint64_t slot_stride, int nslot, const int *cur, int B, int n_k, int n_v,
+                                   int head_dim, float eps, float *out, uint64_t ldo)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (head_dim != GDN_HK) return QGPU_E_RANGE;
+    if (!xq || !beta_raw || !alpha_raw || !dt_bias || !ssm_a || !ring || !cur || !out || B < 1 || B > GDN_MAXB ||
+        nslot < B + 1 || n_k < 1 || n_v < 1 || slot_stride < (uint64_t)n_v * GDN_HK * GDN_HK ||
+        ldq < (uint64_t)(2 * n_k + n_v) * GDN_HK || ldo < (uint64_t)n_v * GDN_HK || ldba < (uint64_t)n_v)
+        return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_gdn_recur, dim3(n_v * (GDN_HK / GDN_RB)), dim3(256), 0, qg::stream, xq, ldq, beta_raw,
+                       alpha_raw, ldba, dt_bias, ssm_a, ring, slot_stride, nslot, cur, B, n_k, n_v, eps, out, ldo);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_rmsnorm_gated(float *out, const float *x, const float *z, const float *w, int n, int rows,
+                                  uint64_t ld, float eps)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!out || !x || !z || !w || n < 1 || rows < 0 || ld < (uint64_t)n) return QGPU_E_ARG;
+    if (!rows) return QGPU_OK;
+    hipLaunchKernelGGL(k_rmsnorm_gated, dim3(rows), dim3(128), 0, qg::stream, out, x, z, w, n, ld, eps);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}

@@ -161,7 +161,47 @@ __global__ void k_copy(uint4 *__restrict__ d, const uint4 *__restrict__ s, uint6
         d[i] = s[i];
 }
 
+__global__ void k_set_i32(int *dst, int v) { *dst = v; }
+
+__global__ void k_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int *pos, int *cur,
+                              int nslot, uint32_t *out)
+{
+    int j = k;
+    if (force_j >= 0)
+        j = force_j < k ? force_j : k;
+    else
+        for (int i = 0; i < k; i++)
+            if (vtok[i] != cand[i + 1]) { j = i; break; }
+    out[0] = (uint32_t)j;
+    for (int i = 0; i <= j; i++) out[1 + i] = cand[i];
+    out[j + 2] = vtok[j];
+    *cur = (*cur + 1 + j) % nslot;
+    *pos = *pos + j + 1;
+}
+
 // ---------------------------------------------------------------- C-ABI
+extern "C" int qgpu_set_i32(int *dst, int value)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!dst) return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(1), 0, qg::stream, dst, value);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int *pos, int *cur,
+                                int nslot, uint32_t *out)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!cand || !vtok || !pos || !cur || !out || k < 0 || k > 15 || nslot < k + 2) return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(1), 0, qg::stream, cand, vtok, k, force_j, pos, cur, nslot,
+                       out);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
 extern "C" int qgpu_copy(void *dst, const void *src, size_t bytes)
 {
     int rc = qg::ensure_init();

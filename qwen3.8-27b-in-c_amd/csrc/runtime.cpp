@@ -101,7 +101,14 @@ extern "C" int qgpu_malloc(void **p, size_t bytes)
     return qg::check(hipMalloc(p, bytes ? bytes : 1));
 }
 
-extern "C" int qgpu_free(void *p) { return p ? qg::check(hipFree(p)) : QGPU_OK; }
+// Work queued on the library stream may still read the allocation: drain the
+// stream first, so a free is always safe right after an asynchronous call.
+extern "C" int qgpu_free(void *p)
+{
+    if (!p) return QGPU_OK;
+    if (qg::stream) QG_CHECK(hipStreamSynchronize(qg::stream));
+    return qg::check(hipFree(p));
+}
 
 extern "C" int qgpu_memcpy_h2d(void *d, const void *s, size_t n)
 {

@@ -1,0 +1,815 @@
+/*
+ * model.c -- the hybrid model on one MI355X behind the reference model.h API.
+ *
+ * Layer sequence per batched forward (B tokens, all buffers on the device):
+ *   GDN  : rmsnorm -> grouped GEMV {qkv, gate, beta, alpha} -> conv1d+SiLU
+ *          (snapshots) -> delta-rule recurrence (snapshots) -> gated rmsnorm
+ *          -> ssm_out GEMV accumulated into the residual -> FFN
+ *   attn : rmsnorm -> grouped GEMV {q, k, v} -> q/k norm + RoPE + KV write ->
+ *          flash-decoding attention with sigmoid gate -> attn_out GEMV
+ *          accumulated into the residual -> FFN
+ *   FFN  : rmsnorm -> grouped GEMV {gate, up} -> silu(gate)*up -> down GEMV
+ *          accumulated into the residual
+ * The order of operations follows the reference model.c:714-1103; binding
+ * and shape checks follow model.c:55-290.
+ */
+#define _POSIX_C_SOURCE 200809L
+#include "model.h"
+#include "qgpu.h"
+#include "quant.h"
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <time.h>
+
+#define NSLOT (SPEC_MAX_B + 1)      /* GDN state ring: current + one snapshot per batch token */
+#define MAXB  SPEC_MAX_B
+
+double qwen_prof_embed, qwen_prof_gdn, qwen_prof_attn, qwen_prof_head;
+uint64_t qwen_prof_calls;
+
+typedef struct {
+    int rec;
+    qgpu_tensor *ffn_gate, *ffn_up, *ffn_down, *q, *k, *v, *o, *wqkv, *wgate, *beta, *alpha, *ssm_out;
+    float *attn_norm, *post_norm, *q_norm, *k_norm, *conv1d, *dt_bias, *ssm_a, *ssm_norm;
+    float *kv_k, *kv_v;           /* attention: [n_ctx][n_kv*head_dim] */
+    float *conv_ring, *ssm_ring;  /* GDN: NSLOT slots of conv (conv_dim*4) / ssm (n_v*128*128) state */
+} glayer_t;
+
+struct qwen_gpu {
+    glayer_t *L, mtp;
+    qgpu_tensor *tok_embd, *output, *eh_proj;
+    float *out_norm, *enorm, *hnorm, *shnorm, *rope_cos, *rope_sin;
+    int *d_pos, *d_cur;
+    uint32_t *d_tok, *d_cand, *d_vtok, *d_acc;
+    float *bx, *bxb, *bqkv, *bk, *bv, *bz, *bbeta, *balpha, *bffn, *battn, *xq, *h_save, *logits_b, *logits1,
+          *mtp_h, *mx, *cat;
+    uint64_t SQ, A, conv_elems, ssm_elems, kvrow;
+    int cur, cur_base;
+    void **allocs;
+    size_t n_allocs, cap_allocs;
+    qgpu_tensor **tensors;
+    size_t n_tensors, cap_tensors;
+};
+
+static double now_s(void)
+{
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+static void fail_rc(const char *what, int rc)
+{
+    fprintf(stderr, "qwen gpu: %s failed: %s\n", what, qgpu_strerror(rc));
+    abort();
+}
+#define K(call) do { int _rc = (call); if (_rc) fail_rc(#call, _rc); } while (0)
+
+/* ------------------------------------------------------------------ allocation */
+static void *dalloc(qwen_gpu_t *g, size_t bytes)
+{
+    void *p = NULL;
+    if (qgpu_malloc(&p, bytes ? bytes : 16)) return NULL;
+    if (g->n_allocs == g->cap_allocs) {
+        g->cap_allocs = g->cap_allocs ? 2 * g->cap_allocs : 256;
+        g->allocs = realloc(g->allocs, g->cap_allocs * sizeof(void *));
+    }
+    g->allocs[g->n_allocs++] = p;
+    qgpu_memset(p, 0, bytes ? bytes : 16);
+    return p;
+}
+
+static void gpu_free(qwen_gpu_t *g)
+{
+    if (!g) return;
+    qgpu_sync();
+    for (size_t i = 0; i < g->n_tensors; i++) qgpu_tensor_free(g->tensors[i]);
+    for (size_t i = 0; i < g->n_allocs; i++) qgpu_free(g->allocs[i]);
+    free(g->tensors);
+    free(g->allocs);
+    free(g->L);
+    free(g);
+}
+
+/* ------------------------------------------------------------------ tensor sources */
+typedef struct {
+    const qwen_synth_spec_t *spec;    /* NULL: tensor bytes are t->data (mmap of a GGUF file) */
+} source_t;
+
+static const void *tensor_bytes(const source_t *src, const gguf_tensor_info_t *t, void **owned)
+{
+    *owned = NULL;
+    if (!src->spec) return t->data;
+    qwen_synth_tensor_t d;
+    if (qwen_synth_describe(src->spec, (uint32_t)t->offset, &d)) return NULL;
+    void *buf = malloc(d.nbytes ? d.nbytes : 1);
+    if (!buf || qwen_synth_fill(src->spec, (uint32_t)t->offset, buf)) { free(buf); return NULL; }
+    *owned = buf;
+    return buf;
+}
+
+static qgpu_tensor *up_matrix(qwen_gpu_t *g, const source_t *src, const gguf_tensor_info_t *t)
+{
+    void *own;
+    const void *bytes = tensor_bytes(src, t, &own);
+    if (!bytes) return NULL;
+    qgpu_tensor *T = NULL;
+    int rc = qgpu_tensor_upload(bytes, (int)t->type, t->ne[0], t->n_dims >= 2 ? t->ne[1] : 1, &T);
+    free(own);
+    if (rc) { fprintf(stderr, "model_init: upload of %s failed: %s\n", t->name, qgpu_strerror(rc)); return NULL; }
+    if (g->n_tensors == g->cap_tensors) {
+        g->cap_tensors = g->cap_tensors ? 2 * g->cap_tensors : 256;
+        g->tensors = realloc(g->tensors, g->cap_tensors * sizeof(qgpu_tensor *));
+    }
+    g->tensors[g->n_tensors++] = T;
+    return T;
+}
+
+static float *up_f32(qwen_gpu_t *g, const source_t *src, const gguf_tensor_info_t *t)
+{
+    if (t->type != GGML_F32) { fprintf(stderr, "model_init: %s must be F32\n", t->name); return NULL; }
+    const size_t n = (size_t)t->ne[0] * (t->n_dims >= 2 ? t->ne[1] : 1);
+    void *own;
+    const void *bytes = tensor_bytes(src, t, &own);
+    float *d = bytes ? dalloc(g, n * sizeof(float)) : NULL;
+    if (d && qgpu_memcpy_h2d(d, bytes, n * sizeof(float))) d = NULL;
+    free(own);
+    return d;
+}
+
+/* ------------------------------------------------------------------ binding (model.c:31-147,239-284) */
+static const gguf_tensor_info_t *need(const gguf_context_t *g, const char *name)
+{
+    const gguf_tensor_info_t *t = gguf_find_tensor(g, name);
+    if (!t) fprintf(stderr, "model_init: missing tensor %s\n", name);
+    return t;
+}
+static int bad2(const gguf_tensor_info_t *t, uint64_t a, uint64_t b, const char *what)
+{
+    if (!t) return 1;
+    if (t->n_dims != 2 || t->ne[0] != a || t->ne[1] != b) { fprintf(stderr, "model_init: %s dimension mismatch\n", what); return 1; }
+    return 0;
+}
+static int bad1(const gguf_tensor_info_t *t, uint64_t a, const char *what)
+{
+    if (!t) return 1;
+    if (t->n_dims != 1 || t->ne[0] != a) { fprintf(stderr, "model_init: %s dimension mismatch\n", what); return 1; }
+    return 0;
+}
+
+static int bind_layer(const gguf_context_t *G, qwen_layer_t *L, uint32_t il, const qwen_dims_t *d, int mtp)
+{
+    char nm[96];
+#define B_(field, fmt) do { snprintf(nm, sizeof nm, fmt, il); if (!(L->field = need(G, nm))) return -1; } while (0)
+    B_(attn_norm, "blk.%u.attn_norm.weight");
+    B_(post_attn_norm, "blk.%u.post_attention_norm.weight");
+    B_(ffn_gate, "blk.%u.ffn_gate.weight");
+    B_(ffn_up, "blk.%u.ffn_up.weight");
+    B_(ffn_down, "blk.%u.ffn_down.weight");
+    if (bad2(L->ffn_gate, d->n_embd, d->n_ff, "ffn_gate") || bad2(L->ffn_up, d->n_embd, d->n_ff, "ffn_up") ||
+        bad2(L->ffn_down, d->n_ff, d->n_embd, "ffn_down") || bad1(L->attn_norm, d->n_embd, "attn_norm") ||
+        bad1(L->post_attn_norm, d->n_embd, "post_attention_norm"))
+        return -1;
+    if (L->is_recurrent) {
+        B_(wqkv, "blk.%u.attn_qkv.weight"); B_(wqkv_gate, "blk.%u.attn_gate.weight");
+        B_(ssm_conv1d, "blk.%u.ssm_conv1d.weight"); B_(ssm_dt_bias, "blk.%u.ssm_dt.bias");
+        B_(ssm_a, "blk.%u.ssm_a"); B_(ssm_beta, "blk.%u.ssm_beta.weight");
+        B_(ssm_alpha, "blk.%u.ssm_alpha.weight"); B_(ssm_norm, "blk.%u.ssm_norm.weight");
+        B_(ssm_out, "blk.%u.ssm_out.weight");
+        if (bad2(L->wqkv, d->n_embd, d->conv_dim, "wqkv") || bad2(L->wqkv_gate, d->n_embd, d->d_inner, "wqkv_gate") ||
+            bad2(L->ssm_conv1d, d->d_conv, d->conv_dim, "ssm_conv1d") ||
+            bad2(L->ssm_beta, d->n_embd, d->n_v_heads, "ssm_beta") ||
+            bad2(L->ssm_alpha, d->n_embd, d->n_v_heads, "ssm_alpha") ||
+            bad2(L->ssm_out, d->d_inner, d->n_embd, "ssm_out") || bad1(L->ssm_dt_bias, d->n_v_heads, "ssm_dt_bias") ||
+            bad1(L->ssm_a, d->n_v_heads, "ssm_a") || bad1(L->ssm_norm, d->head_v_dim, "ssm_norm"))
+            return -1;
+    } else {
+        B_(attn_q, "blk.%u.attn_q.weight"); B_(attn_k, "blk.%u.attn_k.weight"); B_(attn_v, "blk.%u.attn_v.weight");
+        B_(attn_q_norm, "blk.%u.attn_q_norm.weight"); B_(attn_k_norm, "blk.%u.attn_k_norm.weight");
+        B_(attn_out, "blk.%u.attn_output.weight");
+        if (bad2(L->attn_q, d->n_embd, 2 * d->n_head * d->head_dim, "attn_q") ||
+            bad2(L->attn_k, d->n_embd, d->n_kv_head * d->head_dim, "attn_k") ||
+            bad2(L->attn_v, d->n_embd, d->n_kv_head * d->head_dim, "attn_v") ||
+            bad2(L->attn_out, d->n_head * d->head_dim, d->n_embd, "attn_out") ||
+            bad1(L->attn_q_norm, d->head_dim, "attn_q_norm") || bad1(L->attn_k_norm, d->head_dim, "attn_k_norm"))
+            return -1;
+    }
+#undef B_
+    (void)mtp;
+    return 0;
+}
+
+static int upload_layer(qwen_gpu_t *g, const source_t *src, const qwen_layer_t *L, glayer_t *D)
+{
+    D->rec = L->is_recurrent;
+    if (!(D->attn_norm = up_f32(g, src, L->attn_norm)) || !(D->post_norm = up_f32(g, src, L->post_attn_norm)) ||
+        !(D->ffn_gate = up_matrix(g, src, L->ffn_gate)) || !(D->ffn_up = up_matrix(g, src, L->ffn_up)) ||
+        !(D->ffn_down = up_matrix(g, src, L->ffn_down)))
+        return -1;
+    if (L->is_recurrent) {
+        if (!(D->wqkv = up_matrix(g, src, L->wqkv)) || !(D->wgate = up_matrix(g, src, L->wqkv_gate)) ||
+            !(D->beta = up_matrix(g, src, L->ssm_beta)) || !(D->alpha = up_matrix(g, src, L->ssm_alpha)) ||
+            !(D->ssm_out = up_matrix(g, src, L->ssm_out)) || !(D->conv1d = up_f32(g, src, L->ssm_conv1d)) ||
+            !(D->dt_bias = up_f32(g, src, L->ssm_dt_bias)) || !(D->ssm_a = up_f32(g, src, L->ssm_a)) ||
+            !(D->ssm_norm = up_f32(g, src, L->ssm_norm)))
+            return -1;
+    } else {
+        if (!(D->q = up_matrix(g, src, L->attn_q)) || !(D->k = up_matrix(g, src, L->attn_k)) ||
+            !(D->v = up_matrix(g, src, L->attn_v)) || !(D->o = up_matrix(g, src, L->attn_out)) ||
+            !(D->q_norm = up_f32(g, src, L->attn_q_norm)) || !(D->k_norm = up_f32(g, src, L->attn_k_norm)))
+            return -1;
+    }
+    return 0;
+}
+
+static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
+{
+    qwen_config_t *c = &m->cfg;
+    qwen_dims_t *d = &m->dims;
+    *c = m->gguf.config;
+    d->n_embd = c->n_embd; d->n_ff = c->n_ff; d->n_head = c->n_head; d->n_kv_head = c->n_head_kv;
+    d->head_dim = c->head_dim; d->n_k_heads = c->ssm_group_count; d->head_k_dim = d->head_v_dim = c->ssm_state_size;
+    d->d_inner = c->ssm_inner_size; d->d_conv = c->ssm_conv_kernel; d->d_state = c->ssm_state_size;
+    memcpy(d->rope_sections, c->rope_sections, sizeof d->rope_sections);
+    const gguf_tensor_info_t *a0 = gguf_find_tensor(&m->gguf, "blk.0.ssm_a");
+    if (!a0 || a0->n_dims != 1) { fprintf(stderr, "model_init: blk.0.ssm_a missing\n"); return -1; }
+    d->n_v_heads = (uint32_t)a0->ne[0];
+    d->conv_dim = 2 * d->n_k_heads * d->head_k_dim + d->d_inner;
+    d->n_layer = c->n_layer > c->nextn_layers ? c->n_layer - c->nextn_layers : c->n_layer;
+    if (d->d_inner != d->n_v_heads * d->head_v_dim || d->n_v_heads > 256 || d->head_v_dim > 256 ||
+        d->head_k_dim > 256 || !c->full_attn_interval) {
+        fprintf(stderr, "model_init: inconsistent GDN dimensions\n");
+        return -1;
+    }
+    /* shapes the GPU kernels are written for */
+    if (d->head_k_dim != 128 || d->head_dim != 256 || d->d_conv != 4 || c->rope_dim_count > d->head_dim ||
+        d->n_embd % 256 || d->n_ff % 256 || !d->n_kv_head || d->n_head % d->n_kv_head ||
+        (d->n_head / d->n_kv_head) * MAXB > 64) {
+        fprintf(stderr, "model_init: dimensions outside what the GPU kernels support\n");
+        return -1;
+    }
+    m->tok_embd = need(&m->gguf, "token_embd.weight");
+    m->output_norm = need(&m->gguf, "output_norm.weight");
+    m->output = gguf_find_tensor(&m->gguf, "output.weight");
+    if (!m->output) m->output = m->tok_embd;
+    if (!m->tok_embd || !m->output_norm || bad2(m->tok_embd, d->n_embd, c->vocab_size, "token_embd")) return -1;
+    m->layers = calloc(d->n_layer, sizeof *m->layers);
+    if (!m->layers) return -1;
+    for (uint32_t il = 0; il < d->n_layer; il++) {
+        m->layers[il].is_recurrent = ((il + 1) % c->full_attn_interval) != 0;
+        if (bind_layer(&m->gguf, &m->layers[il], il, d, 0)) return -1;
+        if (m->layers[il].is_recurrent) d->n_recr_layer++;
+        else d->n_attn_layer++;
+    }
+    {
+        qwen_layer_t *L = &m->mtp_layer;
+        memset(L, 0, sizeof *L);
+        const uint32_t il = d->n_layer;
+        if (bind_layer(&m->gguf, L, il, d, 1)) return -1;
+        char nm[96];
+        snprintf(nm, sizeof nm, "blk.%u.nextn.eh_proj.weight", il);
+        m->mtp_eh_proj = need(&m->gguf, nm);
+        snprintf(nm, sizeof nm, "blk.%u.nextn.enorm.weight", il);
+        m->mtp_enorm = need(&m->gguf, nm);
+        snprintf(nm, sizeof nm, "blk.%u.nextn.hnorm.weight", il);
+        m->mtp_hnorm = need(&m->gguf, nm);
+        snprintf(nm, sizeof nm, "blk.%u.nextn.shared_head_norm.weight", il);
+        m->mtp_shnorm = need(&m->gguf, nm);
+        if (bad2(m->mtp_eh_proj, 2 * d->n_embd, d->n_embd, "nextn.eh_proj") || bad1(m->mtp_enorm, d->n_embd, "nextn.enorm") ||
+            bad1(m->mtp_hnorm, d->n_embd, "nextn.hnorm") || bad1(m->mtp_shnorm, d->n_embd, "nextn.shared_head_norm"))
+            return -1;
+    }
+    m->n_ctx = n_ctx;
+    m->pos = 0;
+
+    if (qgpu_init(0)) { fprintf(stderr, "model_init: no GPU\n"); return -1; }
+    qwen_gpu_t *g = calloc(1, sizeof *g);
+    m->gpu = g;
+    g->L = calloc(d->n_layer, sizeof *g->L);
+    for (uint32_t il = 0; il < d->n_layer; il++)
+        if (upload_layer(g, src, &m->layers[il], &g->L[il])) return -1;
+    if (upload_layer(g, src, &m->mtp_layer, &g->mtp)) return -1;
+    if (!(g->tok_embd = up_matrix(g, src, m->tok_embd))) return -1;
+    g->output = (m->output == m->tok_embd) ? g->tok_embd : up_matrix(g, src, m->output);
+    if (!g->output || !(g->eh_proj = up_matrix(g, src, m->mtp_eh_proj)) ||
+        !(g->out_norm = up_f32(g, src, m->output_norm)) || !(g->enorm = up_f32(g, src, m->mtp_enorm)) ||
+        !(g->hnorm = up_f32(g, src, m->mtp_hnorm)) || !(g->shnorm = up_f32(g, src, m->mtp_shnorm)))
+        return -1;
+
+    const uint64_t E = d->n_embd, F = d->n_ff, V = c->vocab_size;
+    g->kvrow = (uint64_t)d->n_kv_head * d->head_dim;
+    g->conv_elems = (uint64_t)d->conv_dim * 4;
+    g->ssm_elems = (uint64_t)d->n_v_heads * d->head_v_dim * d->head_k_dim;
+    uint64_t SQ = d->conv_dim;
+    if (2ull * d->n_head * d->head_dim > SQ) SQ = 2ull * d->n_head * d->head_dim;
+    if (F > SQ) SQ = F;
+    if (2 * E > SQ) SQ = 2 * E;
+    g->SQ = (SQ + 3) & ~3ull;
+    g->A = (uint64_t)d->n_head * d->head_dim > d->d_inner ? (uint64_t)d->n_head * d->head_dim : d->d_inner;
+    const size_t kvb = (size_t)n_ctx * g->kvrow * sizeof(float);
+    for (uint32_t il = 0; il <= d->n_layer; il++) {
+        glayer_t *D = il < d->n_layer ? &g->L[il] : &g->mtp;
+        if (D->rec) {
+            D->conv_ring = dalloc(g, NSLOT * g->conv_elems * sizeof(float));
+            D->ssm_ring = dalloc(g, NSLOT * g->ssm_elems * sizeof(float));
+            if (!D->conv_ring || !D->ssm_ring) return -1;
+        } else {
+            D->kv_k = dalloc(g, kvb);
+            D->kv_v = dalloc(g, kvb);
+            if (!D->kv_k || !D->kv_v) return -1;
+        }
+    }
+#define AL(p, n) do { if (!((p) = dalloc(g, (n) * sizeof(*(p))))) return -1; } while (0)
+    AL(g->d_pos, 4); AL(g->d_cur, 4); AL(g->d_tok, 64); AL(g->d_cand, 64); AL(g->d_vtok, 64); AL(g->d_acc, 64);
+    AL(g->bx, MAXB * E); AL(g->bxb, MAXB * E); AL(g->bqkv, MAXB * g->SQ); AL(g->bk, MAXB * g->kvrow);
+    AL(g->bv, MAXB * g->kvrow); AL(g->bz, MAXB * (uint64_t)d->d_inner);
+    AL(g->bbeta, MAXB * (uint64_t)d->n_v_heads + 4); AL(g->balpha, MAXB * (uint64_t)d->n_v_heads + 4);
+    AL(g->bffn, MAXB * F); AL(g->battn, MAXB * g->A); AL(g->xq, MAXB * (uint64_t)d->conv_dim);
+    AL(g->h_save, MAXB * E); AL(g->logits_b, MAXB * V); AL(g->logits1, V); AL(g->mtp_h, E);
+    AL(g->mx, MAXB * E); AL(g->cat, MAXB * 2 * E);
+#undef AL
+    /* RoPE tables with the reference's own expressions (model.c:186-201) */
+    const uint32_t half = c->rope_dim_count / 2;
+    float *cs = malloc((size_t)n_ctx * half * sizeof(float)), *sn = malloc((size_t)n_ctx * half * sizeof(float));
+    for (uint32_t p = 0; p < n_ctx; p++)
+        for (uint32_t i = 0; i < half; i++) {
+            const float angle = (float)p * powf(c->rope_theta, -2.0f * (float)i / (float)c->rope_dim_count);
+            cs[(size_t)p * half + i] = cosf(angle);
+            sn[(size_t)p * half + i] = sinf(angle);
+        }
+    g->rope_cos = dalloc(g, (size_t)n_ctx * half * sizeof(float));
+    g->rope_sin = dalloc(g, (size_t)n_ctx * half * sizeof(float));
+    int rc = (!g->rope_cos || !g->rope_sin) ? -1 :
+             (qgpu_memcpy_h2d(g->rope_cos, cs, (size_t)n_ctx * half * sizeof(float)) ||
+              qgpu_memcpy_h2d(g->rope_sin, sn, (size_t)n_ctx * half * sizeof(float)));
+    free(cs);
+    free(sn);
+    if (rc || qgpu_attn_reserve((int)n_ctx, (int)d->n_kv_head)) return -1;
+    /* host-side result fields */
+    m->mtp_h = calloc(E, sizeof(float));
+    m->x = calloc(E, sizeof(float));
+    m->logits = calloc(V, sizeof(float));
+    m->logits_b = calloc(MAXB * V, sizeof(float));
+    m->h_save = calloc(MAXB * E, sizeof(float));
+    if (!m->mtp_h || !m->x || !m->logits || !m->logits_b || !m->h_save) return -1;
+    m->host_sync = 1;
+    g->cur = g->cur_base = 0;
+    if (qgpu_sync()) return -1;
+    return 0;
+}
+
+int model_init(qwen_model_t *m, const char *path, uint32_t n_ctx)
+{
+    memset(m, 0, sizeof *m);
+    if (gguf_open(&m->gguf, path) != 0) return -1;
+    source_t src = { NULL };
+    if (model_load(m, &src, n_ctx)) { model_free(m); return -1; }
+    return 0;
+}
+
+/* a generated tensor table stands in for the GGUF file: offset = synth index */
+int model_init_synth(qwen_model_t *m, const qwen_synth_spec_t *s, uint32_t n_ctx)
+{
+    memset(m, 0, sizeof *m);
+    m->gguf.fd = -1;
+    m->gguf.alignment = 32;
+    snprintf(m->gguf.arch, sizeof m->gguf.arch, "qwen35");
+    const uint32_t nt = qwen_synth_count(s);
+    m->gguf.tensors = calloc(nt, sizeof(gguf_tensor_info_t));
+    m->gguf.tensor_count = nt;
+    m->gguf.header.tensor_count = nt;
+    for (uint32_t i = 0; i < nt; i++) {
+        qwen_synth_tensor_t d;
+        qwen_synth_describe(s, i, &d);
+        gguf_tensor_info_t *t = &m->gguf.tensors[i];
+        memcpy(t->name, d.name, GGUF_MAX_NAME);
+        t->n_dims = d.n_dims;
+        t->ne[0] = d.ne[0];
+        t->ne[1] = d.n_dims >= 2 ? d.ne[1] : 1;
+        t->ne[2] = t->ne[3] = 1;
+        t->type = (ggml_type_t)d.type;
+        t->offset = i;
+        t->data = NULL;
+    }
+    qwen_config_t *c = &m->gguf.config;
+    c->n_embd = s->n_embd; c->n_head = s->n_head; c->n_head_kv = s->n_kv_head; c->head_dim = s->head_dim;
+    c->n_layer = s->n_layer + 1; c->n_ff = s->n_ff; c->vocab_size = s->vocab; c->context_len = s->context_len;
+    c->rope_theta = s->rope_theta; c->rope_dim_count = s->rope_dim;
+    c->rope_sections[0] = 11; c->rope_sections[1] = 11; c->rope_sections[2] = 10; c->rope_sections[3] = 0;
+    c->rms_norm_eps = s->eps; c->full_attn_interval = s->full_attn_interval; c->ssm_state_size = s->state;
+    c->ssm_conv_kernel = 4; c->ssm_inner_size = s->n_v_heads * s->state; c->ssm_group_count = s->n_k_heads;
+    c->nextn_layers = 1;
+    source_t src = { s };
+    if (model_load(m, &src, n_ctx)) { model_free(m); return -1; }
+    return 0;
+}
+
+void model_free(qwen_model_t *m)
+{
+    if (!m) return;
+    gpu_free(m->gpu);
+    free(m->layers);
+    free(m->mtp_h); free(m->x); free(m->logits); free(m->logits_b); free(m->h_save);
+    if (m->gguf.fd >= 0 || m->gguf.mmap_data) gguf_close(&m->gguf);
+    else free(m->gguf.tensors);
+    memset(m, 0, sizeof *m);
+}
+
+/* ------------------------------------------------------------------ device layers */
+static void ffn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B)
+{
+    qwen_gpu_t *g = m->gpu;
+    const uint64_t E = m->dims.n_embd, F = m->dims.n_ff;
+    const float eps = m->cfg.rms_norm_eps;
+    K(qgpu_rmsnorm(g->bxb, E, R, E, D->post_norm, E, (int)B, eps));
+    const qgpu_tensor *W[2] = { D->ffn_gate, D->ffn_up };
+    float *outs[2] = { g->bffn, g->bqkv };
+    const uint64_t ld[2] = { F, g->SQ };
+    K(qgpu_gemv_multi_batch(W, 2, g->bxb, E, (int)B, outs, ld, 0));
+    K(qgpu_silu_mul(g->bffn, F, g->bqkv, g->SQ, F, (int)B));
+    K(qgpu_gemv_batch(D->ffn_down, g->bffn, F, (int)B, R, E, QGPU_GEMV_ACCUM));
+}
+
+static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_t pos)
+{
+    qwen_gpu_t *g = m->gpu;
+    const qwen_dims_t *d = &m->dims;
+    const uint64_t E = d->n_embd;
+    const float eps = m->cfg.rms_norm_eps;
+    K(qgpu_rmsnorm(g->bxb, E, R, E, D->attn_norm, E, (int)B, eps));
+    const qgpu_tensor *W[3] = { D->q, D->k, D->v };
+    float *outs[3] = { g->bqkv, g->bk, g->bv };
+    const uint64_t ld[3] = { g->SQ, g->kvrow, g->kvrow };
+    K(qgpu_gemv_multi_batch(W, 3, g->bxb, E, (int)B, outs, ld, 0));
+    K(qgpu_attn_prep(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos,
+                     g->rope_sin, (int)m->cfg.rope_dim_count, g->d_pos, (int)B, (int)d->n_head, (int)d->n_kv_head,
+                     (int)d->head_dim, eps));
+    K(qgpu_attn_decode(g->bqkv, g->SQ, D->kv_k, D->kv_v, g->d_pos, (int)(pos + B), (int)B, (int)d->n_head,
+                       (int)d->n_kv_head, (int)d->head_dim, g->battn, g->A));
+    K(qgpu_gemv_batch(D->o, g->battn, g->A, (int)B, R, E, QGPU_GEMV_ACCUM));
+    ffn_dev(m, D, R, B);
+}
+
+static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
+{
+    qwen_gpu_t *g = m->gpu;
+    const qwen_dims_t *d = &m->dims;
+    const uint64_t E = d->n_embd, di = d->d_inner;
+    const float eps = m->cfg.rms_norm_eps;
+    K(qgpu_rmsnorm(g->bxb, E, g->bx, E, D->attn_norm, E, (int)B, eps));
+    const qgpu_tensor *W[4] = { D->wqkv, D->wgate, D->beta, D->alpha };
+    float *outs[4] = { g->bqkv, g->bz, g->bbeta, g->balpha };
+    const uint64_t ld[4] = { g->SQ, di, d->n_v_heads, d->n_v_heads };
+    K(qgpu_gemv_multi_batch(W, 4, g->bxb, E, (int)B, outs, ld, 0));
+    K(qgpu_gdn_conv(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems, NSLOT,
+                    g->d_cur, g->xq, d->conv_dim));
+    K(qgpu_gdn_recurrence(g->xq, d->conv_dim, g->bbeta, g->balpha, d->n_v_heads, D->dt_bias, D->ssm_a, D->ssm_ring,
+                          g->ssm_elems, NSLOT, g->d_cur, (int)B, (int)d->n_k_heads, (int)d->n_v_heads,
+                          (int)d->head_v_dim, eps, g->battn, di));
+    K(qgpu_rmsnorm_gated(g->battn, g->battn, g->bz, D->ssm_norm, (int)d->head_v_dim, (int)(B * d->n_v_heads),
+                         d->head_v_dim, eps));
+    K(qgpu_gemv_batch(D->ssm_out, g->battn, di, (int)B, g->bx, E, QGPU_GEMV_ACCUM));
+    ffn_dev(m, D, g->bx, B);
+}
+
+/* tokens on the device; logits of every token into d_logits ([B][V]); hidden
+ * states into h_save when save_h.  GDN states advance by B (ring index). */
+static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, uint32_t pos, float *d_logits,
+                        int save_h)
+{
+    qwen_gpu_t *g = m->gpu;
+    const qwen_dims_t *d = &m->dims;
+    const uint64_t E = d->n_embd;
+    K(qgpu_set_i32(g->d_pos, (int)pos));
+    K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bx, E));
+    for (uint32_t il = 0; il < d->n_layer; il++) {
+        if (g->L[il].rec) gdn_dev(m, &g->L[il], B);
+        else attn_dev(m, &g->L[il], g->bx, B, pos);
+    }
+    if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
+    K(qgpu_rmsnorm(g->bxb, E, g->bx, E, g->out_norm, E, (int)B, m->cfg.rms_norm_eps));
+    K(qgpu_gemv_batch(g->output, g->bxb, E, (int)B, d_logits, m->cfg.vocab_size, 0));
+    g->cur_base = g->cur;
+    g->cur = (g->cur + (int)B) % NSLOT;
+    K(qgpu_set_i32(g->d_cur, g->cur));
+}
+
+/* MTP layer for B tokens (d_tokens) paired with hidden states h (device, [B][E]);
+ * output rows in mx, mtp_h = last row; logits of every row into d_logits if given */
+static void mtp_dev(qwen_model_t *m, const uint32_t *d_tokens, const float *h, uint32_t B, uint32_t pos,
+                    float *d_logits)
+{
+    qwen_gpu_t *g = m->gpu;
+    const uint64_t E = m->dims.n_embd;
+    const float eps = m->cfg.rms_norm_eps;
+    K(qgpu_set_i32(g->d_pos, (int)pos));
+    K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->cat, 2 * E));
+    K(qgpu_rmsnorm(g->cat, 2 * E, g->cat, 2 * E, g->enorm, E, (int)B, eps));
+    K(qgpu_rmsnorm(g->cat + E, 2 * E, h, E, g->hnorm, E, (int)B, eps));
+    K(qgpu_gemv_batch(g->eh_proj, g->cat, 2 * E, (int)B, g->mx, E, 0));
+    attn_dev(m, &g->mtp, g->mx, B, pos);
+    K(qgpu_copy(g->mtp_h, g->mx + (B - 1) * E, E * sizeof(float)));
+    if (d_logits) {
+        K(qgpu_rmsnorm(g->bxb, E, g->mx, E, g->shnorm, E, (int)B, eps));
+        K(qgpu_gemv_batch(g->output, g->bxb, E, (int)B, d_logits, m->cfg.vocab_size, 0));
+    }
+}
+
+/* ------------------------------------------------------------------ reference API */
+static void put_tokens(qwen_model_t *m, const uint32_t *tokens, uint32_t B)
+{
+    K(qgpu_memcpy_h2d(m->gpu->d_tok, tokens, B * sizeof(uint32_t)));
+}
+
+void model_forward(qwen_model_t *m, pool_t *pool, uint32_t token, uint32_t pos)
+{
+    (void)pool;
+    const double t0 = now_s();
+    put_tokens(m, &token, 1);
+    forward_dev(m, m->gpu->d_tok, 1, pos, m->gpu->logits1, 0);
+    if (m->host_sync) {
+        K(qgpu_memcpy_d2h(m->logits, m->gpu->logits1, (size_t)m->cfg.vocab_size * sizeof(float)));
+        K(qgpu_memcpy_d2h(m->x, m->gpu->bx, m->dims.n_embd * sizeof(float)));
+    }
+    qwen_prof_head += now_s() - t0;
+    qwen_prof_calls++;
+    m->pos = pos + 1;
+}
+
+void model_forward_batch(qwen_model_t *m, pool_t *pool, const uint32_t *tokens, uint32_t pos, uint32_t B, int ckpt)
+{
+    (void)pool;
+    (void)ckpt;
+    if (B < 1 || B > MAXB) { fprintf(stderr, "model_forward_batch: B=%u outside 1..%d\n", B, MAXB); abort(); }
+    put_tokens(m, tokens, B);
+    forward_dev(m, m->gpu->d_tok, B, pos, m->gpu->logits_b, 1);
+    if (m->host_sync) {
+        K(qgpu_memcpy_d2h(m->logits_b, m->gpu->logits_b, (size_t)B * m->cfg.vocab_size * sizeof(float)));
+        K(qgpu_memcpy_d2h(m->h_save, m->gpu->h_save, (size_t)B * m->dims.n_embd * sizeof(float)));
+    }
+    m->pos = pos + B;
+}
+
+int model_snapshot_states(qwen_model_t *m) { (void)m; return 0; }
+void model_rollback_states(qwen_model_t *m) { (void)m; }
+
+void model_rollback_to(qwen_model_t *m, uint32_t b)
+{
+    qwen_gpu_t *g = m->gpu;
+    g->cur = (g->cur_base + 1 + (int)b) % NSLOT;
+    K(qgpu_set_i32(g->d_cur, g->cur));
+}
+
+int mtp_forward(qwen_model_t *m, pool_t *pool, uint32_t token, uint32_t pos, int want_logits)
+{
+    (void)pool;
+    qwen_gpu_t *g = m->gpu;
+    const uint64_t E = m->dims.n_embd;
+    if (m->host_sync) K(qgpu_memcpy_h2d(g->mtp_h, m->mtp_h, E * sizeof(float)));
+    put_tokens(m, &token, 1);
+    mtp_dev(m, g->d_tok, g->mtp_h, 1, pos, want_logits ? g->logits1 : NULL);
+    if (m->host_sync) {
+        K(qgpu_memcpy_d2h(m->mtp_h, g->mtp_h, E * sizeof(float)));
+        if (want_logits) K(qgpu_memcpy_d2h(m->logits, g->logits1, (size_t)m->cfg.vocab_size * sizeof(float)));
+    }
+    return 0;
+}
+
+int mtp_forward_batch(qwen_model_t *m, pool_t *pool, const uint32_t *tokens, uint32_t pos, uint32_t B,
+                      int want_logits)
+{
+    (void)pool;
+    qwen_gpu_t *g = m->gpu;
+    if (B < 1 || B > MAXB) return -1;
+    put_tokens(m, tokens, B);
+    mtp_dev(m, g->d_tok, g->h_save, B, pos, want_logits ? g->logits_b : NULL);
+    if (m->host_sync) {
+        K(qgpu_memcpy_d2h(m->mtp_h, g->mtp_h, m->dims.n_embd * sizeof(float)));
+        if (want_logits)
+            K(qgpu_memcpy_d2h(m->logits_b, g->logits_b, (size_t)B * m->cfg.vocab_size * sizeof(float)));
+    }
+    return 0;
+}
+
+uint32_t model_sample_greedy(const float *logits, uint32_t vocab_size)
+{
+    uint32_t best = 0;
+    float mv = logits[0];
+    for (uint32_t i = 1; i < vocab_size; i++)
+        if (logits[i] > mv) { mv = logits[i]; best = i; }
+    return best;
+}
+
+void attention_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool, uint32_t pos)
+{
+    (void)pool;
+    qwen_gpu_t *g = m->gpu;
+    glayer_t *D = (L == &m->mtp_layer) ? &g->mtp : &g->L[L - m->layers];
+    K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
+    K(qgpu_set_i32(g->d_pos, (int)pos));
+    attn_dev(m, D, g->bx, 1, pos);
+    K(qgpu_memcpy_d2h(m->x, g->bx, m->dims.n_embd * sizeof(float)));
+}
+
+void gdn_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool)
+{
+    (void)pool;
+    qwen_gpu_t *g = m->gpu;
+    K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
+    glayer_t *D = &g->L[L - m->layers];
+    gdn_dev(m, D, 1);
+    /* the reference updates this layer's state in place (model.c:640-661): copy
+     * the new state (slot cur+1) over the current slot so other layers keep theirs */
+    const int nxt = (g->cur + 1) % NSLOT;
+    K(qgpu_copy(D->conv_ring + (size_t)g->cur * g->conv_elems, D->conv_ring + (size_t)nxt * g->conv_elems,
+                g->conv_elems * sizeof(float)));
+    K(qgpu_copy(D->ssm_ring + (size_t)g->cur * g->ssm_elems, D->ssm_ring + (size_t)nxt * g->ssm_elems,
+                g->ssm_elems * sizeof(float)));
+    K(qgpu_memcpy_d2h(m->x, g->bx, m->dims.n_embd * sizeof(float)));
+}
+
+/* ------------------------------------------------------------------ device-resident generation */
+static void prefill_dev(qwen_model_t *m, const uint32_t *prompt, uint32_t n, int with_mtp)
+{
+    qwen_gpu_t *g = m->gpu;
+    uint32_t pos = 0, last = 0;
+    while (pos < n) {
+        const uint32_t B = n - pos > PREFILL_MAX_B ? PREFILL_MAX_B : n - pos;
+        put_tokens(m, prompt + pos, B);
+        forward_dev(m, g->d_tok, B, pos, g->logits_b, 1);
+        if (with_mtp) mtp_dev(m, g->d_tok, g->h_save, B, pos, NULL);
+        pos += B;
+        last = B;
+    }
+    m->pos = n;
+    /* next token = argmax of the last prompt row (main.c:148-151, 175) */
+    K(qgpu_argmax(g->logits_b + (size_t)(last - 1) * m->cfg.vocab_size, m->cfg.vocab_size, m->cfg.vocab_size, 1,
+                  g->d_cand));
+}
+
+uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                             uint32_t k, uint32_t eos, int force_accept, uint32_t *out, uint32_t *cycle_j,
+                             qwen_gen_stats_t *st)
+{
+    qwen_gpu_t *g = m->gpu;
+    const uint32_t V = m->cfg.vocab_size;
+    const uint64_t E = m->dims.n_embd;
+    qwen_gen_stats_t s;
+    memset(&s, 0, sizeof s);
+    if (k > SPEC_MAX_B - 1) k = SPEC_MAX_B - 1;
+    if (n_prompt < 1 || n_prompt >= m->n_ctx) return 0;
+    double t0 = now_s();
+    prefill_dev(m, prompt, n_prompt, k > 0);
+    K(qgpu_sync());
+    s.t_prefill_s = now_s() - t0;
+    t0 = now_s();
+    uint32_t gen = 0;
+    uint32_t acc[24], next0;
+    K(qgpu_memcpy_d2h(&next0, g->d_cand, sizeof next0));
+    while (gen < n_predict) {
+        const uint32_t P = m->pos - 1;
+        const uint32_t room = m->n_ctx - 1 - P;
+        if (room < 1) break;
+        const uint32_t kk = k < room - 1 ? k : room - 1;
+        if (next0 == eos) break;                                   /* main.c:179 */
+        /* drafts: cand[s] = argmax MTP(cand[s-1], P+s) (main.c:182-185) */
+        for (uint32_t j = 1; j <= kk; j++) {
+            mtp_dev(m, g->d_cand + (j - 1), g->mtp_h, 1, P + j, g->logits1);
+            K(qgpu_argmax(g->logits1, V, V, 1, g->d_cand + j));
+        }
+        /* batched verification (main.c:189) and argmax of every row */
+        forward_dev(m, g->d_cand, kk + 1, P + 1, g->logits_b, 1);
+        K(qgpu_argmax(g->logits_b, V, V, (int)(kk + 1), g->d_vtok));
+        /* acceptance + GDN rollback on the device (main.c:191-217) */
+        K(qgpu_set_i32(g->d_pos, (int)(P + 1)));
+        K(qgpu_set_i32(g->d_cur, g->cur_base));
+        const int force_j = force_accept == 1 ? (int)kk : force_accept == 2 ? (int)(s.n_cycles % (kk + 1)) : -1;
+        K(qgpu_spec_accept(g->d_cand, g->d_vtok, (int)kk, force_j, g->d_pos, g->d_cur, NSLOT, g->d_acc));
+        K(qgpu_memcpy_d2h(acc, g->d_acc, (kk + 3) * sizeof(uint32_t)));
+        const uint32_t j = acc[0];
+        g->cur = (g->cur_base + 1 + (int)j) % NSLOT;
+        if (cycle_j) cycle_j[s.n_cycles] = j;
+        for (uint32_t i = 0; i <= j && gen < n_predict; i++) out[gen++] = acc[1 + i];
+        s.n_accepted += j;
+        s.n_drafts += kk;
+        s.n_cycles++;
+        m->pos = P + j + 2;
+        if (m->pos >= m->n_ctx) break;
+        /* MTP re-anchor on the backbone hidden state of the last accepted token (main.c:220-222) */
+        if (k > 0) mtp_dev(m, g->d_cand + j, g->h_save + (size_t)j * E, 1, P + j + 1, NULL);
+        K(qgpu_memcpy_d2d(g->d_cand, g->d_acc + j + 2, sizeof(uint32_t)));   /* next cand[0] = argmax logits_b[j] */
+        next0 = acc[j + 2];
+    }
+    K(qgpu_sync());
+    s.t_decode_s = now_s() - t0;
+    if (st) *st = s;
+    return gen;
+}
+
+uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                               uint32_t eos, uint32_t *out, qwen_gen_stats_t *st)
+{
+    qwen_gpu_t *g = m->gpu;
+    const uint32_t V = m->cfg.vocab_size;
+    qwen_gen_stats_t s;
+    memset(&s, 0, sizeof s);
+    if (n_prompt < 1 || n_prompt >= m->n_ctx) return 0;
+    double t0 = now_s();
+    prefill_dev(m, prompt, n_prompt, 0);
+    K(qgpu_sync());
+    s.t_prefill_s = now_s() - t0;
+    t0 = now_s();
+    uint32_t gen = 0, cur;
+    K(qgpu_memcpy_d2h(&cur, g->d_cand, sizeof cur));
+    out[gen++] = cur;
+    while (gen < n_predict && cur != eos && m->pos < m->n_ctx) {
+        forward_dev(m, g->d_cand, 1, m->pos, g->logits1, 0);
+        K(qgpu_argmax(g->logits1, V, V, 1, g->d_cand));
+        K(qgpu_memcpy_d2h(&cur, g->d_cand, sizeof cur));
+        m->pos++;
+        out[gen++] = cur;
+        s.n_cycles++;
+    }
+    K(qgpu_sync());
+    s.t_decode_s = now_s() - t0;
+    if (st) *st = s;
+    return gen;
+}
+
+int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, float *ms_decode, float *ms_draft)
+{
+    qwen_gpu_t *g = m->gpu;
+    if (B < 1 || B > MAXB || reps < 1 || m->pos + B >= m->n_ctx) return -1;
+    const int cur0 = g->cur, base0 = g->cur_base;
+    const uint32_t pos = m->pos;
+    void *e0, *e1;
+    K(qgpu_event_create(&e0));
+    K(qgpu_event_create(&e1));
+    /* verify: B tokens at pos (states are restored to the ring index after each rep) */
+    forward_dev(m, g->d_cand, B, pos, g->logits_b, 1);
+    g->cur = cur0; g->cur_base = base0; K(qgpu_set_i32(g->d_cur, cur0));
+    K(qgpu_event_record(e0));
+    for (int r = 0; r < reps; r++) {
+        forward_dev(m, g->d_cand, B, pos, g->logits_b, 1);
+        K(qgpu_argmax(g->logits_b, m->cfg.vocab_size, m->cfg.vocab_size, (int)B, g->d_vtok));
+        g->cur = cur0; g->cur_base = base0; K(qgpu_set_i32(g->d_cur, cur0));
+    }
+    K(qgpu_event_record(e1));
+    K(qgpu_event_elapsed_ms(e0, e1, ms_verify));
+    *ms_verify /= (float)reps;
+    K(qgpu_event_record(e0));
+    for (int r = 0; r < reps; r++) {
+        forward_dev(m, g->d_cand, 1, pos, g->logits1, 0);
+        K(qgpu_argmax(g->logits1, m->cfg.vocab_size, m->cfg.vocab_size, 1, g->d_vtok));
+        g->cur = cur0; g->cur_base = base0; K(qgpu_set_i32(g->d_cur, cur0));
+    }
+    K(qgpu_event_record(e1));
+    K(qgpu_event_elapsed_ms(e0, e1, ms_decode));
+    *ms_decode /= (float)reps;
+    if (ms_draft) {
+        const size_t eb = m->dims.n_embd * sizeof(float);
+        float *keep = malloc(eb);                                  /* mtp_h is restored afterwards */
+        K(qgpu_memcpy_d2h(keep, g->mtp_h, eb));
+        K(qgpu_event_record(e0));
+        for (int r = 0; r < reps; r++) {
+            mtp_dev(m, g->d_cand, g->mtp_h, 1, pos, g->logits1);
+            K(qgpu_argmax(g->logits1, m->cfg.vocab_size, m->cfg.vocab_size, 1, g->d_vtok));
+        }
+        K(qgpu_event_record(e1));
+        K(qgpu_event_elapsed_ms(e0, e1, ms_draft));
+        *ms_draft /= (float)reps;
+        K(qgpu_memcpy_h2d(g->mtp_h, keep, eb));
+        free(keep);
+    }
+    K(qgpu_set_i32(g->d_pos, (int)pos));
+    K(qgpu_sync());
+    qgpu_event_destroy(e0);
+    qgpu_event_destroy(e1);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ FFI helpers */
+qwen_model_t *qwen_model_alloc(void) { return calloc(1, sizeof(qwen_model_t)); }
+void qwen_model_dealloc(qwen_model_t *m) { free(m); }
+float *qwen_model_field(qwen_model_t *m, const char *name)
+{
+    if (!strcmp(name, "logits")) return m->logits;
+    if (!strcmp(name, "logits_b")) return m->logits_b;
+    if (!strcmp(name, "h_save")) return m->h_save;
+    if (!strcmp(name, "mtp_h")) return m->mtp_h;
+    if (!strcmp(name, "x")) return m->x;
+    return NULL;
+}
+uint32_t qwen_model_get(const qwen_model_t *m, const char *name)
+{
+    if (!strcmp(name, "pos")) return m->pos;
+    if (!strcmp(name, "vocab")) return m->cfg.vocab_size;
+    if (!strcmp(name, "n_embd")) return m->dims.n_embd;
+    if (!strcmp(name, "n_ctx")) return m->n_ctx;
+    if (!strcmp(name, "n_layer")) return m->dims.n_layer;
+    return 0;
+}
+void qwen_model_set_pos(qwen_model_t *m, uint32_t pos) { m->pos = pos; }
+void qwen_model_set_host_sync(qwen_model_t *m, int on) { m->host_sync = on; }

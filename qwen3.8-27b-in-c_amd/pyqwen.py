@@ -173,11 +173,23 @@ class DevBuf:
                                                out.nbytes))
         return out
 
+    # Typed pointers into the buffer.  Each pointer holds a reference to the
+    # buffer, so `gpu.put(a).f32()` passed straight to a call keeps the device
+    # memory alive until the call returns (qgpu_free then waits for the device).
+    def _ptr(self, offset_elems, typ):
+        assert self.ptr, "buffer already freed"
+        p = ctypes.cast(ctypes.c_void_p(self.ptr + 4 * offset_elems), typ)
+        p._owner = self
+        return p
+
     def f32(self, offset_elems=0):
-        return ctypes.cast(ctypes.c_void_p(self.ptr + 4 * offset_elems), F32P)
+        return self._ptr(offset_elems, F32P)
 
     def u32(self, offset_elems=0):
-        return ctypes.cast(ctypes.c_void_p(self.ptr + 4 * offset_elems), U32P)
+        return self._ptr(offset_elems, U32P)
+
+    def i32(self, offset_elems=0):
+        return self._ptr(offset_elems, ctypes.POINTER(ctypes.c_int))
 
     def close(self):
         if self.ptr:
@@ -240,6 +252,16 @@ class GpuLib:
             "qgpu_argmax": [F32P, u64, ctypes.c_uint32, i32, U32P],
             "qgpu_gemv_prepare": [F32P, u64, i32, u64], "qgpu_gemv_prepared": [vp, i32, F32P, u64, i32],
             "qgpu_copy": [vp, vp, ctypes.c_size_t],
+            "qgpu_gdn_conv": [F32P, u64, i32, i32, F32P, F32P, u64, i32, ctypes.POINTER(i32), F32P, u64],
+            "qgpu_gdn_recurrence": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, u64, i32, ctypes.POINTER(i32),
+                                    i32, i32, i32, i32, f32, F32P, u64],
+            "qgpu_rmsnorm_gated": [F32P, F32P, F32P, F32P, i32, i32, u64, f32],
+            "qgpu_attn_prep": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
+                               ctypes.POINTER(i32), i32, i32, i32, i32, f32],
+            "qgpu_attn_decode": [F32P, u64, F32P, F32P, ctypes.POINTER(i32), i32, i32, i32, i32, i32, F32P, u64],
+            "qgpu_attn_reserve": [i32, i32],
+            "qgpu_set_i32": [ctypes.POINTER(i32), i32],
+            "qgpu_spec_accept": [U32P, U32P, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), i32, U32P],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)
@@ -306,3 +328,129 @@ def gpu_lib():
     if _gpu is None:
         _gpu = GpuLib()
     return _gpu
+
+
+# ---------------------------------------------------------------------- model (include/model.h)
+class GenStats(ctypes.Structure):
+    _fields_ = [("n_cycles", ctypes.c_uint64), ("n_accepted", ctypes.c_uint64), ("n_drafts", ctypes.c_uint64),
+                ("t_prefill_s", ctypes.c_double), ("t_decode_s", ctypes.c_double)]
+
+
+def _model_lib():
+    L = host_lib().L
+    if getattr(L, "_model_sigs", False):
+        return L
+    vp, u32, i32 = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int
+    L.qwen_model_alloc.restype = vp
+    L.qwen_model_dealloc.argtypes = [vp]
+    L.model_init.argtypes = [vp, ctypes.c_char_p, u32]
+    L.model_init_synth.argtypes = [vp, ctypes.POINTER(SynthSpec), u32]
+    L.model_free.argtypes = [vp]
+    L.model_forward.argtypes = [vp, vp, u32, u32]
+    L.model_forward_batch.argtypes = [vp, vp, U32P, u32, u32, i32]
+    L.model_rollback_to.argtypes = [vp, u32]
+    L.mtp_forward.argtypes = [vp, vp, u32, u32, i32]
+    L.mtp_forward_batch.argtypes = [vp, vp, U32P, u32, u32, i32]
+    L.qwen_model_field.argtypes = [vp, ctypes.c_char_p]
+    L.qwen_model_field.restype = F32P
+    L.qwen_model_get.argtypes = [vp, ctypes.c_char_p]
+    L.qwen_model_get.restype = u32
+    L.qwen_model_set_pos.argtypes = [vp, u32]
+    L.qwen_model_set_host_sync.argtypes = [vp, i32]
+    L.model_generate_spec.argtypes = [vp, U32P, u32, u32, u32, u32, i32, U32P, U32P, ctypes.POINTER(GenStats)]
+    L.model_generate_spec.restype = u32
+    L.model_generate_greedy.argtypes = [vp, U32P, u32, u32, u32, U32P, ctypes.POINTER(GenStats)]
+    L.model_generate_greedy.restype = u32
+    L.model_time_steps.argtypes = [vp, u32, i32, F32P, F32P, F32P]
+    L._model_sigs = True
+    return L
+
+
+def uptr(a):
+    assert a.dtype == np.uint32 and a.flags.c_contiguous
+    return a.ctypes.data_as(U32P)
+
+
+class Model:
+    """The GPU model through the reference-compatible C API (include/model.h)."""
+
+    def __init__(self, path=None, n_ctx=256, spec=None):
+        gpu_lib()                                  # HIP layer must load (fails loudly otherwise)
+        self.L = _model_lib()
+        self.h = self.L.qwen_model_alloc()
+        rc = self.L.model_init_synth(self.h, ctypes.byref(spec), n_ctx) if spec is not None else \
+            self.L.model_init(self.h, path.encode(), n_ctx)
+        if rc:
+            self.L.qwen_model_dealloc(self.h)
+            self.h = None
+            raise QgpuError(f"model_init failed ({path or 'synthetic'})")
+        self.V = self.L.qwen_model_get(self.h, b"vocab")
+        self.E = self.L.qwen_model_get(self.h, b"n_embd")
+
+    def close(self):
+        if self.h:
+            self.L.model_free(self.h)
+            self.L.qwen_model_dealloc(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def field(self, name, n):
+        return np.ctypeslib.as_array(self.L.qwen_model_field(self.h, name.encode()), shape=(n,)).copy()
+
+    @property
+    def pos(self):
+        return self.L.qwen_model_get(self.h, b"pos")
+
+    @pos.setter
+    def pos(self, p):
+        self.L.qwen_model_set_pos(self.h, p)
+
+    def forward(self, tok, pos):
+        self.L.model_forward(self.h, None, tok, pos)
+        return self.field("logits", self.V)
+
+    def forward_batch(self, toks, pos, ckpt=1):
+        t = np.ascontiguousarray(toks, np.uint32)
+        self.L.model_forward_batch(self.h, None, uptr(t), pos, len(t), ckpt)
+        return self.field("logits_b", len(t) * self.V).reshape(len(t), self.V)
+
+    def h_save(self, B):
+        return self.field("h_save", B * self.E).reshape(B, self.E)
+
+    def rollback_to(self, b):
+        self.L.model_rollback_to(self.h, b)
+
+    def mtp_forward(self, tok, pos, want_logits=1):
+        self.L.mtp_forward(self.h, None, tok, pos, want_logits)
+        return self.field("logits", self.V) if want_logits else None
+
+    def mtp_forward_batch(self, toks, pos, want_logits=0):
+        t = np.ascontiguousarray(toks, np.uint32)
+        self.L.mtp_forward_batch(self.h, None, uptr(t), pos, len(t), want_logits)
+
+    def generate_spec(self, prompt, n_predict, k, eos=0xFFFFFFFF, force_accept=False):
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(n_predict + 16, np.uint32)
+        js = np.zeros(n_predict + 16, np.uint32)
+        st = GenStats()
+        n = self.L.model_generate_spec(self.h, uptr(p), len(p), n_predict, k, eos, int(force_accept), uptr(out),
+                                       uptr(js), ctypes.byref(st))
+        return out[:n], js[:st.n_cycles], st
+
+    def generate_greedy(self, prompt, n_predict, eos=0xFFFFFFFF):
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(n_predict, np.uint32)
+        st = GenStats()
+        n = self.L.model_generate_greedy(self.h, uptr(p), len(p), n_predict, eos, uptr(out), ctypes.byref(st))
+        return out[:n], st
+
+    def time_steps(self, B, reps):
+        v, d, dr = ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
+        if self.L.model_time_steps(self.h, B, reps, ctypes.byref(v), ctypes.byref(d), ctypes.byref(dr)):
+            raise QgpuError("model_time_steps failed")
+        return v.value, d.value, dr.value

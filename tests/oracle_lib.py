@@ -81,6 +81,9 @@ def lib():
     L.or_generate_spec.argtypes = [vp, U32P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                    ctypes.c_uint32, U32P, ctypes.POINTER(SpecStats), U32P]
     L.or_generate_spec.restype = ctypes.c_uint32
+    L.or_generate_spec_ex.argtypes = [vp, U32P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                      ctypes.c_uint32, i32, U32P, ctypes.POINTER(SpecStats), U32P]
+    L.or_generate_spec_ex.restype = ctypes.c_uint32
     L.or_generate_greedy.argtypes = [vp, U32P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, U32P]
     L.or_generate_greedy.restype = ctypes.c_uint32
     _lib = L
@@ -137,12 +140,13 @@ class Model:
     def h_save(self, B):
         return self.arr(self.L.or_model_h_save, B * self.E).reshape(B, self.E)
 
-    def generate_spec(self, prompt, n_predict, k, eos=0xFFFFFFFF):
+    def generate_spec(self, prompt, n_predict, k, eos=0xFFFFFFFF, force_accept=False):
         p = np.ascontiguousarray(prompt, np.uint32)
         out = np.zeros(n_predict + 16, np.uint32)
         js = np.zeros(n_predict + 16, np.uint32)
         st = SpecStats()
-        n = self.L.or_generate_spec(self.h, uptr(p), len(p), n_predict, k, eos, uptr(out), ctypes.byref(st), uptr(js))
+        n = self.L.or_generate_spec_ex(self.h, uptr(p), len(p), n_predict, k, eos, int(force_accept), uptr(out),
+                                       ctypes.byref(st), uptr(js))
         return out[:n], js[:st.n_cycles], st
 
     def generate_greedy(self, prompt, n_predict, eos=0xFFFFFFFF):

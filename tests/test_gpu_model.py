@@ -1,0 +1,298 @@
+"""GPU parity of the Gated DeltaNet block, the gated GQA attention and the whole
+hybrid model (batched verify, single-token decode, MTP draft, rollback and the
+on-device greedy speculative loop), through the C-ABI (libqgpu) and the
+reference-compatible model API (libqwen).
+
+Checkers: the oracle (CPU restatement, bit-exact with the reference) and the
+golden vectors produced from the compiled reference (tests/golden).
+Bars: GEMV/GDN outputs within 1e-3 relative (normwise, max|d|/max|ref|);
+greedy token streams identical wherever the reference top-2 gap > 1e-2 (every
+gap of the fixtures is above 0.3, so the streams must be identical).
+"""
+import hashlib
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from gpu_util import gpu, rel_err  # noqa: F401
+from qwen_pkg import host_lib, pyqwen
+
+pytestmark = pytest.mark.gpu
+NSLOT = 9
+
+
+def load(name):
+    return np.load(os.path.join(O.GOLDEN, name), allow_pickle=False)
+
+
+# ---------------------------------------------------------------- GDN block (config 3)
+def test_gdn_block_config3_vs_oracle_with_snapshots_and_rollback(gpu):
+    print("\n[gdn] config 3: 48 v-heads x 128x128, 16 k-heads, T=4", flush=True)
+    T, nk, nv, hk = 4, 16, 48, 128
+    cd, eps = 2 * nk * hk + nv * hk, 1e-6
+    host = host_lib()
+    qkv = host.synth_normal(T * cd, 3, 1).reshape(T, cd)
+    br = host.synth_normal(T * nv, 3, 2).reshape(T, nv)
+    ar = host.synth_normal(T * nv, 3, 3).reshape(T, nv)
+    cw = host.synth_normal(cd * 4, 3, 4, 0.0, 0.5)
+    conv0 = host.synth_normal(cd * 4, 3, 5, 0.0, 0.5)
+    ssm0 = host.synth_normal(nv * hk * hk, 3, 6, 0.0, 0.01)
+    dtb = np.zeros(nv, np.float32)
+    sa = -np.ones(nv, np.float32)
+    # oracle
+    L = O.lib()
+    oc, os_ = conv0.copy(), ssm0.copy()
+    oout = np.zeros(T * nv * hk, np.float32)
+    snap_c = np.zeros(T * cd * 4, np.float32)
+    snap_s = np.zeros(T * nv * hk * hk, np.float32)
+    L.or_gdn_block(T, cd, nk, nv, hk, hk, eps, O.fptr(qkv), O.fptr(br), O.fptr(ar), O.fptr(cw), O.fptr(dtb),
+                   O.fptr(sa), O.fptr(oc), O.fptr(os_), O.fptr(oout), O.fptr(snap_c), O.fptr(snap_s))
+    # GPU: ring of NSLOT slots, current slot 5 (exercises the wrap-around)
+    cur0 = 5
+    cstride, sstride = cd * 4, nv * hk * hk
+    cring = gpu.put(np.zeros(NSLOT * cstride, np.float32))
+    sring = gpu.put(np.zeros(NSLOT * sstride, np.float32))
+    cring.upload(conv0, cur0 * cstride * 4)
+    sring.upload(ssm0, cur0 * sstride * 4)
+    curb = gpu.put(np.array([cur0], np.int32))
+    xb, yb, cwb = gpu.put(qkv), gpu.buf(T * cd * 4), gpu.put(cw)
+    dtbb, sab = gpu.put(dtb), gpu.put(sa)
+    gpu.ok(gpu.L.qgpu_gdn_conv(xb.f32(), cd, T, cd, cwb.f32(), cring.f32(), cstride, NSLOT, curb.i32(), yb.f32(), cd))
+    ob = gpu.buf(T * nv * hk * 4)
+    bb, ab = gpu.put(br), gpu.put(ar)
+    gpu.ok(gpu.L.qgpu_gdn_recurrence(yb.f32(), cd, bb.f32(), ab.f32(), nv, dtbb.f32(), sab.f32(),
+                                     sring.f32(), sstride, NSLOT, curb.i32(), T, nk, nv, hk, eps, ob.f32(), nv * hk))
+    got = ob.download(np.float32).reshape(T, -1)
+    for b in range(T):
+        e = rel_err(got[b], oout.reshape(T, -1)[b])
+        print(f"  token {b}: output rel err {e:.2e}", flush=True)
+        assert e < 1e-3, (b, e)
+    cr = cring.download(np.float32).reshape(NSLOT, -1)
+    sr = sring.download(np.float32).reshape(NSLOT, -1)
+    assert np.array_equal(cr[cur0], conv0) and np.array_equal(sr[cur0], ssm0), "current slot must not be written"
+    for b in range(T):
+        slot = (cur0 + 1 + b) % NSLOT
+        ec, es = rel_err(cr[slot], snap_c.reshape(T, -1)[b]), rel_err(sr[slot], snap_s.reshape(T, -1)[b])
+        print(f"  snapshot {b} in slot {slot}: conv {ec:.2e} state {es:.2e}", flush=True)
+        assert ec == 0.0 and es < 1e-3, (b, ec, es)
+    # rollback to accepted position 2 = pointer select, then one more token continues from there
+    gpu.ok(gpu.L.qgpu_set_i32(curb.i32(), (cur0 + 1 + 2) % NSLOT))
+    x1 = host.synth_normal(cd, 3, 7).reshape(1, cd)
+    b1, a1 = host.synth_normal(nv, 3, 8), host.synth_normal(nv, 3, 9)
+    x1b, b1b, a1b = gpu.put(x1), gpu.put(b1), gpu.put(a1)
+    gpu.ok(gpu.L.qgpu_gdn_conv(x1b.f32(), cd, 1, cd, cwb.f32(), cring.f32(), cstride, NSLOT, curb.i32(), yb.f32(), cd))
+    gpu.ok(gpu.L.qgpu_gdn_recurrence(yb.f32(), cd, b1b.f32(), a1b.f32(), nv, dtbb.f32(), sab.f32(), sring.f32(),
+                                     sstride, NSLOT, curb.i32(), 1, nk, nv, hk, eps, ob.f32(), nv * hk))
+    oc2 = snap_c.reshape(T, -1)[2].copy()
+    os2 = snap_s.reshape(T, -1)[2].copy()
+    o2 = np.zeros(nv * hk, np.float32)
+    L.or_gdn_block(1, cd, nk, nv, hk, hk, eps, O.fptr(x1), O.fptr(b1), O.fptr(a1), O.fptr(cw), O.fptr(dtb),
+                   O.fptr(sa), O.fptr(oc2), O.fptr(os2), O.fptr(o2), None, None)
+    assert rel_err(ob.download(np.float32, nv * hk), o2) < 1e-3
+
+
+def test_rmsnorm_gated(gpu):
+    rng = np.random.default_rng(1)
+    rows, n = 12, 128
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    z = rng.standard_normal((rows, n)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    xb, zb, wb = gpu.put(x), gpu.put(z), gpu.put(w)
+    gpu.ok(gpu.L.qgpu_rmsnorm_gated(xb.f32(), xb.f32(), zb.f32(), wb.f32(), n, rows, n, 1e-6))
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-6) * w * (z / (1 + np.exp(-z.astype(np.float64))))
+    assert rel_err(xb.download(np.float32).reshape(rows, n), ref) < 1e-5
+
+
+# ---------------------------------------------------------------- attention
+def attn_fp64(q, k, v, qw, kw, kc, vc, pos, B, nh, nkv, hd, rope_dim, theta, eps):
+    """FP64 statement of model.c:318-406, 784-810 for B query tokens."""
+    half = rope_dim // 2
+    kc, vc = kc.astype(np.float64).copy(), vc.astype(np.float64).copy()
+
+    def norm(x, w):
+        x = x.astype(np.float64)
+        return x / np.sqrt((x ** 2).mean() + eps) * w
+
+    def rope(x, p):
+        i = np.arange(half)
+        ang = np.float32(p) * np.power(np.float32(theta), (-2.0 * i / rope_dim).astype(np.float32))
+        c, s = np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))
+        y = x.copy()
+        y[:half] = x[:half] * c - x[half:2 * half] * s
+        y[half:2 * half] = x[:half] * s + x[half:2 * half] * c
+        return y
+
+    qr = np.zeros((B, nh, hd))
+    for b in range(B):
+        for h in range(nh):
+            qr[b, h] = rope(norm(q[b, h * 2 * hd:h * 2 * hd + hd], qw), pos + b)
+        for g in range(nkv):
+            kc[pos + b, g] = rope(norm(k[b, g * hd:(g + 1) * hd], kw), pos + b)
+            vc[pos + b, g] = v[b, g * hd:(g + 1) * hd]
+    out = np.zeros((B, nh * hd))
+    per = nh // nkv
+    for b in range(B):
+        for h in range(nh):
+            g = h // per
+            s = kc[:pos + b + 1, g] @ qr[b, h] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            gate = q[b, h * 2 * hd + hd:(h + 1) * 2 * hd].astype(np.float64)
+            out[b, h * hd:(h + 1) * hd] = (p @ vc[:pos + b + 1, g]) / (1 + np.exp(-gate))
+    return out, kc, vc
+
+
+@pytest.mark.parametrize("pos,B", [(0, 1), (37, 4), (300, 8), (95, 3)])
+def test_attention_vs_fp64(gpu, pos, B):
+    print(f"\n[attn] pos={pos} B={B}", flush=True)
+    nh, nkv, hd, rope_dim, theta, eps, n_ctx = 24, 4, 256, 64, 1e7, 1e-6, 512
+    rng = np.random.default_rng(pos + B)
+    q = rng.standard_normal((B, nh * 2 * hd)).astype(np.float32)
+    k = rng.standard_normal((B, nkv * hd)).astype(np.float32)
+    v = rng.standard_normal((B, nkv * hd)).astype(np.float32)
+    qw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kc = np.zeros((n_ctx, nkv, hd), np.float32)
+    vc = np.zeros((n_ctx, nkv, hd), np.float32)
+    kc[:pos] = rng.standard_normal((pos, nkv, hd)).astype(np.float32)
+    vc[:pos] = rng.standard_normal((pos, nkv, hd)).astype(np.float32)
+    half = rope_dim // 2
+    i = np.arange(half)
+    ang = np.arange(n_ctx, dtype=np.float32)[:, None] * np.power(np.float32(theta), (-2.0 * i / rope_dim).astype(np.float32))[None]
+    rc, rs = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    ref, kref, vref = attn_fp64(q, k, v, qw, kw, kc, vc, pos, B, nh, nkv, hd, rope_dim, theta, eps)
+    qb, kb, vb = gpu.put(q), gpu.put(k), gpu.put(v)
+    kcb, vcb = gpu.put(kc), gpu.put(vc)
+    posb = gpu.put(np.array([pos], np.int32))
+    qwb, kwb, rcb, rsb = gpu.put(qw), gpu.put(kw), gpu.put(rc), gpu.put(rs)
+    gpu.ok(gpu.L.qgpu_attn_prep(qb.f32(), nh * 2 * hd, kb.f32(), vb.f32(), nkv * hd, qwb.f32(), kwb.f32(),
+                                kcb.f32(), vcb.f32(), rcb.f32(), rsb.f32(), rope_dim, posb.i32(), B, nh, nkv, hd, eps))
+    ob = gpu.buf(B * nh * hd * 4)
+    gpu.ok(gpu.L.qgpu_attn_decode(qb.f32(), nh * 2 * hd, kcb.f32(), vcb.f32(), posb.i32(), n_ctx, B, nh, nkv, hd,
+                                  ob.f32(), nh * hd))
+    got = ob.download(np.float32).reshape(B, nh * hd)
+    assert rel_err(got, ref) < 1e-4
+    kcg = kcb.download(np.float32).reshape(n_ctx, nkv, hd)
+    assert rel_err(kcg[pos:pos + B], kref[pos:pos + B]) < 1e-5
+    assert np.array_equal(vcb.download(np.float32).reshape(n_ctx, nkv, hd)[pos:pos + B], v.reshape(B, nkv, hd))
+
+
+def test_spec_accept_kernel(gpu):
+    cand = gpu.put(np.array([7, 3, 9, 4, 0, 0, 0, 0], np.uint32))
+    for vt, k, fj, j in (([3, 9, 4, 11], 3, -1, 3), ([3, 8, 4, 11], 3, -1, 1), ([5, 9, 4, 11], 3, -1, 0),
+                         ([12], 0, -1, 0), ([5, 9, 4, 11], 3, 2, 2), ([3, 9, 4, 11], 3, 9, 3)):
+        vb = gpu.put(np.array(vt + [0] * (8 - len(vt)), np.uint32))
+        pos, cur = gpu.put(np.array([100], np.int32)), gpu.put(np.array([7], np.int32))
+        out = gpu.buf(16 * 4)
+        gpu.ok(gpu.L.qgpu_spec_accept(cand.u32(), vb.u32(), k, fj, pos.i32(), cur.i32(), NSLOT, out.u32()))
+        o = out.download(np.uint32)
+        assert o[0] == j and list(o[1:j + 2]) == [7, 3, 9, 4][:j + 1] and o[j + 2] == vt[j]
+        assert pos.download(np.int32)[0] == 100 + j + 1 and cur.download(np.int32)[0] == (7 + 1 + j) % NSLOT
+
+
+# ---------------------------------------------------------------- tiny hybrid model
+@pytest.fixture(scope="module", params=["tiny", "tiny_mixed"])
+def tiny(request):
+    z = load(f"model_{request.param}.npz")
+    td = tempfile.mkdtemp()
+    path = os.path.join(td, "m.gguf")
+    host_lib().write_tiny_gguf(path, int(z["seed"]), int(z["mixed"]))
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == str(z["gguf_sha256"])
+    yield path, z
+    os.remove(path)
+
+
+def test_model_forward_batch_and_sequential_vs_reference(gpu, tiny):
+    path, z = tiny
+    print(f"\n[model] {os.path.basename(path)} forward", flush=True)
+    V = 1024
+    p = z["prompt"]
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    lb = m.forward_batch(p[:8], 0, 0)
+    ref = z["batch_logits"].reshape(8, V)
+    for b in range(8):
+        assert rel_err(lb[b], ref[b]) < 1e-3, b
+        assert lb[b].argmax() == ref[b].argmax()
+    assert rel_err(m.h_save(8), z["batch_hsave"].reshape(8, -1)) < 1e-3
+    # MTP prefill + one draft with logits (mtp_forward_batch then mtp_forward)
+    m.mtp_forward_batch(p[:8], 0)
+    ml = m.mtp_forward(int(p[8]), 8)
+    assert rel_err(ml, z["mtp_logits"]) < 1e-3 and ml.argmax() == z["mtp_logits"].argmax()
+    m.close()
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    seq = np.array([m.forward(int(p[i]), i) for i in range(8)])
+    sref = z["seq_logits"].reshape(8, V)
+    for b in range(8):
+        assert rel_err(seq[b], sref[b]) < 1e-3, b
+    m.close()
+
+
+def test_model_rollback_vs_reference(gpu, tiny):
+    path, z = tiny
+    p = z["prompt"]
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    for i in range(5):
+        m.forward(int(p[i]), i)
+    m.forward_batch(p[10:13], 5)
+    m.rollback_to(1)
+    m.pos = 8
+    lb = m.forward_batch(p[13:16], 7)
+    ref = z["rollback_logits"].reshape(3, -1)
+    for b in range(3):
+        assert rel_err(lb[b], ref[b]) < 1e-3 and lb[b].argmax() == ref[b].argmax(), b
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 5, 7])
+def test_model_spec_stream_vs_reference(gpu, tiny, k):
+    """On-device greedy MTP speculative decode == the reference's spec stream == greedy stream."""
+    path, z = tiny
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    toks, js, st = m.generate_spec(z["prompt"][:20], 40, k)
+    key = f"spec_k{k}" if k <= 2 else f"spec_seq_k{k}"
+    assert np.array_equal(toks, z[key])
+    assert np.array_equal(js, z[f"spec_j_k{k}" if k <= 2 else f"spec_seq_j_k{k}"][:len(js)])
+    assert np.array_equal(toks, z["greedy"])
+
+
+def test_model_greedy_stream_vs_reference(gpu, tiny):
+    path, z = tiny
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    toks, st = m.generate_greedy(z["prompt"][:20], 40)
+    assert np.array_equal(toks, z["greedy"])
+
+
+@pytest.mark.parametrize("k,mode", [(3, 1), (7, 1), (3, 2), (7, 2)])
+def test_model_forced_acceptance_vs_oracle(gpu, tiny, k, mode):
+    """Fixed acceptance (mode 1: j = k every cycle; mode 2: j = cycle mod (k+1), every
+    rollback depth in turn) against the oracle running the same loop on the CPU."""
+    path, z = tiny
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    toks, js, st = m.generate_spec(z["prompt"][:20], 48, k, force_accept=mode)
+    om = O.Model(path, int(z["n_ctx"]), k_max=7)
+    otoks, ojs, ost = om.generate_spec(z["prompt"][:20], 48, k, force_accept=mode)
+    assert np.array_equal(toks, otoks)
+    assert np.array_equal(js, ojs)
+    want = np.full(len(js), k) if mode == 1 else np.arange(len(js)) % (k + 1)
+    assert np.array_equal(js, want)
+
+
+def test_model_init_rejects_bad_files(gpu):
+    host = host_lib()
+    td = tempfile.mkdtemp()
+    bad = os.path.join(td, "bad.gguf")
+    with open(bad, "wb") as f:
+        f.write(b"NOTGGUF" + b"\0" * 64)
+    with pytest.raises(pyqwen.QgpuError):
+        pyqwen.Model(bad, 64)
+    path = os.path.join(td, "t.gguf")
+    host.write_tiny_gguf(path, 1, 0)
+    data = bytearray(open(path, "rb").read())
+    i = data.find(b"blk.1.ffn_up.weight")
+    data[i:i + 3] = b"xxx"                                   # missing tensor
+    open(bad, "wb").write(bytes(data))
+    with pytest.raises(pyqwen.QgpuError):
+        pyqwen.Model(bad, 64)
