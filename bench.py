@@ -1,28 +1,45 @@
 #!/usr/bin/env python
 """Benchmark of the MTP speculative-decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode gemv|model]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode model|gemv|longctx]
 
-Prints ONE JSON line.  Modes:
-  gemv  : config 1 of the workload -- one batched IQ4_XS dequant-GEMV,
-          17408 x 5120, B = 4 columns, seeded random super-blocks
-          (d ~ fp16(|N(0,0.02)|), random 6-bit scales and nibbles), x ~ N(0,1).
-          A step is one gemv_batch call (activation prep + GEMV kernel).
-          Weights rotate over 12 copies (568 MB) so the 256 MB MALL cannot
-          serve repeats.
+Prints ONE JSON line on stdout (progress goes to stderr).
 
-Timing: HIP events recorded on the library stream around K back-to-back
-steps (inputs resident in HBM).  roofline.achieved = algorithmic bytes per
-launch / average GEMV kernel duration (events around K launches of the GEMV
-kernel alone).  cpu_baseline: the reference engine's own AVX2 gemv_batch
-(oracle/_ref, compiled from the reference sources) on the host cores, on a
-bounded sample of the same workload.
+mode model (default) -- the headline workload: the random-init 27B hybrid
+    (64 layers: 48 Gated-DeltaNet + 16 gated-GQA, hidden 5120, FFN 17408,
+    vocab 248320, all matrices IQ4_XS, plus the MTP draft layer), greedy MTP
+    speculative decode with k = 3 drafts after a 512-token seeded random-id
+    prompt.  A step is one speculative cycle (k MTP drafts, one batched verify
+    of k+1 tokens, on-device argmax/acceptance, state-ring rollback, MTP
+    re-anchor); K = 256 cycles are timed.  value = tokens emitted per second.
+    Random-init weights make the MTP drafts disagree with the backbone, so
+    about one token is accepted per cycle; the same loop with every draft
+    accepted (forced_accept_tok_s) and the verify/decode/draft step times are
+    reported beside it.
+mode gemv -- one batched IQ4_XS dequant-GEMV, 17408 x 5120, B = 4 columns.
+mode longctx -- the same model after an 8192-token prompt; verify-step
+    latency and forced-acceptance throughput for k in {1, 3, 5, 7}.
+
+roofline (every mode): the dominant kernel, k_gemv_iq4, on the gemv workload
+(17408 x 5120 IQ4_XS, B = 4), run first in the process: W + K gemv_batch calls,
+then W + K launches of the GEMV kernel alone on prepared activations, the last
+K bracketed by HIP events on the library stream.  achieved = algorithmic bytes
+per launch (47,349,760 weight + 4 x (5120 + 17408) x 4 activation/output =
+47,710,208 B) / average launch duration.  Weights rotate over 12 copies
+(568 MB) so the 256 MB MALL cannot serve repeats.
+
+cpu_baseline: the reference engine itself (oracle/_ref, compiled from the
+reference sources; AVX2, its own pinned thread pool) on the host cores:
+model mode runs the reference's speculative cycle on the same 27B model file
+for a bounded sample; gemv mode runs its gemv_batch.
 """
 import argparse
 import ctypes
 import json
 import os
+import shutil
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -33,10 +50,11 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 HBM_PEAK_GBS = 8000.0
 IQ4 = 23
 METRIC = "accepted tok/s, 27B IQ4_XS MTP k=3 on 1 GPU; gemv_batch HBM GB/s (% peak)"
+ROOF_KERNEL = "k_gemv_iq4<1, 4>"
 
 
 def log(*a):
-    print(*a, file=sys.stderr, flush=True)
+    print("[bench]", *a, file=sys.stderr, flush=True)
 
 
 def traffic_for(kernel):
@@ -49,8 +67,13 @@ def traffic_for(kernel):
         return None
 
 
-def cpu_baseline_gemv(W, x, ne0, ne1, n, seconds=10.0):
-    """Reference AVX2 gemv_batch (kernels.c:640) with its own thread pool, pinned."""
+def host_cores():
+    return len(os.sched_getaffinity(0))
+
+
+# ---------------------------------------------------------------------------------- CPU baselines
+def cpu_baseline_gemv(W, x, ne0, ne1, n, seconds):
+    """Reference AVX2 gemv_batch (kernels.c:640) with its own pinned thread pool."""
     ref = os.path.join(ROOT, "oracle", "_ref", "libqwenref.so")
     if not os.path.exists(ref):
         return None
@@ -66,7 +89,7 @@ def cpu_baseline_gemv(W, x, ne0, ne1, n, seconds=10.0):
     L.pool_destroy.argtypes = [ctypes.c_void_p]
     L.gemv_batch.argtypes = [ctypes.c_void_p, ctypes.POINTER(TI), F, ctypes.c_uint64, ctypes.c_int, F,
                              ctypes.c_uint64]
-    cores = len(os.sched_getaffinity(0))
+    cores = host_cores()
     pool = L.pool_create(cores, 1)
     copies = [W.copy() for _ in range(4)]            # 190 MB: larger than the host L3
     tis = []
@@ -85,12 +108,40 @@ def cpu_baseline_gemv(W, x, ne0, ne1, n, seconds=10.0):
         if el >= seconds:
             break
     L.pool_destroy(pool)
-    return calls, el, cores
+    algo = W.nbytes + n * (ne0 + ne1) * 4
+    return {"value": round(algo * calls / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "reference",
+            "sample": f"{calls} calls of the reference gemv_batch (IQ4_XS 17408x5120, B=4) over {el:.1f} s, "
+                      f"4 rotating weight copies, pool of {cores} pinned threads"}
 
 
-def bench_gemv(args):
-    from qwen_pkg import host_lib, pyqwen
-    host, gpu = host_lib(), pyqwen.gpu_lib()
+def cpu_baseline_spec(path, prompt, k, seconds):
+    """The reference's greedy MTP speculative cycle (main.c:158-231) on the same model file."""
+    drv = os.path.join(ROOT, "oracle", "_ref", "librefbench.so")
+    if not os.path.exists(drv):
+        return None
+    L = ctypes.CDLL(drv)
+    U = ctypes.POINTER(ctypes.c_uint32)
+    L.ref_spec_bench.argtypes = [ctypes.c_char_p, ctypes.c_uint32, U, ctypes.c_uint32, ctypes.c_uint32,
+                                 ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double, ctypes.c_int,
+                                 ctypes.POINTER(ctypes.c_double)]
+    p = np.ascontiguousarray(prompt, np.uint32)
+    out = (ctypes.c_double * 5)()
+    cores = host_cores()
+    rc = L.ref_spec_bench(path.encode(), 256, p.ctypes.data_as(U), len(p), k, 1, 1000, seconds, cores, out)
+    if rc == -1 or out[3] < 1:
+        return None
+    tps = out[2] / out[1]
+    return {"value": round(tps, 4), "unit": "tok/s", "cores": cores, "kind": "reference",
+            "sample": f"reference engine, same 27B model file, {len(p)}-token prompt (prefill {out[0]:.1f} s), "
+                      f"then {int(out[3])} greedy speculative cycles with k={k} over {out[1]:.1f} s "
+                      f"({int(out[2])} tokens, {int(out[4])} drafts accepted), pool of {cores} pinned threads"
+                      + ("; stopped early: a cycle accepted 2 drafts, which the reference cannot roll back"
+                         if rc == -2 else "")}
+
+
+# ---------------------------------------------------------------------------------- roofline microbench
+def gemv_roofline(gpu, host, steps, warmup):
+    """config-1 GEMV: gemv_batch calls, then the GEMV kernel alone (roofline)."""
     ne0, ne1, B = 5120, 17408, 4
     W = host.synth_matrix(IQ4, ne0, ne1, 1, 0, 0.02)
     x = host.synth_normal(B * ne0, 1, 1).reshape(B, ne0)
@@ -99,63 +150,183 @@ def bench_gemv(args):
     xb, ob = gpu.put(x), gpu.buf(B * ne1 * 4)
     algo = W.nbytes + B * (ne0 + ne1) * 4
     L = gpu.L
-
-    def step(i):
-        gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
-
-    for i in range(args.warmup):
-        step(i)
-    gpu.sync()
     e0, e1 = gpu.event(), gpu.event()
+    # gemv_batch calls (activation prep + GEMV kernel), the library entry point
+    for i in range(warmup):
+        gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
     gpu.record(e0)
-    for i in range(args.steps):
-        step(i)
+    for i in range(steps):
+        gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
     gpu.record(e1)
-    ms_total = gpu.elapsed_ms(e0, e1)
-    ms_step = ms_total / args.steps
-    # GEMV kernel alone: activations prepared once, K launches of the GEMV kernel
+    ms_call = gpu.elapsed_ms(e0, e1) / steps
+    # the GEMV kernel alone: activations prepared once
     gpu.ok(L.qgpu_gemv_prepare(xb.f32(), ne0, B, ne0))
-    for i in range(args.warmup):
+    for i in range(warmup):
         gpu.ok(L.qgpu_gemv_prepared(Ts[i % R].h, B, ob.f32(), ne1, 0))
     gpu.record(e0)
-    for i in range(args.steps):
+    for i in range(steps):
         gpu.ok(L.qgpu_gemv_prepared(Ts[i % R].h, B, ob.f32(), ne1, 0))
     gpu.record(e1)
-    ms_kernel = gpu.elapsed_ms(e0, e1) / args.steps
+    ms_kernel = gpu.elapsed_ms(e0, e1) / steps
     gpu.sync()
+    for T in Ts:
+        T.close()
     achieved = algo / (ms_kernel * 1e-3) / 1e9
-    value = algo / (ms_step * 1e-3) / 1e9
-    cpu = None
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for("k_gemv_iq4"),
+            "kernel": ROOF_KERNEL, "workload": "IQ4_XS 17408x5120, B=4", "kernel_us": round(ms_kernel * 1e3, 3),
+            "algo_bytes": algo,
+            # dispatch ordinals of this kernel (0-based, in launch order) that the events bracket
+            "dispatches": {"first": 2 * warmup + steps, "count": steps}}
+    gemv_call_gbs = algo / (ms_call * 1e-3) / 1e9
+    return roof, gemv_call_gbs, ms_call, (W, x, ne0, ne1, B)
+
+
+# ---------------------------------------------------------------------------------- model workloads
+def model_file(host, seed, keep_dir=None):
+    """Writes the seeded random-init 27B model as a GGUF file (tmpfs when it fits)."""
+    spec = host.spec_27b(seed)
+    need = sum(t.nbytes for t in host.tensors(spec)) + (64 << 20)
+    for d in ([keep_dir] if keep_dir else []) + ["/dev/shm", tempfile.gettempdir()]:
+        try:
+            if shutil.disk_usage(d).free > need + (2 << 30):
+                path = os.path.join(d, f"qwen27b_synth_{seed}_{os.getpid()}.gguf")
+                t = time.time()
+                host.write_gguf(spec, path)
+                log(f"model file {path}: {os.path.getsize(path) / 1e9:.2f} GB written in {time.time() - t:.1f} s")
+                return path, spec
+        except OSError:
+            continue
+    return None, spec
+
+
+def step_bytes(host, spec, B, pos):
+    """Algorithmic HBM bytes of one verify (B tokens) step and of one MTP draft."""
+    ts = host.tensors(spec)
+    mtp_layer = f"blk.{spec.n_layer}."
+    w_backbone = sum(t.nbytes for t in ts if t.n_dims == 2 and not t.name.startswith(b"token_embd")
+                     and not t.name.decode().startswith(mtp_layer))
+    out_w = next(t.nbytes for t in ts if t.name == b"output.weight")
+    w_mtp = sum(t.nbytes for t in ts if t.n_dims == 2 and t.name.decode().startswith(mtp_layer)) + out_w
+    n_attn = spec.n_layer // spec.full_attn_interval
+    n_gdn = spec.n_layer - n_attn
+    state = spec.n_v_heads * spec.state * spec.state * 4
+    gdn = n_gdn * (state * (1 + B))                       # read current state, write B snapshots
+    kv = n_attn * (pos + B) * 2 * spec.n_kv_head * spec.head_dim * 4
+    return w_backbone + gdn + kv, w_mtp + (pos + 1) * 2 * spec.n_kv_head * spec.head_dim * 4
+
+
+def bench_model(args, gpu, host, roof, gemv_call_gbs):
+    from qwen_pkg import pyqwen
+    k, n_prompt = args.k, args.prompt
+    K, W, F = args.steps, args.warmup, args.forced_cycles
+    path = None
     if not args.no_cpu:
-        r = cpu_baseline_gemv(W, x, ne0, ne1, B, args.cpu_seconds)
-        if r:
-            calls, el, cores = r
-            cpu = {"value": round(algo * calls / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "reference",
-                   "sample": f"{calls} calls of the reference gemv_batch (IQ4_XS 17408x5120, B=4) over {el:.1f} s, "
-                             f"4 rotating weight copies, pool of {cores} pinned threads"}
-    name, ncu, _ = gpu.device_info()
+        path, spec = model_file(host, args.seed)
+    else:
+        spec = host.spec_27b(args.seed)
+    n_ctx = ((n_prompt + (k + 1) * (W + K + F) + 64 + 255) // 256) * 256
+    t = time.time()
+    m = pyqwen.Model(path, n_ctx) if path else pyqwen.Model(spec=spec, n_ctx=n_ctx)
+    log(f"model on the GPU in {time.time() - t:.1f} s (n_ctx {n_ctx})")
+    V = m.V
+    prompt = np.random.default_rng(args.seed + 512).integers(0, V, n_prompt).astype(np.uint32)
+    t = time.time()
+    m.spec_begin(prompt, k)
+    t_prefill = time.time() - t
+    log(f"prefill {n_prompt} tokens: {t_prefill:.2f} s")
+    m.spec_run(k, W)                                         # warm-up cycles
+    gpu.sync()
+    toks, js, st = m.spec_run(k, K)                          # timed: exactly K cycles
+    gpu.sync()
+    t_dec = st.t_decode_s
+    log(f"{K} cycles: {len(toks)} tokens in {t_dec:.3f} s, {st.n_accepted}/{st.n_drafts} drafts accepted")
+    ftoks, fjs, fst = m.spec_run(k, F, force_accept=1)       # every draft accepted
+    log(f"forced acceptance: {F} cycles, {len(ftoks)} tokens in {fst.t_decode_s:.3f} s")
+    ms_verify, ms_decode, ms_draft = m.time_steps(k + 1, 20)
+    pos = m.pos
+    vbytes, dbytes = step_bytes(host, spec, k + 1, pos)
+    dec_bytes, _ = step_bytes(host, spec, 1, pos)
+    m.close()
+    cpu = None
+    if path:
+        try:
+            log("CPU baseline: reference speculative loop on the host cores")
+            cpu = cpu_baseline_spec(path, prompt[:8], k, args.cpu_seconds)
+        finally:
+            os.remove(path)
+    value = len(toks) / t_dec
     return {
-        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "iq4_xs x fp32 (int8 MFMA, exact int32 sub-block sums, fp32 accumulate)",
-        "data": "synthetic (seeded random IQ4_XS super-blocks, x ~ N(0,1))",
-        "config": {"workload": "gemv_batch IQ4_XS 17408x5120, B=4 (1 token + 3 drafts)", "rows": ne1, "cols": ne0,
-                   "B": B, "weight_copies": R, "device": name, "cus": ncu},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for("k_gemv_iq4"),
-                     "kernel": "k_gemv_iq4<1,4>", "kernel_ms": round(ms_kernel, 5), "algo_bytes": algo},
-        "cpu_baseline": cpu,
+        "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(t_dec / K * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32 (IQ4_XS weights; int8-MFMA digit GEMV, fp32 accumulate)",
+        "data": "synthetic: seeded random-init 27B hybrid (IQ4_XS), seeded random-id prompt",
+        "config": {"workload": f"27B hybrid greedy MTP speculative decode, k={k}, {n_prompt}-token prompt, "
+                               f"{K} cycles", "k": k, "prompt_tokens": n_prompt, "n_ctx": n_ctx,
+                   "layers": "48 GDN + 16 GQA + MTP", "device": gpu.device_info()[0]},
+        "tokens": int(len(toks)), "drafts_accepted": int(st.n_accepted), "drafts": int(st.n_drafts),
+        "forced_accept_tok_s": round(len(ftoks) / fst.t_decode_s, 2),
+        "verify_ms": round(ms_verify, 4), "decode_ms": round(ms_decode, 4), "draft_ms": round(ms_draft, 4),
+        "verify_over_decode": round(ms_verify / ms_decode, 4),
+        "verify_hbm_gbs": round(vbytes / (ms_verify * 1e-3) / 1e9, 1),
+        "decode_hbm_gbs": round(dec_bytes / (ms_decode * 1e-3) / 1e9, 1),
+        "draft_hbm_gbs": round(dbytes / (ms_draft * 1e-3) / 1e9, 1),
+        "prefill_s": round(t_prefill, 3),
+        "gemv_batch_gbs": round(gemv_call_gbs, 1), "gemv_batch_frac": round(gemv_call_gbs / HBM_PEAK_GBS, 4),
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+
+
+def bench_longctx(args, gpu, host, roof, gemv_call_gbs):
+    from qwen_pkg import pyqwen
+    spec = host.spec_27b(args.seed)
+    n_prompt, F = args.prompt, args.forced_cycles
+    ks = [1, 3, 5, 7]
+    n_ctx = ((n_prompt + sum((kk + 1) * (F + 1) for kk in ks) + 64 + 255) // 256) * 256
+    m = pyqwen.Model(spec=spec, n_ctx=n_ctx)
+    prompt = np.random.default_rng(args.seed + 8192).integers(0, m.V, n_prompt).astype(np.uint32)
+    t = time.time()
+    m.spec_begin(prompt, 7)
+    t_prefill = time.time() - t
+    log(f"prefill {n_prompt} tokens: {t_prefill:.2f} s")
+    rows, tot_t = {}, 0.0
+    for kk in ks:
+        ms_verify, ms_decode, ms_draft = m.time_steps(kk + 1, 10)
+        m.spec_run(kk, 1, force_accept=1)
+        toks, js, st = m.spec_run(kk, F, force_accept=1)
+        rows[f"k{kk}"] = {"verify_ms": round(ms_verify, 4), "decode_ms": round(ms_decode, 4),
+                          "draft_ms": round(ms_draft, 4), "verify_over_decode": round(ms_verify / ms_decode, 4),
+                          "forced_accept_tok_s": round(len(toks) / st.t_decode_s, 2), "pos": m.pos}
+        tot_t += st.t_decode_s
+        log(f"k={kk}: {rows[f'k{kk}']}")
+    m.close()
+    K = F * len(ks)
+    return {
+        "metric": METRIC, "value": rows["k3"]["forced_accept_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": K,
+        "warmup": len(ks), "ms_per_step": round(tot_t / K * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32 (IQ4_XS weights; int8-MFMA digit GEMV, fp32 accumulate)",
+        "data": "synthetic: seeded random-init 27B hybrid (IQ4_XS), seeded random-id prompt",
+        "config": {"workload": f"27B hybrid, {n_prompt}-token prompt, forced-acceptance k sweep {ks}",
+                   "prompt_tokens": n_prompt, "n_ctx": n_ctx, "cycles_per_k": F},
+        "per_k": rows, "prefill_s": round(t_prefill, 3),
+        "gemv_batch_gbs": round(gemv_call_gbs, 1), "roofline": roof, "cpu_baseline": None,
     }
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--mode", choices=["gemv"], default="gemv")
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (model: cycles; gemv: calls)")
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--mode", choices=["model", "gemv", "longctx"], default="model")
+    ap.add_argument("--k", type=int, default=3, help="drafts per speculative cycle (model mode)")
+    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (model 512, longctx 8192)")
+    ap.add_argument("--forced-cycles", type=int, default=None)
+    ap.add_argument("--seed", type=int, default=27)
+    ap.add_argument("--gemv-steps", type=int, default=200)
+    ap.add_argument("--gemv-warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=None)
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run the k_copy kernel on 256 MiB x 5 (reference point for PMC byte counters)")
     args = ap.parse_args()
@@ -163,17 +334,48 @@ def main():
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    dflt = {"model": (256, 8, 512, 64, 15.0), "gemv": (200, 20, 0, 0, 5.0), "longctx": (0, 0, 8192, 16, 0.0)}
+    s, w, p, f, c = dflt[args.mode]
+    args.steps = s if args.steps is None else args.steps
+    args.warmup = w if args.warmup is None else args.warmup
+    args.prompt = p if args.prompt is None else args.prompt
+    args.forced_cycles = f if args.forced_cycles is None else args.forced_cycles
+    args.cpu_seconds = c if args.cpu_seconds is None else args.cpu_seconds
+
+    from qwen_pkg import host_lib, pyqwen
+    host, gpu = host_lib(), pyqwen.gpu_lib()
+    name, ncu, _ = gpu.device_info()
+    log(f"device {name}, {ncu} CUs; mode {args.mode}")
+    gs, gw = (args.steps, args.warmup) if args.mode == "gemv" else (args.gemv_steps, args.gemv_warmup)
+    roof, gemv_gbs, ms_call, wx = gemv_roofline(gpu, host, gs, gw)
+    log(f"roofline {ROOF_KERNEL}: {roof['kernel_us']} us/launch, {roof['achieved']} GB/s "
+        f"({100 * roof['frac']:.1f}% of peak); gemv_batch call {gemv_gbs:.1f} GB/s")
     if args.copy_calib:
-        from qwen_pkg import pyqwen
-        gpu = pyqwen.gpu_lib()
         nb = 256 << 20
         a, b = gpu.buf(nb), gpu.buf(nb)
         gpu.ok(gpu.L.qgpu_memset(ctypes.c_void_p(a.ptr), 1, nb))
         for _ in range(5):
             gpu.ok(gpu.L.qgpu_copy(ctypes.c_void_p(b.ptr), ctypes.c_void_p(a.ptr), nb))
         gpu.sync()
-    res = bench_gemv(args)
-    print(json.dumps(res))
+        a.close()
+        b.close()
+    if args.mode == "gemv":
+        W, x, ne0, ne1, B = wx
+        res = {
+            "metric": METRIC, "value": round(gemv_gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_call, 5), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp32 (IQ4_XS weights; int8-MFMA digit GEMV, fp32 accumulate)",
+            "data": "synthetic (seeded random IQ4_XS super-blocks, x ~ N(0,1))",
+            "config": {"workload": "gemv_batch IQ4_XS 17408x5120, B=4 (1 token + 3 drafts)", "rows": ne1,
+                       "cols": ne0, "B": B, "weight_copies": 12, "device": name, "cus": ncu},
+            "roofline": roof,
+            "cpu_baseline": None if args.no_cpu else cpu_baseline_gemv(W, x, ne0, ne1, B, args.cpu_seconds),
+        }
+    elif args.mode == "model":
+        res = bench_model(args, gpu, host, roof, gemv_gbs)
+    else:
+        res = bench_longctx(args, gpu, host, roof, gemv_gbs)
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":

@@ -127,6 +127,13 @@ typedef struct {
 uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
                              uint32_t k, uint32_t eos, int force_accept, uint32_t *out, uint32_t *cycle_j,
                              qwen_gen_stats_t *st);
+/* The same loop in two parts, for callers that time or pace the cycles:
+ * model_spec_begin prefills the prompt (0, or -1 on bad arguments);
+ * model_spec_run continues from the current state for at most max_cycles
+ * cycles / max_tokens tokens and may be called again to go on. */
+int      model_spec_begin(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t k);
+uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_accept, uint32_t max_cycles,
+                        uint32_t max_tokens, uint32_t *out, uint32_t *cycle_j, qwen_gen_stats_t *st);
 /* Plain greedy decode with model_forward steps (the lossless reference stream). */
 uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
                                uint32_t eos, uint32_t *out, qwen_gen_stats_t *st);

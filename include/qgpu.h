@@ -89,6 +89,39 @@ int  qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, const float 
  * with ne0 columns on them; several matrices may follow one prepare. */
 int  qgpu_gemv_prepare(const float *x, uint64_t ldx, int n, uint64_t ne0);
 int  qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, int flags);
+/* Fused activation transforms.  The GEMV input is computed from the rows
+ * named here inside the kernel that prepares the activations, so the
+ * normalisation / gating pass of the reference is not a kernel of its own:
+ *   QGPU_ACT_COPY       v = x
+ *   QGPU_ACT_RMSNORM    v = x / sqrt(mean(x^2) + eps) * w          (model.c:433,460,737,996)
+ *                       with seg = ne0 / 2: the two halves [x | y] each
+ *                       normalised with their own row and weight (w, w2):
+ *                       the MTP input concat(enorm(e), hnorm(h)) (model.c:1046-1050)
+ *   QGPU_ACT_SILU_MUL   v = silu(x) * y                            (model.c:477-480)
+ *   QGPU_ACT_GATED_NORM v = rmsnorm_head(x) * w[i % seg] * silu(y)  per head of seg
+ *                       in {64, 128, 256} elements                  (model.c:928-941)
+ * xout (optional, ldxo) receives v in fp32; it is required when a matrix of
+ * the call is not IQ4_XS (those kernels read fp32 rows).  ne0 % 256 == 0. */
+#define QGPU_ACT_COPY        0
+#define QGPU_ACT_RMSNORM     1
+#define QGPU_ACT_SILU_MUL    2
+#define QGPU_ACT_GATED_NORM  3
+typedef struct {
+    int          kind;
+    const float *x;   uint64_t ldx;
+    const float *y;   uint64_t ldy;
+    const float *w;
+    const float *w2;
+    uint64_t     seg;
+    float        eps;
+    float       *xout; uint64_t ldxo;
+} qgpu_act;
+/* qgpu_gemv_multi_batch with the input given as a transform of device rows. */
+int  qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,
+                         float *const *outs, const uint64_t *ldos, int flags);
+/* Transform only: v into act->xout (required) and the IQ4_XS digit planes
+ * (so qgpu_gemv_prepared may follow). */
+int  qgpu_act_prepare(const qgpu_act *act, int n, uint64_t ne0);
 /* Rows [r0, r1) only (reference gemv_rows, kernels.c:298-321). */
 int  qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
                           float *out, uint64_t ldo, uint64_t r0, uint64_t r1);

@@ -126,19 +126,106 @@ int qg_repack_iq4xs(const void *raw, uint64_t ne0, uint64_t ne1, void *packed, i
 // Two consecutive sub-blocks are interleaved so a lane fetches 16 bytes:
 //   byte offset ((sb*4 + ib/2)*64 + l)*16 + (ib%2)*8 + (slot%8).
 // xs[sb*16 + m] = 2^(8*dgt - s_t) converts the integer result of row m.
-__global__ __launch_bounds__(256) void k_prep_digits(const float *__restrict__ x, uint64_t ldx, int ntok,
-                                                     uint8_t *__restrict__ A, float *__restrict__ xs)
+struct ActDev {
+    const float *x, *y, *w, *w2;
+    float *xout;
+    uint64_t ldx, ldy, ldxo, seg;
+    float eps;
+    int ntok, digits;
+};
+
+static __device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + expf(-v)); }
+
+static __device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// One block = one 256-element super-block (blockIdx.x) of the 4 tokens of
+// plane blockIdx.y.  The activation transform KIND (QGPU_ACT_*) is applied
+// first; v may also be stored in fp32 (xout).
+template <int KIND>
+__global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict__ A, float *__restrict__ xs)
 {
     __shared__ uint8_t stage[4096];
     __shared__ float red[4][8];
     __shared__ int shift[4];
     const int e = threadIdx.x, sb = blockIdx.x, a = blockIdx.y;
     const int lane = e & 63, wv = e >> 6;
-    float v[4], m[4];
+    const uint64_t k = (uint64_t)sb * 256 + e;
+    float v[4];
+    if (KIND == QGPU_ACT_RMSNORM) {
+        // row RMS over the segment holding this super-block (each block recomputes it: same order, same value)
+        const uint64_t segl = p.seg;
+        const int part = (uint64_t)sb * 256 >= segl ? 1 : 0;
+        const float *src = part ? p.y : p.x;
+        const float *w = part ? p.w2 : p.w;
+        const uint64_t ld = part ? p.ldy : p.ldx, kk = k - (part ? segl : 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * a + i;
+            float ss = 0.0f;
+            if (t < p.ntok) {
+                const float4 *row = (const float4 *)(src + (uint64_t)t * ld);
+                for (uint64_t j = e; j < segl / 4; j += 256) {
+                    const float4 q = row[j];
+                    ss = fmaf(q.x, q.x, ss); ss = fmaf(q.y, q.y, ss); ss = fmaf(q.z, q.z, ss); ss = fmaf(q.w, q.w, ss);
+                }
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) red[i][wv] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * a + i;
+            const float tot = (red[i][0] + red[i][1]) + (red[i][2] + red[i][3]);
+            const float sc = 1.0f / sqrtf(tot / (float)segl + p.eps);
+            v[i] = t < p.ntok ? (src[(uint64_t)t * ld + kk] * sc) * w[kk] : 0.0f;
+        }
+        __syncthreads();
+    } else if (KIND == QGPU_ACT_GATED_NORM) {
+        // heads of seg = 64 * hw elements: waves [h0, h0 + hw) of this block hold one head
+        const int hw = (int)(p.seg >> 6), h0 = (wv / hw) * hw;
+        float raw[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * a + i;
+            raw[i] = t < p.ntok ? p.x[(uint64_t)t * p.ldx + k] : 0.0f;
+            const float ss = wave_sum(raw[i] * raw[i]);
+            if (lane == 0) red[i][wv] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * a + i;
+            float tot = red[i][h0];
+            for (int q = 1; q < hw; q++) tot += red[i][h0 + q];
+            const float sc = 1.0f / sqrtf(tot / (float)p.seg + p.eps);
+            v[i] = t < p.ntok ? ((raw[i] * sc) * p.w[k & (p.seg - 1)]) * silu_dev(p.y[(uint64_t)t * p.ldy + k])
+                              : 0.0f;
+        }
+        __syncthreads();
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * a + i;
+            if (t >= p.ntok) { v[i] = 0.0f; continue; }
+            const float xv = p.x[(uint64_t)t * p.ldx + k];
+            v[i] = KIND == QGPU_ACT_SILU_MUL ? silu_dev(xv) * p.y[(uint64_t)t * p.ldy + k] : xv;
+        }
+    }
+    if (p.xout) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (4 * a + i < p.ntok) p.xout[(uint64_t)(4 * a + i) * p.ldxo + k] = v[i];
+    }
+    if (!p.digits) return;
+    float m[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int t = 4 * a + i;
-        v[i] = t < ntok ? x[(uint64_t)t * ldx + (uint64_t)sb * 256 + e] : 0.0f;
         m[i] = fabsf(v[i]);
 #pragma unroll
         for (int o = 32; o; o >>= 1) m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
@@ -472,19 +559,59 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
 }
 
 // ---------------------------------------------------------------- launchers
-static int prep_x(const float *x, uint64_t ldx, int n, uint64_t ne0)
+// Validates an activation transform for n rows of ne0 and launches its prep
+// kernel: digit planes into the workspace when `digits`, fp32 rows into xout.
+static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits)
 {
-    if (ne0 > MAX_K || ne0 % 256) return QGPU_E_RANGE;
-    const int na = n > 4 ? 2 : 1;
-    hipLaunchKernelGGL(k_prep_digits, dim3((unsigned)(ne0 / 256), (unsigned)na), dim3(256), 0, qg::stream,
-                       x, ldx, n, (uint8_t *)qg::ws, (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES));
+    if (!act || !act->x || n < 1 || n > QGPU_MAX_B) return QGPU_E_ARG;
+    if (ne0 % 256 || (digits && ne0 > MAX_K)) return QGPU_E_RANGE;
+    ActDev d = {};
+    d.x = act->x; d.y = act->y; d.w = act->w; d.w2 = act->w2; d.xout = act->xout;
+    d.ldx = act->ldx; d.ldy = act->ldy; d.ldxo = act->ldxo; d.eps = act->eps; d.ntok = n; d.digits = digits;
+    const bool rows = n > 1;
+    if (act->xout && rows && act->ldxo < ne0) return QGPU_E_ARG;
+    uint64_t wx = ne0;                                    // columns read from x
+    switch (act->kind) {
+    case QGPU_ACT_COPY: break;
+    case QGPU_ACT_RMSNORM: {
+        d.seg = act->seg ? act->seg : ne0;
+        if ((d.seg != ne0 && 2 * d.seg != ne0) || d.seg % 256 || !act->w) return QGPU_E_ARG;
+        if (d.seg != ne0 && (!act->y || !act->w2 || (rows && act->ldy < d.seg) || act->ldy % 4 ||
+                             ((uintptr_t)act->y & 15)))
+            return QGPU_E_ARG;
+        if (act->ldx % 4 || ((uintptr_t)act->x & 15)) return QGPU_E_ARG;   // float4 row sums
+        wx = d.seg;
+        break;
+    }
+    case QGPU_ACT_SILU_MUL:
+        if (!act->y || (rows && act->ldy < ne0)) return QGPU_E_ARG;
+        break;
+    case QGPU_ACT_GATED_NORM:
+        d.seg = act->seg;
+        if (!act->y || !act->w || (rows && act->ldy < ne0) || (d.seg != 64 && d.seg != 128 && d.seg != 256))
+            return QGPU_E_ARG;
+        break;
+    default: return QGPU_E_ARG;
+    }
+    if (rows && act->ldx < wx) return QGPU_E_ARG;
+    const dim3 grid((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1));
+    uint8_t *A = (uint8_t *)qg::ws;
+    float *xs = (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES);
+    switch (act->kind) {
+    case QGPU_ACT_COPY: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_COPY>, grid, dim3(256), 0, qg::stream, d, A, xs); break;
+    case QGPU_ACT_RMSNORM: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_RMSNORM>, grid, dim3(256), 0, qg::stream, d, A, xs); break;
+    case QGPU_ACT_SILU_MUL: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_SILU_MUL>, grid, dim3(256), 0, qg::stream, d, A, xs); break;
+    default: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_GATED_NORM>, grid, dim3(256), 0, qg::stream, d, A, xs); break;
+    }
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }
 
+// One launch for the matrices idx[0..cnt) of one format.  IQ4_XS reads the
+// digit planes already in the workspace; the other formats read fp32 rows x.
 static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x, uint64_t ldx,
                         int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
-                        const uint64_t *r1s, int prepared)
+                        const uint64_t *r1s)
 {
     const qgpu_tensor *W0 = Ws[idx[0]];
     GemvArgs A = {};
@@ -513,10 +640,6 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
         const int na = n > 4 ? 2 : 1;
         A.A = (const uint8_t *)qg::ws;
         A.xs = (const float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES);
-        if (!prepared) {
-            const int rc = prep_x(x, ldx, n, W0->ne0);
-            if (rc) return rc;
-        }
         // waves per tile (K split inside the block).  Measured on MI355X over the
         // model's shapes (K = 5120..17408, 5120..248320 rows, B = 1..8): 4 waves is
         // best or within 1% everywhere except very tall matrices (lm_head), where
@@ -561,21 +684,40 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
     return QGPU_OK;
 }
 
-static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx, int n,
-                      float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s,
-                      int prepared = 0)
+// act == NULL: IQ4_XS matrices only, on the digit planes of the last prepare.
+static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n, float *const *outs,
+                      const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s)
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
-    if (prepared && !x) x = (const float *)qg::ws;           // activations already in the workspace
-    if (!Ws || !x || !outs || !ldos || n_mat < 1 || n_mat > QGPU_MAX_MULTI || n < 1 || n > QGPU_MAX_B)
+    if (!Ws || !outs || !ldos || n_mat < 1 || n_mat > QGPU_MAX_MULTI || n < 1 || n > QGPU_MAX_B || !Ws[0])
         return QGPU_E_ARG;
+    const uint64_t ne0 = Ws[0]->ne0;
+    bool any_iq4 = false, any_valu = false;
     for (int j = 0; j < n_mat; j++) {
-        if (!Ws[j] || !outs[j] || Ws[j]->ne0 != Ws[0]->ne0 || ldx < Ws[j]->ne0) return QGPU_E_ARG;
+        if (!Ws[j] || !outs[j] || Ws[j]->ne0 != ne0) return QGPU_E_ARG;
         if (n > 1 && ldos[j] < (r1s ? r1s[j] : Ws[j]->ne1)) return QGPU_E_ARG;
         if (r0s && (r0s[j] > r1s[j] || r1s[j] > Ws[j]->ne1)) return QGPU_E_ARG;
+        if (Ws[j]->type == T_IQ4_XS) any_iq4 = true; else any_valu = true;
     }
-    if (Ws[0]->type != T_F32 && (ldx % 4 || ((uintptr_t)x & 15))) return QGPU_E_ARG;   // float4 activation loads
+    const float *xv = nullptr;                              // fp32 rows for the non-IQ4_XS kernels
+    uint64_t ldxv = ne0;
+    if (!act) {
+        if (any_valu) return QGPU_E_TYPE;
+    } else {
+        const bool xform = act->kind != QGPU_ACT_COPY;
+        if (any_valu) {
+            xv = xform ? act->xout : act->x;
+            ldxv = xform ? act->ldxo : act->ldx;
+            if (!xv || (n > 1 && ldxv < ne0)) return QGPU_E_ARG;
+            if (ldxv % 4 || ((uintptr_t)xv & 15)) return QGPU_E_ARG;   // float4 activation loads
+        }
+        if (any_iq4 || xform) {
+            if (!any_iq4 && ne0 % 256) return QGPU_E_RANGE;
+            rc = prep_act(act, n, ne0, any_iq4 ? 1 : 0);
+            if (rc) return rc;
+        }
+    }
     // group matrices of the same format (one launch per group)
     int done[QGPU_MAX_MULTI] = {0};
     for (int j = 0; j < n_mat; j++) {
@@ -583,42 +725,73 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const float *x, u
         int idx[QGPU_MAX_MULTI], cnt = 0;
         for (int i = j; i < n_mat; i++)
             if (!done[i] && Ws[i]->type == Ws[j]->type) { idx[cnt++] = i; done[i] = 1; }
-        rc = launch_group(Ws, idx, cnt, x, ldx, n, outs, ldos, flags, r0s, r1s, prepared && Ws[j]->type == T_IQ4_XS);
+        rc = launch_group(Ws, idx, cnt, xv, ldxv, n, outs, ldos, flags, r0s, r1s);
         if (rc) return rc;
     }
     return QGPU_OK;
 }
 
+static qgpu_act copy_act(const float *x, uint64_t ldx)
+{
+    qgpu_act a = {};
+    a.kind = QGPU_ACT_COPY;
+    a.x = x;
+    a.ldx = ldx;
+    return a;
+}
+
 extern "C" int qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
                                uint64_t ldo, int flags)
 {
-    return gemv_multi(&W, 1, x, ldx, n, &out, &ldo, flags, nullptr, nullptr);
+    if (!x || !W || (n > 1 && ldx < W->ne0)) return QGPU_E_ARG;
+    const qgpu_act a = copy_act(x, ldx);
+    return gemv_multi(&W, 1, &a, n, &out, &ldo, flags, nullptr, nullptr);
 }
 
 extern "C" int qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx, int n,
                                      float *const *outs, const uint64_t *ldos, int flags)
 {
-    return gemv_multi(Ws, n_mat, x, ldx, n, outs, ldos, flags, nullptr, nullptr);
+    if (!x || !Ws || !Ws[0] || (n > 1 && ldx < Ws[0]->ne0)) return QGPU_E_ARG;
+    const qgpu_act a = copy_act(x, ldx);
+    return gemv_multi(Ws, n_mat, &a, n, outs, ldos, flags, nullptr, nullptr);
+}
+
+extern "C" int qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,
+                                   float *const *outs, const uint64_t *ldos, int flags)
+{
+    if (!act) return QGPU_E_ARG;
+    return gemv_multi(Ws, n_mat, act, n, outs, ldos, flags, nullptr, nullptr);
 }
 
 extern "C" int qgpu_gemv_prepare(const float *x, uint64_t ldx, int n, uint64_t ne0)
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
-    if (!x || n < 1 || n > QGPU_MAX_B || ldx < ne0 || ldx % 4 || ((uintptr_t)x & 15)) return QGPU_E_ARG;
-    return prep_x(x, ldx, n, ne0);
+    if (!x || (n > 1 && ldx < ne0)) return QGPU_E_ARG;
+    const qgpu_act a = copy_act(x, ldx);
+    return prep_act(&a, n, ne0, 1);
+}
+
+extern "C" int qgpu_act_prepare(const qgpu_act *act, int n, uint64_t ne0)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!act || !act->xout) return QGPU_E_ARG;
+    return prep_act(act, n, ne0, ne0 <= MAX_K ? 1 : 0);
 }
 
 extern "C" int qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, int flags)
 {
     if (!W || W->type != T_IQ4_XS) return QGPU_E_TYPE;
-    return gemv_multi(&W, 1, nullptr, W->ne0, n, &out, &ldo, flags, nullptr, nullptr, 1);
+    return gemv_multi(&W, 1, nullptr, n, &out, &ldo, flags, nullptr, nullptr);
 }
 
 extern "C" int qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
                                     uint64_t ldo, uint64_t r0, uint64_t r1)
 {
-    return gemv_multi(&W, 1, x, ldx, n, &out, &ldo, 0, &r0, &r1);
+    if (!x || !W || (n > 1 && ldx < W->ne0)) return QGPU_E_ARG;
+    const qgpu_act a = copy_act(x, ldx);
+    return gemv_multi(&W, 1, &a, n, &out, &ldo, 0, &r0, &r1);
 }
 
 // ---------------------------------------------------------------- dequant rows (embedding)

@@ -246,7 +246,7 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     /* shapes the GPU kernels are written for */
     if (d->head_k_dim != 128 || d->head_dim != 256 || d->d_conv != 4 || c->rope_dim_count > d->head_dim ||
         d->n_embd % 256 || d->n_ff % 256 || !d->n_kv_head || d->n_head % d->n_kv_head ||
-        (d->n_head / d->n_kv_head) * MAXB > 64) {
+        (d->n_head / d->n_kv_head) * MAXB > 64 || d->d_inner > d->n_ff) {
         fprintf(stderr, "model_init: dimensions outside what the GPU kernels support\n");
         return -1;
     }
@@ -418,18 +418,32 @@ void model_free(qwen_model_t *m)
 }
 
 /* ------------------------------------------------------------------ device layers */
+/* activation transforms fused into the GEMV input preparation (include/qgpu.h) */
+static qgpu_act act_norm(const float *x, uint64_t ldx, const float *w, float eps, float *xout, uint64_t ldxo)
+{
+    qgpu_act a;
+    memset(&a, 0, sizeof a);
+    a.kind = QGPU_ACT_RMSNORM; a.x = x; a.ldx = ldx; a.w = w; a.eps = eps; a.xout = xout; a.ldxo = ldxo;
+    return a;
+}
+
 static void ffn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B)
 {
     qwen_gpu_t *g = m->gpu;
     const uint64_t E = m->dims.n_embd, F = m->dims.n_ff;
     const float eps = m->cfg.rms_norm_eps;
-    K(qgpu_rmsnorm(g->bxb, E, R, E, D->post_norm, E, (int)B, eps));
+    /* post-attention RMSNorm -> gate/up (model.c:469-476) */
+    const qgpu_act an = act_norm(R, E, D->post_norm, eps, g->bxb, E);
     const qgpu_tensor *W[2] = { D->ffn_gate, D->ffn_up };
     float *outs[2] = { g->bffn, g->bqkv };
     const uint64_t ld[2] = { F, g->SQ };
-    K(qgpu_gemv_multi_batch(W, 2, g->bxb, E, (int)B, outs, ld, 0));
-    K(qgpu_silu_mul(g->bffn, F, g->bqkv, g->SQ, F, (int)B));
-    K(qgpu_gemv_batch(D->ffn_down, g->bffn, F, (int)B, R, E, QGPU_GEMV_ACCUM));
+    K(qgpu_gemv_act_batch(W, 2, &an, (int)B, outs, ld, 0));
+    /* silu(gate) * up -> down, residual add (model.c:477-483) */
+    qgpu_act sm;
+    memset(&sm, 0, sizeof sm);
+    sm.kind = QGPU_ACT_SILU_MUL; sm.x = g->bffn; sm.ldx = F; sm.y = g->bqkv; sm.ldy = g->SQ;
+    sm.xout = g->bffn; sm.ldxo = F;
+    K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&D->ffn_down, 1, &sm, (int)B, &R, &E, QGPU_GEMV_ACCUM));
 }
 
 static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_t pos)
@@ -438,11 +452,11 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     const qwen_dims_t *d = &m->dims;
     const uint64_t E = d->n_embd;
     const float eps = m->cfg.rms_norm_eps;
-    K(qgpu_rmsnorm(g->bxb, E, R, E, D->attn_norm, E, (int)B, eps));
+    const qgpu_act an = act_norm(R, E, D->attn_norm, eps, g->bxb, E);
     const qgpu_tensor *W[3] = { D->q, D->k, D->v };
     float *outs[3] = { g->bqkv, g->bk, g->bv };
     const uint64_t ld[3] = { g->SQ, g->kvrow, g->kvrow };
-    K(qgpu_gemv_multi_batch(W, 3, g->bxb, E, (int)B, outs, ld, 0));
+    K(qgpu_gemv_act_batch(W, 3, &an, (int)B, outs, ld, 0));
     K(qgpu_attn_prep(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos,
                      g->rope_sin, (int)m->cfg.rope_dim_count, g->d_pos, (int)B, (int)d->n_head, (int)d->n_kv_head,
                      (int)d->head_dim, eps));
@@ -458,19 +472,22 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     const qwen_dims_t *d = &m->dims;
     const uint64_t E = d->n_embd, di = d->d_inner;
     const float eps = m->cfg.rms_norm_eps;
-    K(qgpu_rmsnorm(g->bxb, E, g->bx, E, D->attn_norm, E, (int)B, eps));
+    const qgpu_act an = act_norm(g->bx, E, D->attn_norm, eps, g->bxb, E);
     const qgpu_tensor *W[4] = { D->wqkv, D->wgate, D->beta, D->alpha };
     float *outs[4] = { g->bqkv, g->bz, g->bbeta, g->balpha };
     const uint64_t ld[4] = { g->SQ, di, d->n_v_heads, d->n_v_heads };
-    K(qgpu_gemv_multi_batch(W, 4, g->bxb, E, (int)B, outs, ld, 0));
+    K(qgpu_gemv_act_batch(W, 4, &an, (int)B, outs, ld, 0));
     K(qgpu_gdn_conv(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems, NSLOT,
                     g->d_cur, g->xq, d->conv_dim));
     K(qgpu_gdn_recurrence(g->xq, d->conv_dim, g->bbeta, g->balpha, d->n_v_heads, D->dt_bias, D->ssm_a, D->ssm_ring,
                           g->ssm_elems, NSLOT, g->d_cur, (int)B, (int)d->n_k_heads, (int)d->n_v_heads,
                           (int)d->head_v_dim, eps, g->battn, di));
-    K(qgpu_rmsnorm_gated(g->battn, g->battn, g->bz, D->ssm_norm, (int)d->head_v_dim, (int)(B * d->n_v_heads),
-                         d->head_v_dim, eps));
-    K(qgpu_gemv_batch(D->ssm_out, g->battn, di, (int)B, g->bx, E, QGPU_GEMV_ACCUM));
+    /* per-head gated RMSNorm (model.c:928-941) fused into the ssm_out input */
+    qgpu_act gn;
+    memset(&gn, 0, sizeof gn);
+    gn.kind = QGPU_ACT_GATED_NORM; gn.x = g->battn; gn.ldx = di; gn.y = g->bz; gn.ldy = di; gn.w = D->ssm_norm;
+    gn.seg = d->head_v_dim; gn.eps = eps; gn.xout = g->bffn; gn.ldxo = di;
+    K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&D->ssm_out, 1, &gn, (int)B, &g->bx, &E, QGPU_GEMV_ACCUM));
     ffn_dev(m, D, g->bx, B);
 }
 
@@ -481,7 +498,7 @@ static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, u
 {
     qwen_gpu_t *g = m->gpu;
     const qwen_dims_t *d = &m->dims;
-    const uint64_t E = d->n_embd;
+    const uint64_t E = d->n_embd, V = m->cfg.vocab_size;
     K(qgpu_set_i32(g->d_pos, (int)pos));
     K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bx, E));
     for (uint32_t il = 0; il < d->n_layer; il++) {
@@ -489,8 +506,8 @@ static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, u
         else attn_dev(m, &g->L[il], g->bx, B, pos);
     }
     if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
-    K(qgpu_rmsnorm(g->bxb, E, g->bx, E, g->out_norm, E, (int)B, m->cfg.rms_norm_eps));
-    K(qgpu_gemv_batch(g->output, g->bxb, E, (int)B, d_logits, m->cfg.vocab_size, 0));
+    const qgpu_act an = act_norm(g->bx, E, g->out_norm, m->cfg.rms_norm_eps, g->bxb, E);
+    K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
     g->cur_base = g->cur;
     g->cur = (g->cur + (int)B) % NSLOT;
     K(qgpu_set_i32(g->d_cur, g->cur));
@@ -502,18 +519,19 @@ static void mtp_dev(qwen_model_t *m, const uint32_t *d_tokens, const float *h, u
                     float *d_logits)
 {
     qwen_gpu_t *g = m->gpu;
-    const uint64_t E = m->dims.n_embd;
+    const uint64_t E = m->dims.n_embd, V = m->cfg.vocab_size;
     const float eps = m->cfg.rms_norm_eps;
     K(qgpu_set_i32(g->d_pos, (int)pos));
-    K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->cat, 2 * E));
-    K(qgpu_rmsnorm(g->cat, 2 * E, g->cat, 2 * E, g->enorm, E, (int)B, eps));
-    K(qgpu_rmsnorm(g->cat + E, 2 * E, h, E, g->hnorm, E, (int)B, eps));
-    K(qgpu_gemv_batch(g->eh_proj, g->cat, 2 * E, (int)B, g->mx, E, 0));
+    K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bxb, E));
+    /* eh_proj(concat(enorm(e), hnorm(h))) (model.c:1044-1052): both norms in the input preparation */
+    qgpu_act cat = act_norm(g->bxb, E, g->enorm, eps, g->cat, 2 * E);
+    cat.y = h; cat.ldy = E; cat.w2 = g->hnorm; cat.seg = E;
+    K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->eh_proj, 1, &cat, (int)B, &g->mx, &E, 0));
     attn_dev(m, &g->mtp, g->mx, B, pos);
     K(qgpu_copy(g->mtp_h, g->mx + (B - 1) * E, E * sizeof(float)));
     if (d_logits) {
-        K(qgpu_rmsnorm(g->bxb, E, g->mx, E, g->shnorm, E, (int)B, eps));
-        K(qgpu_gemv_batch(g->output, g->bxb, E, (int)B, d_logits, m->cfg.vocab_size, 0));
+        const qgpu_act an = act_norm(g->mx, E, g->shnorm, eps, g->bxb, E);
+        K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
     }
 }
 
@@ -649,9 +667,16 @@ static void prefill_dev(qwen_model_t *m, const uint32_t *prompt, uint32_t n, int
                   g->d_cand));
 }
 
-uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
-                             uint32_t k, uint32_t eos, int force_accept, uint32_t *out, uint32_t *cycle_j,
-                             qwen_gen_stats_t *st)
+int model_spec_begin(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t k)
+{
+    if (!m || !m->gpu || !prompt || n_prompt < 1 || n_prompt >= m->n_ctx) return -1;
+    prefill_dev(m, prompt, n_prompt, k > 0);
+    K(qgpu_sync());
+    return 0;
+}
+
+uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_accept, uint32_t max_cycles,
+                        uint32_t max_tokens, uint32_t *out, uint32_t *cycle_j, qwen_gen_stats_t *st)
 {
     qwen_gpu_t *g = m->gpu;
     const uint32_t V = m->cfg.vocab_size;
@@ -659,16 +684,11 @@ uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n
     qwen_gen_stats_t s;
     memset(&s, 0, sizeof s);
     if (k > SPEC_MAX_B - 1) k = SPEC_MAX_B - 1;
-    if (n_prompt < 1 || n_prompt >= m->n_ctx) return 0;
-    double t0 = now_s();
-    prefill_dev(m, prompt, n_prompt, k > 0);
-    K(qgpu_sync());
-    s.t_prefill_s = now_s() - t0;
-    t0 = now_s();
+    const double t0 = now_s();
     uint32_t gen = 0;
     uint32_t acc[24], next0;
-    K(qgpu_memcpy_d2h(&next0, g->d_cand, sizeof next0));
-    while (gen < n_predict) {
+    K(qgpu_memcpy_d2h(&next0, g->d_cand, sizeof next0));          /* argmax of the last verified row */
+    while (gen < max_tokens && s.n_cycles < max_cycles && m->pos >= 1) {
         const uint32_t P = m->pos - 1;
         const uint32_t room = m->n_ctx - 1 - P;
         if (room < 1) break;
@@ -691,7 +711,7 @@ uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n
         const uint32_t j = acc[0];
         g->cur = (g->cur_base + 1 + (int)j) % NSLOT;
         if (cycle_j) cycle_j[s.n_cycles] = j;
-        for (uint32_t i = 0; i <= j && gen < n_predict; i++) out[gen++] = acc[1 + i];
+        for (uint32_t i = 0; i <= j && gen < max_tokens; i++) out[gen++] = acc[1 + i];
         s.n_accepted += j;
         s.n_drafts += kk;
         s.n_cycles++;
@@ -706,6 +726,18 @@ uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n
     s.t_decode_s = now_s() - t0;
     if (st) *st = s;
     return gen;
+}
+
+uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                             uint32_t k, uint32_t eos, int force_accept, uint32_t *out, uint32_t *cycle_j,
+                             qwen_gen_stats_t *st)
+{
+    const double t0 = now_s();
+    if (model_spec_begin(m, prompt, n_prompt, k)) return 0;
+    const double t_prefill = now_s() - t0;
+    const uint32_t n = model_spec_run(m, k, eos, force_accept, UINT32_MAX, n_predict, out, cycle_j, st);
+    if (st) st->t_prefill_s = t_prefill;
+    return n;
 }
 
 uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,

@@ -32,6 +32,16 @@ def fptr(a):
     return a.ctypes.data_as(F32P)
 
 
+class Act(ctypes.Structure):
+    """qgpu_act (include/qgpu.h): activation transform fused into the GEMV input preparation."""
+    _fields_ = [("kind", ctypes.c_int), ("x", F32P), ("ldx", ctypes.c_uint64), ("y", F32P), ("ldy", ctypes.c_uint64),
+                ("w", F32P), ("w2", F32P), ("seg", ctypes.c_uint64), ("eps", ctypes.c_float), ("xout", F32P),
+                ("ldxo", ctypes.c_uint64)]
+
+
+ACT_COPY, ACT_RMSNORM, ACT_SILU_MUL, ACT_GATED_NORM = 0, 1, 2, 3
+
+
 class SynthSpec(ctypes.Structure):
     _fields_ = ([(n, ctypes.c_uint32) for n in (
         "n_embd n_ff n_layer n_head n_kv_head head_dim n_k_heads n_v_heads state vocab "
@@ -261,6 +271,9 @@ class GpuLib:
             "qgpu_attn_decode": [F32P, u64, F32P, F32P, ctypes.POINTER(i32), i32, i32, i32, i32, i32, F32P, u64],
             "qgpu_attn_reserve": [i32, i32],
             "qgpu_set_i32": [ctypes.POINTER(i32), i32],
+            "qgpu_gemv_act_batch": [ctypes.POINTER(vp), i32, ctypes.POINTER(Act), i32, ctypes.POINTER(F32P),
+                                    ctypes.POINTER(u64), i32],
+            "qgpu_act_prepare": [ctypes.POINTER(Act), i32, u64],
             "qgpu_spec_accept": [U32P, U32P, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), i32, U32P],
         }
         for name, args in sigs.items():
@@ -359,6 +372,9 @@ def _model_lib():
     L.qwen_model_set_host_sync.argtypes = [vp, i32]
     L.model_generate_spec.argtypes = [vp, U32P, u32, u32, u32, u32, i32, U32P, U32P, ctypes.POINTER(GenStats)]
     L.model_generate_spec.restype = u32
+    L.model_spec_begin.argtypes = [vp, U32P, u32, u32]
+    L.model_spec_run.argtypes = [vp, u32, u32, i32, u32, u32, U32P, U32P, ctypes.POINTER(GenStats)]
+    L.model_spec_run.restype = u32
     L.model_generate_greedy.argtypes = [vp, U32P, u32, u32, u32, U32P, ctypes.POINTER(GenStats)]
     L.model_generate_greedy.restype = u32
     L.model_time_steps.argtypes = [vp, u32, i32, F32P, F32P, F32P]
@@ -440,6 +456,21 @@ class Model:
         st = GenStats()
         n = self.L.model_generate_spec(self.h, uptr(p), len(p), n_predict, k, eos, int(force_accept), uptr(out),
                                        uptr(js), ctypes.byref(st))
+        return out[:n], js[:st.n_cycles], st
+
+    def spec_begin(self, prompt, k):
+        p = np.ascontiguousarray(prompt, np.uint32)
+        if self.L.model_spec_begin(self.h, uptr(p), len(p), k):
+            raise QgpuError("model_spec_begin failed")
+
+    def spec_run(self, k, max_cycles, max_tokens=None, force_accept=0, eos=0xFFFFFFFF):
+        """continue the speculative loop: returns (tokens, accepted index per cycle, stats)"""
+        max_tokens = max_cycles * (k + 1) if max_tokens is None else max_tokens
+        out = np.zeros(max_tokens + 16, np.uint32)
+        js = np.zeros(max_cycles + 16, np.uint32)
+        st = GenStats()
+        n = self.L.model_spec_run(self.h, k, eos, int(force_accept), max_cycles, max_tokens, uptr(out), uptr(js),
+                                  ctypes.byref(st))
         return out[:n], js[:st.n_cycles], st
 
     def generate_greedy(self, prompt, n_predict, eos=0xFFFFFFFF):

@@ -296,3 +296,21 @@ def test_model_init_rejects_bad_files(gpu):
     open(bad, "wb").write(bytes(data))
     with pytest.raises(pyqwen.QgpuError):
         pyqwen.Model(bad, 64)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_model_spec_begin_run_resumes(gpu, tiny, mode):
+    """begin + several run() calls of a few cycles each == one uninterrupted generation."""
+    path, z = tiny
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    m.spec_begin(z["prompt"][:20], 3)
+    parts = []
+    for cyc in (1, 5, 2, 12):
+        t, j, st = m.spec_run(3, cyc, force_accept=mode)
+        assert st.n_cycles == cyc and len(t) == cyc * (1 + (3 if mode == 1 else 0))
+        parts.append(t)
+    m.close()
+    got = np.concatenate(parts)
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    toks, js, st = m.generate_spec(z["prompt"][:20], len(got), 3, force_accept=mode)
+    assert np.array_equal(got, toks)
