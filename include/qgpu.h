@@ -184,6 +184,14 @@ int  qgpu_attn_prep(float *q, uint64_t ldq, const float *k, const float *v, uint
 int  qgpu_attn_decode(const float *q, uint64_t ldq, const float *kcache, const float *vcache,
                       const int *pos_dev, int ctx_bound, int B, int n_head, int n_kv, int head_dim,
                       float *out, uint64_t ldo);
+/* qgpu_attn_prep + qgpu_attn_decode in fewer launches: the per-head q/k
+ * RMSNorm, RoPE and the cache writes of the B new rows happen inside the
+ * attention kernel.  q is not modified.  Same arguments and results as the
+ * two calls (model.c:318-406, 760-810). */
+int  qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                     const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                     const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
+                     int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out, uint64_t ldo);
 /* allocates the attention workspace for ctx_bound positions now (no allocation later) */
 int  qgpu_attn_reserve(int ctx_bound, int n_kv);
 

@@ -60,92 +60,215 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
     }
 }
 
-// partials layout: [n_kv][nchunk][ATT_MAXQ] of (m, l) and [n_kv][nchunk][ATT_MAXQ][ATT_HD] of o
-__global__ __launch_bounds__(256) void k_attn_chunk(const float *q, uint64_t ldq, const float *kc, const float *vc,
-                                                    const int *pos_dev, int B, int n_head, int n_kv, int nchunk,
-                                                    float *pml, float *po)
+// Flash-decoding chunk kernel.  Block (g, c): kv head g, positions
+// [c*ATT_CS, c*ATT_CS + ATT_CS).  Serves the QH = (n_head/n_kv) * B query rows
+// of the group: row r = b * per + (h - g*per).
+//   FUSED = 1: the block also applies the per-head q/k RMSNorm and RoPE
+//              (reference model.c:318-406): q rows are prepared in LDS (each
+//              block recomputes them), the new k/v rows of positions pos..pos+B-1
+//              that fall in this chunk are prepared here and written to the caches
+//              (no other block reads them in this launch).
+//   FUSED = 0: q rows already prepared, caches already hold every position.
+// Scores: thread (row group rg = tid/32, position p = tid%32) over rows
+// rg + 8j, K chunk staged row-major in LDS (float4 reads, conflict-free with
+// the 260-float row stride); P.V: thread d over all rows.
+// partials: pml [n_kv][nchunk][ATT_MAXQ][2] (m, l), po [n_kv][nchunk][ATT_MAXQ][ATT_HD]
+#define ATT_LD   260          // padded LDS row stride (floats)
+#define ATT_NJ   (ATT_MAXQ / 8)
+
+struct AttnArgs {
+    const float *q; uint64_t ldq;
+    const float *k, *v; uint64_t ldkv;
+    const float *qw, *kw, *rcos, *rsin;
+    float *kc, *vc;
+    const int *pos_dev;
+    float *pml, *po;
+    int half, B, n_head, n_kv, nchunk;
+    float eps;
+};
+
+// x[0..255] (in LDS, stride-1) <- rmsnorm(x) * w, by one wave (lane: 4 elements)
+static __device__ __forceinline__ void wave_rmsnorm_row(float *x, const float *src, const float *w, float eps, int lane)
 {
-    __shared__ float qs[ATT_MAXQ][ATT_HD];
-    __shared__ float kv[ATT_CS][ATT_HD + 1];
-    __shared__ float ps[ATT_MAXQ][ATT_CS];
-    const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
-    const int per = n_head / n_kv, QH = per * B;
-    const int pos0 = *pos_dev;
-    const int t0 = c * ATT_CS;
-    const int tmax = pos0 + B - 1;                // last position any query may see
-    float *ml = pml + ((uint64_t)g * nchunk + c) * ATT_MAXQ * 2;
-    float *o = po + ((uint64_t)g * nchunk + c) * ATT_MAXQ * ATT_HD;
+    const float4 v = *(const float4 *)(src + 4 * lane);
+    float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+#pragma unroll
+    for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
+    const float sc = 1.0f / sqrtf(ss / (float)ATT_HD + eps);
+    const float4 wv = *(const float4 *)(w + 4 * lane);
+    *(float4 *)(x + 4 * lane) = make_float4((v.x * sc) * wv.x, (v.y * sc) * wv.y, (v.z * sc) * wv.z, (v.w * sc) * wv.w);
+}
+
+template <int FUSED>
+__global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
+{
+    __shared__ float Ql[ATT_MAXQ][ATT_LD];
+    __shared__ float KV[ATT_CS][ATT_LD];
+    __shared__ float Pl[ATT_MAXQ][ATT_CS];
+    const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int per = p.n_head / p.n_kv, QH = per * p.B;
+    const int pos0 = *p.pos_dev, tmax = pos0 + p.B - 1, t0 = c * ATT_CS;
+    float *ml = p.pml + ((uint64_t)g * p.nchunk + c) * ATT_MAXQ * 2;
+    float *o = p.po + ((uint64_t)g * p.nchunk + c) * ATT_MAXQ * ATT_HD;
     if (t0 > tmax) {                              // chunk beyond the context: empty partial
-        for (int qi = tid; qi < QH; qi += blockDim.x) { ml[2 * qi] = -INFINITY; ml[2 * qi + 1] = 0.0f; }
+        for (int qi = tid; qi < QH; qi += 256) { ml[2 * qi] = -INFINITY; ml[2 * qi + 1] = 0.0f; }
         return;
     }
-    // queries qi = b * per + (h - g*per)
-    for (int e = tid; e < QH * ATT_HD; e += blockDim.x) {
-        const int qi = e / ATT_HD, d = e % ATT_HD, b = qi / per, h = g * per + qi % per;
-        qs[qi][d] = q[(uint64_t)b * ldq + (uint64_t)h * 2 * ATT_HD + d];
+    const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD;
+    const int nt = min(ATT_CS, tmax - t0 + 1);    // positions of this chunk that exist
+    // ---- K rows: cache rows below pos0; new rows (FUSED) prepared here
+    for (int e = tid; e < nt * 64; e += 256) {
+        const int pp = e >> 6, d4 = e & 63, t = t0 + pp;
+        if (!FUSED || t < pos0)
+            *(float4 *)&KV[pp][4 * d4] = *(const float4 *)(p.kc + (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * d4);
     }
-    const uint64_t kvrow = (uint64_t)n_kv * ATT_HD;
-    for (int e = tid; e < ATT_CS * ATT_HD; e += blockDim.x) {
-        const int tt = e / ATT_HD, d = e % ATT_HD, t = t0 + tt;
-        kv[tt][d] = t <= tmax ? kc[(uint64_t)t * kvrow + (uint64_t)g * ATT_HD + d] : 0.0f;
+    if (FUSED) {
+        for (int b = wv; b < p.B; b += 4) {
+            const int t = pos0 + b;
+            if (t >= t0 && t < t0 + ATT_CS)
+                wave_rmsnorm_row(KV[t - t0], p.k + (uint64_t)b * p.ldkv + (uint64_t)g * ATT_HD, p.kw, p.eps, lane);
+        }
+        for (int r = wv; r < QH; r += 4) {
+            const int b = r / per, h = g * per + r % per;
+            wave_rmsnorm_row(Ql[r], p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD, p.qw, p.eps, lane);
+        }
+        __syncthreads();
+        // NeoX RoPE on (i, i + half), i < half, position pos0 + b
+        for (int e = tid; e < (QH + p.B) * p.half; e += 256) {
+            const int r = e / p.half, i = e % p.half;
+            float *x;
+            int t;
+            if (r < QH) { x = Ql[r]; t = pos0 + r / per; }
+            else {
+                t = pos0 + (r - QH);
+                if (t < t0 || t >= t0 + ATT_CS) continue;
+                x = KV[t - t0];
+            }
+            const float cs = p.rcos[(uint64_t)t * p.half + i], sn = p.rsin[(uint64_t)t * p.half + i];
+            const float v0 = x[i], v1 = x[i + p.half];
+            x[i] = v0 * cs - v1 * sn;
+            x[i + p.half] = v0 * sn + v1 * cs;
+        }
+        __syncthreads();
+        // the new k rows go to the cache, the new v rows too
+        for (int e = tid; e < p.B * 64; e += 256) {
+            const int b = e >> 6, d4 = e & 63, t = pos0 + b;
+            if (t < t0 || t >= t0 + ATT_CS) continue;
+            const uint64_t row = (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * d4;
+            *(float4 *)(p.kc + row) = *(const float4 *)&KV[t - t0][4 * d4];
+            *(float4 *)(p.vc + row) = *(const float4 *)(p.v + (uint64_t)b * p.ldkv + (uint64_t)g * ATT_HD + 4 * d4);
+        }
+    } else {
+        for (int e = tid; e < QH * 64; e += 256) {
+            const int r = e >> 6, d4 = e & 63, b = r / per, h = g * per + r % per;
+            *(float4 *)&Ql[r][4 * d4] = *(const float4 *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + 4 * d4);
+        }
+        __syncthreads();
     }
-    __syncthreads();
+    // ---- scores for rows rg + 8j at position t0 + pp
+    const int rg = tid >> 5, pp = tid & 31;
+    float s[ATT_NJ];
+#pragma unroll
+    for (int j = 0; j < ATT_NJ; j++) s[j] = 0.0f;
+    if (pp < nt) {
+        for (int d4 = 0; d4 < 64; d4++) {
+            const float4 kq = *(const float4 *)&KV[pp][4 * d4];
+#pragma unroll
+            for (int j = 0; j < ATT_NJ; j++) {
+                const int r = rg + 8 * j;
+                if (r < QH) {
+                    const float4 qv = *(const float4 *)&Ql[r][4 * d4];
+                    s[j] = fmaf(qv.x, kq.x, s[j]); s[j] = fmaf(qv.y, kq.y, s[j]);
+                    s[j] = fmaf(qv.z, kq.z, s[j]); s[j] = fmaf(qv.w, kq.w, s[j]);
+                }
+            }
+        }
+    }
+    // ---- chunk softmax statistics: row r's 32 scores are the 32 lanes of a half-wave
     const float scale = 1.0f / sqrtf((float)ATT_HD);
-    for (int e = tid; e < QH * ATT_CS; e += blockDim.x) {
-        const int qi = e / ATT_CS, tt = e % ATT_CS, t = t0 + tt, b = qi / per;
-        float s = 0.0f;
-#pragma unroll 8
-        for (int d = 0; d < ATT_HD; d++) s = fmaf(qs[qi][d], kv[tt][d], s);
-        ps[qi][tt] = (t <= pos0 + b) ? s * scale : -INFINITY;
-    }
-    __syncthreads();
-    // chunk softmax statistics (one wave per query row, lanes over positions)
-    for (int qi = tid >> 6; qi < QH; qi += blockDim.x >> 6) {
-        const int l = tid & 63;
-        float v = l < ATT_CS ? ps[qi][l] : -INFINITY;
-        float m = v;
 #pragma unroll
-        for (int off = 32; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        const float p = (l < ATT_CS && m > -INFINITY) ? expf(v - m) : 0.0f;
-        float sum = p;
+    for (int j = 0; j < ATT_NJ; j++) {
+        const int r = rg + 8 * j;
+        if (r >= QH) break;                       // uniform over the half-wave
+        const int t = t0 + pp;
+        const float sv = (pp < nt && t <= pos0 + r / per) ? s[j] * scale : -INFINITY;
+        float m = sv;
 #pragma unroll
-        for (int off = 32; off; off >>= 1) sum += __shfl_xor(sum, off);
-        if (l < ATT_CS) ps[qi][l] = p;
-        if (l == 0) { ml[2 * qi] = m; ml[2 * qi + 1] = sum; }
+        for (int off = 16; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float pr = m > -INFINITY ? expf(sv - m) : 0.0f;
+        float sum = pr;
+#pragma unroll
+        for (int off = 16; off; off >>= 1) sum += __shfl_xor(sum, off);
+        Pl[r][pp] = pr;
+        if (pp == 0) { ml[2 * r] = m; ml[2 * r + 1] = sum; }
     }
     __syncthreads();
-    for (int e = tid; e < ATT_CS * ATT_HD; e += blockDim.x) {
-        const int tt = e / ATT_HD, d = e % ATT_HD, t = t0 + tt;
-        kv[tt][d] = t <= tmax ? vc[(uint64_t)t * kvrow + (uint64_t)g * ATT_HD + d] : 0.0f;
+    // ---- V rows into the (now free) K buffer
+    for (int e = tid; e < nt * 64; e += 256) {
+        const int q4 = e >> 6, d4 = e & 63, t = t0 + q4;
+        const float *src = (FUSED && t >= pos0) ? p.v + (uint64_t)(t - pos0) * p.ldkv + (uint64_t)g * ATT_HD
+                                                : p.vc + (uint64_t)t * kvrow + (uint64_t)g * ATT_HD;
+        *(float4 *)&KV[q4][4 * d4] = *(const float4 *)(src + 4 * d4);
     }
     __syncthreads();
-    const int d = tid;                            // blockDim == ATT_HD
-    for (int qi = 0; qi < QH; qi++) {
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int tt = 0; tt < ATT_CS; tt++) acc = fmaf(ps[qi][tt], kv[tt][d], acc);
-        o[(uint64_t)qi * ATT_HD + d] = acc;
+    // ---- P.V: thread d, rows in groups of 16
+    const int d = tid;
+    for (int r0 = 0; r0 < QH; r0 += 16) {
+        float acc[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+        for (int q4 = 0; q4 < nt; q4++) {
+            const float vv = KV[q4][d];
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[i] = fmaf(Pl[r0 + i < QH ? r0 + i : 0][q4], vv, acc[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            if (r0 + i < QH) o[(uint64_t)(r0 + i) * ATT_HD + d] = acc[i];
     }
 }
 
+// out[b][h*hd + d] = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) * sigmoid(gate); chunks past
+// the last position (m = -inf) are skipped by the bound taken from *pos_dev
 __global__ __launch_bounds__(ATT_HD) void k_attn_combine(const float *q, uint64_t ldq, const float *pml,
-                                                         const float *po, int B, int n_head, int n_kv, int nchunk,
-                                                         float *out, uint64_t ldo)
+                                                         const float *po, const int *pos_dev, int B, int n_head,
+                                                         int n_kv, int nchunk, float *out, uint64_t ldo)
 {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int per = n_head / n_kv, g = h / per, qi = b * per + (h % per);
+    const int nc = min(nchunk, (*pos_dev + B - 1) / ATT_CS + 1);
+    const float *mlg = pml + (uint64_t)g * nchunk * ATT_MAXQ * 2 + 2 * qi;
+    const float *pog = po + (uint64_t)g * nchunk * ATT_MAXQ * ATT_HD + (uint64_t)qi * ATT_HD + d;
     float m = -INFINITY;
-    for (int c = 0; c < nchunk; c++) m = fmaxf(m, pml[((uint64_t)g * nchunk + c) * ATT_MAXQ * 2 + 2 * qi]);
+#pragma unroll 8
+    for (int c = 0; c < nc; c++) m = fmaxf(m, mlg[(uint64_t)c * ATT_MAXQ * 2]);
     float l = 0.0f, acc = 0.0f;
-    for (int c = 0; c < nchunk; c++) {
-        const float mc = pml[((uint64_t)g * nchunk + c) * ATT_MAXQ * 2 + 2 * qi];
-        if (mc == -INFINITY) continue;
-        const float f = expf(mc - m);
-        l += pml[((uint64_t)g * nchunk + c) * ATT_MAXQ * 2 + 2 * qi + 1] * f;
-        acc += po[((uint64_t)g * nchunk + c) * ATT_MAXQ * ATT_HD + (uint64_t)qi * ATT_HD + d] * f;
+#pragma unroll 8
+    for (int c = 0; c < nc; c++) {
+        const float mc = mlg[(uint64_t)c * ATT_MAXQ * 2];
+        const float f = mc > -INFINITY ? expf(mc - m) : 0.0f;
+        l = fmaf(mlg[(uint64_t)c * ATT_MAXQ * 2 + 1], f, l);
+        acc = fmaf(pog[(uint64_t)c * ATT_MAXQ * ATT_HD], f, acc);
     }
     const float gate = q[(uint64_t)b * ldq + (uint64_t)h * 2 * ATT_HD + ATT_HD + d];
     out[(uint64_t)b * ldo + (uint64_t)h * ATT_HD + d] = (acc / l) * (1.0f / (1.0f + expf(-gate)));
+}
+
+static int attn_ws(int ctx_bound, int n_kv, int *nchunk)
+{
+    *nchunk = (ctx_bound + ATT_CS - 1) / ATT_CS;
+    const size_t need = (size_t)n_kv * *nchunk * ATT_MAXQ * (2 + ATT_HD) * sizeof(float);
+    if (need > qg::ws_attn_bytes) {
+        if (qg::ws_attn) {
+            QG_CHECK(hipStreamSynchronize(qg::stream));
+            QG_CHECK(hipFree(qg::ws_attn));
+        }
+        qg::ws_attn = nullptr;
+        qg::ws_attn_bytes = 0;
+        QG_CHECK(hipMalloc(&qg::ws_attn, need));
+        qg::ws_attn_bytes = need;
+    }
+    return QGPU_OK;
 }
 
 extern "C" int qgpu_attn_prep(float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
@@ -166,6 +289,24 @@ extern "C" int qgpu_attn_prep(float *q, uint64_t ldq, const float *k, const floa
     return QGPU_OK;
 }
 
+static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out, uint64_t ldo)
+{
+    AttnArgs a = a0;
+    int rc = attn_ws(ctx_bound, a.n_kv, &a.nchunk);
+    if (rc) return rc;
+    a.pml = (float *)qg::ws_attn;
+    a.po = a.pml + (size_t)a.n_kv * a.nchunk * ATT_MAXQ * 2;
+    if (fused)
+        hipLaunchKernelGGL(k_attn_chunk<1>, dim3(a.n_kv, a.nchunk), dim3(256), 0, qg::stream, a);
+    else
+        hipLaunchKernelGGL(k_attn_chunk<0>, dim3(a.n_kv, a.nchunk), dim3(256), 0, qg::stream, a);
+    QG_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_attn_combine, dim3(a.n_head, a.B), dim3(ATT_HD), 0, qg::stream, a.q, a.ldq, a.pml, a.po,
+                       a.pos_dev, a.B, a.n_head, a.n_kv, a.nchunk, out, ldo);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
 extern "C" int qgpu_attn_decode(const float *q, uint64_t ldq, const float *kcache, const float *vcache,
                                 const int *pos_dev, int ctx_bound, int B, int n_head, int n_kv, int head_dim,
                                 float *out, uint64_t ldo)
@@ -173,30 +314,37 @@ extern "C" int qgpu_attn_decode(const float *q, uint64_t ldq, const float *kcach
     int rc = qg::ensure_init();
     if (rc) return rc;
     if (head_dim != ATT_HD) return QGPU_E_RANGE;
-    if (!q || !kcache || !vcache || !pos_dev || !out || B < 1 || n_kv < 1 || n_head % n_kv || ctx_bound < B)
+    if (!q || !kcache || !vcache || !pos_dev || !out || B < 1 || n_kv < 1 || n_head % n_kv || ctx_bound < B ||
+        ldq % 4 || ((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
         return QGPU_E_ARG;
     if ((n_head / n_kv) * B > ATT_MAXQ) return QGPU_E_RANGE;
-    const int nchunk = (ctx_bound + ATT_CS - 1) / ATT_CS;
-    const size_t need = (size_t)n_kv * nchunk * ATT_MAXQ * (2 + ATT_HD) * sizeof(float);
-    if (need > qg::ws_attn_bytes) {
-        if (qg::ws_attn) {
-            QG_CHECK(hipStreamSynchronize(qg::stream));
-            QG_CHECK(hipFree(qg::ws_attn));
-        }
-        qg::ws_attn = nullptr;
-        qg::ws_attn_bytes = 0;
-        QG_CHECK(hipMalloc(&qg::ws_attn, need));
-        qg::ws_attn_bytes = need;
-    }
-    float *pml = (float *)qg::ws_attn;
-    float *po = pml + (size_t)n_kv * nchunk * ATT_MAXQ * 2;
-    hipLaunchKernelGGL(k_attn_chunk, dim3(n_kv, nchunk), dim3(256), 0, qg::stream, q, ldq, kcache, vcache, pos_dev,
-                       B, n_head, n_kv, nchunk, pml, po);
-    QG_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_attn_combine, dim3(n_head, B), dim3(ATT_HD), 0, qg::stream, q, ldq, pml, po, B, n_head,
-                       n_kv, nchunk, out, ldo);
-    QG_LAUNCH_CHECK();
-    return QGPU_OK;
+    AttnArgs a = {};
+    a.q = q; a.ldq = ldq; a.kc = (float *)kcache; a.vc = (float *)vcache; a.pos_dev = pos_dev;
+    a.B = B; a.n_head = n_head; a.n_kv = n_kv;
+    return attn_launch(a, 0, ctx_bound, out, ldo);
+}
+
+extern "C" int qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                               const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                               const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
+                               int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out,
+                               uint64_t ldo)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (head_dim != ATT_HD) return QGPU_E_RANGE;
+    if (!q || !k || !v || !q_norm_w || !k_norm_w || !kcache || !vcache || !rope_cos || !rope_sin || !pos_dev ||
+        !out || B < 1 || n_kv < 1 || n_head % n_kv || rope_dim < 2 || rope_dim > ATT_HD || rope_dim % 2 ||
+        ctx_bound < B || ldq % 4 || ldkv % 4 || ((uintptr_t)q & 15) || ((uintptr_t)k & 15) || ((uintptr_t)v & 15) ||
+        ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15) || ((uintptr_t)q_norm_w & 15) ||
+        ((uintptr_t)k_norm_w & 15))
+        return QGPU_E_ARG;
+    if ((n_head / n_kv) * B > ATT_MAXQ) return QGPU_E_RANGE;
+    AttnArgs a = {};
+    a.q = q; a.ldq = ldq; a.k = k; a.v = v; a.ldkv = ldkv; a.qw = q_norm_w; a.kw = k_norm_w;
+    a.rcos = rope_cos; a.rsin = rope_sin; a.kc = kcache; a.vc = vcache; a.pos_dev = pos_dev;
+    a.half = rope_dim / 2; a.B = B; a.n_head = n_head; a.n_kv = n_kv; a.eps = eps;
+    return attn_launch(a, 1, ctx_bound, out, ldo);
 }
 
 // Reserve the attention workspace up front (so later calls never allocate,
@@ -205,15 +353,7 @@ extern "C" int qgpu_attn_reserve(int ctx_bound, int n_kv)
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
-    const int nchunk = (ctx_bound + ATT_CS - 1) / ATT_CS;
-    const size_t need = (size_t)n_kv * nchunk * ATT_MAXQ * (2 + ATT_HD) * sizeof(float);
-    if (need <= qg::ws_attn_bytes) return QGPU_OK;
-    if (qg::ws_attn) {
-        QG_CHECK(hipStreamSynchronize(qg::stream));
-        QG_CHECK(hipFree(qg::ws_attn));
-        qg::ws_attn = nullptr;
-    }
-    QG_CHECK(hipMalloc(&qg::ws_attn, need));
-    qg::ws_attn_bytes = need;
-    return QGPU_OK;
+    if (ctx_bound < 1 || n_kv < 1) return QGPU_E_ARG;
+    int nchunk;
+    return attn_ws(ctx_bound, n_kv, &nchunk);
 }

@@ -157,33 +157,37 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
     const uint64_t k = (uint64_t)sb * 256 + e;
     float v[4];
     if (KIND == QGPU_ACT_RMSNORM) {
-        // row RMS over the segment holding this super-block (each block recomputes it: same order, same value)
+        // row RMS over the segment holding this super-block (each block recomputes it: same order, same value);
+        // all row loads are issued before any reduction
         const uint64_t segl = p.seg;
         const int part = (uint64_t)sb * 256 >= segl ? 1 : 0;
         const float *src = part ? p.y : p.x;
         const float *w = part ? p.w2 : p.w;
         const uint64_t ld = part ? p.ldy : p.ldx, kk = k - (part ? segl : 0);
+        const int nt = p.ntok - 4 * a < 4 ? p.ntok - 4 * a : 4;     // tokens of this plane (>= 1)
+        float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint64_t j = e; j < segl / 4; j += 256) {
+            float4 q[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                q[i] = i < nt ? ((const float4 *)(src + (uint64_t)(4 * a + i) * ld))[j] : make_float4(0, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                ss[i] = fmaf(q[i].x, q[i].x, ss[i]); ss[i] = fmaf(q[i].y, q[i].y, ss[i]);
+                ss[i] = fmaf(q[i].z, q[i].z, ss[i]); ss[i] = fmaf(q[i].w, q[i].w, ss[i]);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int t = 4 * a + i;
-            float ss = 0.0f;
-            if (t < p.ntok) {
-                const float4 *row = (const float4 *)(src + (uint64_t)t * ld);
-                for (uint64_t j = e; j < segl / 4; j += 256) {
-                    const float4 q = row[j];
-                    ss = fmaf(q.x, q.x, ss); ss = fmaf(q.y, q.y, ss); ss = fmaf(q.z, q.z, ss); ss = fmaf(q.w, q.w, ss);
-                }
-            }
-            ss = wave_sum(ss);
-            if (lane == 0) red[i][wv] = ss;
+            ss[i] = wave_sum(ss[i]);
+            if (lane == 0) red[i][wv] = ss[i];
         }
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int t = 4 * a + i;
             const float tot = (red[i][0] + red[i][1]) + (red[i][2] + red[i][3]);
             const float sc = 1.0f / sqrtf(tot / (float)segl + p.eps);
-            v[i] = t < p.ntok ? (src[(uint64_t)t * ld + kk] * sc) * w[kk] : 0.0f;
+            v[i] = i < nt ? (src[(uint64_t)(4 * a + i) * ld + kk] * sc) * w[kk] : 0.0f;
         }
         __syncthreads();
     } else if (KIND == QGPU_ACT_GATED_NORM) {
@@ -279,85 +283,123 @@ struct GemvArgs {
     uint64_t ldx, ne0;
 };
 
-static __device__ __forceinline__ void iq4_decode8(uint32_t q, uint32_t &lo, uint32_t &hi)
+// v_and_or_b32 with every operand in a VGPR (a VOP3 encoding takes no 32-bit
+// literal and one scalar operand at most, so the constants live in VGPRs)
+static __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c)
+{
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+    return r;
+}
+
+// a * b + c on the low 24 bits of a and b (signed), 32-bit result.  Plain
+// code, not inline asm: its input comes straight from an MFMA, and the
+// compiler inserts the MFMA-to-VALU wait states only for instructions it
+// generates itself.
+static __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+struct DecodeK {               // decode constants, held in VGPRs
+    uint32_t m4, sel0;
+};
+
+// 8 IQ4_NL codebook bytes (low nibbles -> lo, high nibbles -> hi) from one
+// dword of nibbles: two 8-entry lookups (v_perm_b32 over the codebook halves)
+// and a byte select on the nibble's bit 3.  13 VALU operations.
+static __device__ __forceinline__ void iq4_decode8(uint32_t q, const DecodeK &K, uint32_t &lo, uint32_t &hi)
 {
     // IQ4_NL codebook as int8 bytes {-127,-104,-83,-65 | -49,-35,-22,-10 | 1,13,25,38 | 53,69,89,113}
     const uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
     uint32_t s = q & 0x07070707u;
     uint32_t a = __builtin_amdgcn_perm(T1, T0, s), b = __builtin_amdgcn_perm(T3, T2, s);
-    lo = __builtin_amdgcn_perm(b, a, ((q >> 1) & 0x04040404u) | 0x03020100u);
-    const uint32_t q4 = q >> 4;
-    s = q4 & 0x07070707u;
+    lo = __builtin_amdgcn_perm(b, a, and_or(q >> 1, K.m4, K.sel0));
+    s = (q >> 4) & 0x07070707u;
     a = __builtin_amdgcn_perm(T1, T0, s);
     b = __builtin_amdgcn_perm(T3, T2, s);
-    hi = __builtin_amdgcn_perm(b, a, ((q4 >> 1) & 0x04040404u) | 0x03020100u);
+    hi = __builtin_amdgcn_perm(b, a, and_or(q >> 5, K.m4, K.sel0));
 }
 
-template <int NA>
-struct IQ4Stage {
+// Weight records come from HBM and activation digits from L2, so the two are
+// prefetched to different depths: weights IQ4_WDEPTH super-blocks ahead
+// (10 VGPRs each), digits IQ4_ADEPTH ahead (16 * NA + 4 * NA VGPRs each).
+struct IQ4W {
     uint2 hdr;
     uint4 qa, qb;
+};
+template <int NA>
+struct IQ4A {
     uint4 av[NA][4];
     float4 xv[NA];
 };
 
-template <int NA>
-static __device__ __forceinline__ void iq4_load(IQ4Stage<NA> &st, const uint8_t *rec, const uint8_t *Aall,
-                                                const float *xs, int sb, int lane, int n, int g)
+// rec, Ab, xsb are wave-uniform (scalar) addresses of this super-block's weight
+// record, digit plane 0 and digit scales; lanes add their own offsets.
+static __device__ __forceinline__ void iq4_load_w(IQ4W &w, const uint8_t *rec, int lane, int n)
 {
-    st.hdr = *(const uint2 *)(rec + n * 8);
-    st.qa = *(const uint4 *)(rec + IQ4_HDR_BYTES + lane * 16);
-    st.qb = *(const uint4 *)(rec + IQ4_HDR_BYTES + (64 + lane) * 16);
+    w.hdr = *(const uint2 *)(rec + n * 8);
+    w.qa = *(const uint4 *)(rec + IQ4_HDR_BYTES + lane * 16);
+    w.qb = *(const uint4 *)(rec + IQ4_HDR_BYTES + 1024 + lane * 16);
+}
+
+template <int NA>
+static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab, const float *xsb, int lane, int g)
+{
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        const uint8_t *Ab = Aall + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * 4096 + lane * 16;
+        const uint8_t *Aa = Ab + (uint64_t)a * PLANE_BYTES;
 #pragma unroll
-        for (int p = 0; p < 4; p++) st.av[a][p] = *(const uint4 *)(Ab + p * 1024);
-        st.xv[a] = *(const float4 *)(xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16 + 4 * g);
+        for (int p = 0; p < 4; p++) x.av[a][p] = *(const uint4 *)(Aa + p * 1024 + lane * 16);
+        x.xv[a] = *(const float4 *)(xsb + (uint64_t)a * XS_FLOATS + 4 * g);
     }
 }
 
 template <int NA>
-static __device__ __forceinline__ void iq4_compute(const IQ4Stage<NA> &st, float (&accf)[NA][4])
+static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA> &x, const DecodeK &K,
+                                                   float (&accf)[NA][4])
 {
-    const uint32_t qd[8] = { st.qa.x, st.qa.y, st.qa.z, st.qa.w, st.qb.x, st.qb.y, st.qb.z, st.qb.w };
+    const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
     v4i acci[NA];
 #pragma unroll
     for (int a = 0; a < NA; a++) acci[a] = (v4i){0, 0, 0, 0};
 #pragma unroll
     for (int ib = 0; ib < 8; ib++) {
         uint32_t lo, hi;
-        iq4_decode8(qd[ib], lo, hi);
+        iq4_decode8(qd[ib], K, lo, hi);
         const long bop = (long)(((uint64_t)hi << 32) | lo);
-        const int wsc = hdr_scale(st.hdr, ib);
+        const int wsc = hdr_scale(w.hdr, ib);
 #pragma unroll
         for (int a = 0; a < NA; a++) {
-            const uint4 q4 = st.av[a][ib >> 1];
+            const uint4 q4 = x.av[a][ib >> 1];
             const long aop = (ib & 1) ? (long)(((uint64_t)q4.w << 32) | q4.z)
                                       : (long)(((uint64_t)q4.y << 32) | q4.x);
             const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, (v4i){0, 0, 0, 0}, 0, 0, 0);
             // |D| < 2^19, |wsc| <= 32: exact 24-bit multiply-add
 #pragma unroll
-            for (int i = 0; i < 4; i++) acci[a][i] = __mul24(D[i], wsc) + acci[a][i];
+            for (int i = 0; i < 4; i++) acci[a][i] = mad24(D[i], wsc, acci[a][i]);
         }
     }
-    const float d = h2f(st.hdr.x & 0xFFFFu);
+    const float d = h2f(w.hdr.x & 0xFFFFu);
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        accf[a][0] += (float)acci[a][0] * (d * st.xv[a].x);
-        accf[a][1] += (float)acci[a][1] * (d * st.xv[a].y);
-        accf[a][2] += (float)acci[a][2] * (d * st.xv[a].z);
-        accf[a][3] += (float)acci[a][3] * (d * st.xv[a].w);
+        accf[a][0] += (float)acci[a][0] * (d * x.xv[a].x);
+        accf[a][1] += (float)acci[a][1] * (d * x.xv[a].y);
+        accf[a][2] += (float)acci[a][2] * (d * x.xv[a].z);
+        accf[a][3] += (float)acci[a][3] * (d * x.xv[a].w);
     }
 }
 
-#define IQ4_DEPTH 3     // super-blocks in flight per wave
+#ifndef IQ4_WDEPTH
+#define IQ4_WDEPTH 4    // weight records in flight per wave
+#endif
+#ifndef IQ4_ADEPTH
+#define IQ4_ADEPTH 2    // digit super-blocks in flight per wave (divides IQ4_WDEPTH)
+#endif
 
 template <int NA, int NW>
 __global__ __launch_bounds__(NW * 64) void k_gemv_iq4(const GemvArgs args)
 {
     __shared__ float red[NW][NA][4][16];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, n = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar loop control
     const uint32_t tile = blockIdx.x;
     int k = 0;
     while (k + 1 < args.n_mat && tile >= args.m[k + 1].tile0) k++;
@@ -366,6 +408,9 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_iq4(const GemvArgs args)
     const int nsb = args.nsb;
     const uint8_t *rec0 = M.W + (uint64_t)T * nsb * IQ4_REC_BYTES;
     const int sb0 = wv * nsb / NW, sb1 = (wv + 1) * nsb / NW;
+    DecodeK K;
+    K.m4 = 0x04040404u;
+    K.sel0 = 0x03020100u;
 
     float accf[NA][4];
 #pragma unroll
@@ -373,25 +418,32 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_iq4(const GemvArgs args)
 #pragma unroll
         for (int i = 0; i < 4; i++) accf[a][i] = 0.0f;
 
-    // ring of IQ4_DEPTH register stages: super-block sb+IQ4_DEPTH-1 is loading
-    // while sb is decoded and multiplied (indices are compile-time after unrolling)
-    IQ4Stage<NA> st[IQ4_DEPTH];
+    // two register rings: weights of super-block sb+IQ4_WDEPTH-1 and digits of
+    // sb+IQ4_ADEPTH-1 are loading while sb is decoded and multiplied (ring
+    // indices are compile-time after unrolling by IQ4_WDEPTH)
+    IQ4W wr[IQ4_WDEPTH];
+    IQ4A<NA> ar[IQ4_ADEPTH];
+#define LOAD_W(slot, sbx) iq4_load_w(wr[slot], rec0 + (uint64_t)(sbx) * IQ4_REC_BYTES, lane, n)
+#define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * 4096, args.xs + (uint64_t)(sbx) * 16, lane, g)
 #pragma unroll
-    for (int d = 0; d < IQ4_DEPTH - 1; d++)
-        if (sb0 + d < sb1)
-            iq4_load<NA>(st[d], rec0 + (uint64_t)(sb0 + d) * IQ4_REC_BYTES, args.A, args.xs, sb0 + d, lane, n, g);
-    for (int sb = sb0; sb < sb1; sb += IQ4_DEPTH) {
+    for (int d = 0; d < IQ4_WDEPTH - 1; d++)
+        if (sb0 + d < sb1) LOAD_W(d, sb0 + d);
 #pragma unroll
-        for (int d = 0; d < IQ4_DEPTH; d++) {
+    for (int d = 0; d < IQ4_ADEPTH - 1; d++)
+        if (sb0 + d < sb1) LOAD_A(d, sb0 + d);
+    for (int sb = sb0; sb < sb1; sb += IQ4_WDEPTH) {
+#pragma unroll
+        for (int d = 0; d < IQ4_WDEPTH; d++) {
             if (sb + d < sb1) {
-                const int pf = sb + d + IQ4_DEPTH - 1;
-                if (pf < sb1)
-                    iq4_load<NA>(st[(d + IQ4_DEPTH - 1) % IQ4_DEPTH], rec0 + (uint64_t)pf * IQ4_REC_BYTES, args.A,
-                                 args.xs, pf, lane, n, g);
-                iq4_compute<NA>(st[d], accf);
+                const int pw = sb + d + IQ4_WDEPTH - 1, pa = sb + d + IQ4_ADEPTH - 1;
+                if (pw < sb1) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
+                if (pa < sb1) LOAD_A((d + IQ4_ADEPTH - 1) % IQ4_ADEPTH, pa);
+                iq4_compute<NA>(wr[d], ar[d % IQ4_ADEPTH], K, accf);
             }
         }
     }
+#undef LOAD_W
+#undef LOAD_A
     // lanes n, n+16, n+32, n+48 hold digits 0..3 of the same (token, row): sum them
 #pragma unroll
     for (int a = 0; a < NA; a++)

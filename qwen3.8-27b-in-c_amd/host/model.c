@@ -457,11 +457,10 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     float *outs[3] = { g->bqkv, g->bk, g->bv };
     const uint64_t ld[3] = { g->SQ, g->kvrow, g->kvrow };
     K(qgpu_gemv_act_batch(W, 3, &an, (int)B, outs, ld, 0));
-    K(qgpu_attn_prep(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos,
-                     g->rope_sin, (int)m->cfg.rope_dim_count, g->d_pos, (int)B, (int)d->n_head, (int)d->n_kv_head,
-                     (int)d->head_dim, eps));
-    K(qgpu_attn_decode(g->bqkv, g->SQ, D->kv_k, D->kv_v, g->d_pos, (int)(pos + B), (int)B, (int)d->n_head,
-                       (int)d->n_kv_head, (int)d->head_dim, g->battn, g->A));
+    /* q/k norm + RoPE + cache write + attention in one kernel, then the chunk merge */
+    K(qgpu_attn_fused(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos,
+                      g->rope_sin, (int)m->cfg.rope_dim_count, g->d_pos, (int)(pos + B), (int)B, (int)d->n_head,
+                      (int)d->n_kv_head, (int)d->head_dim, eps, g->battn, g->A));
     K(qgpu_gemv_batch(D->o, g->battn, g->A, (int)B, R, E, QGPU_GEMV_ACCUM));
     ffn_dev(m, D, R, B);
 }

@@ -269,6 +269,8 @@ class GpuLib:
             "qgpu_attn_prep": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
                                ctypes.POINTER(i32), i32, i32, i32, i32, f32],
             "qgpu_attn_decode": [F32P, u64, F32P, F32P, ctypes.POINTER(i32), i32, i32, i32, i32, i32, F32P, u64],
+            "qgpu_attn_fused": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
+                                ctypes.POINTER(i32), i32, i32, i32, i32, i32, f32, F32P, u64],
             "qgpu_attn_reserve": [i32, i32],
             "qgpu_set_i32": [ctypes.POINTER(i32), i32],
             "qgpu_gemv_act_batch": [ctypes.POINTER(vp), i32, ctypes.POINTER(Act), i32, ctypes.POINTER(F32P),

@@ -146,7 +146,7 @@ def attn_fp64(q, k, v, qw, kw, kc, vc, pos, B, nh, nkv, hd, rope_dim, theta, eps
     return out, kc, vc
 
 
-@pytest.mark.parametrize("pos,B", [(0, 1), (37, 4), (300, 8), (95, 3)])
+@pytest.mark.parametrize("pos,B", [(0, 1), (37, 4), (300, 8), (95, 3), (31, 2), (504, 8)])
 def test_attention_vs_fp64(gpu, pos, B):
     print(f"\n[attn] pos={pos} B={B}", flush=True)
     nh, nkv, hd, rope_dim, theta, eps, n_ctx = 24, 4, 256, 64, 1e7, 1e-6, 512
@@ -179,6 +179,20 @@ def test_attention_vs_fp64(gpu, pos, B):
     kcg = kcb.download(np.float32).reshape(n_ctx, nkv, hd)
     assert rel_err(kcg[pos:pos + B], kref[pos:pos + B]) < 1e-5
     assert np.array_equal(vcb.download(np.float32).reshape(n_ctx, nkv, hd)[pos:pos + B], v.reshape(B, nkv, hd))
+    # fused form (norm + RoPE + cache write inside the attention kernel), tight context bound
+    qb2, kcb2, vcb2 = gpu.put(q), gpu.put(kc), gpu.put(vc)
+    ob2 = gpu.buf(B * nh * hd * 4)
+    gpu.ok(gpu.L.qgpu_attn_fused(qb2.f32(), nh * 2 * hd, kb.f32(), vb.f32(), nkv * hd, qwb.f32(), kwb.f32(),
+                                 kcb2.f32(), vcb2.f32(), rcb.f32(), rsb.f32(), rope_dim, posb.i32(), pos + B, B, nh,
+                                 nkv, hd, eps, ob2.f32(), nh * hd))
+    got2 = ob2.download(np.float32).reshape(B, nh * hd)
+    print(f"  decode {rel_err(got, ref):.2e} fused {rel_err(got2, ref):.2e}", flush=True)
+    assert rel_err(got2, ref) < 1e-4
+    assert np.array_equal(qb2.download(np.float32).reshape(B, -1), q), "fused attention must not modify q"
+    kcg2 = kcb2.download(np.float32).reshape(n_ctx, nkv, hd)
+    assert rel_err(kcg2[pos:pos + B], kref[pos:pos + B]) < 1e-5
+    assert np.array_equal(kcg2[:pos], kc[:pos]) and np.array_equal(kcg2[pos + B:], kc[pos + B:])
+    assert np.array_equal(vcb2.download(np.float32).reshape(n_ctx, nkv, hd)[pos:pos + B], v.reshape(B, nkv, hd))
 
 
 def test_spec_accept_kernel(gpu):
