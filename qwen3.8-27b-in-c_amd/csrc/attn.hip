@@ -87,23 +87,26 @@ struct AttnArgs {
     float eps;
 };
 
-// x[0..255] (in LDS, stride-1) <- rmsnorm(x) * w, by one wave (lane: 4 elements)
-static __device__ __forceinline__ void wave_rmsnorm_row(float *x, const float *src, const float *w, float eps, int lane)
+static __device__ __forceinline__ float4 norm4(float4 v, float4 w, float sc)
 {
-    const float4 v = *(const float4 *)(src + 4 * lane);
-    float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-#pragma unroll
-    for (int o = 32; o; o >>= 1) ss += __shfl_xor(ss, o);
-    const float sc = 1.0f / sqrtf(ss / (float)ATT_HD + eps);
-    const float4 wv = *(const float4 *)(w + 4 * lane);
-    *(float4 *)(x + 4 * lane) = make_float4((v.x * sc) * wv.x, (v.y * sc) * wv.y, (v.z * sc) * wv.z, (v.w * sc) * wv.w);
+    return make_float4((v.x * sc) * w.x, (v.y * sc) * w.y, (v.z * sc) * w.z, (v.w * sc) * w.w);
 }
+
+static __device__ __forceinline__ float wsum64(float v)
+{
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+#define ATT_NQ (ATT_MAXQ / 4)   // q rows per wave
 
 template <int FUSED>
 __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
 {
     __shared__ float Ql[ATT_MAXQ][ATT_LD];
-    __shared__ float KV[ATT_CS][ATT_LD];
+    __shared__ float KL[ATT_CS][ATT_LD];
+    __shared__ float VL[ATT_CS][ATT_LD];
     __shared__ float Pl[ATT_MAXQ][ATT_CS];
     const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int per = p.n_head / p.n_kv, QH = per * p.B;
@@ -116,24 +119,65 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
     }
     const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD;
     const int nt = min(ATT_CS, tmax - t0 + 1);    // positions of this chunk that exist
-    // ---- K rows: cache rows below pos0; new rows (FUSED) prepared here
-    for (int e = tid; e < nt * 64; e += 256) {
-        const int pp = e >> 6, d4 = e & 63, t = t0 + pp;
-        if (!FUSED || t < pos0)
-            *(float4 *)&KV[pp][4 * d4] = *(const float4 *)(p.kc + (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * d4);
+    // ---- every global load first: K and V rows of the chunk (row pp = wv + 4i, lane = float4),
+    //      q rows of the group (row r = wv + 4i), norm weights
+    float4 kr[ATT_CS / 4], vr[ATT_CS / 4], qr[ATT_NQ];
+#pragma unroll
+    for (int i = 0; i < ATT_CS / 4; i++) {
+        const int pp = wv + 4 * i, t = t0 + pp;
+        kr[i] = vr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (pp < nt) {
+            if (FUSED && t >= pos0) {             // new row: raw k/v of token t - pos0
+                const uint64_t off = (uint64_t)(t - pos0) * p.ldkv + (uint64_t)g * ATT_HD + 4 * lane;
+                kr[i] = *(const float4 *)(p.k + off);
+                vr[i] = *(const float4 *)(p.v + off);
+            } else {
+                const uint64_t off = (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * lane;
+                kr[i] = *(const float4 *)(p.kc + off);
+                vr[i] = *(const float4 *)(p.vc + off);
+            }
+        }
     }
-    if (FUSED) {
-        for (int b = wv; b < p.B; b += 4) {
-            const int t = pos0 + b;
-            if (t >= t0 && t < t0 + ATT_CS)
-                wave_rmsnorm_row(KV[t - t0], p.k + (uint64_t)b * p.ldkv + (uint64_t)g * ATT_HD, p.kw, p.eps, lane);
-        }
-        for (int r = wv; r < QH; r += 4) {
+#pragma unroll
+    for (int i = 0; i < ATT_NQ; i++) {
+        const int r = wv + 4 * i;
+        qr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (r < QH) {
             const int b = r / per, h = g * per + r % per;
-            wave_rmsnorm_row(Ql[r], p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD, p.qw, p.eps, lane);
+            qr[i] = *(const float4 *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + 4 * lane);
         }
-        __syncthreads();
-        // NeoX RoPE on (i, i + half), i < half, position pos0 + b
+    }
+    float4 qw = make_float4(1.0f, 1.0f, 1.0f, 1.0f), kw = qw;
+    if (FUSED) {
+        qw = *(const float4 *)(p.qw + 4 * lane);
+        kw = *(const float4 *)(p.kw + 4 * lane);
+    }
+    // ---- to LDS (per-head RMSNorm of q and of the new k rows on the way)
+#pragma unroll
+    for (int i = 0; i < ATT_CS / 4; i++) {
+        const int pp = wv + 4 * i, t = t0 + pp;
+        float4 kv = kr[i];
+        if (FUSED && pp < nt && t >= pos0) {
+            const float ss = wsum64(kv.x * kv.x + kv.y * kv.y + kv.z * kv.z + kv.w * kv.w);
+            kv = norm4(kv, kw, 1.0f / sqrtf(ss / (float)ATT_HD + p.eps));
+        }
+        *(float4 *)&KL[pp][4 * lane] = kv;
+        *(float4 *)&VL[pp][4 * lane] = vr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < ATT_NQ; i++) {
+        const int r = wv + 4 * i;
+        if (r >= QH) break;                       // wave-uniform
+        float4 qv = qr[i];
+        if (FUSED) {
+            const float ss = wsum64(qv.x * qv.x + qv.y * qv.y + qv.z * qv.z + qv.w * qv.w);
+            qv = norm4(qv, qw, 1.0f / sqrtf(ss / (float)ATT_HD + p.eps));
+        }
+        *(float4 *)&Ql[r][4 * lane] = qv;
+    }
+    __syncthreads();
+    if (FUSED) {
+        // NeoX RoPE on (i, i + half) at position pos0 + b: q rows and the new k rows of this chunk
         for (int e = tid; e < (QH + p.B) * p.half; e += 256) {
             const int r = e / p.half, i = e % p.half;
             float *x;
@@ -142,7 +186,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
             else {
                 t = pos0 + (r - QH);
                 if (t < t0 || t >= t0 + ATT_CS) continue;
-                x = KV[t - t0];
+                x = KL[t - t0];
             }
             const float cs = p.rcos[(uint64_t)t * p.half + i], sn = p.rsin[(uint64_t)t * p.half + i];
             const float v0 = x[i], v1 = x[i + p.half];
@@ -150,20 +194,14 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
             x[i + p.half] = v0 * sn + v1 * cs;
         }
         __syncthreads();
-        // the new k rows go to the cache, the new v rows too
+        // the new rows go to the caches (no other block of this launch reads them)
         for (int e = tid; e < p.B * 64; e += 256) {
             const int b = e >> 6, d4 = e & 63, t = pos0 + b;
             if (t < t0 || t >= t0 + ATT_CS) continue;
             const uint64_t row = (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * d4;
-            *(float4 *)(p.kc + row) = *(const float4 *)&KV[t - t0][4 * d4];
-            *(float4 *)(p.vc + row) = *(const float4 *)(p.v + (uint64_t)b * p.ldkv + (uint64_t)g * ATT_HD + 4 * d4);
+            *(float4 *)(p.kc + row) = *(const float4 *)&KL[t - t0][4 * d4];
+            *(float4 *)(p.vc + row) = *(const float4 *)&VL[t - t0][4 * d4];
         }
-    } else {
-        for (int e = tid; e < QH * 64; e += 256) {
-            const int r = e >> 6, d4 = e & 63, b = r / per, h = g * per + r % per;
-            *(float4 *)&Ql[r][4 * d4] = *(const float4 *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + 4 * d4);
-        }
-        __syncthreads();
     }
     // ---- scores for rows rg + 8j at position t0 + pp
     const int rg = tid >> 5, pp = tid & 31;
@@ -172,7 +210,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
     for (int j = 0; j < ATT_NJ; j++) s[j] = 0.0f;
     if (pp < nt) {
         for (int d4 = 0; d4 < 64; d4++) {
-            const float4 kq = *(const float4 *)&KV[pp][4 * d4];
+            const float4 kq = *(const float4 *)&KL[pp][4 * d4];
 #pragma unroll
             for (int j = 0; j < ATT_NJ; j++) {
                 const int r = rg + 8 * j;
@@ -203,14 +241,6 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
         if (pp == 0) { ml[2 * r] = m; ml[2 * r + 1] = sum; }
     }
     __syncthreads();
-    // ---- V rows into the (now free) K buffer
-    for (int e = tid; e < nt * 64; e += 256) {
-        const int q4 = e >> 6, d4 = e & 63, t = t0 + q4;
-        const float *src = (FUSED && t >= pos0) ? p.v + (uint64_t)(t - pos0) * p.ldkv + (uint64_t)g * ATT_HD
-                                                : p.vc + (uint64_t)t * kvrow + (uint64_t)g * ATT_HD;
-        *(float4 *)&KV[q4][4 * d4] = *(const float4 *)(src + 4 * d4);
-    }
-    __syncthreads();
     // ---- P.V: thread d, rows in groups of 16
     const int d = tid;
     for (int r0 = 0; r0 < QH; r0 += 16) {
@@ -218,7 +248,7 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[i] = 0.0f;
         for (int q4 = 0; q4 < nt; q4++) {
-            const float vv = KV[q4][d];
+            const float vv = VL[q4][d];
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[i] = fmaf(Pl[r0 + i < QH ? r0 + i : 0][q4], vv, acc[i]);
         }

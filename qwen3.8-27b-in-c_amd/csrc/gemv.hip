@@ -395,7 +395,10 @@ static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA>
 #endif
 
 template <int NA, int NW>
-__global__ __launch_bounds__(NW * 64) void k_gemv_iq4(const GemvArgs args)
+#ifndef IQ4_MINW
+#define IQ4_MINW 1
+#endif
+__global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs args)
 {
     __shared__ float red[NW][NA][4][16];
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
