@@ -8,6 +8,9 @@
  */
 #ifndef QWEN_GGUF_H
 #define QWEN_GGUF_H
+/* the reference header of the same name is superseded by this one when both
+   are on the include path (reference drivers compiled against this library) */
+#define GGUF_H
 
 #include <stdbool.h>
 #include <stddef.h>

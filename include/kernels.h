@@ -11,6 +11,9 @@
  */
 #ifndef QWEN_KERNELS_H
 #define QWEN_KERNELS_H
+/* the reference header of the same name is superseded by this one when both
+   are on the include path (reference drivers compiled against this library) */
+#define KERNELS_H
 
 #include "gguf.h"
 #include "threadpool.h"

@@ -20,6 +20,9 @@
  */
 #ifndef QWEN_MODEL_H
 #define QWEN_MODEL_H
+/* the reference header of the same name is superseded by this one when both
+   are on the include path (reference drivers compiled against this library) */
+#define MODEL_H
 
 #include "gguf.h"
 #include "qwen_synth.h"

@@ -6,6 +6,9 @@
  */
 #ifndef QWEN_QUANT_H
 #define QWEN_QUANT_H
+/* the reference header of the same name is superseded by this one when both
+   are on the include path (reference drivers compiled against this library) */
+#define QUANT_H
 
 #include "gguf.h"
 #include <stddef.h>

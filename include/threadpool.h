@@ -6,6 +6,9 @@
  */
 #ifndef QWEN_THREADPOOL_H
 #define QWEN_THREADPOOL_H
+/* the reference header of the same name is superseded by this one when both
+   are on the include path (reference drivers compiled against this library) */
+#define THREADPOOL_H
 
 #ifdef __cplusplus
 extern "C" {

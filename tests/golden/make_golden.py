@@ -13,9 +13,12 @@ to the inputs and the reference outputs:
                                deq [ne1][ne0] (dequant_row of every row)
   ops.npz                    : test_ops.c:171-240 random-dimension cases
   model_<variant>.npz        : tiny hybrid model scenarios (ref_harness.c)
+  model_27b.npz              : full-size 27B greedy stream + top-2 gaps
+                               (`python tests/golden/make_golden.py 27b`, ~10 min)
 """
 import ctypes
 import hashlib
+import json
 import os
 import subprocess
 import sys
@@ -145,14 +148,57 @@ def model_fixtures(host):
             print(variant, sha[:16], {k: v.shape for k, v in arrs.items()})
 
 
+SEED_27B = 27            # the benchmark's model seed
+PROMPT_SEED_27B = 20251201
+
+
+def model27b_fixture(host, n_prompt=512, n_gen=48, n_ctx=1024):
+    """Full-size random-init 27B: reference greedy stream after a seeded
+    random-id prompt, with the top-2 gap of every step (the streams must agree
+    wherever the gap exceeds 1e-2), plus the prefill logits."""
+    with tempfile.TemporaryDirectory(dir=os.environ.get("GOLDEN_TMP", None)) as td:
+        exe = os.path.join(td, "ref_harness")
+        subprocess.check_call(["gcc", "-O2", "-std=c11", f"-I{REF_INC}", os.path.join(HERE, "ref_harness.c"),
+                               REF_LIB, f"-Wl,-rpath,{os.path.dirname(REF_LIB)}", "-lm", "-lpthread", "-o", exe])
+        spec = host.spec_27b(SEED_27B)
+        path = os.path.join(td, "m27.gguf")
+        host.write_gguf(spec, path)
+        V = spec.vocab
+        prompt = np.random.default_rng(PROMPT_SEED_27B).integers(0, V, n_prompt).astype(np.uint32)
+        pf = os.path.join(td, "prompt.u32")
+        prompt.tofile(pf)
+        outd = os.path.join(td, "out")
+        os.makedirs(outd)
+        subprocess.check_call([exe, path, outd, str(n_ctx), "greedy", pf, str(n_gen)])
+        # fingerprint of the generated weights: sha256 of a few tensors' bytes
+        names = [b"blk.0.attn_qkv.weight", b"blk.3.attn_q.weight", b"blk.63.ffn_down.weight", b"output.weight"]
+        ts = host.tensors(spec)
+        fp = {}
+        for i, t in enumerate(ts):
+            if t.name in names:
+                fp[t.name.decode()] = hashlib.sha256(host.fill(spec, i, t.nbytes).tobytes()).hexdigest()
+        np.savez(os.path.join(HERE, "model_27b.npz"), seed=np.uint64(SEED_27B), prompt=prompt,
+                 n_ctx=np.int32(n_ctx), stream=np.fromfile(os.path.join(outd, "stream.u32"), np.uint32),
+                 gap=np.fromfile(os.path.join(outd, "gap.f32"), np.float32),
+                 prefill_logits=np.fromfile(os.path.join(outd, "prefill_logits.f32"), np.float32),
+                 fingerprint=np.array(json.dumps(fp)))
+        print("27b fixture", fp)
+
+
 def main():
     if not os.path.exists(REF_LIB):
         sys.exit("build the reference first: make -C oracle")
     ref = ctypes.CDLL(REF_LIB)
     host = qwen_pkg.host_lib()
-    gemv_fixtures(ref, host)
-    ops_fixtures(ref)
-    model_fixtures(host)
+    which = sys.argv[1:] or ["gemv", "ops", "model"]
+    if "gemv" in which:
+        gemv_fixtures(ref, host)
+    if "ops" in which:
+        ops_fixtures(ref)
+    if "model" in which:
+        model_fixtures(host)
+    if "27b" in which:
+        model27b_fixture(host)
 
 
 if __name__ == "__main__":

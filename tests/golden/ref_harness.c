@@ -5,6 +5,12 @@
  * as fixtures next to this file.
  *
  * usage: ref_harness <model.gguf> <out_dir> <n_ctx>
+ *        ref_harness <model.gguf> <out_dir> <n_ctx> greedy <prompt.u32> <n_gen>
+ * The second form (full-size model) prefills the prompt in chunks of 8 and
+ * decodes n_gen tokens greedily with model_forward, writing
+ *   stream.u32        the greedy tokens
+ *   gap.f32           top-1 minus top-2 logit of the logits each token was taken from
+ *   prefill_logits.f32 logits of the last prompt token
  * Writes raw little-endian arrays (see make_golden.py for the manifest):
  *   seq_logits.f32      sequential model_forward logits for prompt[0..7]
  *   batch_logits.f32    model_forward_batch(prompt[0..7], pos 0, B=8) logits_b
@@ -18,9 +24,11 @@
  */
 #define _POSIX_C_SOURCE 200809L
 #include "model.h"
+#include "threadpool.h"
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 static void dump(const char *dir, const char *name, const void *p, size_t bytes)
 {
@@ -46,6 +54,53 @@ static void prefill(qwen_model_t *m, const uint32_t *p, uint32_t n, int mtp)
     }
     memcpy(m->logits, m->logits_b + (size_t)(last - 1) * m->cfg.vocab_size,
            (size_t)m->cfg.vocab_size * sizeof(float));
+}
+
+/* top-1 index (lowest on ties, as model_sample_greedy) and top-1 minus top-2 value */
+static uint32_t top2(const float *l, uint32_t V, float *gap)
+{
+    uint32_t b = 0;
+    for (uint32_t i = 1; i < V; i++) if (l[i] > l[b]) b = i;
+    float second = -3.4e38f;
+    for (uint32_t i = 0; i < V; i++) if (i != b && l[i] > second) second = l[i];
+    *gap = l[b] - second;
+    return b;
+}
+
+static int greedy_mode(const char *path, const char *dir, uint32_t n_ctx, const char *prompt_file, uint32_t n_gen)
+{
+    FILE *f = fopen(prompt_file, "rb");
+    if (!f) { perror(prompt_file); return 1; }
+    uint32_t prompt[4096];
+    const uint32_t n_prompt = (uint32_t)fread(prompt, 4, 4096, f);
+    fclose(f);
+    qwen_model_t *m = calloc(1, sizeof *m);
+    if (!m || model_init(m, path, n_ctx)) return 1;
+    const long ncpu = sysconf(_SC_NPROCESSORS_ONLN);
+    pool_t *pool = pool_create(ncpu > 0 ? (int)ncpu : 1, 1);
+    const uint32_t V = m->cfg.vocab_size;
+    uint32_t pos = 0, last = 0;
+    while (pos < n_prompt) {
+        uint32_t B = n_prompt - pos > PREFILL_MAX_B ? PREFILL_MAX_B : n_prompt - pos;
+        model_forward_batch(m, pool, prompt + pos, pos, B, 0);
+        pos += B;
+        last = B;
+    }
+    memcpy(m->logits, m->logits_b + (size_t)(last - 1) * V, (size_t)V * sizeof(float));
+    dump(dir, "prefill_logits.f32", m->logits, (size_t)V * sizeof(float));
+    uint32_t *out = calloc(n_gen, 4);
+    float *gap = calloc(n_gen, 4);
+    for (uint32_t i = 0; i < n_gen; i++) {
+        out[i] = top2(m->logits, V, &gap[i]);
+        fprintf(stderr, "[greedy] %u: token %u gap %.4f\n", i, out[i], gap[i]);
+        if (i + 1 < n_gen) model_forward(m, pool, out[i], n_prompt + i);
+    }
+    dump(dir, "stream.u32", out, (size_t)n_gen * 4);
+    dump(dir, "gap.f32", gap, (size_t)n_gen * 4);
+    pool_destroy(pool);
+    model_free(m);
+    free(m); free(out); free(gap);
+    return 0;
 }
 
 /* the spec loop of main.c:166-225 (k <= SPEC_MAX_B-1) */
@@ -123,6 +178,8 @@ static uint32_t spec_seq(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n
 int main(int argc, char **argv)
 {
     if (argc < 4) { fprintf(stderr, "usage: %s model.gguf outdir n_ctx\n", argv[0]); return 1; }
+    if (argc >= 7 && !strcmp(argv[4], "greedy")) return greedy_mode(argv[1], argv[2], (uint32_t)atoi(argv[3]), argv[5],
+                                                                  (uint32_t)atoi(argv[6]));
     const char *path = argv[1], *dir = argv[2];
     const uint32_t n_ctx = (uint32_t)atoi(argv[3]);
     qwen_model_t *m = calloc(1, sizeof *m);
