@@ -100,6 +100,11 @@ void model_rollback_states(qwen_model_t *m);             /* no-op (model.c:1009)
  * the caller sets m->pos. */
 void model_rollback_to(qwen_model_t *m, uint32_t b);
 
+/* Start a new sequence on a loaded model (no reference counterpart: the
+ * reference loads a fresh model per run): recurrent states zeroed, ring index
+ * and position 0.  KV rows are overwritten before they are read. */
+void model_reset(qwen_model_t *m);
+
 /* MTP draft layer (reference model.c:1038-1063): token at pos with m->mtp_h;
  * m->mtp_h = output; logits into m->logits when want_logits.  Returns 0. */
 int  mtp_forward(qwen_model_t *m, pool_t *pool, uint32_t token, uint32_t pos, int want_logits);

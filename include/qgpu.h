@@ -168,6 +168,13 @@ int  qgpu_gdn_recurrence(const float *xq, uint64_t ldq, const float *beta_raw, c
                          uint64_t slot_stride, int nslot, const int *cur, int B, int n_k, int n_v,
                          int head_dim, float eps, float *out, uint64_t ldo);
 /* rows x n: out = rmsnorm(x, w) * silu(z)  (per-head gated norm, model.c:928-941) */
+/* qgpu_gdn_conv + qgpu_gdn_recurrence in one launch (same arguments, results
+ * and ring slots; the conv output is not stored): conv_dim = (2 n_k + n_v) * 128,
+ * x = the raw wqkv projection rows. */
+int  qgpu_gdn_fused(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w, float *conv_ring,
+                    uint64_t conv_stride, const float *beta_raw, const float *alpha_raw, uint64_t ldba,
+                    const float *dt_bias, const float *ssm_a, float *ssm_ring, uint64_t ssm_stride, int nslot,
+                    const int *cur, int n_k, int n_v, int head_dim, float eps, float *out, uint64_t ldo);
 int  qgpu_rmsnorm_gated(float *out, const float *x, const float *z, const float *w, int n, int rows,
                         uint64_t ld, float eps);
 

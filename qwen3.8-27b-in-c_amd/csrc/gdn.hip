@@ -117,6 +117,107 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float *__restrict__ xq,
     }
 }
 
+// Conv and recurrence in one launch.  Block (v-head h, rows rb*16..rb*16+15)
+// first runs the 4-tap conv + SiLU of the channels it reads: the 128 q and 128
+// k channels of k-head h % n_k (recomputed by every block of that k-head; the
+// window is a few floats per channel) and its own 16 v channels, for all B
+// tokens, into LDS.  Conv-state snapshots are written once per channel: q/k
+// channels by the block (h < n_k, rb = 0), v channels by their own block.
+__global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, uint64_t ldx, const float *__restrict__ cw,
+                                                   float *__restrict__ cring, uint64_t cstride,
+                                                   const float *__restrict__ beta_raw, const float *__restrict__ alpha_raw,
+                                                   uint64_t ldba, const float *__restrict__ dt_bias,
+                                                   const float *__restrict__ ssm_a, float *__restrict__ sring,
+                                                   uint64_t sstride, int nslot, const int *__restrict__ cur_dev, int B,
+                                                   int n_k, int n_v, float eps, float *__restrict__ out, uint64_t ldo)
+{
+    __shared__ float Yq[GDN_MAXB][GDN_HK], Yk[GDN_MAXB][GDN_HK], Yv[GDN_MAXB][GDN_RB];
+    const int h = blockIdx.x / (GDN_HK / GDN_RB);
+    const int rb = blockIdx.x % (GDN_HK / GDN_RB);
+    const int tid = threadIdx.x;
+    const int kh = h % n_k;                          // tiled v-head -> k-head map (model.c:565)
+    const int cur = *cur_dev;
+    const bool own_qk = h < n_k && rb == 0;
+    // ---- conv + SiLU of the 2*128 + 16 channels this block reads
+    for (int e = tid; e < 2 * GDN_HK + GDN_RB; e += 256) {
+        int c;
+        float *dst;
+        bool own;
+        if (e < GDN_HK) { c = kh * GDN_HK + e; dst = &Yq[0][e]; own = own_qk; }
+        else if (e < 2 * GDN_HK) { c = n_k * GDN_HK + kh * GDN_HK + (e - GDN_HK); dst = &Yk[0][e - GDN_HK]; own = own_qk; }
+        else { c = 2 * n_k * GDN_HK + h * GDN_HK + rb * GDN_RB + (e - 2 * GDN_HK); dst = &Yv[0][e - 2 * GDN_HK]; own = true; }
+        const int dstride = e < 2 * GDN_HK ? GDN_HK : GDN_RB;
+        const float4 s0 = *(const float4 *)(cring + (uint64_t)cur * cstride + (uint64_t)c * 4);
+        const float4 wc = *(const float4 *)(cw + (uint64_t)c * 4);
+        float win[4 + GDN_MAXB];
+        win[0] = s0.x; win[1] = s0.y; win[2] = s0.z; win[3] = s0.w;
+#pragma unroll
+        for (int b = 0; b < GDN_MAXB; b++) {
+            if (b >= B) break;
+            win[4 + b] = x[(uint64_t)b * ldx + c];
+            const float a0 = win[b + 1], a1 = win[b + 2], a2 = win[b + 3], a3 = win[b + 4];
+            dst[b * dstride] = silu_f(((a0 * wc.x + a1 * wc.y) + a2 * wc.z) + a3 * wc.w);
+            if (own) {
+                const int slot = (cur + 1 + b) % nslot;
+                *(float4 *)(cring + (uint64_t)slot * cstride + (uint64_t)c * 4) = make_float4(a0, a1, a2, a3);
+            }
+        }
+    }
+    __syncthreads();
+    // ---- delta-rule recurrence (as k_gdn_recur), inputs from LDS
+    const int r = tid >> 4, cc = tid & 15;
+    const int j = rb * GDN_RB + r;                   // state row (v index)
+    const uint64_t hoff = (uint64_t)h * GDN_HK * GDN_HK + (uint64_t)j * GDN_HK + cc * 8;
+    const float *S0 = sring + (uint64_t)cur * sstride + hoff;
+    float S[8];
+    {
+        const float4 a = *(const float4 *)S0, b = *(const float4 *)(S0 + 4);
+        S[0] = a.x; S[1] = a.y; S[2] = a.z; S[3] = a.w; S[4] = b.x; S[5] = b.y; S[6] = b.z; S[7] = b.w;
+    }
+    const float qscale = 1.0f / sqrtf((float)GDN_HK);
+    const float ah = ssm_a[h], dtb = dt_bias[h];
+    for (int b = 0; b < B; b++) {
+        float q[8], k[8];
+        {
+            const float4 q0 = *(const float4 *)&Yq[b][cc * 8], q1 = *(const float4 *)&Yq[b][cc * 8 + 4];
+            const float4 k0 = *(const float4 *)&Yk[b][cc * 8], k1 = *(const float4 *)&Yk[b][cc * 8 + 4];
+            q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w; q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
+            k[0] = k0.x; k[1] = k0.y; k[2] = k0.z; k[3] = k0.w; k[4] = k1.x; k[5] = k1.y; k[6] = k1.z; k[7] = k1.w;
+        }
+        float qq = 0.0f, kk = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) { qq = fmaf(q[i], q[i], qq); kk = fmaf(k[i], k[i], kk); }
+        qq = sum16(qq);
+        kk = sum16(kk);
+        const float qn = sqrtf(qq), kn = sqrtf(kk);
+        const float qs = 1.0f / (qn > eps ? qn : eps), ks = 1.0f / (kn > eps ? kn : eps);   // l2norm (kernels.c:780-805)
+        float kq = 0.0f, sk = 0.0f, sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            q[i] *= qs;
+            k[i] *= ks;
+            kq = fmaf(k[i], q[i], kq);
+            sk = fmaf(S[i], k[i], sk);
+            sq = fmaf(S[i], q[i], sq);
+        }
+        kq = sum16(kq);
+        sk = sum16(sk);
+        sq = sum16(sq);
+        const float beta = 1.0f / (1.0f + expf(-beta_raw[(uint64_t)b * ldba + h]));
+        const float araw = alpha_raw[(uint64_t)b * ldba + h] + dtb;
+        const float sp = araw > 30.0f ? araw : log1pf(expf(araw));
+        const float decay = expf(ah * sp);
+        const float vj = Yv[b][r];
+        const float dj = (vj - decay * sk) * beta;
+        if (cc == 0) out[(uint64_t)b * ldo + (uint64_t)h * GDN_HK + j] = (decay * sq + dj * kq) * qscale;
+#pragma unroll
+        for (int i = 0; i < 8; i++) S[i] = fmaf(dj, k[i], decay * S[i]);
+        float *Sn = sring + (uint64_t)((cur + 1 + b) % nslot) * sstride + hoff;
+        *(float4 *)Sn = make_float4(S[0], S[1], S[2], S[3]);
+        *(float4 *)(Sn + 4) = make_float4(S[4], S[5], S[6], S[7]);
+    }
+}
+
 // out[r] = rmsnorm(x[r], w) * silu(z[r]) for rows of n (per-head gated norm, model.c:928-941)
 __global__ __launch_bounds__(128) void k_rmsnorm_gated(float *out, const float *x, const float *z, const float *w,
                                                        int n, uint64_t ld, float eps)
@@ -177,6 +278,28 @@ extern "C" int qgpu_rmsnorm_gated(float *out, const float *x, const float *z, co
     if (!out || !x || !z || !w || n < 1 || rows < 0 || ld < (uint64_t)n) return QGPU_E_ARG;
     if (!rows) return QGPU_OK;
     hipLaunchKernelGGL(k_rmsnorm_gated, dim3(rows), dim3(128), 0, qg::stream, out, x, z, w, n, ld, eps);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_gdn_fused(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w, float *conv_ring,
+                              uint64_t conv_stride, const float *beta_raw, const float *alpha_raw, uint64_t ldba,
+                              const float *dt_bias, const float *ssm_a, float *ssm_ring, uint64_t ssm_stride, int nslot,
+                              const int *cur, int n_k, int n_v, int head_dim, float eps, float *out, uint64_t ldo)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (head_dim != GDN_HK) return QGPU_E_RANGE;
+    if (!x || !conv_w || !conv_ring || !beta_raw || !alpha_raw || !dt_bias || !ssm_a || !ssm_ring || !cur || !out ||
+        B < 1 || B > GDN_MAXB || nslot < B + 1 || n_k < 1 || n_v < 1 ||
+        conv_dim != (2 * n_k + n_v) * GDN_HK || conv_stride < (uint64_t)conv_dim * 4 ||
+        ssm_stride < (uint64_t)n_v * GDN_HK * GDN_HK || ldx < (uint64_t)conv_dim || ldo < (uint64_t)n_v * GDN_HK ||
+        ldba < (uint64_t)n_v || ((uintptr_t)conv_ring & 15) || ((uintptr_t)conv_w & 15) || ((uintptr_t)ssm_ring & 15) ||
+        conv_stride % 4 || ssm_stride % 4)
+        return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_gdn_fused, dim3(n_v * (GDN_HK / GDN_RB)), dim3(256), 0, qg::stream, x, ldx, conv_w, conv_ring,
+                       conv_stride, beta_raw, alpha_raw, ldba, dt_bias, ssm_a, ssm_ring, ssm_stride, nslot, cur, B, n_k,
+                       n_v, eps, out, ldo);
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }

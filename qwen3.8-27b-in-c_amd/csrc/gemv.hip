@@ -321,6 +321,9 @@ static __device__ __forceinline__ void iq4_decode8(uint32_t q, const DecodeK &K,
 // Weight records come from HBM and activation digits from L2, so the two are
 // prefetched to different depths: weights IQ4_WDEPTH super-blocks ahead
 // (10 VGPRs each), digits IQ4_ADEPTH ahead (16 * NA + 4 * NA VGPRs each).
+// Measured on MI355X over the model's shapes (rings of 2..8 x 1..2, occupancy
+// caps): 3 / 1 is within noise of the best everywhere and keeps the kernel at
+// 100 VGPRs.
 struct IQ4W {
     uint2 hdr;
     uint4 qa, qb;
@@ -388,10 +391,10 @@ static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA>
 }
 
 #ifndef IQ4_WDEPTH
-#define IQ4_WDEPTH 4    // weight records in flight per wave
+#define IQ4_WDEPTH 3    // weight records in flight per wave
 #endif
 #ifndef IQ4_ADEPTH
-#define IQ4_ADEPTH 2    // digit super-blocks in flight per wave (divides IQ4_WDEPTH)
+#define IQ4_ADEPTH 1    // digit super-blocks in flight per wave (divides IQ4_WDEPTH)
 #endif
 
 template <int NA, int NW>
@@ -696,15 +699,16 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
         A.A = (const uint8_t *)qg::ws;
         A.xs = (const float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES);
         // waves per tile (K split inside the block).  Measured on MI355X over the
-        // model's shapes (K = 5120..17408, 5120..248320 rows, B = 1..8): 4 waves is
-        // best or within 1% everywhere except very tall matrices (lm_head), where
-        // 2 is marginally better.  QGPU_GEMV_NW=1|2|4|8 forces the split.
+        // model's shapes with the 3/1 prefetch rings: 4 waves is best or within
+        // noise everywhere except narrow outputs (<= 512 tiles, e.g. 5120 rows,
+        // fewer blocks than 2 per CU), where 8 waves per tile hide more latency.
+        // QGPU_GEMV_NW=1|2|4|8 forces the split.
         static int force_nw = -1;
         if (force_nw < 0) {
             const char *e = getenv("QGPU_GEMV_NW");
             force_nw = e ? atoi(e) : 0;
         }
-        int nw = tiles >= 8192 ? 2 : 4;
+        int nw = tiles <= 512 ? 8 : 4;
         if (force_nw == 1 || force_nw == 2 || force_nw == 4 || force_nw == 8) nw = force_nw;
         while (nw > 1 && A.nsb < nw) nw >>= 1;              // no idle waves on short K
 #define IQ4_GO(NA_, NW_) hipLaunchKernelGGL((k_gemv_iq4<NA_, NW_>), dim3(tiles), dim3(64 * NW_), 0, qg::stream, A)

@@ -476,11 +476,10 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     float *outs[4] = { g->bqkv, g->bz, g->bbeta, g->balpha };
     const uint64_t ld[4] = { g->SQ, di, d->n_v_heads, d->n_v_heads };
     K(qgpu_gemv_act_batch(W, 4, &an, (int)B, outs, ld, 0));
-    K(qgpu_gdn_conv(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems, NSLOT,
-                    g->d_cur, g->xq, d->conv_dim));
-    K(qgpu_gdn_recurrence(g->xq, d->conv_dim, g->bbeta, g->balpha, d->n_v_heads, D->dt_bias, D->ssm_a, D->ssm_ring,
-                          g->ssm_elems, NSLOT, g->d_cur, (int)B, (int)d->n_k_heads, (int)d->n_v_heads,
-                          (int)d->head_v_dim, eps, g->battn, di));
+    /* conv1d + SiLU + L2 norms + delta rule over the B tokens, state snapshots into the ring */
+    K(qgpu_gdn_fused(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems, g->bbeta,
+                     g->balpha, d->n_v_heads, D->dt_bias, D->ssm_a, D->ssm_ring, g->ssm_elems, NSLOT, g->d_cur,
+                     (int)d->n_k_heads, (int)d->n_v_heads, (int)d->head_v_dim, eps, g->battn, di));
     /* per-head gated RMSNorm (model.c:928-941) fused into the ssm_out input */
     qgpu_act gn;
     memset(&gn, 0, sizeof gn);
@@ -567,6 +566,22 @@ void model_forward_batch(qwen_model_t *m, pool_t *pool, const uint32_t *tokens, 
         K(qgpu_memcpy_d2h(m->h_save, m->gpu->h_save, (size_t)B * m->dims.n_embd * sizeof(float)));
     }
     m->pos = pos + B;
+}
+
+void model_reset(qwen_model_t *m)
+{
+    qwen_gpu_t *g = m->gpu;
+    for (uint32_t il = 0; il < m->dims.n_layer; il++) {
+        const glayer_t *D = &g->L[il];
+        if (!D->rec) continue;
+        K(qgpu_memset(D->conv_ring, 0, NSLOT * g->conv_elems * sizeof(float)));
+        K(qgpu_memset(D->ssm_ring, 0, NSLOT * g->ssm_elems * sizeof(float)));
+    }
+    g->cur = g->cur_base = 0;
+    K(qgpu_set_i32(g->d_cur, 0));
+    K(qgpu_set_i32(g->d_pos, 0));
+    K(qgpu_sync());
+    m->pos = 0;
 }
 
 int model_snapshot_states(qwen_model_t *m) { (void)m; return 0; }

@@ -266,6 +266,8 @@ class GpuLib:
             "qgpu_gdn_recurrence": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, u64, i32, ctypes.POINTER(i32),
                                     i32, i32, i32, i32, f32, F32P, u64],
             "qgpu_rmsnorm_gated": [F32P, F32P, F32P, F32P, i32, i32, u64, f32],
+            "qgpu_gdn_fused": [F32P, u64, i32, i32, F32P, F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, u64, i32,
+                               ctypes.POINTER(i32), i32, i32, i32, f32, F32P, u64],
             "qgpu_attn_prep": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
                                ctypes.POINTER(i32), i32, i32, i32, i32, f32],
             "qgpu_attn_decode": [F32P, u64, F32P, F32P, ctypes.POINTER(i32), i32, i32, i32, i32, i32, F32P, u64],
@@ -364,6 +366,7 @@ def _model_lib():
     L.model_forward.argtypes = [vp, vp, u32, u32]
     L.model_forward_batch.argtypes = [vp, vp, U32P, u32, u32, i32]
     L.model_rollback_to.argtypes = [vp, u32]
+    L.model_reset.argtypes = [vp]
     L.mtp_forward.argtypes = [vp, vp, u32, u32, i32]
     L.mtp_forward_batch.argtypes = [vp, vp, U32P, u32, u32, i32]
     L.qwen_model_field.argtypes = [vp, ctypes.c_char_p]
@@ -439,6 +442,9 @@ class Model:
 
     def h_save(self, B):
         return self.field("h_save", B * self.E).reshape(B, self.E)
+
+    def reset(self):
+        self.L.model_reset(self.h)
 
     def rollback_to(self, b):
         self.L.model_rollback_to(self.h, b)

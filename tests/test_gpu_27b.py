@@ -1,0 +1,77 @@
+"""Full-size parity: the seeded random-init 27B hybrid (64 layers + MTP, all
+IQ4_XS, generated on the box from the same seed as the fixture) against the
+reference engine's own run on the same weights (tests/golden/model_27b.npz,
+made by make_golden.py from the compiled reference):
+  * the logits of the last prompt token after a 512-token prefill, within 1e-3;
+  * the greedy stream (device greedy decode, and the device MTP speculative
+    loop at k = 3) identical to the reference's wherever the reference top-2
+    gap exceeds 1e-2, up to the first step at or below that gap."""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from gpu_util import gpu, rel_err  # noqa: F401
+from qwen_pkg import host_lib, pyqwen
+
+pytestmark = pytest.mark.gpu
+FIX = os.path.join(O.GOLDEN, "model_27b.npz")
+
+
+@pytest.fixture(scope="module")
+def m27():
+    if not os.path.exists(FIX):
+        pytest.skip("model_27b.npz fixture absent")
+    z = np.load(FIX, allow_pickle=False)
+    host = host_lib()
+    spec = host.spec_27b(int(z["seed"]))
+    # the generator must reproduce the fixture's weights byte for byte
+    fp = json.loads(str(z["fingerprint"]))
+    for i, t in enumerate(host.tensors(spec)):
+        name = t.name.decode()
+        if name in fp:
+            assert hashlib.sha256(host.fill(spec, i, t.nbytes).tobytes()).hexdigest() == fp[name], name
+    print("\n[27b] building the model on the GPU", flush=True)
+    m = pyqwen.Model(spec=spec, n_ctx=int(z["n_ctx"]))
+    yield m, z
+    m.close()
+
+
+def agreeing_prefix(gap):
+    """steps up to (excluding) the first whose reference top-2 gap is <= 1e-2"""
+    low = np.nonzero(gap <= 1e-2)[0]
+    return int(low[0]) if len(low) else len(gap)
+
+
+def test_27b_prefill_logits(gpu, m27):
+    m, z = m27
+    m.reset()
+    p = z["prompt"]
+    last = None
+    for i in range(0, len(p), 8):
+        last = m.forward_batch(p[i:i + 8], i, 0)[-1]
+    e = rel_err(last, z["prefill_logits"])
+    print(f"  prefill logits rel err {e:.2e}", flush=True)
+    assert e < 1e-3
+    assert last.argmax() == z["prefill_logits"].argmax()
+
+
+def test_27b_greedy_stream(gpu, m27):
+    m, z = m27
+    m.reset()
+    n = agreeing_prefix(z["gap"])
+    toks, st = m.generate_greedy(z["prompt"], len(z["stream"]))
+    print(f"  greedy: {n} steps with gap > 1e-2", flush=True)
+    assert np.array_equal(toks[:n], z["stream"][:n])
+
+
+@pytest.mark.parametrize("k", [3])
+def test_27b_spec_stream(gpu, m27, k):
+    m, z = m27
+    m.reset()
+    n = agreeing_prefix(z["gap"])
+    toks, js, st = m.generate_spec(z["prompt"], len(z["stream"]), k)
+    assert np.array_equal(toks[:n], z["stream"][:n])

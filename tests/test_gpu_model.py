@@ -29,8 +29,9 @@ def load(name):
 
 
 # ---------------------------------------------------------------- GDN block (config 3)
-def test_gdn_block_config3_vs_oracle_with_snapshots_and_rollback(gpu):
-    print("\n[gdn] config 3: 48 v-heads x 128x128, 16 k-heads, T=4", flush=True)
+@pytest.mark.parametrize("fused", [False, True])
+def test_gdn_block_config3_vs_oracle_with_snapshots_and_rollback(gpu, fused):
+    print(f"\n[gdn] config 3: 48 v-heads x 128x128, 16 k-heads, T=4, fused={fused}", flush=True)
     T, nk, nv, hk = 4, 16, 48, 128
     cd, eps = 2 * nk * hk + nv * hk, 1e-6
     host = host_lib()
@@ -60,11 +61,21 @@ def test_gdn_block_config3_vs_oracle_with_snapshots_and_rollback(gpu):
     curb = gpu.put(np.array([cur0], np.int32))
     xb, yb, cwb = gpu.put(qkv), gpu.buf(T * cd * 4), gpu.put(cw)
     dtbb, sab = gpu.put(dtb), gpu.put(sa)
-    gpu.ok(gpu.L.qgpu_gdn_conv(xb.f32(), cd, T, cd, cwb.f32(), cring.f32(), cstride, NSLOT, curb.i32(), yb.f32(), cd))
     ob = gpu.buf(T * nv * hk * 4)
     bb, ab = gpu.put(br), gpu.put(ar)
-    gpu.ok(gpu.L.qgpu_gdn_recurrence(yb.f32(), cd, bb.f32(), ab.f32(), nv, dtbb.f32(), sab.f32(),
-                                     sring.f32(), sstride, NSLOT, curb.i32(), T, nk, nv, hk, eps, ob.f32(), nv * hk))
+
+    def run(xbuf, ntok, bbuf, abuf):
+        if fused:
+            gpu.ok(gpu.L.qgpu_gdn_fused(xbuf.f32(), cd, ntok, cd, cwb.f32(), cring.f32(), cstride, bbuf.f32(),
+                                        abuf.f32(), nv, dtbb.f32(), sab.f32(), sring.f32(), sstride, NSLOT,
+                                        curb.i32(), nk, nv, hk, eps, ob.f32(), nv * hk))
+        else:
+            gpu.ok(gpu.L.qgpu_gdn_conv(xbuf.f32(), cd, ntok, cd, cwb.f32(), cring.f32(), cstride, NSLOT, curb.i32(),
+                                       yb.f32(), cd))
+            gpu.ok(gpu.L.qgpu_gdn_recurrence(yb.f32(), cd, bbuf.f32(), abuf.f32(), nv, dtbb.f32(), sab.f32(),
+                                             sring.f32(), sstride, NSLOT, curb.i32(), ntok, nk, nv, hk, eps, ob.f32(),
+                                             nv * hk))
+    run(xb, T, bb, ab)
     got = ob.download(np.float32).reshape(T, -1)
     for b in range(T):
         e = rel_err(got[b], oout.reshape(T, -1)[b])
@@ -83,9 +94,7 @@ def test_gdn_block_config3_vs_oracle_with_snapshots_and_rollback(gpu):
     x1 = host.synth_normal(cd, 3, 7).reshape(1, cd)
     b1, a1 = host.synth_normal(nv, 3, 8), host.synth_normal(nv, 3, 9)
     x1b, b1b, a1b = gpu.put(x1), gpu.put(b1), gpu.put(a1)
-    gpu.ok(gpu.L.qgpu_gdn_conv(x1b.f32(), cd, 1, cd, cwb.f32(), cring.f32(), cstride, NSLOT, curb.i32(), yb.f32(), cd))
-    gpu.ok(gpu.L.qgpu_gdn_recurrence(yb.f32(), cd, b1b.f32(), a1b.f32(), nv, dtbb.f32(), sab.f32(), sring.f32(),
-                                     sstride, NSLOT, curb.i32(), 1, nk, nv, hk, eps, ob.f32(), nv * hk))
+    run(x1b, 1, b1b, a1b)
     oc2 = snap_c.reshape(T, -1)[2].copy()
     os2 = snap_s.reshape(T, -1)[2].copy()
     o2 = np.zeros(nv * hk, np.float32)
