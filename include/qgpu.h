@@ -101,7 +101,13 @@ int  qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, i
  *   QGPU_ACT_GATED_NORM v = rmsnorm_head(x) * w[i % seg] * silu(y)  per head of seg
  *                       in {64, 128, 256} elements                  (model.c:928-941)
  * xout (optional, ldxo) receives v in fp32; it is required when a matrix of
- * the call is not IQ4_XS (those kernels read fp32 rows).  ne0 % 256 == 0. */
+ * the call is not IQ4_XS (those kernels read fp32 rows).  ne0 % 256 == 0.
+ * Single-segment QGPU_ACT_RMSNORM inside a GEMV call is computed as
+ * s * (W (x w)) with s = 1/sqrt(mean(x^2) + eps) applied to the GEMV output,
+ * so xout then holds x * w (the row factor is not in it).
+ * Pending K-split partial sums (qgpu_gemv_act_split): with n_part > 0 the
+ * RMSNORM input is x_eff = x + sum_{q < n_part} part[q*n*ldp + t*ldp + i];
+ * xnew (ldxn; may equal x) receives x_eff.  Single-segment RMSNORM only. */
 #define QGPU_ACT_COPY        0
 #define QGPU_ACT_RMSNORM     1
 #define QGPU_ACT_SILU_MUL    2
@@ -115,6 +121,8 @@ typedef struct {
     uint64_t     seg;
     float        eps;
     float       *xout; uint64_t ldxo;
+    const float *part; uint64_t ldp; int n_part;
+    float       *xnew; uint64_t ldxn;
 } qgpu_act;
 /* qgpu_gemv_multi_batch with the input given as a transform of device rows. */
 int  qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,
@@ -122,6 +130,17 @@ int  qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act
 /* Transform only: v into act->xout (required) and the IQ4_XS digit planes
  * (so qgpu_gemv_prepared may follow). */
 int  qgpu_act_prepare(const qgpu_act *act, int n, uint64_t ne0);
+/* K-split form for narrow outputs (ne1 rows spread over too few tiles to load
+ * every compute unit): ks blocks per 16-row tile each reduce one K range and
+ * write partial plane q: part[q*n*ldp + t*ldp + r] (no accumulation).  The
+ * planes are summed, in q order, by the next QGPU_ACT_RMSNORM that names them
+ * (n_part = ks) or by qgpu_add_partials.  IQ4_XS only; ks in 1..8. */
+int  qgpu_gemv_act_split(const qgpu_tensor *W, const qgpu_act *act, int n, float *part, uint64_t ldp, int ks);
+/* ks that balances W over the device's compute units (1: no split). */
+int  qgpu_gemv_split_ks(const qgpu_tensor *W);
+/* rows x n: y = x + sum_{q < n_part} part[q*rows*ldp + r*ldp + i] (y may equal x). */
+int  qgpu_add_partials(float *y, uint64_t ldy, const float *x, uint64_t ldx, const float *part, uint64_t ldp,
+                       int n_part, uint64_t n, int rows);
 /* Rows [r0, r1) only (reference gemv_rows, kernels.c:298-321). */
 int  qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
                           float *out, uint64_t ldo, uint64_t r0, uint64_t r1);

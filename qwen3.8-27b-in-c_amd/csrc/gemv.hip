@@ -27,8 +27,11 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 #define MAX_NSB     (MAX_K / 256)
 #define PLANE_BYTES ((size_t)MAX_NSB * 4096)
 #define XS_FLOATS   ((size_t)MAX_NSB * 16)
+#define RSS_FLOATS  ((size_t)QGPU_MAX_B * MAX_NSB)
+#define ACT_RMS_DEFER 4      // internal prep kind: RMSNORM with the 1/rms factor applied by the GEMV
 
-size_t qg_gemv_workspace_bytes() { return 2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float); }
+size_t qg_gemv_workspace_bytes() { return 2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float) + RSS_FLOATS * sizeof(float); }
+static float *ws_rss() { return (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float)); }
 
 static __device__ __forceinline__ float h2f(uint32_t h16) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h16); }
 
@@ -132,6 +135,13 @@ struct ActDev {
     uint64_t ldx, ldy, ldxo, seg;
     float eps;
     int ntok, digits;
+    // ACT_RMS_DEFER: x_eff = x + sum of n_part partial planes (part + q*pstride + t*ldp), written
+    // back to xnew when set (may alias x: a block reads and writes only its own super-block);
+    // rss[t*nsb + sb] = sum over the super-block of x_eff^2
+    const float *part;
+    uint64_t ldp, pstride, ldxn;
+    int n_part, nsb;
+    float *xnew, *rss;
 };
 
 static __device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + expf(-v)); }
@@ -156,7 +166,32 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
     const int lane = e & 63, wv = e >> 6;
     const uint64_t k = (uint64_t)sb * 256 + e;
     float v[4];
-    if (KIND == QGPU_ACT_RMSNORM) {
+    if (KIND == ACT_RMS_DEFER) {
+        // v = x_eff * w; the row factor 1/sqrt(mean(x_eff^2) + eps) multiplies the GEMV output
+        // (W (x s w) = s W (x w)), from the per-super-block sums of squares written here
+        float ssq[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = 4 * a + i;
+            float xe = 0.0f;
+            if (t < p.ntok) {
+                xe = p.x[(uint64_t)t * p.ldx + k];
+                if (p.n_part) {
+                    float ps = p.part[(uint64_t)t * p.ldp + k];
+                    for (int q = 1; q < p.n_part; q++) ps += p.part[(uint64_t)q * p.pstride + (uint64_t)t * p.ldp + k];
+                    xe += ps;
+                }
+                if (p.xnew) p.xnew[(uint64_t)t * p.ldxn + k] = xe;
+            }
+            v[i] = xe * p.w[k];
+            ssq[i] = wave_sum(xe * xe);
+            if (lane == 0) red[i][wv] = ssq[i];
+        }
+        __syncthreads();
+        if (e < 4 && 4 * a + e < p.ntok)
+            p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[e][0] + red[e][1]) + (red[e][2] + red[e][3]);
+        __syncthreads();
+    } else if (KIND == QGPU_ACT_RMSNORM) {
         // row RMS over the segment holding this super-block (each block recomputes it: same order, same value);
         // all row loads are issued before any reduction
         const uint64_t segl = p.seg;
@@ -166,16 +201,23 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
         const uint64_t ld = part ? p.ldy : p.ldx, kk = k - (part ? segl : 0);
         const int nt = p.ntok - 4 * a < 4 ? p.ntok - 4 * a : 4;     // tokens of this plane (>= 1)
         float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint64_t j = e; j < segl / 4; j += 256) {
-            float4 q[4];
+        for (uint64_t j0 = e; j0 < segl / 4; j0 += 5 * 256) {
+            float4 q[5][4];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                q[i] = i < nt ? ((const float4 *)(src + (uint64_t)(4 * a + i) * ld))[j] : make_float4(0, 0, 0, 0);
+            for (int u = 0; u < 5; u++) {
+                const uint64_t j = j0 + (uint64_t)u * 256;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                ss[i] = fmaf(q[i].x, q[i].x, ss[i]); ss[i] = fmaf(q[i].y, q[i].y, ss[i]);
-                ss[i] = fmaf(q[i].z, q[i].z, ss[i]); ss[i] = fmaf(q[i].w, q[i].w, ss[i]);
+                for (int i = 0; i < 4; i++)
+                    q[u][i] = (i < nt && j < segl / 4) ? ((const float4 *)(src + (uint64_t)(4 * a + i) * ld))[j]
+                                                      : make_float4(0, 0, 0, 0);
             }
+#pragma unroll
+            for (int u = 0; u < 5; u++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    ss[i] = fmaf(q[u][i].x, q[u][i].x, ss[i]); ss[i] = fmaf(q[u][i].y, q[u][i].y, ss[i]);
+                    ss[i] = fmaf(q[u][i].z, q[u][i].z, ss[i]); ss[i] = fmaf(q[u][i].w, q[u][i].w, ss[i]);
+                }
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -281,7 +323,39 @@ struct GemvArgs {
     const float *xs;
     const float *x;        // VALU path: fp32 activations
     uint64_t ldx, ne0;
+    int ks;                // K split: ks blocks per tile, block q writes partial plane q (out + q*pstride)
+    uint64_t pstride;
+    const float *rss;      // deferred RMSNorm: outputs *= 1/sqrt(sum_sb rss[t*rss_nsb+sb] * rss_inv_n + eps)
+    int rss_nsb;
+    float rss_inv_n, eps;
 };
+
+// Row factors of the deferred RMSNorm, one per token, into rsc[]: wave w owns tokens
+// w, w + nw (<= 2 per wave for nw >= 4); the per-super-block sums of squares are
+// added in the same fixed order in every block.  rms_load issues the loads (before
+// the main loop, so their latency is hidden), rms_reduce finishes after it.
+// (rss_nsb <= 64: one sum per lane and token)
+struct RmsPart { float v[2]; };
+static __device__ __forceinline__ void rms_load(const GemvArgs &args, int wv, int nw, int lane, RmsPart &rp)
+{
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int t = wv + u * nw;
+        rp.v[u] = (t < args.ntok && lane < args.rss_nsb) ? args.rss[(uint64_t)t * args.rss_nsb + lane] : 0.0f;
+    }
+}
+static __device__ __forceinline__ void rms_reduce(const GemvArgs &args, int wv, int nw, int lane, const RmsPart &rp,
+                                                  float *rsc)
+{
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int t = wv + u * nw;
+        float s = rp.v[u];
+#pragma unroll
+        for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+        if (lane == 0 && t < args.ntok) rsc[t] = 1.0f / sqrtf(s * args.rss_inv_n + args.eps);
+    }
+}
 
 // v_and_or_b32 with every operand in a VGPR (a VOP3 encoding takes no 32-bit
 // literal and one scalar operand at most, so the constants live in VGPRs)
@@ -397,23 +471,33 @@ static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA>
 #define IQ4_ADEPTH 1    // digit super-blocks in flight per wave (divides IQ4_WDEPTH)
 #endif
 
-template <int NA, int NW>
+// MODE bit 0 (IQ4_RMS): deferred RMSNorm row factors; bit 1 (IQ4_SPLIT): K split
+// into partial planes.  Plain launches (MODE 0) compile without either.
+#define IQ4_RMS   1
+#define IQ4_SPLIT 2
+template <int NA, int NW, int MODE>
 #ifndef IQ4_MINW
 #define IQ4_MINW 1
 #endif
 __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs args)
 {
     __shared__ float red[NW][NA][4][16];
+    __shared__ float rsc[QGPU_MAX_B];
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar loop control
-    const uint32_t tile = blockIdx.x;
+    const uint32_t tile = (MODE & IQ4_SPLIT) ? blockIdx.x / args.ks : blockIdx.x;
+    const int kq = (MODE & IQ4_SPLIT) ? blockIdx.x % args.ks : 0;   // K range of this block (split GEMV)
+    const int ks = (MODE & IQ4_SPLIT) ? args.ks : 1;
     int k = 0;
     while (k + 1 < args.n_mat && tile >= args.m[k + 1].tile0) k++;
     const GemvMat &M = args.m[k];
     const uint32_t T = tile - M.tile0 + M.tile_first;
     const int nsb = args.nsb;
     const uint8_t *rec0 = M.W + (uint64_t)T * nsb * IQ4_REC_BYTES;
-    const int sb0 = wv * nsb / NW, sb1 = (wv + 1) * nsb / NW;
+    const int kb0 = kq * nsb / ks, nkb = (kq + 1) * nsb / ks - kb0;
+    const int sb0 = kb0 + wv * nkb / NW, sb1 = kb0 + (wv + 1) * nkb / NW;
+    RmsPart rp;
+    if (MODE & IQ4_RMS) rms_load(args, wv, NW, lane, rp);
     DecodeK K;
     K.m4 = 0x04040404u;
     K.sel0 = 0x03020100u;
@@ -450,6 +534,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
     }
 #undef LOAD_W
 #undef LOAD_A
+    if (MODE & IQ4_RMS) rms_reduce(args, wv, NW, lane, rp, rsc);
     // lanes n, n+16, n+32, n+48 hold digits 0..3 of the same (token, row): sum them
 #pragma unroll
     for (int a = 0; a < NA; a++)
@@ -469,8 +554,13 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
         const int t = 4 * a + i;
         const uint32_t r = T * IQ4_TILE_ROWS + nn;
         if (t < args.ntok && r >= M.row_lo && r < M.row_hi) {
-            float *o = M.out + (uint64_t)t * M.ldo + r;
-            *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + s : s;
+            if (MODE & IQ4_RMS) s *= rsc[t];
+            if (MODE & IQ4_SPLIT) {
+                M.out[(uint64_t)kq * args.pstride + (uint64_t)t * M.ldo + r] = s;
+            } else {
+                float *o = M.out + (uint64_t)t * M.ldo + r;
+                *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + s : s;
+            }
         }
     }
 }
@@ -541,7 +631,14 @@ static __device__ __forceinline__ void decode_chunk(const uint8_t *__restrict__ 
 template <int FMT, int NT>
 __global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
 {
+    __shared__ float rsc[QGPU_MAX_B];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    if (args.rss) {
+        RmsPart rp;
+        rms_load(args, wv, 4, lane, rp);
+        rms_reduce(args, wv, 4, lane, rp, rsc);
+        __syncthreads();
+    }
     const uint32_t grp = blockIdx.x;                  // flat row-group (8 rows) index
     int k = 0;
     while (k + 1 < args.n_mat && grp >= args.m[k + 1].tile0) k++;
@@ -611,7 +708,8 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
             if (row < M.row_lo) continue;
             for (int t = 0; t < NT && t < args.ntok; t++) {
                 float *o = M.out + (uint64_t)t * M.ldo + row;
-                *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + acc[r][t] : acc[r][t];
+                const float v = args.rss ? acc[r][t] * rsc[t] : acc[r][t];
+                *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + v : v;
             }
         }
 }
@@ -619,14 +717,34 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
 // ---------------------------------------------------------------- launchers
 // Validates an activation transform for n rows of ne0 and launches its prep
 // kernel: digit planes into the workspace when `digits`, fp32 rows into xout.
-static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits)
+// defer: single-segment RMSNORM is prepared as x*w plus per-super-block sums of
+// squares (ws_rss) for the GEMV to apply the row factor; *deferred tells the caller.
+static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits, bool defer = false,
+                    bool *deferred = nullptr)
 {
+    if (deferred) *deferred = false;
     if (!act || !act->x || n < 1 || n > QGPU_MAX_B) return QGPU_E_ARG;
     if (ne0 % 256 || (digits && ne0 > MAX_K)) return QGPU_E_RANGE;
     ActDev d = {};
     d.x = act->x; d.y = act->y; d.w = act->w; d.w2 = act->w2; d.xout = act->xout;
     d.ldx = act->ldx; d.ldy = act->ldy; d.ldxo = act->ldxo; d.eps = act->eps; d.ntok = n; d.digits = digits;
     const bool rows = n > 1;
+    const bool single = act->kind == QGPU_ACT_RMSNORM && (!act->seg || act->seg == ne0);
+    if (act->n_part < 0 || act->n_part > 8) return QGPU_E_ARG;
+    if ((act->n_part || act->xnew) && !(single && defer)) return QGPU_E_ARG;   // deferred RMSNORM only
+    if (act->n_part && (!act->part || (rows && act->ldp < ne0))) return QGPU_E_ARG;
+    if (act->xnew && rows && act->ldxn < ne0) return QGPU_E_ARG;
+    if (single && defer) {
+        if (!act->w || (rows && act->ldx < ne0) || (act->xout && rows && act->ldxo < ne0)) return QGPU_E_ARG;
+        d.part = act->part; d.ldp = act->ldp; d.pstride = (uint64_t)n * act->ldp; d.n_part = act->n_part;
+        d.xnew = act->xnew; d.ldxn = act->ldxn; d.rss = ws_rss(); d.nsb = (int)(ne0 / 256);
+        const dim3 grid((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1));
+        hipLaunchKernelGGL(k_prep_act<ACT_RMS_DEFER>, grid, dim3(256), 0, qg::stream, d, (uint8_t *)qg::ws,
+                           (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES));
+        QG_LAUNCH_CHECK();
+        if (deferred) *deferred = true;
+        return QGPU_OK;
+    }
     if (act->xout && rows && act->ldxo < ne0) return QGPU_E_ARG;
     uint64_t wx = ne0;                                    // columns read from x
     switch (act->kind) {
@@ -669,11 +787,16 @@ static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits)
 // digit planes already in the workspace; the other formats read fp32 rows x.
 static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x, uint64_t ldx,
                         int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
-                        const uint64_t *r1s)
+                        const uint64_t *r1s, int ks, float eps, bool deferred)
 {
     const qgpu_tensor *W0 = Ws[idx[0]];
     GemvArgs A = {};
     A.n_mat = cnt; A.ntok = n; A.flags = flags; A.x = x; A.ldx = ldx; A.ne0 = W0->ne0;
+    A.ks = ks;
+    A.pstride = (uint64_t)n * ldos[idx[0]];
+    if (deferred) {
+        A.rss = ws_rss(); A.rss_nsb = (int)(W0->ne0 / 256); A.rss_inv_n = 1.0f / (float)W0->ne0; A.eps = eps;
+    }
     A.nsb = (int)(W0->ne0 / 256);
     const bool iq4 = W0->type == T_IQ4_XS;
     const uint32_t per = iq4 ? IQ4_TILE_ROWS : 8;
@@ -708,15 +831,19 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
             const char *e = getenv("QGPU_GEMV_NW");
             force_nw = e ? atoi(e) : 0;
         }
-        int nw = tiles <= 512 ? 8 : 4;
+        int nw = (ks == 1 && tiles <= 512) ? 8 : 4;
         if (force_nw == 1 || force_nw == 2 || force_nw == 4 || force_nw == 8) nw = force_nw;
-        while (nw > 1 && A.nsb < nw) nw >>= 1;              // no idle waves on short K
-#define IQ4_GO(NA_, NW_) hipLaunchKernelGGL((k_gemv_iq4<NA_, NW_>), dim3(tiles), dim3(64 * NW_), 0, qg::stream, A)
-        if (na == 1) {
-            if (nw == 1) IQ4_GO(1, 1); else if (nw == 2) IQ4_GO(1, 2); else if (nw == 4) IQ4_GO(1, 4); else IQ4_GO(1, 8);
-        } else {
-            if (nw == 1) IQ4_GO(2, 1); else if (nw == 2) IQ4_GO(2, 2); else if (nw == 4) IQ4_GO(2, 4); else IQ4_GO(2, 8);
-        }
+        while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
+        if (A.rss && nw < 4) nw = 4;                        // row factors: <= 2 tokens per wave
+        const int mode = (A.rss ? IQ4_RMS : 0) | (ks > 1 ? IQ4_SPLIT : 0);
+#define IQ4_GO(NA_, NW_, M_) hipLaunchKernelGGL((k_gemv_iq4<NA_, NW_, M_>), dim3(tiles * ks), dim3(64 * NW_), 0, qg::stream, A)
+#define IQ4_NW(NA_, M_) do { if (nw == 1) IQ4_GO(NA_, 1, M_); else if (nw == 2) IQ4_GO(NA_, 2, M_); \
+                             else if (nw == 4) IQ4_GO(NA_, 4, M_); else IQ4_GO(NA_, 8, M_); } while (0)
+#define IQ4_MODE(NA_) do { if (mode == 0) IQ4_NW(NA_, 0); else if (mode == IQ4_RMS) IQ4_NW(NA_, IQ4_RMS); \
+                           else if (mode == IQ4_SPLIT) IQ4_NW(NA_, IQ4_SPLIT); else IQ4_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
+        if (na == 1) IQ4_MODE(1); else IQ4_MODE(2);
+#undef IQ4_MODE
+#undef IQ4_NW
 #undef IQ4_GO
         QG_LAUNCH_CHECK();
         return QGPU_OK;
@@ -745,7 +872,7 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
 
 // act == NULL: IQ4_XS matrices only, on the digit planes of the last prepare.
 static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n, float *const *outs,
-                      const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s)
+                      const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s, int ks = 1)
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
@@ -759,8 +886,10 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *a
         if (r0s && (r0s[j] > r1s[j] || r1s[j] > Ws[j]->ne1)) return QGPU_E_ARG;
         if (Ws[j]->type == T_IQ4_XS) any_iq4 = true; else any_valu = true;
     }
+    if (ks < 1 || ks > 8 || (ks > 1 && (n_mat != 1 || any_valu || r0s || (int)(ne0 / 256) < ks))) return QGPU_E_ARG;
     const float *xv = nullptr;                              // fp32 rows for the non-IQ4_XS kernels
     uint64_t ldxv = ne0;
+    bool deferred = false;
     if (!act) {
         if (any_valu) return QGPU_E_TYPE;
     } else {
@@ -773,10 +902,11 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *a
         }
         if (any_iq4 || xform) {
             if (!any_iq4 && ne0 % 256) return QGPU_E_RANGE;
-            rc = prep_act(act, n, ne0, any_iq4 ? 1 : 0);
+            rc = prep_act(act, n, ne0, any_iq4 ? 1 : 0, ne0 <= 64 * 256, &deferred);    // row factors: <= 64 sums
             if (rc) return rc;
         }
     }
+    const float eps = act ? act->eps : 0.0f;
     // group matrices of the same format (one launch per group)
     int done[QGPU_MAX_MULTI] = {0};
     for (int j = 0; j < n_mat; j++) {
@@ -784,7 +914,7 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *a
         int idx[QGPU_MAX_MULTI], cnt = 0;
         for (int i = j; i < n_mat; i++)
             if (!done[i] && Ws[i]->type == Ws[j]->type) { idx[cnt++] = i; done[i] = 1; }
-        rc = launch_group(Ws, idx, cnt, xv, ldxv, n, outs, ldos, flags, r0s, r1s);
+        rc = launch_group(Ws, idx, cnt, xv, ldxv, n, outs, ldos, flags, r0s, r1s, ks, eps, deferred);
         if (rc) return rc;
     }
     return QGPU_OK;
@@ -820,6 +950,55 @@ extern "C" int qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, cons
 {
     if (!act) return QGPU_E_ARG;
     return gemv_multi(Ws, n_mat, act, n, outs, ldos, flags, nullptr, nullptr);
+}
+
+extern "C" int qgpu_gemv_act_split(const qgpu_tensor *W, const qgpu_act *act, int n, float *part, uint64_t ldp,
+                                   int ks)
+{
+    if (!act || !W || !part || W->type != T_IQ4_XS) return QGPU_E_ARG;
+    if (n > 1 && ldp < W->ne1) return QGPU_E_ARG;
+    if (ks == 1) return gemv_multi(&W, 1, act, n, &part, &ldp, 0, nullptr, nullptr, 1);
+    return gemv_multi(&W, 1, act, n, &part, &ldp, 0, nullptr, nullptr, ks);
+}
+
+// Splits narrow IQ4_XS matrices so that the blocks (tiles x ks, 4 waves each)
+// cover the compute units about 4-5 times; measured on MI355X: 5120 x 17408
+// runs best at ks 4, 5120 x 6144 at ks 2..4 (a single-pass grid of 320 tiles
+// leaves 1.6x more work on the CUs that get two tiles).
+extern "C" int qgpu_gemv_split_ks(const qgpu_tensor *W)
+{
+    if (!W || W->type != T_IQ4_XS) return 1;
+    const uint64_t tiles = (W->ne1 + IQ4_TILE_ROWS - 1) / IQ4_TILE_ROWS, nsb = W->ne0 / 256;
+    if (tiles > 640) return 1;
+    int ks = (int)(1280 / tiles);
+    if (ks > 8) ks = 8;
+    while (ks > 1 && (uint64_t)ks * 4 > nsb) ks--;          // at least 4 super-blocks per block
+    return ks < 1 ? 1 : ks;
+}
+
+__global__ void k_add_partials(float *__restrict__ y, uint64_t ldy, const float *__restrict__ x, uint64_t ldx,
+                               const float *__restrict__ part, uint64_t ldp, uint64_t pstride, int n_part,
+                               uint64_t n)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int r = blockIdx.y;
+    if (i >= n) return;
+    float ps = part[(uint64_t)r * ldp + i];
+    for (int q = 1; q < n_part; q++) ps += part[(uint64_t)q * pstride + (uint64_t)r * ldp + i];
+    y[(uint64_t)r * ldy + i] = x[(uint64_t)r * ldx + i] + ps;
+}
+
+extern "C" int qgpu_add_partials(float *y, uint64_t ldy, const float *x, uint64_t ldx, const float *part,
+                                 uint64_t ldp, int n_part, uint64_t n, int rows)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!y || !x || !part || n_part < 1 || n_part > 8 || rows < 1 || rows > QGPU_MAX_B || !n) return QGPU_E_ARG;
+    if (rows > 1 && (ldy < n || ldx < n || ldp < n)) return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_add_partials, dim3((unsigned)((n + 255) / 256), (unsigned)rows), dim3(256), 0, qg::stream,
+                       y, ldy, x, ldx, part, ldp, (uint64_t)rows * ldp, n_part, n);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
 }
 
 extern "C" int qgpu_gemv_prepare(const float *x, uint64_t ldx, int n, uint64_t ne0)

@@ -47,6 +47,11 @@ struct qwen_gpu {
           *mtp_h, *mx, *cat;
     uint64_t SQ, A, conv_elems, ssm_elems, kvrow;
     int cur, cur_base;
+    /* K-split residual GEMVs leave partial planes (part, [ks][B][n_embd]) that the
+     * next RMSNorm of that residual adds in (or materialize() when none follows) */
+    float *part, *pend;
+    int pend_ks;
+    uint32_t pend_B;
     void **allocs;
     size_t n_allocs, cap_allocs;
     qgpu_tensor **tensors;
@@ -328,7 +333,7 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     AL(g->bbeta, MAXB * (uint64_t)d->n_v_heads + 4); AL(g->balpha, MAXB * (uint64_t)d->n_v_heads + 4);
     AL(g->bffn, MAXB * F); AL(g->battn, MAXB * g->A); AL(g->xq, MAXB * (uint64_t)d->conv_dim);
     AL(g->h_save, MAXB * E); AL(g->logits_b, MAXB * V); AL(g->logits1, V); AL(g->mtp_h, E);
-    AL(g->mx, MAXB * E); AL(g->cat, MAXB * 2 * E);
+    AL(g->mx, MAXB * E); AL(g->cat, MAXB * 2 * E); AL(g->part, 8 * MAXB * E);
 #undef AL
     /* RoPE tables with the reference's own expressions (model.c:186-201) */
     const uint32_t half = c->rope_dim_count / 2;
@@ -427,13 +432,57 @@ static qgpu_act act_norm(const float *x, uint64_t ldx, const float *w, float eps
     return a;
 }
 
+/* adds the pending partial planes into their residual (in place) */
+static void materialize(qwen_model_t *m)
+{
+    qwen_gpu_t *g = m->gpu;
+    if (!g->pend_ks) return;
+    const uint64_t E = m->dims.n_embd;
+    K(qgpu_add_partials(g->pend, E, g->pend, E, g->part, E, g->pend_ks, E, (int)g->pend_B));
+    g->pend_ks = 0;
+    g->pend = NULL;
+}
+
+/* RMSNorm of residual R as a GEMV input; pending partial planes of R are added
+ * in (and written back to R) by the same preparation kernel */
+static qgpu_act act_norm_res(qwen_model_t *m, float *R, const float *w, float *xout)
+{
+    qwen_gpu_t *g = m->gpu;
+    const uint64_t E = m->dims.n_embd;
+    if (g->pend_ks && g->pend != R) materialize(m);
+    qgpu_act a = act_norm(R, E, w, m->cfg.rms_norm_eps, xout, E);
+    if (g->pend_ks) {
+        a.part = g->part; a.ldp = E; a.n_part = g->pend_ks; a.xnew = R; a.ldxn = E;
+        g->pend_ks = 0;
+        g->pend = NULL;
+    }
+    return a;
+}
+
+/* R += W v (reference residual adds, model.c:466,483,942): narrow matrices run
+ * K-split and leave their partial planes pending on R */
+static void residual_gemv(qwen_model_t *m, const qgpu_tensor *W, const qgpu_act *act, uint32_t B, float *R)
+{
+    qwen_gpu_t *g = m->gpu;
+    const uint64_t E = m->dims.n_embd;
+    materialize(m);
+    const int ks = qgpu_gemv_split_ks(W);
+    if (ks > 1) {
+        K(qgpu_gemv_act_split(W, act, (int)B, g->part, E, ks));
+        g->pend = R; g->pend_ks = ks; g->pend_B = B;
+    } else {
+        K(qgpu_gemv_act_batch(&W, 1, act, (int)B, &R, &E, QGPU_GEMV_ACCUM));
+    }
+}
+
 static void ffn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B)
 {
     qwen_gpu_t *g = m->gpu;
     const uint64_t E = m->dims.n_embd, F = m->dims.n_ff;
     const float eps = m->cfg.rms_norm_eps;
     /* post-attention RMSNorm -> gate/up (model.c:469-476) */
-    const qgpu_act an = act_norm(R, E, D->post_norm, eps, g->bxb, E);
+    (void)eps;
+    const qgpu_act an = act_norm_res(m, R, D->post_norm, g->bxb);
     const qgpu_tensor *W[2] = { D->ffn_gate, D->ffn_up };
     float *outs[2] = { g->bffn, g->bqkv };
     const uint64_t ld[2] = { F, g->SQ };
@@ -443,7 +492,7 @@ static void ffn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B)
     memset(&sm, 0, sizeof sm);
     sm.kind = QGPU_ACT_SILU_MUL; sm.x = g->bffn; sm.ldx = F; sm.y = g->bqkv; sm.ldy = g->SQ;
     sm.xout = g->bffn; sm.ldxo = F;
-    K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&D->ffn_down, 1, &sm, (int)B, &R, &E, QGPU_GEMV_ACCUM));
+    residual_gemv(m, D->ffn_down, &sm, B, R);
 }
 
 static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_t pos)
@@ -452,7 +501,7 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     const qwen_dims_t *d = &m->dims;
     const uint64_t E = d->n_embd;
     const float eps = m->cfg.rms_norm_eps;
-    const qgpu_act an = act_norm(R, E, D->attn_norm, eps, g->bxb, E);
+    const qgpu_act an = act_norm_res(m, R, D->attn_norm, g->bxb);
     const qgpu_tensor *W[3] = { D->q, D->k, D->v };
     float *outs[3] = { g->bqkv, g->bk, g->bv };
     const uint64_t ld[3] = { g->SQ, g->kvrow, g->kvrow };
@@ -461,7 +510,10 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     K(qgpu_attn_fused(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos,
                       g->rope_sin, (int)m->cfg.rope_dim_count, g->d_pos, (int)(pos + B), (int)B, (int)d->n_head,
                       (int)d->n_kv_head, (int)d->head_dim, eps, g->battn, g->A));
-    K(qgpu_gemv_batch(D->o, g->battn, g->A, (int)B, R, E, QGPU_GEMV_ACCUM));
+    qgpu_act oc;
+    memset(&oc, 0, sizeof oc);
+    oc.kind = QGPU_ACT_COPY; oc.x = g->battn; oc.ldx = g->A;
+    residual_gemv(m, D->o, &oc, B, R);
     ffn_dev(m, D, R, B);
 }
 
@@ -471,7 +523,7 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     const qwen_dims_t *d = &m->dims;
     const uint64_t E = d->n_embd, di = d->d_inner;
     const float eps = m->cfg.rms_norm_eps;
-    const qgpu_act an = act_norm(g->bx, E, D->attn_norm, eps, g->bxb, E);
+    const qgpu_act an = act_norm_res(m, g->bx, D->attn_norm, g->bxb);
     const qgpu_tensor *W[4] = { D->wqkv, D->wgate, D->beta, D->alpha };
     float *outs[4] = { g->bqkv, g->bz, g->bbeta, g->balpha };
     const uint64_t ld[4] = { g->SQ, di, d->n_v_heads, d->n_v_heads };
@@ -485,7 +537,7 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     memset(&gn, 0, sizeof gn);
     gn.kind = QGPU_ACT_GATED_NORM; gn.x = g->battn; gn.ldx = di; gn.y = g->bz; gn.ldy = di; gn.w = D->ssm_norm;
     gn.seg = d->head_v_dim; gn.eps = eps; gn.xout = g->bffn; gn.ldxo = di;
-    K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&D->ssm_out, 1, &gn, (int)B, &g->bx, &E, QGPU_GEMV_ACCUM));
+    residual_gemv(m, D->ssm_out, &gn, B, g->bx);
     ffn_dev(m, D, g->bx, B);
 }
 
@@ -503,9 +555,9 @@ static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, u
         if (g->L[il].rec) gdn_dev(m, &g->L[il], B);
         else attn_dev(m, &g->L[il], g->bx, B, pos);
     }
-    if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
-    const qgpu_act an = act_norm(g->bx, E, g->out_norm, m->cfg.rms_norm_eps, g->bxb, E);
+    const qgpu_act an = act_norm_res(m, g->bx, g->out_norm, g->bxb);
     K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
+    if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
     g->cur_base = g->cur;
     g->cur = (g->cur + (int)B) % NSLOT;
     K(qgpu_set_i32(g->d_cur, g->cur));
@@ -526,11 +578,13 @@ static void mtp_dev(qwen_model_t *m, const uint32_t *d_tokens, const float *h, u
     cat.y = h; cat.ldy = E; cat.w2 = g->hnorm; cat.seg = E;
     K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->eh_proj, 1, &cat, (int)B, &g->mx, &E, 0));
     attn_dev(m, &g->mtp, g->mx, B, pos);
-    K(qgpu_copy(g->mtp_h, g->mx + (B - 1) * E, E * sizeof(float)));
     if (d_logits) {
-        const qgpu_act an = act_norm(g->mx, E, g->shnorm, eps, g->bxb, E);
+        const qgpu_act an = act_norm_res(m, g->mx, g->shnorm, g->bxb);
         K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
+    } else {
+        materialize(m);
     }
+    K(qgpu_copy(g->mtp_h, g->mx + (B - 1) * E, E * sizeof(float)));
 }
 
 /* ------------------------------------------------------------------ reference API */
@@ -578,6 +632,8 @@ void model_reset(qwen_model_t *m)
         K(qgpu_memset(D->ssm_ring, 0, NSLOT * g->ssm_elems * sizeof(float)));
     }
     g->cur = g->cur_base = 0;
+    g->pend_ks = 0;
+    g->pend = NULL;
     K(qgpu_set_i32(g->d_cur, 0));
     K(qgpu_set_i32(g->d_pos, 0));
     K(qgpu_sync());
@@ -642,6 +698,7 @@ void attention_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool, uint32_t po
     K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
     K(qgpu_set_i32(g->d_pos, (int)pos));
     attn_dev(m, D, g->bx, 1, pos);
+    materialize(m);
     K(qgpu_memcpy_d2h(m->x, g->bx, m->dims.n_embd * sizeof(float)));
 }
 
@@ -652,6 +709,7 @@ void gdn_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool)
     K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
     glayer_t *D = &g->L[L - m->layers];
     gdn_dev(m, D, 1);
+    materialize(m);
     /* the reference updates this layer's state in place (model.c:640-661): copy
      * the new state (slot cur+1) over the current slot so other layers keep theirs */
     const int nxt = (g->cur + 1) % NSLOT;

@@ -36,7 +36,8 @@ class Act(ctypes.Structure):
     """qgpu_act (include/qgpu.h): activation transform fused into the GEMV input preparation."""
     _fields_ = [("kind", ctypes.c_int), ("x", F32P), ("ldx", ctypes.c_uint64), ("y", F32P), ("ldy", ctypes.c_uint64),
                 ("w", F32P), ("w2", F32P), ("seg", ctypes.c_uint64), ("eps", ctypes.c_float), ("xout", F32P),
-                ("ldxo", ctypes.c_uint64)]
+                ("ldxo", ctypes.c_uint64), ("part", F32P), ("ldp", ctypes.c_uint64), ("n_part", ctypes.c_int),
+                ("xnew", F32P), ("ldxn", ctypes.c_uint64)]
 
 
 ACT_COPY, ACT_RMSNORM, ACT_SILU_MUL, ACT_GATED_NORM = 0, 1, 2, 3
@@ -278,6 +279,9 @@ class GpuLib:
             "qgpu_gemv_act_batch": [ctypes.POINTER(vp), i32, ctypes.POINTER(Act), i32, ctypes.POINTER(F32P),
                                     ctypes.POINTER(u64), i32],
             "qgpu_act_prepare": [ctypes.POINTER(Act), i32, u64],
+            "qgpu_gemv_act_split": [vp, ctypes.POINTER(Act), i32, F32P, u64, i32],
+            "qgpu_gemv_split_ks": [vp],
+            "qgpu_add_partials": [F32P, u64, F32P, u64, F32P, u64, i32, u64, i32],
             "qgpu_spec_accept": [U32P, U32P, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), i32, U32P],
         }
         for name, args in sigs.items():

@@ -2,7 +2,12 @@
 (qgpu_gemv_act_batch): RMSNorm, two-segment RMSNorm (MTP input), SiLU*up and
 per-head gated RMSNorm, against the oracle's ops (pinned to the reference)
 followed by the oracle's GEMV.  Bars: GEMV outputs within 1e-3 normwise; the
-transformed fp32 rows (xout) within 1e-5."""
+transformed fp32 rows (xout) within 1e-5.  Single-segment RMSNorm applies its
+row factor to the GEMV output, so its xout holds x * w.
+
+Also the K-split GEMV of narrow outputs: partial planes (qgpu_gemv_act_split)
+summed by qgpu_add_partials or by the next RMSNorm preparation, which writes
+the summed residual back in place."""
 import ctypes
 
 import numpy as np
@@ -59,9 +64,11 @@ def test_act_transform_gemv(gpu, t, B, kind):
     xb, yb, wb, w2b = gpu.put(x), gpu.put(y), gpu.put(w), gpu.put(w2)
     a = pyqwen.Act()
     a.x, a.ldx, a.eps = xb.f32(), ne0, EPS
+    xo_ref = None
     if kind == "rmsnorm":
         a.kind, a.w = pyqwen.ACT_RMSNORM, wb.f32()
         xin = np.stack([o_rmsnorm(x[b], w) for b in range(B)])
+        xo_ref = x * w                                 # row factor applied to the GEMV output
     elif kind == "rmsnorm2":                          # [x | y] halves, each with its own row norm
         h = ne0 // 2
         xs, ys = np.ascontiguousarray(x[:, :h]), np.ascontiguousarray(y[:, :h])
@@ -81,7 +88,7 @@ def test_act_transform_gemv(gpu, t, B, kind):
                 sl = slice(hh * hd, (hh + 1) * hd)
                 xin[b, sl] = o_rmsnorm(x[b, sl], w[:hd]) * o_silu(y[b, sl])
     out, xo = run(gpu, t, W, ne0, ne1, a, B, (xb, yb, wb, w2b))
-    ex = rel_err(xo, xin)
+    ex = rel_err(xo, xin if xo_ref is None else xo_ref)
     ref = O.gemv(t, W, ne0, ne1, xin, B)
     eo = rel_err(out, ref)
     print(f"  xout {ex:.2e}  gemv {eo:.2e}", flush=True)
@@ -105,4 +112,84 @@ def test_act_rejects_bad_args(gpu):
     assert gpu.L.qgpu_gemv_act_batch(Ws, 1, ctypes.byref(a), 2, outs, lds, 0) != 0
     a.kind = 9
     assert gpu.L.qgpu_gemv_act_batch(Ws, 1, ctypes.byref(a), 2, outs, lds, 0) != 0
+    gpu.sync()
+
+
+def _split(gpu, T, a, B, ne1, ks):
+    pb = gpu.buf(ks * B * ne1 * 4)
+    gpu.ok(gpu.L.qgpu_gemv_act_split(T.h, ctypes.byref(a), B, pb.f32(), ne1, ks))
+    return pb, pb.download(np.float32).reshape(ks, B, ne1)
+
+
+@pytest.mark.parametrize("B", [1, 4, 6])
+def test_split_gemv_partials(gpu, B):
+    """K-split planes of a narrow IQ4_XS GEMV sum to the oracle GEMV; qgpu_add_partials adds them in order."""
+    print(f"\n[split] B={B}", flush=True)
+    host = host_lib()
+    ne0, ne1 = 5120, 320
+    W = host.synth_matrix(23, ne0, ne1, 21, 4, 0.02)
+    T = gpu.tensor(W, 23, ne0, ne1)
+    ks = gpu.L.qgpu_gemv_split_ks(T.h)
+    assert 2 <= ks <= 8
+    x = np.random.default_rng(B).standard_normal((B, ne0)).astype(np.float32)
+    xb = gpu.put(x)
+    a = pyqwen.Act()
+    a.kind, a.x, a.ldx = pyqwen.ACT_COPY, xb.f32(), ne0
+    pb, planes = _split(gpu, T, a, B, ne1, ks)
+    ref = O.gemv(23, W, ne0, ne1, x, B)
+    e = rel_err(planes.sum(0), ref)
+    print(f"  ks={ks} rel err {e:.2e}", flush=True)
+    assert e < 2e-5
+    # y = r + (p0 + p1 + ...), in place
+    r = np.random.default_rng(B + 50).standard_normal((B, ne1)).astype(np.float32)
+    rb = gpu.put(r)
+    gpu.ok(gpu.L.qgpu_add_partials(rb.f32(), ne1, rb.f32(), ne1, pb.f32(), ne1, ks, ne1, B))
+    ps = planes[0].copy()
+    for q in range(1, ks):
+        ps = (ps + planes[q]).astype(np.float32)
+    assert np.array_equal(rb.download(np.float32).reshape(B, ne1), (r + ps).astype(np.float32))
+
+
+@pytest.mark.parametrize("B", [1, 4, 7])
+def test_rmsnorm_consumes_partials(gpu, B):
+    """The residual's pending partial planes are added by the next RMSNorm preparation (written back in
+    place) and the GEMV that follows sees rmsnorm(R + sum of planes)."""
+    print(f"\n[rms-partials] B={B}", flush=True)
+    host = host_lib()
+    E, n_out = 1024, 384
+    Wd = host.synth_matrix(23, 4096, E, 31, 5, 0.02)          # narrow producer: 4096 -> 1024 (64 tiles)
+    Td = gpu.tensor(Wd, 23, 4096, E)
+    Wn = host.synth_matrix(23, E, n_out, 32, 6, 0.02)          # consumer: 1024 -> 384
+    Tn = gpu.tensor(Wn, 23, E, n_out)
+    rng = np.random.default_rng(100 + B)
+    h = rng.standard_normal((B, 4096)).astype(np.float32)
+    R = (3 * rng.standard_normal((B, E))).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(E)).astype(np.float32)
+    hb, Rb, wb = gpu.put(h), gpu.put(R), gpu.put(w)
+    a = pyqwen.Act()
+    a.kind, a.x, a.ldx = pyqwen.ACT_COPY, hb.f32(), 4096
+    ks = gpu.L.qgpu_gemv_split_ks(Td.h)
+    assert ks > 1
+    pb, planes = _split(gpu, Td, a, B, E, ks)
+    ps = planes[0].copy()
+    for q in range(1, ks):
+        ps = (ps + planes[q]).astype(np.float32)
+    R_new = (R + ps).astype(np.float32)
+    an = pyqwen.Act()
+    an.kind, an.x, an.ldx, an.w, an.eps = pyqwen.ACT_RMSNORM, Rb.f32(), E, wb.f32(), EPS
+    an.part, an.ldp, an.n_part, an.xnew, an.ldxn = pb.f32(), E, ks, Rb.f32(), E
+    ob = gpu.buf(B * n_out * 4)
+    Ws = (ctypes.c_void_p * 1)(Tn.h)
+    outs = (pyqwen.F32P * 1)(ob.f32())
+    lds = (ctypes.c_uint64 * 1)(n_out)
+    gpu.ok(gpu.L.qgpu_gemv_act_batch(Ws, 1, ctypes.byref(an), B, outs, lds, 0))
+    assert np.array_equal(Rb.download(np.float32).reshape(B, E), R_new)
+    xin = np.stack([o_rmsnorm(R_new[b], w) for b in range(B)])
+    e = rel_err(ob.download(np.float32).reshape(B, n_out), O.gemv(23, Wn, E, n_out, xin, B))
+    print(f"  ks={ks} gemv rel err {e:.2e}", flush=True)
+    assert e < 1e-4
+    # partial planes are rejected by every transform but single-segment RMSNorm
+    a2 = pyqwen.Act()
+    a2.kind, a2.x, a2.ldx, a2.part, a2.ldp, a2.n_part = pyqwen.ACT_COPY, Rb.f32(), E, pb.f32(), E, ks
+    assert gpu.L.qgpu_gemv_act_batch(Ws, 1, ctypes.byref(a2), B, outs, lds, 0) != 0
     gpu.sync()
