@@ -6,7 +6,7 @@
 //                     written to the cache at position pos + b.
 //  qgpu_attn_decode : softmax(q K^T / sqrt(hd)) V over positions t <= pos + b,
 //                     times sigmoid(gate).  Flash-decoding: one block per
-//                     (kv head, 32-position chunk) serves every query head of
+//                     (kv head, 64-position chunk) serves every query head of
 //                     the group and every token of the batch (each K/V row is
 //                     read once per chunk), then a combine pass merges chunks.
 // Positions come from device memory (*pos_dev) so the launch sequence can be
@@ -14,8 +14,9 @@
 #include "qgpu_internal.h"
 
 #define ATT_HD   256
-#define ATT_CS   32
-#define ATT_MAXQ 64             // query heads per kv head x batch
+#define ATT_CS   64             // positions per chunk block
+#define ATT_MAXQ 64             // row stride of the chunk partials
+#define ATT_MAXR 48             // query rows (heads per kv head x batch) one chunk block serves
 
 namespace qg {
 void *ws_attn = nullptr;
@@ -61,20 +62,24 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
 }
 
 // Flash-decoding chunk kernel.  Block (g, c): kv head g, positions
-// [c*ATT_CS, c*ATT_CS + ATT_CS).  Serves the QH = (n_head/n_kv) * B query rows
-// of the group: row r = b * per + (h - g*per).
+// [c*ATT_CS, c*ATT_CS + ATT_CS), 8 waves.  Serves the QH = (n_head/n_kv) * B
+// query rows of the group (row r = b * per + (h - g*per)); wave w owns rows
+// w, w + 8, ... (<= ATT_RW of them).
 //   FUSED = 1: the block also applies the per-head q/k RMSNorm and RoPE
 //              (reference model.c:318-406): q rows are prepared in LDS (each
 //              block recomputes them), the new k/v rows of positions pos..pos+B-1
 //              that fall in this chunk are prepared here and written to the caches
 //              (no other block reads them in this launch).
 //   FUSED = 0: q rows already prepared, caches already hold every position.
-// Scores: thread (row group rg = tid/32, position p = tid%32) over rows
-// rg + 8j, K chunk staged row-major in LDS (float4 reads, conflict-free with
-// the 260-float row stride); P.V: thread d over all rows.
+// Every global load is issued first (K and V rows of the chunk, q rows).
+// Scores: lane = position, K rows in LDS, q values broadcast from LDS, one
+// running fp32 sum per row over d = 0..255.  Softmax statistics of a row are a
+// reduction over the 64 lanes of one wave.  P.V: lane = 4 output dims, V rows
+// (written over the K rows once the scores are done) and P from LDS.
 // partials: pml [n_kv][nchunk][ATT_MAXQ][2] (m, l), po [n_kv][nchunk][ATT_MAXQ][ATT_HD]
-#define ATT_LD   260          // padded LDS row stride (floats)
-#define ATT_NJ   (ATT_MAXQ / 8)
+#define ATT_KLD  260          // K row stride in LDS (floats)
+#define ATT_NWV  8            // waves per chunk block
+#define ATT_RW   (ATT_MAXR / ATT_NWV)
 
 struct AttnArgs {
     const float *q; uint64_t ldq;
@@ -99,32 +104,35 @@ static __device__ __forceinline__ float wsum64(float v)
     return v;
 }
 
-#define ATT_NQ (ATT_MAXQ / 4)   // q rows per wave
+static __device__ __forceinline__ float wmax64(float v)
+{
+#pragma unroll
+    for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
 
 template <int FUSED>
-__global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
+__global__ __launch_bounds__(ATT_NWV * 64) void k_attn_chunk(const AttnArgs p)
 {
-    __shared__ float Ql[ATT_MAXQ][ATT_LD];
-    __shared__ float KL[ATT_CS][ATT_LD];
-    __shared__ float VL[ATT_CS][ATT_LD];
-    __shared__ float Pl[ATT_MAXQ][ATT_CS];
+    __shared__ float KV[ATT_CS * ATT_KLD];        // K rows (stride ATT_KLD), then V rows (stride ATT_HD)
+    __shared__ float Qs[ATT_MAXR][ATT_HD];
+    __shared__ float Ps[ATT_MAXR][ATT_CS];
     const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int per = p.n_head / p.n_kv, QH = per * p.B;
     const int pos0 = *p.pos_dev, tmax = pos0 + p.B - 1, t0 = c * ATT_CS;
     float *ml = p.pml + ((uint64_t)g * p.nchunk + c) * ATT_MAXQ * 2;
     float *o = p.po + ((uint64_t)g * p.nchunk + c) * ATT_MAXQ * ATT_HD;
     if (t0 > tmax) {                              // chunk beyond the context: empty partial
-        for (int qi = tid; qi < QH; qi += 256) { ml[2 * qi] = -INFINITY; ml[2 * qi + 1] = 0.0f; }
+        for (int qi = tid; qi < QH; qi += ATT_NWV * 64) { ml[2 * qi] = -INFINITY; ml[2 * qi + 1] = 0.0f; }
         return;
     }
     const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD;
     const int nt = min(ATT_CS, tmax - t0 + 1);    // positions of this chunk that exist
-    // ---- every global load first: K and V rows of the chunk (row pp = wv + 4i, lane = float4),
-    //      q rows of the group (row r = wv + 4i), norm weights
-    float4 kr[ATT_CS / 4], vr[ATT_CS / 4], qr[ATT_NQ];
+    // ---- every global load first: K and V rows pp = wv + 8i (lane = float4), q rows r = wv + 8i
+    float4 kr[ATT_CS / ATT_NWV], vr[ATT_CS / ATT_NWV], qr[ATT_RW];
 #pragma unroll
-    for (int i = 0; i < ATT_CS / 4; i++) {
-        const int pp = wv + 4 * i, t = t0 + pp;
+    for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
+        const int pp = wv + ATT_NWV * i, t = t0 + pp;
         kr[i] = vr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (pp < nt) {
             if (FUSED && t >= pos0) {             // new row: raw k/v of token t - pos0
@@ -139,8 +147,8 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
         }
     }
 #pragma unroll
-    for (int i = 0; i < ATT_NQ; i++) {
-        const int r = wv + 4 * i;
+    for (int i = 0; i < ATT_RW; i++) {
+        const int r = wv + ATT_NWV * i;
         qr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (r < QH) {
             const int b = r / per, h = g * per + r % per;
@@ -154,39 +162,38 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
     }
     // ---- to LDS (per-head RMSNorm of q and of the new k rows on the way)
 #pragma unroll
-    for (int i = 0; i < ATT_CS / 4; i++) {
-        const int pp = wv + 4 * i, t = t0 + pp;
+    for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
+        const int pp = wv + ATT_NWV * i, t = t0 + pp;
         float4 kv = kr[i];
         if (FUSED && pp < nt && t >= pos0) {
             const float ss = wsum64(kv.x * kv.x + kv.y * kv.y + kv.z * kv.z + kv.w * kv.w);
             kv = norm4(kv, kw, 1.0f / sqrtf(ss / (float)ATT_HD + p.eps));
         }
-        *(float4 *)&KL[pp][4 * lane] = kv;
-        *(float4 *)&VL[pp][4 * lane] = vr[i];
+        *(float4 *)&KV[pp * ATT_KLD + 4 * lane] = kv;
     }
 #pragma unroll
-    for (int i = 0; i < ATT_NQ; i++) {
-        const int r = wv + 4 * i;
+    for (int i = 0; i < ATT_RW; i++) {
+        const int r = wv + ATT_NWV * i;
         if (r >= QH) break;                       // wave-uniform
         float4 qv = qr[i];
         if (FUSED) {
             const float ss = wsum64(qv.x * qv.x + qv.y * qv.y + qv.z * qv.z + qv.w * qv.w);
             qv = norm4(qv, qw, 1.0f / sqrtf(ss / (float)ATT_HD + p.eps));
         }
-        *(float4 *)&Ql[r][4 * lane] = qv;
+        *(float4 *)&Qs[r][4 * lane] = qv;
     }
     __syncthreads();
     if (FUSED) {
         // NeoX RoPE on (i, i + half) at position pos0 + b: q rows and the new k rows of this chunk
-        for (int e = tid; e < (QH + p.B) * p.half; e += 256) {
+        for (int e = tid; e < (QH + p.B) * p.half; e += ATT_NWV * 64) {
             const int r = e / p.half, i = e % p.half;
             float *x;
             int t;
-            if (r < QH) { x = Ql[r]; t = pos0 + r / per; }
+            if (r < QH) { x = Qs[r]; t = pos0 + r / per; }
             else {
                 t = pos0 + (r - QH);
                 if (t < t0 || t >= t0 + ATT_CS) continue;
-                x = KL[t - t0];
+                x = &KV[(t - t0) * ATT_KLD];
             }
             const float cs = p.rcos[(uint64_t)t * p.half + i], sn = p.rsin[(uint64_t)t * p.half + i];
             const float v0 = x[i], v1 = x[i + p.half];
@@ -195,66 +202,79 @@ __global__ __launch_bounds__(256) void k_attn_chunk(const AttnArgs p)
         }
         __syncthreads();
         // the new rows go to the caches (no other block of this launch reads them)
-        for (int e = tid; e < p.B * 64; e += 256) {
+        for (int e = tid; e < p.B * 64; e += ATT_NWV * 64) {
             const int b = e >> 6, d4 = e & 63, t = pos0 + b;
             if (t < t0 || t >= t0 + ATT_CS) continue;
             const uint64_t row = (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * d4;
-            *(float4 *)(p.kc + row) = *(const float4 *)&KL[t - t0][4 * d4];
-            *(float4 *)(p.vc + row) = *(const float4 *)&VL[t - t0][4 * d4];
+            *(float4 *)(p.kc + row) = *(const float4 *)&KV[(t - t0) * ATT_KLD + 4 * d4];
+        }
+#pragma unroll
+        for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
+            const int pp = wv + ATT_NWV * i, t = t0 + pp;
+            if (pp < nt && t >= pos0)
+                *(float4 *)(p.vc + (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * lane) = vr[i];
         }
     }
-    // ---- scores for rows rg + 8j at position t0 + pp
-    const int rg = tid >> 5, pp = tid & 31;
-    float s[ATT_NJ];
+    // ---- scores of this wave's rows at position t0 + lane
+    const float scale = 1.0f / sqrtf((float)ATT_HD);
+    {
+        float s[ATT_RW];
 #pragma unroll
-    for (int j = 0; j < ATT_NJ; j++) s[j] = 0.0f;
-    if (pp < nt) {
-        for (int d4 = 0; d4 < 64; d4++) {
-            const float4 kq = *(const float4 *)&KL[pp][4 * d4];
+        for (int j = 0; j < ATT_RW; j++) s[j] = 0.0f;
+        const float *krow = &KV[lane * ATT_KLD];
+        for (int d4 = 0; d4 < ATT_HD / 4; d4++) {
+            const float4 kq = *(const float4 *)(krow + 4 * d4);
 #pragma unroll
-            for (int j = 0; j < ATT_NJ; j++) {
-                const int r = rg + 8 * j;
+            for (int j = 0; j < ATT_RW; j++) {
+                const int r = wv + ATT_NWV * j;
                 if (r < QH) {
-                    const float4 qv = *(const float4 *)&Ql[r][4 * d4];
+                    const float4 qv = *(const float4 *)&Qs[r][4 * d4];
                     s[j] = fmaf(qv.x, kq.x, s[j]); s[j] = fmaf(qv.y, kq.y, s[j]);
                     s[j] = fmaf(qv.z, kq.z, s[j]); s[j] = fmaf(qv.w, kq.w, s[j]);
                 }
             }
         }
+        // ---- chunk softmax statistics: a row's 64 scores are the 64 lanes of the wave
+        const int t = t0 + lane;
+#pragma unroll
+        for (int j = 0; j < ATT_RW; j++) {
+            const int r = wv + ATT_NWV * j;
+            if (r >= QH) break;                   // wave-uniform
+            const float sv = (lane < nt && t <= pos0 + r / per) ? s[j] * scale : -INFINITY;
+            const float m = wmax64(sv);
+            const float pr = m > -INFINITY ? expf(sv - m) : 0.0f;
+            const float sum = wsum64(pr);
+            Ps[r][lane] = pr;
+            if (lane == 0) { ml[2 * r] = m; ml[2 * r + 1] = sum; }
+        }
     }
-    // ---- chunk softmax statistics: row r's 32 scores are the 32 lanes of a half-wave
-    const float scale = 1.0f / sqrtf((float)ATT_HD);
+    __syncthreads();                              // scores done: the K rows may be overwritten
 #pragma unroll
-    for (int j = 0; j < ATT_NJ; j++) {
-        const int r = rg + 8 * j;
-        if (r >= QH) break;                       // uniform over the half-wave
-        const int t = t0 + pp;
-        const float sv = (pp < nt && t <= pos0 + r / per) ? s[j] * scale : -INFINITY;
-        float m = sv;
-#pragma unroll
-        for (int off = 16; off; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        const float pr = m > -INFINITY ? expf(sv - m) : 0.0f;
-        float sum = pr;
-#pragma unroll
-        for (int off = 16; off; off >>= 1) sum += __shfl_xor(sum, off);
-        Pl[r][pp] = pr;
-        if (pp == 0) { ml[2 * r] = m; ml[2 * r + 1] = sum; }
+    for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
+        const int pp = wv + ATT_NWV * i;
+        *(float4 *)&KV[pp * ATT_HD + 4 * lane] = vr[i];
     }
     __syncthreads();
-    // ---- P.V: thread d, rows in groups of 16
-    const int d = tid;
-    for (int r0 = 0; r0 < QH; r0 += 16) {
-        float acc[16];
+    // ---- P.V: lane = output dims 4*lane .. 4*lane+3 of this wave's rows
+    float4 acc[ATT_RW];
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[i] = 0.0f;
-        for (int q4 = 0; q4 < nt; q4++) {
-            const float vv = VL[q4][d];
+    for (int j = 0; j < ATT_RW; j++) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int pp = 0; pp < nt; pp++) {
+        const float4 vv = *(const float4 *)&KV[pp * ATT_HD + 4 * lane];
 #pragma unroll
-            for (int i = 0; i < 16; i++) acc[i] = fmaf(Pl[r0 + i < QH ? r0 + i : 0][q4], vv, acc[i]);
+        for (int j = 0; j < ATT_RW; j++) {
+            const int r = wv + ATT_NWV * j;
+            if (r < QH) {
+                const float pr = Ps[r][pp];
+                acc[j].x = fmaf(pr, vv.x, acc[j].x); acc[j].y = fmaf(pr, vv.y, acc[j].y);
+                acc[j].z = fmaf(pr, vv.z, acc[j].z); acc[j].w = fmaf(pr, vv.w, acc[j].w);
+            }
         }
+    }
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            if (r0 + i < QH) o[(uint64_t)(r0 + i) * ATT_HD + d] = acc[i];
+    for (int j = 0; j < ATT_RW; j++) {
+        const int r = wv + ATT_NWV * j;
+        if (r < QH) *(float4 *)(o + (uint64_t)r * ATT_HD + 4 * lane) = acc[j];
     }
 }
 
@@ -327,9 +347,9 @@ static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out,
     a.pml = (float *)qg::ws_attn;
     a.po = a.pml + (size_t)a.n_kv * a.nchunk * ATT_MAXQ * 2;
     if (fused)
-        hipLaunchKernelGGL(k_attn_chunk<1>, dim3(a.n_kv, a.nchunk), dim3(256), 0, qg::stream, a);
+        hipLaunchKernelGGL(k_attn_chunk<1>, dim3(a.n_kv, a.nchunk), dim3(ATT_NWV * 64), 0, qg::stream, a);
     else
-        hipLaunchKernelGGL(k_attn_chunk<0>, dim3(a.n_kv, a.nchunk), dim3(256), 0, qg::stream, a);
+        hipLaunchKernelGGL(k_attn_chunk<0>, dim3(a.n_kv, a.nchunk), dim3(ATT_NWV * 64), 0, qg::stream, a);
     QG_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_attn_combine, dim3(a.n_head, a.B), dim3(ATT_HD), 0, qg::stream, a.q, a.ldq, a.pml, a.po,
                        a.pos_dev, a.B, a.n_head, a.n_kv, a.nchunk, out, ldo);
@@ -347,7 +367,7 @@ extern "C" int qgpu_attn_decode(const float *q, uint64_t ldq, const float *kcach
     if (!q || !kcache || !vcache || !pos_dev || !out || B < 1 || n_kv < 1 || n_head % n_kv || ctx_bound < B ||
         ldq % 4 || ((uintptr_t)q & 15) || ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15))
         return QGPU_E_ARG;
-    if ((n_head / n_kv) * B > ATT_MAXQ) return QGPU_E_RANGE;
+    if ((n_head / n_kv) * B > ATT_MAXR) return QGPU_E_RANGE;
     AttnArgs a = {};
     a.q = q; a.ldq = ldq; a.kc = (float *)kcache; a.vc = (float *)vcache; a.pos_dev = pos_dev;
     a.B = B; a.n_head = n_head; a.n_kv = n_kv;
@@ -369,7 +389,7 @@ extern "C" int qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, con
         ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15) || ((uintptr_t)q_norm_w & 15) ||
         ((uintptr_t)k_norm_w & 15))
         return QGPU_E_ARG;
-    if ((n_head / n_kv) * B > ATT_MAXQ) return QGPU_E_RANGE;
+    if ((n_head / n_kv) * B > ATT_MAXR) return QGPU_E_RANGE;
     AttnArgs a = {};
     a.q = q; a.ldq = ldq; a.k = k; a.v = v; a.ldkv = ldkv; a.qw = q_norm_w; a.kw = k_norm_w;
     a.rcos = rope_cos; a.rsin = rope_sin; a.kc = kcache; a.vc = vcache; a.pos_dev = pos_dev;

@@ -132,12 +132,31 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
                                                    int n_k, int n_v, float eps, float *__restrict__ out, uint64_t ldo)
 {
     __shared__ float Yq[GDN_MAXB][GDN_HK], Yk[GDN_MAXB][GDN_HK], Yv[GDN_MAXB][GDN_RB];
+    __shared__ float Gbeta[GDN_MAXB], Gdec[GDN_MAXB];
     const int h = blockIdx.x / (GDN_HK / GDN_RB);
     const int rb = blockIdx.x % (GDN_HK / GDN_RB);
     const int tid = threadIdx.x;
     const int kh = h % n_k;                          // tiled v-head -> k-head map (model.c:565)
     const int cur = *cur_dev;
     const bool own_qk = h < n_k && rb == 0;
+    // ---- this thread's 8 state columns first: their load overlaps the conv phase
+    const int r = tid >> 4, cc = tid & 15;
+    const int j = rb * GDN_RB + r;                   // state row (v index)
+    const uint64_t hoff = (uint64_t)h * GDN_HK * GDN_HK + (uint64_t)j * GDN_HK + cc * 8;
+    const float *S0 = sring + (uint64_t)cur * sstride + hoff;
+    float S[8];
+    {
+        const float4 a = *(const float4 *)S0, b = *(const float4 *)(S0 + 4);
+        S[0] = a.x; S[1] = a.y; S[2] = a.z; S[3] = a.w; S[4] = b.x; S[5] = b.y; S[6] = b.z; S[7] = b.w;
+    }
+    // ---- per-token gates of this head: beta = sigmoid(b), decay = exp(a * softplus(alpha + dt_bias))
+    //      (model.c:572-575), by threads 0..B-1 while the state loads are in flight
+    if (tid < B) {
+        Gbeta[tid] = 1.0f / (1.0f + expf(-beta_raw[(uint64_t)tid * ldba + h]));
+        const float araw = alpha_raw[(uint64_t)tid * ldba + h] + dt_bias[h];
+        const float sp = araw > 30.0f ? araw : log1pf(expf(araw));
+        Gdec[tid] = expf(ssm_a[h] * sp);
+    }
     // ---- conv + SiLU of the 2*128 + 16 channels this block reads
     for (int e = tid; e < 2 * GDN_HK + GDN_RB; e += 256) {
         int c;
@@ -165,15 +184,6 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
     }
     __syncthreads();
     // ---- delta-rule recurrence (as k_gdn_recur), inputs from LDS
-    const int r = tid >> 4, cc = tid & 15;
-    const int j = rb * GDN_RB + r;                   // state row (v index)
-    const uint64_t hoff = (uint64_t)h * GDN_HK * GDN_HK + (uint64_t)j * GDN_HK + cc * 8;
-    const float *S0 = sring + (uint64_t)cur * sstride + hoff;
-    float S[8];
-    {
-        const float4 a = *(const float4 *)S0, b = *(const float4 *)(S0 + 4);
-        S[0] = a.x; S[1] = a.y; S[2] = a.z; S[3] = a.w; S[4] = b.x; S[5] = b.y; S[6] = b.z; S[7] = b.w;
-    }
     const float qscale = 1.0f / sqrtf((float)GDN_HK);
     const float ah = ssm_a[h], dtb = dt_bias[h];
     for (int b = 0; b < B; b++) {
@@ -203,10 +213,7 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
         kq = sum16(kq);
         sk = sum16(sk);
         sq = sum16(sq);
-        const float beta = 1.0f / (1.0f + expf(-beta_raw[(uint64_t)b * ldba + h]));
-        const float araw = alpha_raw[(uint64_t)b * ldba + h] + dtb;
-        const float sp = araw > 30.0f ? araw : log1pf(expf(araw));
-        const float decay = expf(ah * sp);
+        const float beta = Gbeta[b], decay = Gdec[b];
         const float vj = Yv[b][r];
         const float dj = (vj - decay * sk) * beta;
         if (cc == 0) out[(uint64_t)b * ldo + (uint64_t)h * GDN_HK + j] = (decay * sq + dj * kq) * qscale;
