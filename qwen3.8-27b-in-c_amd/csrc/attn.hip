@@ -111,12 +111,13 @@ static __device__ __forceinline__ float wmax64(float v)
     return v;
 }
 
-template <int FUSED>
+// RW: rows per wave, ceil(QH / 8) (1..ATT_RW): the row loops carry no branches
+template <int FUSED, int RW>
 __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_chunk(const AttnArgs p)
 {
-    __shared__ float KV[ATT_CS * ATT_KLD];        // K rows (stride ATT_KLD), then V rows (stride ATT_HD)
-    __shared__ float Qs[ATT_MAXR][ATT_HD];
+    __shared__ float Qs[ATT_MAXR][ATT_HD];       // first: its reads fit the 16-bit LDS offset field
     __shared__ float Ps[ATT_MAXR][ATT_CS];
+    __shared__ float KV[ATT_CS * ATT_KLD];        // K rows (stride ATT_KLD), then V rows (stride ATT_HD)
     const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int per = p.n_head / p.n_kv, QH = per * p.B;
     const int pos0 = *p.pos_dev, tmax = pos0 + p.B - 1, t0 = c * ATT_CS;
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_chunk(const AttnArgs p)
     const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD;
     const int nt = min(ATT_CS, tmax - t0 + 1);    // positions of this chunk that exist
     // ---- every global load first: K and V rows pp = wv + 8i (lane = float4), q rows r = wv + 8i
-    float4 kr[ATT_CS / ATT_NWV], vr[ATT_CS / ATT_NWV], qr[ATT_RW];
+    float4 kr[ATT_CS / ATT_NWV], vr[ATT_CS / ATT_NWV], qr[RW];
 #pragma unroll
     for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
         const int pp = wv + ATT_NWV * i, t = t0 + pp;
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_chunk(const AttnArgs p)
         }
     }
 #pragma unroll
-    for (int i = 0; i < ATT_RW; i++) {
+    for (int i = 0; i < RW; i++) {
         const int r = wv + ATT_NWV * i;
         qr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (r < QH) {
@@ -172,11 +173,10 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_chunk(const AttnArgs p)
         *(float4 *)&KV[pp * ATT_KLD + 4 * lane] = kv;
     }
 #pragma unroll
-    for (int i = 0; i < ATT_RW; i++) {
+    for (int i = 0; i < RW; i++) {                // rows r >= QH hold zeros (their results are not used)
         const int r = wv + ATT_NWV * i;
-        if (r >= QH) break;                       // wave-uniform
         float4 qv = qr[i];
-        if (FUSED) {
+        if (FUSED && r < QH) {
             const float ss = wsum64(qv.x * qv.x + qv.y * qv.y + qv.z * qv.z + qv.w * qv.w);
             qv = norm4(qv, qw, 1.0f / sqrtf(ss / (float)ATT_HD + p.eps));
         }
@@ -218,26 +218,26 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_chunk(const AttnArgs p)
     // ---- scores of this wave's rows at position t0 + lane
     const float scale = 1.0f / sqrtf((float)ATT_HD);
     {
-        float s[ATT_RW];
+        float s[RW];
 #pragma unroll
-        for (int j = 0; j < ATT_RW; j++) s[j] = 0.0f;
+        for (int j = 0; j < RW; j++) s[j] = 0.0f;
         const float *krow = &KV[lane * ATT_KLD];
+#pragma unroll 4
         for (int d4 = 0; d4 < ATT_HD / 4; d4++) {
             const float4 kq = *(const float4 *)(krow + 4 * d4);
+            float4 qv[RW];
 #pragma unroll
-            for (int j = 0; j < ATT_RW; j++) {
-                const int r = wv + ATT_NWV * j;
-                if (r < QH) {
-                    const float4 qv = *(const float4 *)&Qs[r][4 * d4];
-                    s[j] = fmaf(qv.x, kq.x, s[j]); s[j] = fmaf(qv.y, kq.y, s[j]);
-                    s[j] = fmaf(qv.z, kq.z, s[j]); s[j] = fmaf(qv.w, kq.w, s[j]);
-                }
+            for (int j = 0; j < RW; j++) qv[j] = *(const float4 *)&Qs[wv + ATT_NWV * j][4 * d4];
+#pragma unroll
+            for (int j = 0; j < RW; j++) {
+                s[j] = fmaf(qv[j].x, kq.x, s[j]); s[j] = fmaf(qv[j].y, kq.y, s[j]);
+                s[j] = fmaf(qv[j].z, kq.z, s[j]); s[j] = fmaf(qv[j].w, kq.w, s[j]);
             }
         }
         // ---- chunk softmax statistics: a row's 64 scores are the 64 lanes of the wave
         const int t = t0 + lane;
 #pragma unroll
-        for (int j = 0; j < ATT_RW; j++) {
+        for (int j = 0; j < RW; j++) {
             const int r = wv + ATT_NWV * j;
             if (r >= QH) break;                   // wave-uniform
             const float sv = (lane < nt && t <= pos0 + r / per) ? s[j] * scale : -INFINITY;
@@ -256,23 +256,24 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_chunk(const AttnArgs p)
     }
     __syncthreads();
     // ---- P.V: lane = output dims 4*lane .. 4*lane+3 of this wave's rows
-    float4 acc[ATT_RW];
+    float4 acc[RW];
 #pragma unroll
-    for (int j = 0; j < ATT_RW; j++) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int pp = 0; pp < nt; pp++) {
+    for (int j = 0; j < RW; j++) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // positions beyond nt have P = 0 and V rows of zeros
+#pragma unroll 4
+    for (int pp = 0; pp < ATT_CS; pp++) {
         const float4 vv = *(const float4 *)&KV[pp * ATT_HD + 4 * lane];
+        float pr[RW];
 #pragma unroll
-        for (int j = 0; j < ATT_RW; j++) {
-            const int r = wv + ATT_NWV * j;
-            if (r < QH) {
-                const float pr = Ps[r][pp];
-                acc[j].x = fmaf(pr, vv.x, acc[j].x); acc[j].y = fmaf(pr, vv.y, acc[j].y);
-                acc[j].z = fmaf(pr, vv.z, acc[j].z); acc[j].w = fmaf(pr, vv.w, acc[j].w);
-            }
+        for (int j = 0; j < RW; j++) pr[j] = Ps[wv + ATT_NWV * j][pp];
+#pragma unroll
+        for (int j = 0; j < RW; j++) {
+            acc[j].x = fmaf(pr[j], vv.x, acc[j].x); acc[j].y = fmaf(pr[j], vv.y, acc[j].y);
+            acc[j].z = fmaf(pr[j], vv.z, acc[j].z); acc[j].w = fmaf(pr[j], vv.w, acc[j].w);
         }
     }
 #pragma unroll
-    for (int j = 0; j < ATT_RW; j++) {
+    for (int j = 0; j < RW; j++) {
         const int r = wv + ATT_NWV * j;
         if (r < QH) *(float4 *)(o + (uint64_t)r * ATT_HD + 4 * lane) = acc[j];
     }
@@ -346,10 +347,15 @@ static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out,
     if (rc) return rc;
     a.pml = (float *)qg::ws_attn;
     a.po = a.pml + (size_t)a.n_kv * a.nchunk * ATT_MAXQ * 2;
-    if (fused)
-        hipLaunchKernelGGL(k_attn_chunk<1>, dim3(a.n_kv, a.nchunk), dim3(ATT_NWV * 64), 0, qg::stream, a);
-    else
-        hipLaunchKernelGGL(k_attn_chunk<0>, dim3(a.n_kv, a.nchunk), dim3(ATT_NWV * 64), 0, qg::stream, a);
+    const int rw = ((a.n_head / a.n_kv) * a.B + ATT_NWV - 1) / ATT_NWV;
+    const dim3 grid(a.n_kv, a.nchunk), blk(ATT_NWV * 64);
+#define ATT_GO(F_, R_) hipLaunchKernelGGL((k_attn_chunk<F_, R_>), grid, blk, 0, qg::stream, a)
+#define ATT_RWS(F_) do { switch (rw) { case 1: ATT_GO(F_, 1); break; case 2: ATT_GO(F_, 2); break; \
+                         case 3: ATT_GO(F_, 3); break; case 4: ATT_GO(F_, 4); break; case 5: ATT_GO(F_, 5); break; \
+                         default: ATT_GO(F_, 6); break; } } while (0)
+    if (fused) ATT_RWS(1); else ATT_RWS(0);
+#undef ATT_RWS
+#undef ATT_GO
     QG_LAUNCH_CHECK();
     hipLaunchKernelGGL(k_attn_combine, dim3(a.n_head, a.B), dim3(ATT_HD), 0, qg::stream, a.q, a.ldq, a.pml, a.po,
                        a.pos_dev, a.B, a.n_head, a.n_kv, a.nchunk, out, ldo);
