@@ -157,6 +157,9 @@ float        *qwen_model_field(qwen_model_t *m, const char *name);   /* "logits"
 uint32_t      qwen_model_get(const qwen_model_t *m, const char *name); /* "pos", "vocab", "n_embd", "n_ctx", "n_layer" */
 void          qwen_model_set_pos(qwen_model_t *m, uint32_t pos);
 void          qwen_model_set_host_sync(qwen_model_t *m, int on);
+/* 1: the launch sequences of the forward and MTP bodies are captured once as
+ * HIP graphs and replayed (default 0; environment QWEN_GRAPHS=1 sets 1) */
+void          qwen_model_set_graphs(qwen_model_t *m, int on);
 
 /* Profiling counters (reference model.h:151-152): seconds per section. */
 extern double qwen_prof_embed, qwen_prof_gdn, qwen_prof_attn, qwen_prof_head;

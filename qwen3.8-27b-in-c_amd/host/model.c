@@ -52,6 +52,10 @@ struct qwen_gpu {
     float *part, *pend;
     int pend_ks;
     uint32_t pend_B;
+    /* replayable launch sequences (HIP graphs) of the forward / MTP bodies, one per
+     * (kind, token pointer, hidden-state pointer, logits pointer, B, flag) */
+    int use_graphs, n_graphs;
+    struct { int kind, flag; uint32_t B; const void *tok, *h, *lg; void *exec; } graphs[48];
     void **allocs;
     size_t n_allocs, cap_allocs;
     qgpu_tensor **tensors;
@@ -90,6 +94,7 @@ static void gpu_free(qwen_gpu_t *g)
 {
     if (!g) return;
     qgpu_sync();
+    for (int i = 0; i < g->n_graphs; i++) qgpu_graph_destroy(g->graphs[i].exec);
     for (size_t i = 0; i < g->n_tensors; i++) qgpu_tensor_free(g->tensors[i]);
     for (size_t i = 0; i < g->n_allocs; i++) qgpu_free(g->allocs[i]);
     free(g->tensors);
@@ -292,6 +297,13 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     if (qgpu_init(0)) { fprintf(stderr, "model_init: no GPU\n"); return -1; }
     qwen_gpu_t *g = calloc(1, sizeof *g);
     m->gpu = g;
+    {
+        /* QWEN_GRAPHS=1: replay captured launch sequences.  Measured on MI355X the
+         * 27B verify step is the same either way (the per-kernel cost is inside the
+         * kernels, not the dispatch), so kernels are launched from the host by default. */
+        const char *ge = getenv("QWEN_GRAPHS");
+        g->use_graphs = ge && ge[0] == '1';
+    }
     g->L = calloc(d->n_layer, sizeof *g->L);
     for (uint32_t il = 0; il < d->n_layer; il++)
         if (upload_layer(g, src, &m->layers[il], &g->L[il])) return -1;
@@ -507,8 +519,9 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     const uint64_t ld[3] = { g->SQ, g->kvrow, g->kvrow };
     K(qgpu_gemv_act_batch(W, 3, &an, (int)B, outs, ld, 0));
     /* q/k norm + RoPE + cache write + attention in one kernel, then the chunk merge */
+    (void)pos;   /* positions come from g->d_pos; the grid covers n_ctx (chunks past the live end exit) */
     K(qgpu_attn_fused(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos,
-                      g->rope_sin, (int)m->cfg.rope_dim_count, g->d_pos, (int)(pos + B), (int)B, (int)d->n_head,
+                      g->rope_sin, (int)m->cfg.rope_dim_count, g->d_pos, (int)m->n_ctx, (int)B, (int)d->n_head,
                       (int)d->n_kv_head, (int)d->head_dim, eps, g->battn, g->A));
     qgpu_act oc;
     memset(&oc, 0, sizeof oc);
@@ -541,43 +554,89 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     ffn_dev(m, D, g->bx, B);
 }
 
+/* Graph cache: the launch sequence of a body depends only on its pointers, B
+ * and flag (positions and the GDN ring index are read from device memory), so
+ * it is captured once and replayed; replay cuts the per-kernel launch gap. */
+enum { G_FWD = 1, G_MTP = 2 };
+typedef void (*body_fn)(qwen_model_t *, const uint32_t *, const float *, uint32_t, float *, int);
+
+static void run_body(qwen_model_t *m, int kind, body_fn fn, const uint32_t *tok, const float *h, uint32_t B,
+                     float *lg, int flag)
+{
+    qwen_gpu_t *g = m->gpu;
+    if (!g->use_graphs) { fn(m, tok, h, B, lg, flag); return; }
+    for (int i = 0; i < g->n_graphs; i++)
+        if (g->graphs[i].kind == kind && g->graphs[i].tok == tok && g->graphs[i].h == h && g->graphs[i].lg == lg &&
+            g->graphs[i].B == B && g->graphs[i].flag == flag) {
+            K(qgpu_graph_launch(g->graphs[i].exec));
+            return;
+        }
+    if (g->n_graphs == (int)(sizeof g->graphs / sizeof g->graphs[0])) { fn(m, tok, h, B, lg, flag); return; }
+    void *exec = NULL;
+    K(qgpu_graph_begin());
+    fn(m, tok, h, B, lg, flag);
+    K(qgpu_graph_end(&exec));
+    const int i = g->n_graphs++;
+    g->graphs[i].kind = kind; g->graphs[i].tok = tok; g->graphs[i].h = h; g->graphs[i].lg = lg;
+    g->graphs[i].B = B; g->graphs[i].flag = flag; g->graphs[i].exec = exec;
+    K(qgpu_graph_launch(exec));
+}
+
+static void forward_body(qwen_model_t *m, const uint32_t *d_tokens, const float *unused, uint32_t B,
+                         float *d_logits, int save_h)
+{
+    (void)unused;
+    qwen_gpu_t *g = m->gpu;
+    const qwen_dims_t *d = &m->dims;
+    const uint64_t E = d->n_embd, V = m->cfg.vocab_size;
+    K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bx, E));
+    for (uint32_t il = 0; il < d->n_layer; il++) {
+        if (g->L[il].rec) gdn_dev(m, &g->L[il], B);
+        else attn_dev(m, &g->L[il], g->bx, B, 0);
+    }
+    const qgpu_act an = act_norm_res(m, g->bx, g->out_norm, g->bxb);
+    K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
+    if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
+}
+
 /* tokens on the device; logits of every token into d_logits ([B][V]); hidden
  * states into h_save when save_h.  GDN states advance by B (ring index). */
 static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, uint32_t pos, float *d_logits,
                         int save_h)
 {
     qwen_gpu_t *g = m->gpu;
-    const qwen_dims_t *d = &m->dims;
-    const uint64_t E = d->n_embd, V = m->cfg.vocab_size;
     K(qgpu_set_i32(g->d_pos, (int)pos));
-    K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bx, E));
-    for (uint32_t il = 0; il < d->n_layer; il++) {
-        if (g->L[il].rec) gdn_dev(m, &g->L[il], B);
-        else attn_dev(m, &g->L[il], g->bx, B, pos);
-    }
-    const qgpu_act an = act_norm_res(m, g->bx, g->out_norm, g->bxb);
-    K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
-    if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
+    run_body(m, G_FWD, forward_body, d_tokens, NULL, B, d_logits, save_h);
     g->cur_base = g->cur;
     g->cur = (g->cur + (int)B) % NSLOT;
     K(qgpu_set_i32(g->d_cur, g->cur));
 }
+
+static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, uint32_t B, float *d_logits,
+                     int unused);
 
 /* MTP layer for B tokens (d_tokens) paired with hidden states h (device, [B][E]);
  * output rows in mx, mtp_h = last row; logits of every row into d_logits if given */
 static void mtp_dev(qwen_model_t *m, const uint32_t *d_tokens, const float *h, uint32_t B, uint32_t pos,
                     float *d_logits)
 {
+    K(qgpu_set_i32(m->gpu->d_pos, (int)pos));
+    run_body(m, G_MTP, mtp_body, d_tokens, h, B, d_logits, 0);
+}
+
+static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, uint32_t B, float *d_logits,
+                     int unused)
+{
+    (void)unused;
     qwen_gpu_t *g = m->gpu;
     const uint64_t E = m->dims.n_embd, V = m->cfg.vocab_size;
     const float eps = m->cfg.rms_norm_eps;
-    K(qgpu_set_i32(g->d_pos, (int)pos));
     K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bxb, E));
     /* eh_proj(concat(enorm(e), hnorm(h))) (model.c:1044-1052): both norms in the input preparation */
     qgpu_act cat = act_norm(g->bxb, E, g->enorm, eps, g->cat, 2 * E);
     cat.y = h; cat.ldy = E; cat.w2 = g->hnorm; cat.seg = E;
     K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->eh_proj, 1, &cat, (int)B, &g->mx, &E, 0));
-    attn_dev(m, &g->mtp, g->mx, B, pos);
+    attn_dev(m, &g->mtp, g->mx, B, 0);
     if (d_logits) {
         const qgpu_act an = act_norm_res(m, g->mx, g->shnorm, g->bxb);
         K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
@@ -917,3 +976,4 @@ uint32_t qwen_model_get(const qwen_model_t *m, const char *name)
 }
 void qwen_model_set_pos(qwen_model_t *m, uint32_t pos) { m->pos = pos; }
 void qwen_model_set_host_sync(qwen_model_t *m, int on) { m->host_sync = on; }
+void qwen_model_set_graphs(qwen_model_t *m, int on) { if (m && m->gpu) m->gpu->use_graphs = on ? 1 : 0; }

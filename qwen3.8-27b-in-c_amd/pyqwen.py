@@ -379,6 +379,7 @@ def _model_lib():
     L.qwen_model_get.restype = u32
     L.qwen_model_set_pos.argtypes = [vp, u32]
     L.qwen_model_set_host_sync.argtypes = [vp, i32]
+    L.qwen_model_set_graphs.argtypes = [vp, i32]
     L.model_generate_spec.argtypes = [vp, U32P, u32, u32, u32, u32, i32, U32P, U32P, ctypes.POINTER(GenStats)]
     L.model_generate_spec.restype = u32
     L.model_spec_begin.argtypes = [vp, U32P, u32, u32]
@@ -411,6 +412,10 @@ class Model:
             raise QgpuError(f"model_init failed ({path or 'synthetic'})")
         self.V = self.L.qwen_model_get(self.h, b"vocab")
         self.E = self.L.qwen_model_get(self.h, b"n_embd")
+
+    def set_graphs(self, on):
+        """replay captured launch sequences (HIP graphs) of the forward / MTP bodies (default off)"""
+        self.L.qwen_model_set_graphs(self.h, 1 if on else 0)
 
     def close(self):
         if self.h:

@@ -337,3 +337,22 @@ def test_model_spec_begin_run_resumes(gpu, tiny, mode):
     m = pyqwen.Model(path, int(z["n_ctx"]))
     toks, js, st = m.generate_spec(z["prompt"][:20], len(got), 3, force_accept=mode)
     assert np.array_equal(got, toks)
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_model_graphs_match_eager(gpu, tiny, mode):
+    """Replayed launch sequences (HIP graphs) give bit-identical streams and
+    logits to kernel-by-kernel launches: every cycle replays the draft, verify and
+    anchor graphs at new positions and ring slots, with host reads between replays,
+    then a host-API forward runs after the device loop."""
+    path, z = tiny
+    res = []
+    for graphs in (False, True):
+        m = pyqwen.Model(path, int(z["n_ctx"]))
+        m.set_graphs(graphs)
+        toks, js, st = m.generate_spec(z["prompt"][:20], 40, 3, force_accept=mode)
+        lb = m.forward_batch(z["prompt"][20:24], m.pos, 1)
+        res.append((toks.copy(), js.copy(), lb.copy()))
+        m.close()
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1])
+    assert np.array_equal(res[0][2], res[1][2])
