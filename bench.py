@@ -50,7 +50,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 HBM_PEAK_GBS = 8000.0
 IQ4 = 23
 METRIC = "accepted tok/s, 27B IQ4_XS MTP k=3 on 1 GPU; gemv_batch HBM GB/s (% peak)"
-ROOF_KERNEL = "k_gemv_iq4<1, 4>"
+ROOF_KERNEL = "k_gemv_iq4<1, 4, 0>"
 
 
 def log(*a):

@@ -65,7 +65,7 @@ def cmd_stats(a):
         s[3] = max(s[3], dur)
     total = sum(v[1] for v in agg.values()) or 1.0
     out = [f"# rocprofv3 kernel trace: {a.title or os.path.basename(find_db(a.db))}", "",
-           "Command (run from the repository root on the GPU box):", "", "```", a.cmd, "```", "",
+           "Command (`/root/repo` is the repository root):", "", "```", a.cmd, "```", "",
            f"{len(rows)} kernel dispatches, {total / 1e6:.3f} ms of kernel time.", "",
            "| kernel | calls | total ms | avg us | min us | max us | % |", "|---|---:|---:|---:|---:|---:|---:|"]
     for name, (n, t, lo, hi) in sorted(agg.items(), key=lambda kv: -kv[1][1])[:a.top]:
