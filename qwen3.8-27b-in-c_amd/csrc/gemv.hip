@@ -155,51 +155,77 @@ static __device__ __forceinline__ float wave_sum(float v)
 
 // One block = one 256-element super-block (blockIdx.x) of the 4 tokens of
 // plane blockIdx.y.  The activation transform KIND (QGPU_ACT_*) is applied
-// first; v may also be stored in fp32 (xout).
+// first; v may also be stored in fp32 (xout).  Every global load a thread
+// needs (4 tokens; partial planes; gate and weight rows) is issued before the
+// first use, so a block waits for one memory latency, not one per token.
 template <int KIND>
 __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict__ A, float *__restrict__ xs)
 {
     __shared__ uint8_t stage[4096];
-    __shared__ float red[4][8];
-    __shared__ int shift[4];
+    __shared__ float red[2][4][4];       // [sum of squares | max |v|][token][wave]
     const int e = threadIdx.x, sb = blockIdx.x, a = blockIdx.y;
     const int lane = e & 63, wv = e >> 6;
     const uint64_t k = (uint64_t)sb * 256 + e;
+    const int nt = p.ntok - 4 * a < 4 ? p.ntok - 4 * a : 4;      // tokens of this plane (>= 1)
+    int tr[4];                                                     // row of token i (clamped: always loadable)
+#pragma unroll
+    for (int i = 0; i < 4; i++) tr[i] = 4 * a + (i < nt ? i : 0);
     float v[4];
+    bool have_max = false;                                         // m[] already holds the per-wave max |v|
+    float m[4];
     if (KIND == ACT_RMS_DEFER) {
-        // v = x_eff * w; the row factor 1/sqrt(mean(x_eff^2) + eps) multiplies the GEMV output
-        // (W (x s w) = s W (x w)), from the per-super-block sums of squares written here
-        float ssq[4];
+        // v = x_eff * w, x_eff = x + (p_0 + p_1 + ...) over the n_part partial planes; the row factor
+        // 1/sqrt(mean(x_eff^2) + eps) multiplies the GEMV output (W (x s w) = s W (x w)), from the
+        // per-super-block sums of squares written here
+        float xr[4], pr[8][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) xr[i] = p.x[(uint64_t)tr[i] * p.ldx + k];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const uint64_t qo = (uint64_t)(q < p.n_part ? q : 0) * p.pstride;
+#pragma unroll
+            for (int i = 0; i < 4; i++) pr[q][i] = p.n_part ? p.part[qo + (uint64_t)tr[i] * p.ldp + k] : 0.0f;
+        }
+        const float wk = p.w[k];
+        float ss[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int t = 4 * a + i;
-            float xe = 0.0f;
-            if (t < p.ntok) {
-                xe = p.x[(uint64_t)t * p.ldx + k];
-                if (p.n_part) {
-                    float ps = p.part[(uint64_t)t * p.ldp + k];
-                    for (int q = 1; q < p.n_part; q++) ps += p.part[(uint64_t)q * p.pstride + (uint64_t)t * p.ldp + k];
-                    xe += ps;
-                }
-                if (p.xnew) p.xnew[(uint64_t)t * p.ldxn + k] = xe;
+            float xe = xr[i];
+            if (p.n_part) {
+                float ps = pr[0][i];
+#pragma unroll
+                for (int q = 1; q < 8; q++)
+                    if (q < p.n_part) ps += pr[q][i];
+                xe += ps;
             }
-            v[i] = xe * p.w[k];
-            ssq[i] = wave_sum(xe * xe);
-            if (lane == 0) red[i][wv] = ssq[i];
+            if (i >= nt) xe = 0.0f;
+            else if (p.xnew) p.xnew[(uint64_t)(4 * a + i) * p.ldxn + k] = xe;
+            v[i] = xe * wk;
+            ss[i] = xe * xe;
+            m[i] = fabsf(v[i]);
         }
-        __syncthreads();
-        if (e < 4 && 4 * a + e < p.ntok)
-            p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[e][0] + red[e][1]) + (red[e][2] + red[e][3]);
-        __syncthreads();
+#pragma unroll
+        for (int o = 32; o; o >>= 1)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                ss[i] += __shfl_xor(ss[i], o);
+                m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
+            }
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[0][i][wv] = ss[i];
+        have_max = true;
     } else if (KIND == QGPU_ACT_RMSNORM) {
-        // row RMS over the segment holding this super-block (each block recomputes it: same order, same value);
-        // all row loads are issued before any reduction
+        // row RMS over the segment holding this super-block (each block recomputes it: same order, same value)
         const uint64_t segl = p.seg;
         const int part = (uint64_t)sb * 256 >= segl ? 1 : 0;
         const float *src = part ? p.y : p.x;
         const float *w = part ? p.w2 : p.w;
         const uint64_t ld = part ? p.ldy : p.ldx, kk = k - (part ? segl : 0);
-        const int nt = p.ntok - 4 * a < 4 ? p.ntok - 4 * a : 4;     // tokens of this plane (>= 1)
+        float own[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) own[i] = src[(uint64_t)tr[i] * ld + kk];
+        const float wk = w[kk];
         float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         for (uint64_t j0 = e; j0 < segl / 4; j0 += 5 * 256) {
             float4 q[5][4];
@@ -220,72 +246,94 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
                 }
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            ss[i] = wave_sum(ss[i]);
-            if (lane == 0) red[i][wv] = ss[i];
-        }
+        for (int o = 32; o; o >>= 1)
+#pragma unroll
+            for (int i = 0; i < 4; i++) ss[i] += __shfl_xor(ss[i], o);
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[0][i][wv] = ss[i];
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float tot = (red[i][0] + red[i][1]) + (red[i][2] + red[i][3]);
+            const float tot = (red[0][i][0] + red[0][i][1]) + (red[0][i][2] + red[0][i][3]);
             const float sc = 1.0f / sqrtf(tot / (float)segl + p.eps);
-            v[i] = i < nt ? (src[(uint64_t)(4 * a + i) * ld + kk] * sc) * w[kk] : 0.0f;
+            v[i] = i < nt ? (own[i] * sc) * wk : 0.0f;
         }
-        __syncthreads();
     } else if (KIND == QGPU_ACT_GATED_NORM) {
         // heads of seg = 64 * hw elements: waves [h0, h0 + hw) of this block hold one head
         const int hw = (int)(p.seg >> 6), h0 = (wv / hw) * hw;
-        float raw[4];
+        float raw[4], gy[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int t = 4 * a + i;
-            raw[i] = t < p.ntok ? p.x[(uint64_t)t * p.ldx + k] : 0.0f;
-            const float ss = wave_sum(raw[i] * raw[i]);
-            if (lane == 0) red[i][wv] = ss;
+            raw[i] = p.x[(uint64_t)tr[i] * p.ldx + k];
+            gy[i] = p.y[(uint64_t)tr[i] * p.ldy + k];
         }
+        const float wk = p.w[k & (p.seg - 1)];
+        float ss[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) ss[i] = raw[i] * raw[i];
+#pragma unroll
+        for (int o = 32; o; o >>= 1)
+#pragma unroll
+            for (int i = 0; i < 4; i++) ss[i] += __shfl_xor(ss[i], o);
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[0][i][wv] = ss[i];
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int t = 4 * a + i;
-            float tot = red[i][h0];
-            for (int q = 1; q < hw; q++) tot += red[i][h0 + q];
+            float tot = red[0][i][h0];
+            for (int q = 1; q < hw; q++) tot += red[0][i][h0 + q];
             const float sc = 1.0f / sqrtf(tot / (float)p.seg + p.eps);
-            v[i] = t < p.ntok ? ((raw[i] * sc) * p.w[k & (p.seg - 1)]) * silu_dev(p.y[(uint64_t)t * p.ldy + k])
-                              : 0.0f;
+            v[i] = i < nt ? ((raw[i] * sc) * wk) * silu_dev(gy[i]) : 0.0f;
         }
-        __syncthreads();
     } else {
+        float xv[4], yv[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int t = 4 * a + i;
-            if (t >= p.ntok) { v[i] = 0.0f; continue; }
-            const float xv = p.x[(uint64_t)t * p.ldx + k];
-            v[i] = KIND == QGPU_ACT_SILU_MUL ? silu_dev(xv) * p.y[(uint64_t)t * p.ldy + k] : xv;
+            xv[i] = p.x[(uint64_t)tr[i] * p.ldx + k];
+            yv[i] = KIND == QGPU_ACT_SILU_MUL ? p.y[(uint64_t)tr[i] * p.ldy + k] : 0.0f;
         }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            v[i] = i >= nt ? 0.0f : KIND == QGPU_ACT_SILU_MUL ? silu_dev(xv[i]) * yv[i] : xv[i];
     }
     if (p.xout) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            if (4 * a + i < p.ntok) p.xout[(uint64_t)(4 * a + i) * p.ldxo + k] = v[i];
+            if (i < nt) p.xout[(uint64_t)(4 * a + i) * p.ldxo + k] = v[i];
     }
-    if (!p.digits) return;
-    float m[4];
+    if (!p.digits) {                  // fp32 rows only (VALU formats); the deferred norm still needs its sums
+        if (KIND == ACT_RMS_DEFER) {
+            __syncthreads();
+            if (e < nt)
+                p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] =
+                    (red[0][e][0] + red[0][e][1]) + (red[0][e][2] + red[0][e][3]);
+        }
+        return;
+    }
+    if (!have_max) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        m[i] = fabsf(v[i]);
+        for (int i = 0; i < 4; i++) m[i] = fabsf(v[i]);
 #pragma unroll
-        for (int o = 32; o; o >>= 1) m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
+        for (int o = 32; o; o >>= 1)
+#pragma unroll
+            for (int i = 0; i < 4; i++) m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
     }
     if (lane == 0)
-        for (int i = 0; i < 4; i++) red[i][wv] = m[i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) red[1][i][wv] = m[i];
     __syncthreads();
-    if (e < 4) {
-        const float mx = fmaxf(fmaxf(red[e][0], red[e][1]), fmaxf(red[e][2], red[e][3]));
+    if (KIND == ACT_RMS_DEFER && e < nt)
+        p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[0][e][0] + red[0][e][1]) + (red[0][e][2] + red[0][e][3]);
+    int shift[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float mx = fmaxf(fmaxf(red[1][i][0], red[1][i][1]), fmaxf(red[1][i][2], red[1][i][3]));
         int E = 0;
-        if (mx > 0.0f && isfinite(mx)) { frexpf(mx, &E); shift[e] = 30 - E; }
-        else shift[e] = 0;
+        if (mx > 0.0f && isfinite(mx)) { frexpf(mx, &E); shift[i] = 30 - E; }
+        else shift[i] = 0;
     }
-    __syncthreads();
     const int ib = e >> 5, w = e & 31, up = w >> 4, jj = w & 15, gg = jj >> 2, c = jj & 3;
     const int boff = ((ib >> 1) * 64) * 16 + (ib & 1) * 8 + up * 4 + c;   // + lane*16
 #pragma unroll
@@ -395,9 +443,9 @@ static __device__ __forceinline__ void iq4_decode8(uint32_t q, const DecodeK &K,
 // Weight records come from HBM and activation digits from L2, so the two are
 // prefetched to different depths: weights IQ4_WDEPTH super-blocks ahead
 // (10 VGPRs each), digits IQ4_ADEPTH ahead (16 * NA + 4 * NA VGPRs each).
-// Measured on MI355X over the model's shapes (rings of 2..8 x 1..2, occupancy
-// caps): 3 / 1 is within noise of the best everywhere and keeps the kernel at
-// 100 VGPRs.
+// Measured on MI355X (rings of 2..5 x 1..2, with and without tail loads that
+// keep the wait counts exact): all within +-3%, deeper rings slightly slower;
+// 3 / 1 keeps the plain kernel at 93 VGPRs (5 waves per SIMD).
 struct IQ4W {
     uint2 hdr;
     uint4 qa, qb;
@@ -468,8 +516,10 @@ static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA>
 #define IQ4_WDEPTH 3    // weight records in flight per wave
 #endif
 #ifndef IQ4_ADEPTH
-#define IQ4_ADEPTH 1    // digit super-blocks in flight per wave (divides IQ4_WDEPTH)
+#define IQ4_ADEPTH 1    // digit super-blocks in flight per wave
 #endif
+// main-loop unroll: a common multiple of the two ring depths (compile-time ring slots)
+#define IQ4_UNROLL ((IQ4_WDEPTH % IQ4_ADEPTH) == 0 ? IQ4_WDEPTH : IQ4_WDEPTH * IQ4_ADEPTH)
 
 // MODE bit 0 (IQ4_RMS): deferred RMSNorm row factors; bit 1 (IQ4_SPLIT): K split
 // into partial planes.  Plain launches (MODE 0) compile without either.
@@ -510,25 +560,26 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
 
     // two register rings: weights of super-block sb+IQ4_WDEPTH-1 and digits of
     // sb+IQ4_ADEPTH-1 are loading while sb is decoded and multiplied (ring
-    // indices are compile-time after unrolling by IQ4_WDEPTH)
+    // indices are compile-time after unrolling by IQ4_UNROLL).  Each step
+    // issues its digit loads before its weight loads (vmcnt retires loads in
+    // issue order, so a wait for the digits need not cover the newer weights).
     IQ4W wr[IQ4_WDEPTH];
     IQ4A<NA> ar[IQ4_ADEPTH];
 #define LOAD_W(slot, sbx) iq4_load_w(wr[slot], rec0 + (uint64_t)(sbx) * IQ4_REC_BYTES, lane, n)
 #define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * 4096, args.xs + (uint64_t)(sbx) * 16, lane, g)
 #pragma unroll
-    for (int d = 0; d < IQ4_WDEPTH - 1; d++)
-        if (sb0 + d < sb1) LOAD_W(d, sb0 + d);
+    for (int d = 0; d < IQ4_WDEPTH - 1 || d < IQ4_ADEPTH - 1; d++) {
+        if (d < IQ4_ADEPTH - 1 && sb0 + d < sb1) LOAD_A(d, sb0 + d);
+        if (d < IQ4_WDEPTH - 1 && sb0 + d < sb1) LOAD_W(d, sb0 + d);
+    }
+    for (int sb = sb0; sb < sb1; sb += IQ4_UNROLL) {
 #pragma unroll
-    for (int d = 0; d < IQ4_ADEPTH - 1; d++)
-        if (sb0 + d < sb1) LOAD_A(d, sb0 + d);
-    for (int sb = sb0; sb < sb1; sb += IQ4_WDEPTH) {
-#pragma unroll
-        for (int d = 0; d < IQ4_WDEPTH; d++) {
+        for (int d = 0; d < IQ4_UNROLL; d++) {
             if (sb + d < sb1) {
                 const int pw = sb + d + IQ4_WDEPTH - 1, pa = sb + d + IQ4_ADEPTH - 1;
-                if (pw < sb1) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
                 if (pa < sb1) LOAD_A((d + IQ4_ADEPTH - 1) % IQ4_ADEPTH, pa);
-                iq4_compute<NA>(wr[d], ar[d % IQ4_ADEPTH], K, accf);
+                if (pw < sb1) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
+                iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], K, accf);
             }
         }
     }
