@@ -5,7 +5,8 @@
 //     super-block) a 2176-byte record holds the 16 row headers (d, scales_h,
 //     scales_l: 8 B each) and the 2048 nibble bytes arranged so that lane l of
 //     a wave loads its MFMA B operand for 4 sub-blocks with one 16-byte load;
-//   * a nibble dword decodes to 8 int8 codebook values with 6 v_perm_b32;
+//   * a nibble dword decodes with 4 v_perm_b32 into two int8 halves of the
+//     codebook values, which two chained MFMAs multiply by the same operand;
 //   * the activations are turned once per call into 4 balanced int8 "digits"
 //     of a 30-bit fixed-point value per (token, super-block):
 //       x = 2^-s * (d0 + 2^8 d1 + 2^16 d2 + 2^24 d3),  |x| 2^s < 2^30,
@@ -405,39 +406,32 @@ static __device__ __forceinline__ void rms_reduce(const GemvArgs &args, int wv, 
     }
 }
 
-// v_and_or_b32 with every operand in a VGPR (a VOP3 encoding takes no 32-bit
-// literal and one scalar operand at most, so the constants live in VGPRs)
-static __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c)
-{
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
-    return r;
-}
-
 // a * b + c on the low 24 bits of a and b (signed), 32-bit result.  Plain
 // code, not inline asm: its input comes straight from an MFMA, and the
 // compiler inserts the MFMA-to-VALU wait states only for instructions it
 // generates itself.
 static __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
 
-struct DecodeK {               // decode constants, held in VGPRs
-    uint32_t m4, sel0;
-};
-
-// 8 IQ4_NL codebook bytes (low nibbles -> lo, high nibbles -> hi) from one
-// dword of nibbles: two 8-entry lookups (v_perm_b32 over the codebook halves)
-// and a byte select on the nibble's bit 3.  13 VALU operations.
-static __device__ __forceinline__ void iq4_decode8(uint32_t q, const DecodeK &K, uint32_t &lo, uint32_t &hi)
+// IQ4_NL codebook split across two 8-entry v_perm_b32 tables indexed by the
+// whole nibble q: perm(XH:XL, q) + perm(YH:YL, q ^ 8) = c(q).  Selectors 8..15
+// of v_perm_b32 give constants (8..11: sign of bytes 1, 3, 5, 7 as 0x00/0xFF;
+// 12: 0x00; 13..15: 0xFF), so each table is exact for its own half and
+// contributes 0 or -1 to the other, which the other table absorbs:
+//   X = c(0..7) - {0, 0, 0, 0, 0, -1, -1, -1}   (Y bytes are positive)
+//   Y = c(8..15) - {-1, -1, -1, -1, 0, -1, -1, -1} (X bytes are negative)
+// The two halves are multiplied by the same activation operand in two chained
+// MFMAs, so the integer dot product equals the one with the codebook bytes.
+// 9 VALU operations per 8 weights (4 v_perm_b32).
+static __device__ __forceinline__ void iq4_decode8(uint32_t q, uint32_t &x_lo, uint32_t &x_hi, uint32_t &y_lo,
+                                                   uint32_t &y_hi)
 {
-    // IQ4_NL codebook as int8 bytes {-127,-104,-83,-65 | -49,-35,-22,-10 | 1,13,25,38 | 53,69,89,113}
-    const uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
-    uint32_t s = q & 0x07070707u;
-    uint32_t a = __builtin_amdgcn_perm(T1, T0, s), b = __builtin_amdgcn_perm(T3, T2, s);
-    lo = __builtin_amdgcn_perm(b, a, and_or(q >> 1, K.m4, K.sel0));
-    s = (q >> 4) & 0x07070707u;
-    a = __builtin_amdgcn_perm(T1, T0, s);
-    b = __builtin_amdgcn_perm(T3, T2, s);
-    hi = __builtin_amdgcn_perm(b, a, and_or(q >> 5, K.m4, K.sel0));
+    const uint32_t XL = 0xBFAD9881u, XH = 0xF7EBDECFu;      // -127 -104 -83 -65 | -49 -34 -21 -9
+    const uint32_t YL = 0x271A0E02u, YH = 0x725A4635u;      //    2   14  26  39 |  53  70  90 114
+    const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;
+    x_lo = __builtin_amdgcn_perm(XH, XL, lo);
+    x_hi = __builtin_amdgcn_perm(XH, XL, hi);
+    y_lo = __builtin_amdgcn_perm(YH, YL, lo ^ 0x08080808u);
+    y_hi = __builtin_amdgcn_perm(YH, YL, hi ^ 0x08080808u);
 }
 
 // Weight records come from HBM and activation digits from L2, so the two are
@@ -453,11 +447,13 @@ struct IQ4W {
 template <int NA>
 struct IQ4A {
     uint4 av[NA][4];
-    float4 xv[NA];
+    float4 xt[NA];       // 2^-s of tokens 0..3 of each plane (wave-uniform: scalar registers)
 };
 
 // rec, Ab, xsb are wave-uniform (scalar) addresses of this super-block's weight
-// record, digit plane 0 and digit scales; lanes add their own offsets.
+// record, digit plane 0 and digit scales; lanes add their own offsets.  The
+// digit scale of lane group g (digit g) and token t is 2^(8 g) xs[t]: only the
+// four token scales are loaded (scalar loads), 2^(8 g) is a lane constant.
 static __device__ __forceinline__ void iq4_load_w(IQ4W &w, const uint8_t *rec, int lane, int n)
 {
     w.hdr = *(const uint2 *)(rec + n * 8);
@@ -466,20 +462,19 @@ static __device__ __forceinline__ void iq4_load_w(IQ4W &w, const uint8_t *rec, i
 }
 
 template <int NA>
-static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab, const float *xsb, int lane, int g)
+static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab, const float *xsb, int lane)
 {
 #pragma unroll
     for (int a = 0; a < NA; a++) {
         const uint8_t *Aa = Ab + (uint64_t)a * PLANE_BYTES;
 #pragma unroll
         for (int p = 0; p < 4; p++) x.av[a][p] = *(const uint4 *)(Aa + p * 1024 + lane * 16);
-        x.xv[a] = *(const float4 *)(xsb + (uint64_t)a * XS_FLOATS + 4 * g);
+        x.xt[a] = *(const float4 *)(xsb + (uint64_t)a * XS_FLOATS);
     }
 }
 
 template <int NA>
-static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA> &x, const DecodeK &K,
-                                                   float (&accf)[NA][4])
+static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA> &x, float p8g, float (&accf)[NA][4])
 {
     const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
     v4i acci[NA];
@@ -487,28 +482,29 @@ static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA>
     for (int a = 0; a < NA; a++) acci[a] = (v4i){0, 0, 0, 0};
 #pragma unroll
     for (int ib = 0; ib < 8; ib++) {
-        uint32_t lo, hi;
-        iq4_decode8(qd[ib], K, lo, hi);
-        const long bop = (long)(((uint64_t)hi << 32) | lo);
+        uint32_t x_lo, x_hi, y_lo, y_hi;
+        iq4_decode8(qd[ib], x_lo, x_hi, y_lo, y_hi);
+        const long bx = (long)(((uint64_t)x_hi << 32) | x_lo), by = (long)(((uint64_t)y_hi << 32) | y_lo);
         const int wsc = hdr_scale(w.hdr, ib);
 #pragma unroll
         for (int a = 0; a < NA; a++) {
             const uint4 q4 = x.av[a][ib >> 1];
             const long aop = (ib & 1) ? (long)(((uint64_t)q4.w << 32) | q4.z)
                                       : (long)(((uint64_t)q4.y << 32) | q4.x);
-            const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bop, (v4i){0, 0, 0, 0}, 0, 0, 0);
+            const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                aop, by, __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bx, (v4i){0, 0, 0, 0}, 0, 0, 0), 0, 0, 0);
             // |D| < 2^19, |wsc| <= 32: exact 24-bit multiply-add
 #pragma unroll
             for (int i = 0; i < 4; i++) acci[a][i] = mad24(D[i], wsc, acci[a][i]);
         }
     }
-    const float d = h2f(w.hdr.x & 0xFFFFu);
+    const float dg = h2f(w.hdr.x & 0xFFFFu) * p8g;             // d 2^(8 g): exact
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        accf[a][0] += (float)acci[a][0] * (d * x.xv[a].x);
-        accf[a][1] += (float)acci[a][1] * (d * x.xv[a].y);
-        accf[a][2] += (float)acci[a][2] * (d * x.xv[a].z);
-        accf[a][3] += (float)acci[a][3] * (d * x.xv[a].w);
+        accf[a][0] += (float)acci[a][0] * (dg * x.xt[a].x);
+        accf[a][1] += (float)acci[a][1] * (dg * x.xt[a].y);
+        accf[a][2] += (float)acci[a][2] * (dg * x.xt[a].z);
+        accf[a][3] += (float)acci[a][3] * (dg * x.xt[a].w);
     }
 }
 
@@ -548,9 +544,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
     const int sb0 = kb0 + wv * nkb / NW, sb1 = kb0 + (wv + 1) * nkb / NW;
     RmsPart rp;
     if (MODE & IQ4_RMS) rms_load(args, wv, NW, lane, rp);
-    DecodeK K;
-    K.m4 = 0x04040404u;
-    K.sel0 = 0x03020100u;
+    const float p8g = __builtin_bit_cast(float, (uint32_t)(127 + 8 * g) << 23);   // 2^(8 g)
 
     float accf[NA][4];
 #pragma unroll
@@ -566,7 +560,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
     IQ4W wr[IQ4_WDEPTH];
     IQ4A<NA> ar[IQ4_ADEPTH];
 #define LOAD_W(slot, sbx) iq4_load_w(wr[slot], rec0 + (uint64_t)(sbx) * IQ4_REC_BYTES, lane, n)
-#define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * 4096, args.xs + (uint64_t)(sbx) * 16, lane, g)
+#define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * 4096, args.xs + (uint64_t)(sbx) * 16, lane)
 #pragma unroll
     for (int d = 0; d < IQ4_WDEPTH - 1 || d < IQ4_ADEPTH - 1; d++) {
         if (d < IQ4_ADEPTH - 1 && sb0 + d < sb1) LOAD_A(d, sb0 + d);
@@ -579,7 +573,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
                 const int pw = sb + d + IQ4_WDEPTH - 1, pa = sb + d + IQ4_ADEPTH - 1;
                 if (pa < sb1) LOAD_A((d + IQ4_ADEPTH - 1) % IQ4_ADEPTH, pa);
                 if (pw < sb1) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
-                iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], K, accf);
+                iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], p8g, accf);
             }
         }
     }
