@@ -48,6 +48,24 @@ static __device__ __forceinline__ float sum16(float v)
     return v;
 }
 
+// The same row sum with DPP lane moves (VALU, no LDS round trip): lane ^ 1,
+// lane ^ 2 (quad_perm), the other quad of the half row (row_half_mirror), the
+// other half row (row_mirror).  Each step adds a value to its mirror image, so
+// every lane of the row ends with the same bits.
+template <int CTRL>
+static __device__ __forceinline__ float dpp_mov(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+static __device__ __forceinline__ float rowsum16(float v)
+{
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);   // row_half_mirror
+    v += dpp_mov<0x140>(v);   // row_mirror
+    return v;
+}
+
 // block = 16 state rows of one v-head; thread (row r = tid/16, column chunk cc = tid%16, 8 columns)
 __global__ __launch_bounds__(256) void k_gdn_recur(const float *__restrict__ xq, uint64_t ldq,
                                                    const float *__restrict__ beta_raw,
@@ -123,6 +141,10 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float *__restrict__ xq,
 // window is a few floats per channel) and its own 16 v channels, for all B
 // tokens, into LDS.  Conv-state snapshots are written once per channel: q/k
 // channels by the block (h < n_k, rb = 0), v channels by their own block.
+// Every global load of the block (state rows, conv windows and inputs of all
+// tokens, gates) is issued before the first use; the norms and q.k of all
+// tokens are reduced together before the (sequential) recurrence, which then
+// needs two row sums per token.
 __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, uint64_t ldx, const float *__restrict__ cw,
                                                    float *__restrict__ cring, uint64_t cstride,
                                                    const float *__restrict__ beta_raw, const float *__restrict__ alpha_raw,
@@ -139,80 +161,113 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
     const int kh = h % n_k;                          // tiled v-head -> k-head map (model.c:565)
     const int cur = *cur_dev;
     const bool own_qk = h < n_k && rb == 0;
-    // ---- this thread's 8 state columns first: their load overlaps the conv phase
+    // ---- loads: this thread's 8 state columns
     const int r = tid >> 4, cc = tid & 15;
     const int j = rb * GDN_RB + r;                   // state row (v index)
     const uint64_t hoff = (uint64_t)h * GDN_HK * GDN_HK + (uint64_t)j * GDN_HK + cc * 8;
     const float *S0 = sring + (uint64_t)cur * sstride + hoff;
-    float S[8];
-    {
-        const float4 a = *(const float4 *)S0, b = *(const float4 *)(S0 + 4);
-        S[0] = a.x; S[1] = a.y; S[2] = a.z; S[3] = a.w; S[4] = b.x; S[5] = b.y; S[6] = b.z; S[7] = b.w;
+    const float4 sa = *(const float4 *)S0, sbv = *(const float4 *)(S0 + 4);
+    // ---- loads: conv channel A (q or k channel tid) and, for tid < 16, channel B (v channel)
+    const int cA = tid < GDN_HK ? kh * GDN_HK + tid : n_k * GDN_HK + kh * GDN_HK + (tid - GDN_HK);
+    const bool hasB = tid < GDN_RB;
+    const int cB = 2 * n_k * GDN_HK + h * GDN_HK + rb * GDN_RB + (tid & (GDN_RB - 1));
+    const float4 s0A = *(const float4 *)(cring + (uint64_t)cur * cstride + (uint64_t)cA * 4);
+    const float4 wA = *(const float4 *)(cw + (uint64_t)cA * 4);
+    float xA[GDN_MAXB], xB[GDN_MAXB];
+#pragma unroll
+    for (int b = 0; b < GDN_MAXB; b++) xA[b] = x[(uint64_t)(b < B ? b : B - 1) * ldx + cA];
+    float4 s0B = make_float4(0, 0, 0, 0), wB = make_float4(0, 0, 0, 0);
+    if (hasB) {
+        s0B = *(const float4 *)(cring + (uint64_t)cur * cstride + (uint64_t)cB * 4);
+        wB = *(const float4 *)(cw + (uint64_t)cB * 4);
+#pragma unroll
+        for (int b = 0; b < GDN_MAXB; b++) xB[b] = x[(uint64_t)(b < B ? b : B - 1) * ldx + cB];
     }
-    // ---- per-token gates of this head: beta = sigmoid(b), decay = exp(a * softplus(alpha + dt_bias))
-    //      (model.c:572-575), by threads 0..B-1 while the state loads are in flight
+    // ---- loads: per-token gates of this head
+    float braw = 0.0f, araw = 0.0f;
     if (tid < B) {
-        Gbeta[tid] = 1.0f / (1.0f + expf(-beta_raw[(uint64_t)tid * ldba + h]));
-        const float araw = alpha_raw[(uint64_t)tid * ldba + h] + dt_bias[h];
-        const float sp = araw > 30.0f ? araw : log1pf(expf(araw));
-        Gdec[tid] = expf(ssm_a[h] * sp);
+        braw = beta_raw[(uint64_t)tid * ldba + h];
+        araw = alpha_raw[(uint64_t)tid * ldba + h];
     }
-    // ---- conv + SiLU of the 2*128 + 16 channels this block reads
-    for (int e = tid; e < 2 * GDN_HK + GDN_RB; e += 256) {
-        int c;
-        float *dst;
-        bool own;
-        if (e < GDN_HK) { c = kh * GDN_HK + e; dst = &Yq[0][e]; own = own_qk; }
-        else if (e < 2 * GDN_HK) { c = n_k * GDN_HK + kh * GDN_HK + (e - GDN_HK); dst = &Yk[0][e - GDN_HK]; own = own_qk; }
-        else { c = 2 * n_k * GDN_HK + h * GDN_HK + rb * GDN_RB + (e - 2 * GDN_HK); dst = &Yv[0][e - 2 * GDN_HK]; own = true; }
-        const int dstride = e < 2 * GDN_HK ? GDN_HK : GDN_RB;
-        const float4 s0 = *(const float4 *)(cring + (uint64_t)cur * cstride + (uint64_t)c * 4);
-        const float4 wc = *(const float4 *)(cw + (uint64_t)c * 4);
+    const float ah = ssm_a[h], dtb = dt_bias[h];
+    // ---- gates: beta = sigmoid(b), decay = exp(a * softplus(alpha + dt_bias)) (model.c:572-575)
+    if (tid < B) {
+        Gbeta[tid] = 1.0f / (1.0f + expf(-braw));
+        const float av = araw + dtb;
+        const float sp = av > 30.0f ? av : log1pf(expf(av));
+        Gdec[tid] = expf(ah * sp);
+    }
+    // ---- conv + SiLU, conv-state snapshots
+    {
+        float *dA = tid < GDN_HK ? &Yq[0][tid] : &Yk[0][tid - GDN_HK];
         float win[4 + GDN_MAXB];
-        win[0] = s0.x; win[1] = s0.y; win[2] = s0.z; win[3] = s0.w;
+        win[0] = s0A.x; win[1] = s0A.y; win[2] = s0A.z; win[3] = s0A.w;
 #pragma unroll
         for (int b = 0; b < GDN_MAXB; b++) {
             if (b >= B) break;
-            win[4 + b] = x[(uint64_t)b * ldx + c];
+            win[4 + b] = xA[b];
             const float a0 = win[b + 1], a1 = win[b + 2], a2 = win[b + 3], a3 = win[b + 4];
-            dst[b * dstride] = silu_f(((a0 * wc.x + a1 * wc.y) + a2 * wc.z) + a3 * wc.w);
-            if (own) {
+            dA[b * GDN_HK] = silu_f(((a0 * wA.x + a1 * wA.y) + a2 * wA.z) + a3 * wA.w);
+            if (own_qk) {
                 const int slot = (cur + 1 + b) % nslot;
-                *(float4 *)(cring + (uint64_t)slot * cstride + (uint64_t)c * 4) = make_float4(a0, a1, a2, a3);
+                *(float4 *)(cring + (uint64_t)slot * cstride + (uint64_t)cA * 4) = make_float4(a0, a1, a2, a3);
             }
         }
     }
-    __syncthreads();
-    // ---- delta-rule recurrence (as k_gdn_recur), inputs from LDS
-    const float qscale = 1.0f / sqrtf((float)GDN_HK);
-    const float ah = ssm_a[h], dtb = dt_bias[h];
-    for (int b = 0; b < B; b++) {
-        float q[8], k[8];
-        {
-            const float4 q0 = *(const float4 *)&Yq[b][cc * 8], q1 = *(const float4 *)&Yq[b][cc * 8 + 4];
-            const float4 k0 = *(const float4 *)&Yk[b][cc * 8], k1 = *(const float4 *)&Yk[b][cc * 8 + 4];
-            q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w; q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
-            k[0] = k0.x; k[1] = k0.y; k[2] = k0.z; k[3] = k0.w; k[4] = k1.x; k[5] = k1.y; k[6] = k1.z; k[7] = k1.w;
-        }
-        float qq = 0.0f, kk = 0.0f;
+    if (hasB) {
+        float win[4 + GDN_MAXB];
+        win[0] = s0B.x; win[1] = s0B.y; win[2] = s0B.z; win[3] = s0B.w;
 #pragma unroll
-        for (int i = 0; i < 8; i++) { qq = fmaf(q[i], q[i], qq); kk = fmaf(k[i], k[i], kk); }
-        qq = sum16(qq);
-        kk = sum16(kk);
-        const float qn = sqrtf(qq), kn = sqrtf(kk);
-        const float qs = 1.0f / (qn > eps ? qn : eps), ks = 1.0f / (kn > eps ? kn : eps);   // l2norm (kernels.c:780-805)
-        float kq = 0.0f, sk = 0.0f, sq = 0.0f;
+        for (int b = 0; b < GDN_MAXB; b++) {
+            if (b >= B) break;
+            win[4 + b] = xB[b];
+            const float a0 = win[b + 1], a1 = win[b + 2], a2 = win[b + 3], a3 = win[b + 4];
+            Yv[b][tid] = silu_f(((a0 * wB.x + a1 * wB.y) + a2 * wB.z) + a3 * wB.w);
+            const int slot = (cur + 1 + b) % nslot;
+            *(float4 *)(cring + (uint64_t)slot * cstride + (uint64_t)cB * 4) = make_float4(a0, a1, a2, a3);
+        }
+    }
+    __syncthreads();
+    // ---- L2 norms (kernels.c:780-805) and q.k of every token: independent of the state
+    float qsv[GDN_MAXB], ksv[GDN_MAXB], kqv[GDN_MAXB];
+#pragma unroll
+    for (int b = 0; b < GDN_MAXB; b++) {
+        qsv[b] = ksv[b] = kqv[b] = 0.0f;
+        if (b >= B) continue;
+        const float4 q0 = *(const float4 *)&Yq[b][cc * 8], q1 = *(const float4 *)&Yq[b][cc * 8 + 4];
+        const float4 k0 = *(const float4 *)&Yk[b][cc * 8], k1 = *(const float4 *)&Yk[b][cc * 8 + 4];
+        const float q[8] = { q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w };
+        const float k[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+        float qq = 0.0f, kk = 0.0f, kq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) { qq = fmaf(q[i], q[i], qq); kk = fmaf(k[i], k[i], kk); kq = fmaf(k[i], q[i], kq); }
+        qsv[b] = rowsum16(qq);
+        ksv[b] = rowsum16(kk);
+        kqv[b] = rowsum16(kq);
+    }
+    // ---- delta-rule recurrence: o = (g S q + d (k.q)) / sqrt(128), S <- g S + d k^T (model.c:494-615)
+    const float qscale = 1.0f / sqrtf((float)GDN_HK);
+    float S[8] = { sa.x, sa.y, sa.z, sa.w, sbv.x, sbv.y, sbv.z, sbv.w };
+#pragma unroll
+    for (int b = 0; b < GDN_MAXB; b++) {
+        if (b >= B) break;
+        const float qn = sqrtf(qsv[b]), kn = sqrtf(ksv[b]);
+        const float qs = 1.0f / (qn > eps ? qn : eps), ks = 1.0f / (kn > eps ? kn : eps);
+        const float kq = kqv[b] * qs * ks;
+        const float4 q0 = *(const float4 *)&Yq[b][cc * 8], q1 = *(const float4 *)&Yq[b][cc * 8 + 4];
+        const float4 k0 = *(const float4 *)&Yk[b][cc * 8], k1 = *(const float4 *)&Yk[b][cc * 8 + 4];
+        float q[8] = { q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w };
+        float k[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+        float sk = 0.0f, sq = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             q[i] *= qs;
             k[i] *= ks;
-            kq = fmaf(k[i], q[i], kq);
             sk = fmaf(S[i], k[i], sk);
             sq = fmaf(S[i], q[i], sq);
         }
-        kq = sum16(kq);
-        sk = sum16(sk);
-        sq = sum16(sq);
+        sk = rowsum16(sk);
+        sq = rowsum16(sq);
         const float beta = Gbeta[b], decay = Gdec[b];
         const float vj = Yv[b][r];
         const float dj = (vj - decay * sk) * beta;
