@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """Benchmark of the MTP speculative-decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode model|gemv|longctx]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode model|gemv|longctx|sweep]
 
 Prints ONE JSON line on stdout (progress goes to stderr).
 
@@ -19,6 +19,11 @@ mode model (default) -- the headline workload: the random-init 27B hybrid
 mode gemv -- one batched IQ4_XS dequant-GEMV, 17408 x 5120, B = 4 columns.
 mode longctx -- the same model after an 8192-token prompt; verify-step
     latency and forced-acceptance throughput for k in {1, 3, 5, 7}.
+mode sweep -- gemv_batch over every weight format of the path (IQ4_XS, Q4_K,
+    Q5_K, Q6_K, Q8_0) x shapes 5120->17408, 17408->5120, 5120->248320 x B in
+    {1, 2, 4, 8}; HBM GB/s of algorithmic bytes per call (weights rotate over
+    enough copies to exceed the 256 MB MALL).  value = the IQ4_XS 17408x5120
+    B=4 point.
 
 roofline (every mode): the dominant kernel, k_gemv_iq4, on the gemv workload
 (17408 x 5120 IQ4_XS, B = 4), run first in the process: W + K gemv_batch calls,
@@ -182,6 +187,44 @@ def gemv_roofline(gpu, host, steps, warmup):
     return roof, gemv_call_gbs, ms_call, (W, x, ne0, ne1, B)
 
 
+SWEEP_FORMATS = [("IQ4_XS", 23), ("Q4_K", 12), ("Q5_K", 13), ("Q6_K", 14), ("Q8_0", 8)]
+SWEEP_SHAPES = [(5120, 17408), (17408, 5120), (5120, 248320)]     # (columns ne0, rows ne1)
+
+
+def bench_sweep(gpu, host, steps, warmup):
+    """gemv_batch GB/s over formats x shapes x B (algorithmic bytes: weights + B x (in + out) x 4)."""
+    L = gpu.L
+    e0, e1 = gpu.event(), gpu.event()
+    rows = []
+    for fname, t in SWEEP_FORMATS:
+        for ne0, ne1 in SWEEP_SHAPES:
+            W = host.synth_matrix(t, ne0, ne1, 7, t, 0.02)
+            R = max(2, -(-(600 << 20) // W.nbytes))
+            Ts = [gpu.tensor(W, t, ne0, ne1) for _ in range(R)]
+            x = host.synth_normal(8 * ne0, 1, 3).reshape(8, ne0)
+            xb, ob = gpu.put(x), gpu.buf(8 * ne1 * 4)
+            for B in (1, 2, 4, 8):
+                for i in range(warmup):
+                    gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
+                gpu.record(e0)
+                for i in range(steps):
+                    gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
+                gpu.record(e1)
+                us = gpu.elapsed_ms(e0, e1) / steps * 1e3
+                algo = W.nbytes + B * (ne0 + ne1) * 4
+                rows.append({"format": fname, "rows": ne1, "cols": ne0, "B": B, "us": round(us, 2),
+                             "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 4),
+                             "weight_bytes": W.nbytes})
+                log(f"sweep {fname:6s} {ne1:6d}x{ne0:<5d} B={B}: {us:8.2f} us {algo / us / 1e3:7.1f} GB/s")
+            gpu.sync()
+            for T in Ts:
+                T.close()
+            xb.close()
+            ob.close()
+            del W
+    return rows
+
+
 # ---------------------------------------------------------------------------------- model workloads
 def model_file(host, seed, keep_dir=None):
     """Writes the seeded random-init 27B model as a GGUF file (tmpfs when it fits)."""
@@ -318,7 +361,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (model: cycles; gemv: calls)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["model", "gemv", "longctx"], default="model")
+    ap.add_argument("--mode", choices=["model", "gemv", "longctx", "sweep"], default="model")
     ap.add_argument("--k", type=int, default=3, help="drafts per speculative cycle (model mode)")
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (model 512, longctx 8192)")
     ap.add_argument("--forced-cycles", type=int, default=None)
@@ -334,7 +377,8 @@ def main():
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    dflt = {"model": (256, 8, 512, 64, 15.0), "gemv": (200, 20, 0, 0, 5.0), "longctx": (0, 0, 8192, 16, 0.0)}
+    dflt = {"model": (256, 8, 512, 64, 15.0), "gemv": (200, 20, 0, 0, 5.0), "longctx": (0, 0, 8192, 16, 0.0),
+            "sweep": (40, 5, 0, 0, 0.0)}
     s, w, p, f, c = dflt[args.mode]
     args.steps = s if args.steps is None else args.steps
     args.warmup = w if args.warmup is None else args.warmup
@@ -370,6 +414,19 @@ def main():
                        "cols": ne0, "B": B, "weight_copies": 12, "device": name, "cus": ncu},
             "roofline": roof,
             "cpu_baseline": None if args.no_cpu else cpu_baseline_gemv(W, x, ne0, ne1, B, args.cpu_seconds),
+        }
+    elif args.mode == "sweep":
+        sweep = bench_sweep(gpu, host, args.steps, args.warmup)
+        pick = next(r for r in sweep if r["format"] == "IQ4_XS" and r["rows"] == 17408 and r["B"] == 4)
+        res = {
+            "metric": METRIC, "value": pick["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(pick["us"] / 1e3, 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp32 (IQ4_XS: int8-MFMA digit GEMV; K-quants / Q8_0: fp32 VALU GEMV)",
+            "data": "synthetic (seeded random super-blocks per format, x ~ N(0,1))",
+            "config": {"workload": "gemv_batch sweep: 5 formats x 3 shapes x B in {1,2,4,8}", "device": name,
+                       "cus": ncu},
+            "sweep": sweep, "roofline": roof, "cpu_baseline": None,
         }
     elif args.mode == "model":
         res = bench_model(args, gpu, host, roof, gemv_gbs)
