@@ -25,7 +25,7 @@ mode sweep -- gemv_batch over every weight format of the path (IQ4_XS, Q4_K,
     enough copies to exceed the 256 MB MALL).  value = the IQ4_XS 17408x5120
     B=4 point.
 
-roofline (every mode): the dominant kernel, k_gemv_iq4, on the gemv workload
+roofline (every mode): the dominant kernel, k_gemv_mfma (IQ4_XS), on the gemv workload
 (17408 x 5120 IQ4_XS, B = 4), run first in the process: W + K gemv_batch calls,
 then W + K launches of the GEMV kernel alone on prepared activations, the last
 K bracketed by HIP events on the library stream.  achieved = algorithmic bytes
@@ -55,7 +55,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 HBM_PEAK_GBS = 8000.0
 IQ4 = 23
 METRIC = "accepted tok/s, 27B IQ4_XS MTP k=3 on 1 GPU; gemv_batch HBM GB/s (% peak)"
-ROOF_KERNEL = "k_gemv_iq4<1, 4, 0>"
+ROOF_KERNEL = "k_gemv_mfma<23, 1, 4, 0>"
 
 
 def log(*a):
@@ -178,7 +178,7 @@ def gemv_roofline(gpu, host, steps, warmup):
         T.close()
     achieved = algo / (ms_kernel * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for("k_gemv_iq4"),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(ROOF_KERNEL.split("<")[0]),
             "kernel": ROOF_KERNEL, "workload": "IQ4_XS 17408x5120, B=4", "kernel_us": round(ms_kernel * 1e3, 3),
             "algo_bytes": algo,
             # dispatch ordinals of this kernel (0-based, in launch order) that the events bracket

@@ -121,6 +121,228 @@ int qg_repack_iq4xs(const void *raw, uint64_t ne0, uint64_t ne1, void *packed, i
     return QGPU_OK;
 }
 
+// ---------------------------------------------------------------- K-quant and Q8_0 records
+// Every packed format keeps the IQ4_XS nibble arrangement for its low four
+// bits: per sub-block ib (32 elements), "virtual byte" j < 16 holds element j
+// in its low nibble and element j + 16 in its high nibble, and dword
+// (row n, lane group g, ib) at KQ_Q + ((ib/4)*64 + g*16 + n)*16 + (ib%4)*4
+// holds virtual bytes 4g..4g+3.  Lane l = 16 g + n then loads its MFMA B
+// operand of four sub-blocks with one 16-byte load, K-slot 8g+c standing for
+// element 4g+c and slot 8g+4+c for element 16+4g+c, exactly as the activation
+// digits are laid out.  Per format:
+//   Q4_K  [0,256)     row n: d | dmin << 16, scales and mins as 6-bit fields
+//                     (sc0..sc4 | m7 bits 0-1 << 30), (m0..m4 | m7 bits 2-3 << 30),
+//                     (sc5, sc6, sc7, m5, m6 | m7 bits 4-5 << 30)
+//         [256,2304)  nibbles
+//   Q5_K  as Q4_K, then [2304,2816): lane l's 8 bytes at 2304 + 8 l, byte ib =
+//                     fifth bits of its elements 4g+c (bits 0-3) and 16+4g+c (bits 4-7)
+//   Q6_K  [0,256)     row n: the 16 int8 scales; [256,288) row n: fp16 d at 256 + 2n
+//         [288,2336)  low nibbles
+//         [2336,3360) lane l's 16 bytes at 2336 + 16 l: dword ib/2, byte c, bit pair
+//                     4 (ib%2) + {0: element 4g+c, 2: element 16+4g+c} = top two bits
+//   Q8_0  [0,256)     row n: the 8 fp16 d of its 32-element blocks
+//         [256,4352)  lane l's 64 bytes at 256 + (p*64 + l)*16, p < 4: int8 elements
+//                     4g..4g+3, 16+4g..16+4g+3 of sub-block 2p, then of sub-block 2p+1
+#define KQ_HB5 2304
+#define KQ_D6  256
+#define KQ_Q6  288
+#define KQ_HB6 2336
+#define KQ_Q   256
+
+static __device__ __forceinline__ uint32_t kq_qoff(int fmt, int n, int g, int ib)
+{
+    return (fmt == T_Q6_K ? KQ_Q6 : KQ_Q) + ((ib / 4) * 64 + g * 16 + n) * 16 + (ib % 4) * 4;
+}
+
+// get_scale_min_k4 of the reference (quant.h:21-29) for all eight sub-blocks
+static __device__ __forceinline__ void kq_scales(const uint8_t *sc12, uint32_t sc[8], uint32_t m[8])
+{
+    for (int j = 0; j < 8; j++) {
+        if (j < 4) { sc[j] = sc12[j] & 63; m[j] = sc12[j + 4] & 63; }
+        else {
+            sc[j] = (sc12[j + 4] & 15) | ((sc12[j - 4] >> 6) << 4);
+            m[j] = (sc12[j + 4] >> 4) | ((sc12[j] >> 6) << 4);
+        }
+    }
+}
+static __device__ __forceinline__ uint4 kq_hdr_pack(uint32_t dd, const uint32_t sc[8], const uint32_t m[8])
+{
+    uint4 h;
+    h.x = dd;
+    h.y = sc[0] | (sc[1] << 6) | (sc[2] << 12) | (sc[3] << 18) | (sc[4] << 24) | ((m[7] & 3u) << 30);
+    h.z = m[0] | (m[1] << 6) | (m[2] << 12) | (m[3] << 18) | (m[4] << 24) | (((m[7] >> 2) & 3u) << 30);
+    h.w = sc[5] | (sc[6] << 6) | (sc[7] << 12) | (m[5] << 18) | (m[6] << 24) | ((m[7] >> 4) << 30);
+    return h;
+}
+static __device__ __forceinline__ uint32_t kq_sc(uint4 h, int ib)
+{
+    return ib < 5 ? (h.y >> (6 * ib)) & 63u : (h.w >> (6 * (ib - 5))) & 63u;
+}
+static __device__ __forceinline__ uint32_t kq_m(uint4 h, int ib)
+{
+    if (ib < 5) return (h.z >> (6 * ib)) & 63u;
+    if (ib < 7) return (h.w >> (18 + 6 * (ib - 5))) & 63u;
+    return (h.y >> 30) | ((h.z >> 30) << 2) | ((h.w >> 30) << 4);
+}
+
+// One thread per (row, super-block): GGUF block(s) <-> this row's slices of the record.
+template <int FMT>
+__global__ void k_repack_kq(const uint8_t *__restrict__ raw, uint8_t *__restrict__ pk, uint64_t ne1, uint32_t nsb,
+                            uint64_t rows_pad, int unpack)
+{
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows_pad * nsb) return;
+    const uint64_t r = i / nsb;
+    const uint32_t s = (uint32_t)(i % nsb);
+    const uint32_t n = (uint32_t)(r % IQ4_TILE_ROWS);
+    const uint32_t BS = FMT == T_Q4_K ? 144 : FMT == T_Q5_K ? 176 : FMT == T_Q6_K ? 210 : 8 * 34;
+    uint8_t *rec = pk + ((r / IQ4_TILE_ROWS) * nsb + s) * packed_rec_bytes(FMT);
+    if (unpack && r >= ne1) return;
+    const bool live = r < ne1;
+    uint8_t *blk = (uint8_t *)raw + (live ? r * nsb * (uint64_t)BS + (uint64_t)s * BS : 0);
+    // element values of the super-block: low four bits lo4[e], upper bits hi[e] (Q5_K 1, Q6_K 2), Q8_0 bytes
+    uint8_t lo4[256], hi[256];
+    if (!unpack) {
+        if (FMT == T_Q8_0) {
+            for (int b = 0; b < 8; b++)
+                for (int e = 0; e < 32; e++) lo4[32 * b + e] = live ? blk[34 * b + 2 + e] : 0;
+        } else if (FMT == T_Q6_K) {
+            for (int e = 0; e < 256; e++) {
+                const int h = e / 128, qt = (e % 128) / 32, l = e % 32;
+                const uint8_t qlb = live ? blk[64 * h + (qt & 1) * 32 + l] : 0, qhb = live ? blk[128 + 32 * h + l] : 0;
+                lo4[e] = (qt < 2) ? (qlb & 15) : (qlb >> 4);
+                hi[e] = (qhb >> (2 * qt)) & 3;
+            }
+        } else {
+            const uint8_t *qs = blk + (FMT == T_Q5_K ? 48 : 16);
+            for (int e = 0; e < 256; e++) {
+                const int ib = e / 32, ep = e % 32;
+                const uint8_t b = live ? qs[32 * (ib / 2) + ep] : 0;
+                lo4[e] = (ib & 1) ? (b >> 4) : (b & 15);
+                hi[e] = FMT == T_Q5_K && live ? (blk[16 + ep] >> ib) & 1 : 0;
+            }
+        }
+        // headers
+        if (FMT == T_Q4_K || FMT == T_Q5_K) {
+            uint32_t sc[8], m[8];
+            kq_scales(blk + 4, sc, m);
+            *(uint4 *)(rec + n * 16) = live ? kq_hdr_pack(*(const uint32_t *)blk, sc, m) : make_uint4(0, 0, 0, 0);
+        } else if (FMT == T_Q6_K) {
+            for (int j = 0; j < 16; j++) rec[n * 16 + j] = live ? blk[192 + j] : 0;
+            *(uint16_t *)(rec + KQ_D6 + 2 * n) = live ? *(const uint16_t *)(blk + 208) : 0;
+        } else {
+            for (int b = 0; b < 8; b++) *(uint16_t *)(rec + n * 16 + 2 * b) = live ? *(const uint16_t *)(blk + 34 * b) : 0;
+        }
+        // quants
+        for (int ib = 0; ib < 8; ib++)
+            for (int g = 0; g < 4; g++) {
+                if (FMT == T_Q8_0) {
+                    uint8_t *q = rec + KQ_Q + ((ib / 2) * 64 + g * 16 + n) * 16 + (ib & 1) * 8;
+                    for (int c = 0; c < 4; c++) { q[c] = lo4[32 * ib + 4 * g + c]; q[4 + c] = lo4[32 * ib + 16 + 4 * g + c]; }
+                    continue;
+                }
+                uint32_t w = 0;
+                for (int c = 0; c < 4; c++)
+                    w |= (uint32_t)(lo4[32 * ib + 4 * g + c] | (lo4[32 * ib + 16 + 4 * g + c] << 4)) << (8 * c);
+                *(uint32_t *)(rec + kq_qoff(FMT, n, g, ib)) = w;
+                if (FMT == T_Q5_K) {
+                    uint32_t b = 0;
+                    for (int c = 0; c < 4; c++) b |= (uint32_t)(hi[32 * ib + 4 * g + c] << c) | (uint32_t)(hi[32 * ib + 16 + 4 * g + c] << (4 + c));
+                    rec[KQ_HB5 + (g * 16 + n) * 8 + ib] = (uint8_t)b;
+                }
+                if (FMT == T_Q6_K) {
+                    uint8_t *hb = rec + KQ_HB6 + (g * 16 + n) * 16 + (ib / 2) * 4;
+                    for (int c = 0; c < 4; c++) {
+                        const uint32_t v = hi[32 * ib + 4 * g + c] | (hi[32 * ib + 16 + 4 * g + c] << 2);
+                        hb[c] = (uint8_t)((hb[c] & ~(15u << (4 * (ib & 1)))) | (v << (4 * (ib & 1))));
+                    }
+                }
+            }
+        return;
+    }
+    // unpack: gather the element values back, then write the GGUF block(s)
+    for (int ib = 0; ib < 8; ib++)
+        for (int g = 0; g < 4; g++) {
+            if (FMT == T_Q8_0) {
+                const uint8_t *q = rec + KQ_Q + ((ib / 2) * 64 + g * 16 + n) * 16 + (ib & 1) * 8;
+                for (int c = 0; c < 4; c++) { lo4[32 * ib + 4 * g + c] = q[c]; lo4[32 * ib + 16 + 4 * g + c] = q[4 + c]; }
+                continue;
+            }
+            const uint32_t w = *(const uint32_t *)(rec + kq_qoff(FMT, n, g, ib));
+            for (int c = 0; c < 4; c++) {
+                lo4[32 * ib + 4 * g + c] = (w >> (8 * c)) & 15;
+                lo4[32 * ib + 16 + 4 * g + c] = (w >> (8 * c + 4)) & 15;
+            }
+            if (FMT == T_Q5_K) {
+                const uint32_t b = rec[KQ_HB5 + (g * 16 + n) * 8 + ib];
+                for (int c = 0; c < 4; c++) { hi[32 * ib + 4 * g + c] = (b >> c) & 1; hi[32 * ib + 16 + 4 * g + c] = (b >> (4 + c)) & 1; }
+            }
+            if (FMT == T_Q6_K) {
+                const uint8_t *hb = rec + KQ_HB6 + (g * 16 + n) * 16 + (ib / 2) * 4;
+                for (int c = 0; c < 4; c++) {
+                    const uint32_t v = hb[c] >> (4 * (ib & 1));
+                    hi[32 * ib + 4 * g + c] = v & 3;
+                    hi[32 * ib + 16 + 4 * g + c] = (v >> 2) & 3;
+                }
+            }
+        }
+    if (FMT == T_Q8_0) {
+        for (int b = 0; b < 8; b++) {
+            *(uint16_t *)(blk + 34 * b) = *(const uint16_t *)(rec + n * 16 + 2 * b);
+            for (int e = 0; e < 32; e++) blk[34 * b + 2 + e] = lo4[32 * b + e];
+        }
+    } else if (FMT == T_Q6_K) {
+        for (int j = 0; j < 16; j++) blk[192 + j] = rec[n * 16 + j];
+        *(uint16_t *)(blk + 208) = *(const uint16_t *)(rec + KQ_D6 + 2 * n);
+        for (int h = 0; h < 2; h++)
+            for (int l = 0; l < 32; l++) {
+                const int e0 = 128 * h + l;
+                blk[64 * h + l] = (uint8_t)(lo4[e0] | (lo4[e0 + 64] << 4));
+                blk[64 * h + 32 + l] = (uint8_t)(lo4[e0 + 32] | (lo4[e0 + 96] << 4));
+                blk[128 + 32 * h + l] = (uint8_t)(hi[e0] | (hi[e0 + 32] << 2) | (hi[e0 + 64] << 4) | (hi[e0 + 96] << 6));
+            }
+    } else {
+        const uint4 h = *(const uint4 *)(rec + n * 16);
+        *(uint32_t *)blk = h.x;
+        uint32_t sc[8], m[8];
+        for (int j = 0; j < 8; j++) { sc[j] = kq_sc(h, j); m[j] = kq_m(h, j); }
+        uint8_t *s12 = blk + 4;
+        for (int j = 0; j < 4; j++) {
+            s12[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+            s12[j + 4] = (uint8_t)(m[j] | ((m[j + 4] >> 4) << 6));
+            s12[j + 8] = (uint8_t)((sc[j + 4] & 15) | ((m[j + 4] & 15) << 4));
+        }
+        uint8_t *qs = blk + (FMT == T_Q5_K ? 48 : 16);
+        for (int j = 0; j < 4; j++)
+            for (int ep = 0; ep < 32; ep++) qs[32 * j + ep] = (uint8_t)(lo4[64 * j + ep] | (lo4[64 * j + 32 + ep] << 4));
+        if (FMT == T_Q5_K)
+            for (int ep = 0; ep < 32; ep++) {
+                uint32_t b = 0;
+                for (int ib = 0; ib < 8; ib++) b |= (uint32_t)hi[32 * ib + ep] << ib;
+                blk[16 + ep] = (uint8_t)b;
+            }
+    }
+}
+
+// packed <-> GGUF rows for every packed format (unpack = 1: packed -> raw)
+int qg_repack(int type, const void *raw, uint64_t ne0, uint64_t ne1, void *packed, int unpack)
+{
+    if (type == T_IQ4_XS) return qg_repack_iq4xs(raw, ne0, ne1, packed, unpack);
+    const uint32_t nsb = (uint32_t)(ne0 / 256);
+    const uint64_t rows_pad = (ne1 + IQ4_TILE_ROWS - 1) / IQ4_TILE_ROWS * IQ4_TILE_ROWS;
+    const uint64_t n = rows_pad * nsb;
+    const dim3 grid((unsigned)((n + 63) / 64)), blk(64);
+    switch (type) {
+    case T_Q4_K: hipLaunchKernelGGL(k_repack_kq<T_Q4_K>, grid, blk, 0, qg::stream, (const uint8_t *)raw, (uint8_t *)packed, ne1, nsb, rows_pad, unpack); break;
+    case T_Q5_K: hipLaunchKernelGGL(k_repack_kq<T_Q5_K>, grid, blk, 0, qg::stream, (const uint8_t *)raw, (uint8_t *)packed, ne1, nsb, rows_pad, unpack); break;
+    case T_Q6_K: hipLaunchKernelGGL(k_repack_kq<T_Q6_K>, grid, blk, 0, qg::stream, (const uint8_t *)raw, (uint8_t *)packed, ne1, nsb, rows_pad, unpack); break;
+    case T_Q8_0: hipLaunchKernelGGL(k_repack_kq<T_Q8_0>, grid, blk, 0, qg::stream, (const uint8_t *)raw, (uint8_t *)packed, ne1, nsb, rows_pad, unpack); break;
+    default: return QGPU_E_TYPE;
+    }
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
 // ---------------------------------------------------------------- activation prep
 // A operand of K-step (sb, ib) for plane a (tokens 4a..4a+3): 64 lanes x 8 bytes;
 // lane l = g*16 + m holds, for A row m = dgt*4 + t, the digit dgt of token t at
@@ -440,10 +662,8 @@ static __device__ __forceinline__ void iq4_decode8(uint32_t q, uint32_t &x_lo, u
 // Measured on MI355X (rings of 2..5 x 1..2, with and without tail loads that
 // keep the wait counts exact): all within +-3%, deeper rings slightly slower;
 // 3 / 1 keeps the plain kernel at 93 VGPRs (5 waves per SIMD).
-struct IQ4W {
-    uint2 hdr;
-    uint4 qa, qb;
-};
+template <int FMT> struct WRec;                              // a lane's slice of one record
+template <> struct WRec<T_IQ4_XS> { uint2 hdr; uint4 qa, qb; };
 template <int NA>
 struct IQ4A {
     uint4 av[NA][4];
@@ -454,13 +674,6 @@ struct IQ4A {
 // record, digit plane 0 and digit scales; lanes add their own offsets.  The
 // digit scale of lane group g (digit g) and token t is 2^(8 g) xs[t]: only the
 // four token scales are loaded (scalar loads), 2^(8 g) is a lane constant.
-static __device__ __forceinline__ void iq4_load_w(IQ4W &w, const uint8_t *rec, int lane, int n)
-{
-    w.hdr = *(const uint2 *)(rec + n * 8);
-    w.qa = *(const uint4 *)(rec + IQ4_HDR_BYTES + lane * 16);
-    w.qb = *(const uint4 *)(rec + IQ4_HDR_BYTES + 1024 + lane * 16);
-}
-
 template <int NA>
 static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab, const float *xsb, int lane)
 {
@@ -474,7 +687,7 @@ static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab
 }
 
 template <int NA>
-static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA> &x, float p8g, float (&accf)[NA][4])
+static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, const IQ4A<NA> &x, float p8g, float (&accf)[NA][4])
 {
     const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
     v4i acci[NA];
@@ -508,6 +721,157 @@ static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA>
     }
 }
 
+// ---- K-quant and Q8_0 records on the same int8 matrix-core path.  A lane's
+// slice of one record (see the record layouts above), then the per-sub-block
+// work: the integer B operand (0..15 / 0..31 / 0..63 / int8 bytes), the exact
+// int32 sub-block products, the scales.
+//   Q4_K, Q5_K: sum_ib sc_ib D_ib in int32 (24-bit products, as IQ4_XS) and the
+//     min term sum_ib m_ib (sum of the sub-block's activations) in the matrix
+//     core itself: a second MFMA chain whose B operand is m_ib in every K slot;
+//     output d * first - dmin * second.
+//   Q6_K: two scale groups of 16 per sub-block = the lane's two dwords (elements
+//     4g+c in 0..15, 16+4g+c in 16..31): one MFMA per group with the other
+//     dword zero, and the -32 offset of the 6-bit values as one more chained
+//     MFMA with the constant byte -32.
+//   Q8_0: int8 quants as they are; the fp16 scale of each 32-element block in fp32.
+template <> struct WRec<T_Q4_K> { uint4 hdr; uint4 qa, qb; };
+template <> struct WRec<T_Q5_K> { uint4 hdr; uint4 qa, qb; uint2 hb; };
+template <> struct WRec<T_Q6_K> { uint4 sc; uint4 qa, qb; uint4 hb; uint32_t d; };
+template <> struct WRec<T_Q8_0> { uint4 hdr; uint4 q[4]; };
+
+template <int FMT>
+static __device__ __forceinline__ void kq_load_w(WRec<FMT> &w, const uint8_t *rec, int lane, int n)
+{
+    if constexpr (FMT == T_IQ4_XS) {
+        w.hdr = *(const uint2 *)(rec + n * 8);
+        w.qa = *(const uint4 *)(rec + IQ4_HDR_BYTES + lane * 16);
+        w.qb = *(const uint4 *)(rec + IQ4_HDR_BYTES + 1024 + lane * 16);
+    } else if constexpr (FMT == T_Q8_0) {
+        w.hdr = *(const uint4 *)(rec + n * 16);
+#pragma unroll
+        for (int p = 0; p < 4; p++) w.q[p] = *(const uint4 *)(rec + KQ_Q + (p * 64 + lane) * 16);
+    } else if constexpr (FMT == T_Q6_K) {
+        w.sc = *(const uint4 *)(rec + n * 16);
+        w.d = *(const uint16_t *)(rec + KQ_D6 + 2 * n);
+        w.qa = *(const uint4 *)(rec + KQ_Q6 + lane * 16);
+        w.qb = *(const uint4 *)(rec + KQ_Q6 + 1024 + lane * 16);
+        w.hb = *(const uint4 *)(rec + KQ_HB6 + lane * 16);
+    } else {
+        w.hdr = *(const uint4 *)(rec + n * 16);
+        w.qa = *(const uint4 *)(rec + KQ_Q + lane * 16);
+        w.qb = *(const uint4 *)(rec + KQ_Q + 1024 + lane * 16);
+        if constexpr (FMT == T_Q5_K) w.hb = *(const uint2 *)(rec + KQ_HB5 + lane * 8);
+    }
+}
+
+static __device__ __forceinline__ uint32_t u4_get(uint4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+// bit c (c < 4) of x to bit 0 of byte c
+static __device__ __forceinline__ uint32_t spread4(uint32_t x) { return (x * 0x00204081u) & 0x01010101u; }
+
+template <int NA>
+static __device__ __forceinline__ long kq_aop(const IQ4A<NA> &x, int a, int ib)
+{
+    const uint4 q4 = x.av[a][ib >> 1];
+    return (ib & 1) ? (long)(((uint64_t)q4.w << 32) | q4.z) : (long)(((uint64_t)q4.y << 32) | q4.x);
+}
+static __device__ __forceinline__ long kq_b(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
+
+template <int FMT, int NA>
+static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A<NA> &x, float p8g, float (&accf)[NA][4])
+{
+    const v4i z4 = (v4i){0, 0, 0, 0};
+    if constexpr (FMT == T_Q8_0) {
+        float accs[NA][4];
+#pragma unroll
+        for (int a = 0; a < NA; a++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) accs[a][i] = 0.0f;
+#pragma unroll
+        for (int ib = 0; ib < 8; ib++) {
+            const uint4 q = w.q[ib >> 1];
+            const long b = (ib & 1) ? kq_b(q.z, q.w) : kq_b(q.x, q.y);
+            const float dib = h2f((u4_get(w.hdr, ib >> 1) >> (16 * (ib & 1))) & 0xFFFFu);
+#pragma unroll
+            for (int a = 0; a < NA; a++) {
+                const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(kq_aop<NA>(x, a, ib), b, z4, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) accs[a][i] = fmaf((float)D[i], dib, accs[a][i]);
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            accf[a][0] += accs[a][0] * (p8g * x.xt[a].x);
+            accf[a][1] += accs[a][1] * (p8g * x.xt[a].y);
+            accf[a][2] += accs[a][2] * (p8g * x.xt[a].z);
+            accf[a][3] += accs[a][3] * (p8g * x.xt[a].w);
+        }
+    } else if constexpr (FMT == T_Q6_K) {
+        const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
+        const uint32_t NEG32 = 0xE0E0E0E0u;                     // int8 -32 in every byte
+        v4i acc[NA];
+#pragma unroll
+        for (int a = 0; a < NA; a++) acc[a] = z4;
+#pragma unroll
+        for (int ib = 0; ib < 8; ib++) {
+            const uint32_t hw = u4_get(w.hb, ib >> 1) >> (4 * (ib & 1));
+            const uint32_t lo = (qd[ib] & 0x0F0F0F0Fu) | ((hw << 4) & 0x30303030u);
+            const uint32_t hi = ((qd[ib] >> 4) & 0x0F0F0F0Fu) | ((hw << 2) & 0x30303030u);
+            const uint32_t scw = u4_get(w.sc, ib >> 1);
+            const int sa = (int)(int8_t)((scw >> (16 * (ib & 1))) & 0xFF), sb2 = (int)(int8_t)((scw >> (16 * (ib & 1) + 8)) & 0xFF);
+#pragma unroll
+            for (int a = 0; a < NA; a++) {
+                const long aop = kq_aop<NA>(x, a, ib);
+                const v4i DA = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                    aop, kq_b(lo, 0), __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, kq_b(NEG32, 0), z4, 0, 0, 0), 0, 0, 0);
+                const v4i DB = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                    aop, kq_b(0, hi), __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, kq_b(0, NEG32), z4, 0, 0, 0), 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[a][i] = mad24(DA[i], sa, mad24(DB[i], sb2, acc[a][i]));
+            }
+        }
+        const float dg = h2f(w.d & 0xFFFFu) * p8g;
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            accf[a][0] += (float)acc[a][0] * (dg * x.xt[a].x);
+            accf[a][1] += (float)acc[a][1] * (dg * x.xt[a].y);
+            accf[a][2] += (float)acc[a][2] * (dg * x.xt[a].z);
+            accf[a][3] += (float)acc[a][3] * (dg * x.xt[a].w);
+        }
+    } else {                                                   // Q4_K, Q5_K
+        const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
+        v4i acq[NA], acm[NA];
+#pragma unroll
+        for (int a = 0; a < NA; a++) { acq[a] = z4; acm[a] = z4; }
+#pragma unroll
+        for (int ib = 0; ib < 8; ib++) {
+            uint32_t lo = qd[ib] & 0x0F0F0F0Fu, hi = (qd[ib] >> 4) & 0x0F0F0F0Fu;
+            if constexpr (FMT == T_Q5_K) {
+                const uint32_t hbb = ((ib < 4 ? w.hb.x : w.hb.y) >> (8 * (ib & 3))) & 0xFFu;
+                lo |= spread4(hbb & 15u) << 4;
+                hi |= spread4(hbb >> 4) << 4;
+            }
+            const int sc = (int)kq_sc(w.hdr, ib);
+            const uint32_t mrep = kq_m(w.hdr, ib) * 0x01010101u;
+#pragma unroll
+            for (int a = 0; a < NA; a++) {
+                const long aop = kq_aop<NA>(x, a, ib);
+                const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, kq_b(lo, hi), z4, 0, 0, 0);
+                acm[a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, kq_b(mrep, mrep), acm[a], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; i++) acq[a][i] = mad24(D[i], sc, acq[a][i]);
+            }
+        }
+        const float dg = h2f(w.hdr.x & 0xFFFFu) * p8g, mg = h2f(w.hdr.x >> 16) * p8g;
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            const float xt[4] = { x.xt[a].x, x.xt[a].y, x.xt[a].z, x.xt[a].w };
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                accf[a][i] += (float)acq[a][i] * (dg * xt[i]) - (float)acm[a][i] * (mg * xt[i]);
+        }
+    }
+}
+
 #ifndef IQ4_WDEPTH
 #define IQ4_WDEPTH 3    // weight records in flight per wave
 #endif
@@ -521,11 +885,11 @@ static __device__ __forceinline__ void iq4_compute(const IQ4W &w, const IQ4A<NA>
 // into partial planes.  Plain launches (MODE 0) compile without either.
 #define IQ4_RMS   1
 #define IQ4_SPLIT 2
-template <int NA, int NW, int MODE>
+template <int FMT, int NA, int NW, int MODE>
 #ifndef IQ4_MINW
 #define IQ4_MINW 1
 #endif
-__global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs args)
+__global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs args)
 {
     __shared__ float red[NW][NA][4][16];
     __shared__ float rsc[QGPU_MAX_B];
@@ -539,7 +903,8 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
     const GemvMat &M = args.m[k];
     const uint32_t T = tile - M.tile0 + M.tile_first;
     const int nsb = args.nsb;
-    const uint8_t *rec0 = M.W + (uint64_t)T * nsb * IQ4_REC_BYTES;
+    constexpr uint32_t REC = FMT == T_IQ4_XS ? IQ4_REC_BYTES : FMT == T_Q4_K ? 2304 : FMT == T_Q5_K ? 2816 : FMT == T_Q6_K ? 3360 : 4352;
+    const uint8_t *rec0 = M.W + (uint64_t)T * nsb * REC;
     const int kb0 = kq * nsb / ks, nkb = (kq + 1) * nsb / ks - kb0;
     const int sb0 = kb0 + wv * nkb / NW, sb1 = kb0 + (wv + 1) * nkb / NW;
     RmsPart rp;
@@ -557,9 +922,9 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
     // indices are compile-time after unrolling by IQ4_UNROLL).  Each step
     // issues its digit loads before its weight loads (vmcnt retires loads in
     // issue order, so a wait for the digits need not cover the newer weights).
-    IQ4W wr[IQ4_WDEPTH];
+    WRec<FMT> wr[IQ4_WDEPTH];
     IQ4A<NA> ar[IQ4_ADEPTH];
-#define LOAD_W(slot, sbx) iq4_load_w(wr[slot], rec0 + (uint64_t)(sbx) * IQ4_REC_BYTES, lane, n)
+#define LOAD_W(slot, sbx) kq_load_w<FMT>(wr[slot], rec0 + (uint64_t)(sbx) * REC, lane, n)
 #define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * 4096, args.xs + (uint64_t)(sbx) * 16, lane)
 #pragma unroll
     for (int d = 0; d < IQ4_WDEPTH - 1 || d < IQ4_ADEPTH - 1; d++) {
@@ -573,7 +938,8 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_iq4(const GemvArgs a
                 const int pw = sb + d + IQ4_WDEPTH - 1, pa = sb + d + IQ4_ADEPTH - 1;
                 if (pa < sb1) LOAD_A((d + IQ4_ADEPTH - 1) % IQ4_ADEPTH, pa);
                 if (pw < sb1) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
-                iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], p8g, accf);
+                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], p8g, accf);
+                else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], p8g, accf);
             }
         }
     }
@@ -830,6 +1196,21 @@ static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits, bool d
 
 // One launch for the matrices idx[0..cnt) of one format.  IQ4_XS reads the
 // digit planes already in the workspace; the other formats read fp32 rows x.
+// one matrix-core GEMV launch: format FMT, NA digit planes, nw waves per tile, MODE bits
+template <int FMT>
+static void launch_mfma(const GemvArgs &A, uint32_t blocks, int na, int nw, int mode)
+{
+#define MF_GO(NA_, NW_, M_) hipLaunchKernelGGL((k_gemv_mfma<FMT, NA_, NW_, M_>), dim3(blocks), dim3(64 * NW_), 0, qg::stream, A)
+#define MF_NW(NA_, M_) do { if (nw == 1) MF_GO(NA_, 1, M_); else if (nw == 2) MF_GO(NA_, 2, M_); \
+                            else if (nw == 4) MF_GO(NA_, 4, M_); else MF_GO(NA_, 8, M_); } while (0)
+#define MF_MODE(NA_) do { if (mode == 0) MF_NW(NA_, 0); else if (mode == IQ4_RMS) MF_NW(NA_, IQ4_RMS); \
+                          else if (mode == IQ4_SPLIT) MF_NW(NA_, IQ4_SPLIT); else MF_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
+    if (na == 1) MF_MODE(1); else MF_MODE(2);
+#undef MF_MODE
+#undef MF_NW
+#undef MF_GO
+}
+
 static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x, uint64_t ldx,
                         int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
                         const uint64_t *r1s, int ks, float eps, bool deferred)
@@ -843,8 +1224,8 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
         A.rss = ws_rss(); A.rss_nsb = (int)(W0->ne0 / 256); A.rss_inv_n = 1.0f / (float)W0->ne0; A.eps = eps;
     }
     A.nsb = (int)(W0->ne0 / 256);
-    const bool iq4 = W0->type == T_IQ4_XS;
-    const uint32_t per = iq4 ? IQ4_TILE_ROWS : 8;
+    const bool mfma = W0->packed;
+    const uint32_t per = mfma ? IQ4_TILE_ROWS : 8;
     uint32_t tiles = 0;
     for (int j = 0; j < cnt; j++) {
         const qgpu_tensor *W = Ws[idx[j]];
@@ -861,7 +1242,7 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
         tiles += (uint32_t)((hi + per - 1) / per - lo / per);
     }
     if (!tiles) return QGPU_OK;
-    if (iq4) {
+    if (mfma) {
         if (W0->ne0 > MAX_K) return QGPU_E_RANGE;
         const int na = n > 4 ? 2 : 1;
         A.A = (const uint8_t *)qg::ws;
@@ -881,15 +1262,14 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
         if (A.rss && nw < 4) nw = 4;                        // row factors: <= 2 tokens per wave
         const int mode = (A.rss ? IQ4_RMS : 0) | (ks > 1 ? IQ4_SPLIT : 0);
-#define IQ4_GO(NA_, NW_, M_) hipLaunchKernelGGL((k_gemv_iq4<NA_, NW_, M_>), dim3(tiles * ks), dim3(64 * NW_), 0, qg::stream, A)
-#define IQ4_NW(NA_, M_) do { if (nw == 1) IQ4_GO(NA_, 1, M_); else if (nw == 2) IQ4_GO(NA_, 2, M_); \
-                             else if (nw == 4) IQ4_GO(NA_, 4, M_); else IQ4_GO(NA_, 8, M_); } while (0)
-#define IQ4_MODE(NA_) do { if (mode == 0) IQ4_NW(NA_, 0); else if (mode == IQ4_RMS) IQ4_NW(NA_, IQ4_RMS); \
-                           else if (mode == IQ4_SPLIT) IQ4_NW(NA_, IQ4_SPLIT); else IQ4_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
-        if (na == 1) IQ4_MODE(1); else IQ4_MODE(2);
-#undef IQ4_MODE
-#undef IQ4_NW
-#undef IQ4_GO
+        switch (W0->type) {
+        case T_IQ4_XS: launch_mfma<T_IQ4_XS>(A, tiles * ks, na, nw, mode); break;
+        case T_Q4_K: launch_mfma<T_Q4_K>(A, tiles * ks, na, nw, mode); break;
+        case T_Q5_K: launch_mfma<T_Q5_K>(A, tiles * ks, na, nw, mode); break;
+        case T_Q6_K: launch_mfma<T_Q6_K>(A, tiles * ks, na, nw, mode); break;
+        case T_Q8_0: launch_mfma<T_Q8_0>(A, tiles * ks, na, nw, mode); break;
+        default: return QGPU_E_TYPE;
+        }
         QG_LAUNCH_CHECK();
         return QGPU_OK;
     }
@@ -915,7 +1295,7 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
     return QGPU_OK;
 }
 
-// act == NULL: IQ4_XS matrices only, on the digit planes of the last prepare.
+// act == NULL: packed matrices only, on the digit planes of the last prepare.
 static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n, float *const *outs,
                       const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s, int ks = 1)
 {
@@ -924,15 +1304,15 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *a
     if (!Ws || !outs || !ldos || n_mat < 1 || n_mat > QGPU_MAX_MULTI || n < 1 || n > QGPU_MAX_B || !Ws[0])
         return QGPU_E_ARG;
     const uint64_t ne0 = Ws[0]->ne0;
-    bool any_iq4 = false, any_valu = false;
+    bool any_mfma = false, any_valu = false;
     for (int j = 0; j < n_mat; j++) {
         if (!Ws[j] || !outs[j] || Ws[j]->ne0 != ne0) return QGPU_E_ARG;
         if (n > 1 && ldos[j] < (r1s ? r1s[j] : Ws[j]->ne1)) return QGPU_E_ARG;
         if (r0s && (r0s[j] > r1s[j] || r1s[j] > Ws[j]->ne1)) return QGPU_E_ARG;
-        if (Ws[j]->type == T_IQ4_XS) any_iq4 = true; else any_valu = true;
+        if (Ws[j]->packed) any_mfma = true; else any_valu = true;
     }
     if (ks < 1 || ks > 8 || (ks > 1 && (n_mat != 1 || any_valu || r0s || (int)(ne0 / 256) < ks))) return QGPU_E_ARG;
-    const float *xv = nullptr;                              // fp32 rows for the non-IQ4_XS kernels
+    const float *xv = nullptr;                              // fp32 rows for the VALU kernel (unpacked formats)
     uint64_t ldxv = ne0;
     bool deferred = false;
     if (!act) {
@@ -945,9 +1325,9 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *a
             if (!xv || (n > 1 && ldxv < ne0)) return QGPU_E_ARG;
             if (ldxv % 4 || ((uintptr_t)xv & 15)) return QGPU_E_ARG;   // float4 activation loads
         }
-        if (any_iq4 || xform) {
-            if (!any_iq4 && ne0 % 256) return QGPU_E_RANGE;
-            rc = prep_act(act, n, ne0, any_iq4 ? 1 : 0, ne0 <= 64 * 256, &deferred);    // row factors: <= 64 sums
+        if (any_mfma || xform) {
+            if (!any_mfma && ne0 % 256) return QGPU_E_RANGE;
+            rc = prep_act(act, n, ne0, any_mfma ? 1 : 0, ne0 <= 64 * 256, &deferred);   // row factors: <= 64 sums
             if (rc) return rc;
         }
     }
@@ -1000,7 +1380,7 @@ extern "C" int qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, cons
 extern "C" int qgpu_gemv_act_split(const qgpu_tensor *W, const qgpu_act *act, int n, float *part, uint64_t ldp,
                                    int ks)
 {
-    if (!act || !W || !part || W->type != T_IQ4_XS) return QGPU_E_ARG;
+    if (!act || !W || !part || !W->packed) return QGPU_E_ARG;
     if (n > 1 && ldp < W->ne1) return QGPU_E_ARG;
     if (ks == 1) return gemv_multi(&W, 1, act, n, &part, &ldp, 0, nullptr, nullptr, 1);
     return gemv_multi(&W, 1, act, n, &part, &ldp, 0, nullptr, nullptr, ks);
@@ -1012,7 +1392,7 @@ extern "C" int qgpu_gemv_act_split(const qgpu_tensor *W, const qgpu_act *act, in
 // leaves 1.6x more work on the CUs that get two tiles).
 extern "C" int qgpu_gemv_split_ks(const qgpu_tensor *W)
 {
-    if (!W || W->type != T_IQ4_XS) return 1;
+    if (!W || !W->packed) return 1;
     const uint64_t tiles = (W->ne1 + IQ4_TILE_ROWS - 1) / IQ4_TILE_ROWS, nsb = W->ne0 / 256;
     if (tiles > 640) return 1;
     int ks = (int)(1280 / tiles);
@@ -1065,7 +1445,7 @@ extern "C" int qgpu_act_prepare(const qgpu_act *act, int n, uint64_t ne0)
 
 extern "C" int qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, int flags)
 {
-    if (!W || W->type != T_IQ4_XS) return QGPU_E_TYPE;
+    if (!W || !W->packed) return QGPU_E_TYPE;
     return gemv_multi(&W, 1, nullptr, n, &out, &ldo, flags, nullptr, nullptr);
 }
 
@@ -1078,7 +1458,10 @@ extern "C" int qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64
 }
 
 // ---------------------------------------------------------------- dequant rows (embedding)
-template <int FMT>
+// Scalar dequant of whole rows, bit-exact with the reference dequant_row
+// (quant.c:86-208: round-to-nearest products, no FMA), from the packed tile
+// records (PK) or the GGUF row layout.
+template <int FMT, int PK>
 __global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t *__restrict__ W, uint64_t ne0, uint64_t ne1,
                                                       const uint32_t *__restrict__ rows, float *__restrict__ out,
                                                       uint64_t ldo)
@@ -1109,6 +1492,58 @@ __global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t *__restrict_
                     w[16 + 4 * g + cc] = __fmul_rn(dl, (float)kv[byte >> 4]);
                 }
             }
+        } else if (PK) {
+            const uint32_t nsb = (uint32_t)(ne0 / 256), sb = c >> 3, ib = c & 7;
+            const uint8_t *rec = W + ((uint64_t)(r / IQ4_TILE_ROWS) * nsb + sb) * packed_rec_bytes(FMT);
+            const int n = (int)(r % IQ4_TILE_ROWS);
+            float d1 = 0.0f, m1 = 0.0f, ds0 = 0.0f, ds1 = 0.0f;
+            if (FMT == T_Q4_K || FMT == T_Q5_K) {
+                const uint4 h = *(const uint4 *)(rec + n * 16);
+                d1 = __fmul_rn(h2f(h.x & 0xFFFFu), (float)kq_sc(h, (int)ib));
+                m1 = __fmul_rn(h2f(h.x >> 16), (float)kq_m(h, (int)ib));
+            } else if (FMT == T_Q6_K) {
+                const float d = h2f(*(const uint16_t *)(rec + KQ_D6 + 2 * n));
+                ds0 = __fmul_rn(d, (float)(int8_t)rec[n * 16 + 2 * ib]);
+                ds1 = __fmul_rn(d, (float)(int8_t)rec[n * 16 + 2 * ib + 1]);
+            } else {
+                ds0 = h2f(*(const uint16_t *)(rec + n * 16 + 2 * ib));
+            }
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++) {
+                    int qa, qb;                           // elements 4g+cc and 16+4g+cc of the sub-block
+                    if (FMT == T_Q8_0) {
+                        const uint8_t *q = rec + KQ_Q + ((ib / 2) * 64 + g * 16 + n) * 16 + (ib & 1) * 8;
+                        qa = (int8_t)q[cc];
+                        qb = (int8_t)q[4 + cc];
+                    } else {
+                        const uint32_t byte = (*(const uint32_t *)(rec + kq_qoff(FMT, n, g, (int)ib)) >> (8 * cc)) & 0xFF;
+                        qa = byte & 15;
+                        qb = byte >> 4;
+                        if (FMT == T_Q5_K) {
+                            const uint32_t hb = rec[KQ_HB5 + (g * 16 + n) * 8 + ib];
+                            qa += ((hb >> cc) & 1) << 4;
+                            qb += ((hb >> (4 + cc)) & 1) << 4;
+                        }
+                        if (FMT == T_Q6_K) {
+                            const uint32_t hb = rec[KQ_HB6 + (g * 16 + n) * 16 + (ib / 2) * 4 + cc] >> (4 * (ib & 1));
+                            qa = (qa | ((hb & 3) << 4)) - 32;
+                            qb = (qb | (((hb >> 2) & 3) << 4)) - 32;
+                        }
+                    }
+                    if (FMT == T_Q4_K || FMT == T_Q5_K) {
+                        w[4 * g + cc] = __fsub_rn(__fmul_rn(d1, (float)qa), m1);
+                        w[16 + 4 * g + cc] = __fsub_rn(__fmul_rn(d1, (float)qb), m1);
+                    } else if (FMT == T_Q6_K) {
+                        w[4 * g + cc] = __fmul_rn(ds0, (float)qa);
+                        w[16 + 4 * g + cc] = __fmul_rn(ds1, (float)qb);
+                    } else {
+                        w[4 * g + cc] = __fmul_rn(ds0, (float)qa);
+                        w[16 + 4 * g + cc] = __fmul_rn(ds0, (float)qb);
+                    }
+                }
+            }
         } else {
             const uint64_t rb = (FMT == T_F32) ? ne0 * 4 : (FMT == T_Q8_0 ? ne0 / 32 * 34 :
                                 ne0 / 256 * (FMT == T_Q4_K ? 144 : FMT == T_Q5_K ? 176 : 210));
@@ -1126,15 +1561,19 @@ extern "C" int qgpu_dequant_rows(const qgpu_tensor *W, const uint32_t *rows, int
     if (!W || !rows || !out || n < 0 || (n > 1 && ldo < W->ne0) || W->ne0 % 32) return QGPU_E_ARG;
     if (!n) return QGPU_OK;
     const dim3 grid((unsigned)n), blk(256);
+#define DQ(F, P) hipLaunchKernelGGL((k_dequant_rows<F, P>), grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo)
+#define DQ2(F) do { if (W->packed) DQ(F, 1); else DQ(F, 0); } while (0)
     switch (W->type) {
-    case T_IQ4_XS: hipLaunchKernelGGL(k_dequant_rows<T_IQ4_XS>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
-    case T_F32: hipLaunchKernelGGL(k_dequant_rows<T_F32>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
-    case T_Q8_0: hipLaunchKernelGGL(k_dequant_rows<T_Q8_0>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
-    case T_Q4_K: hipLaunchKernelGGL(k_dequant_rows<T_Q4_K>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
-    case T_Q5_K: hipLaunchKernelGGL(k_dequant_rows<T_Q5_K>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
-    case T_Q6_K: hipLaunchKernelGGL(k_dequant_rows<T_Q6_K>, grid, blk, 0, qg::stream, (const uint8_t *)W->data, W->ne0, W->ne1, rows, out, ldo); break;
+    case T_IQ4_XS: DQ(T_IQ4_XS, 1); break;
+    case T_F32: DQ(T_F32, 0); break;
+    case T_Q8_0: DQ2(T_Q8_0); break;
+    case T_Q4_K: DQ2(T_Q4_K); break;
+    case T_Q5_K: DQ2(T_Q5_K); break;
+    case T_Q6_K: DQ2(T_Q6_K); break;
     default: return QGPU_E_TYPE;
     }
+#undef DQ2
+#undef DQ
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }

@@ -6,12 +6,28 @@
 
 enum { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
 
-// Packed IQ4_XS: rows grouped in tiles of 16; per (tile, super-block) one
-// 2176-byte record = 16 x 8-byte row headers (d, scales_h, scales_l) followed by
-// 2048 bytes of nibbles ordered for the matrix core (see gemv.hip).
+// Packed matrices: rows grouped in tiles of 16; per (tile, 256-column
+// super-block) one record holding the 16 row slices, ordered for the matrix
+// core (see gemv.hip).  The record is as large as the 16 GGUF row slices.
+//   IQ4_XS 2176 = 16 x 8 B headers (d, scales) + 2048 B nibbles
+//   Q4_K   2304 = 16 x 16 B headers (d, dmin, 6-bit scales and mins) + 2048 B nibbles
+//   Q5_K   2816 = Q4_K + 512 B fifth bits
+//   Q6_K   3360 = 16 x 16 B int8 scales + 16 x 2 B d + 2048 B low nibbles + 1024 B high bit pairs
+//   Q8_0   4352 = 16 x 8 fp16 d + 4096 B int8 quants
 #define IQ4_TILE_ROWS   16
 #define IQ4_REC_BYTES   2176
 #define IQ4_HDR_BYTES   128
+static inline __host__ __device__ uint32_t packed_rec_bytes(int type)
+{
+    switch (type) {
+    case T_IQ4_XS: return 2176;
+    case T_Q4_K: return 2304;
+    case T_Q5_K: return 2816;
+    case T_Q6_K: return 3360;
+    case T_Q8_0: return 4352;
+    default: return 0;
+    }
+}
 
 struct qgpu_tensor {
     int      type;
@@ -19,7 +35,7 @@ struct qgpu_tensor {
     void    *data;        // device bytes
     uint64_t bytes;       // device allocation size
     uint64_t algo_bytes;  // GGUF size of the matrix
-    int      packed;      // 1: IQ4_XS tile layout
+    int      packed;      // 1: tile records (IQ4_XS, Q4_K, Q5_K, Q6_K, Q8_0 with ne0 % 256 == 0)
 };
 
 namespace qg {

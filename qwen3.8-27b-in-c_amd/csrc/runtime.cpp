@@ -43,7 +43,7 @@ size_t row_bytes(int t, uint64_t ne0)
 }  // namespace qg
 
 // implemented in gemv.hip
-int qg_repack_iq4xs(const void *raw, uint64_t ne0, uint64_t ne1, void *packed, int unpack);
+int qg_repack(int type, const void *raw, uint64_t ne0, uint64_t ne1, void *packed, int unpack);
 size_t qg_gemv_workspace_bytes();
 
 extern "C" int qgpu_init(int device)
@@ -185,13 +185,13 @@ static int make_tensor(const void *dev_raw, int type, uint64_t ne0, uint64_t ne1
     qgpu_tensor *t = new qgpu_tensor();
     t->type = type; t->ne0 = ne0; t->ne1 = ne1;
     t->algo_bytes = (uint64_t)rb * ne1;
-    if (type == T_IQ4_XS) {
+    if (packed_rec_bytes(type) && ne0 % 256 == 0) {        // matrix-core tile records
         const uint64_t tiles = (ne1 + IQ4_TILE_ROWS - 1) / IQ4_TILE_ROWS;
-        t->bytes = tiles * (ne0 / 256) * IQ4_REC_BYTES;
+        t->bytes = tiles * (ne0 / 256) * packed_rec_bytes(type);
         t->packed = 1;
         hipError_t e = hipMalloc(&t->data, t->bytes);
         if (e != hipSuccess) { delete t; return (int)e; }
-        int rc = qg_repack_iq4xs(dev_raw, ne0, ne1, t->data, 0);
+        int rc = qg_repack(type, dev_raw, ne0, ne1, t->data, 0);
         if (rc) { hipFree(t->data); delete t; return rc; }
     } else {
         t->bytes = t->algo_bytes;
@@ -245,7 +245,7 @@ extern "C" int qgpu_tensor_download(const qgpu_tensor *t, void *host)
     if (!t->packed) return qgpu_memcpy_d2h(host, t->data, t->algo_bytes);
     void *tmp = nullptr;
     QG_CHECK(hipMalloc(&tmp, t->algo_bytes));
-    rc = qg_repack_iq4xs(tmp, t->ne0, t->ne1, t->data, 1);
+    rc = qg_repack(t->type, tmp, t->ne0, t->ne1, t->data, 1);
     if (!rc) rc = qgpu_memcpy_d2h(host, tmp, t->algo_bytes);
     hipFree(tmp);
     return rc;
