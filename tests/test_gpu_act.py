@@ -7,7 +7,7 @@ row factor to the GEMV output, so its xout holds x * w.
 
 Also the K-split GEMV of narrow outputs: partial planes (qgpu_gemv_act_split)
 summed by qgpu_add_partials or by the next RMSNorm preparation, which writes
-the summed residual back in place."""
+the summed residual back in place, for every format of the matrix-core GEMV."""
 import ctypes
 
 import numpy as np
@@ -48,7 +48,7 @@ def run(gpu, t, W, ne0, ne1, act, B, bufs):
     return r
 
 
-@pytest.mark.parametrize("t", [23, 14])          # IQ4_XS (digit MFMA path), Q6_K (fp32 path via xout)
+@pytest.mark.parametrize("t", [23, 12, 14, 0])   # IQ4_XS, Q4_K, Q6_K (matrix-core digit path), F32 (VALU path via xout)
 @pytest.mark.parametrize("B", [1, 4, 7])
 @pytest.mark.parametrize("kind", ["rmsnorm", "rmsnorm2", "silu_mul", "gated"])
 def test_act_transform_gemv(gpu, t, B, kind):
@@ -121,14 +121,15 @@ def _split(gpu, T, a, B, ne1, ks):
     return pb, pb.download(np.float32).reshape(ks, B, ne1)
 
 
+@pytest.mark.parametrize("t", [23, 12, 13, 14, 8])     # every format of the matrix-core GEMV
 @pytest.mark.parametrize("B", [1, 4, 6])
-def test_split_gemv_partials(gpu, B):
-    """K-split planes of a narrow IQ4_XS GEMV sum to the oracle GEMV; qgpu_add_partials adds them in order."""
-    print(f"\n[split] B={B}", flush=True)
+def test_split_gemv_partials(gpu, t, B):
+    """K-split planes of a narrow GEMV sum to the oracle GEMV; qgpu_add_partials adds them in order."""
+    print(f"\n[split] type={t} B={B}", flush=True)
     host = host_lib()
     ne0, ne1 = 5120, 320
-    W = host.synth_matrix(23, ne0, ne1, 21, 4, 0.02)
-    T = gpu.tensor(W, 23, ne0, ne1)
+    W = host.synth_matrix(t, ne0, ne1, 21, 4, 0.02)
+    T = gpu.tensor(W, t, ne0, ne1)
     ks = gpu.L.qgpu_gemv_split_ks(T.h)
     assert 2 <= ks <= 8
     x = np.random.default_rng(B).standard_normal((B, ne0)).astype(np.float32)
@@ -136,7 +137,7 @@ def test_split_gemv_partials(gpu, B):
     a = pyqwen.Act()
     a.kind, a.x, a.ldx = pyqwen.ACT_COPY, xb.f32(), ne0
     pb, planes = _split(gpu, T, a, B, ne1, ks)
-    ref = O.gemv(23, W, ne0, ne1, x, B)
+    ref = O.gemv(t, W, ne0, ne1, x, B)
     e = rel_err(planes.sum(0), ref)
     print(f"  ks={ks} rel err {e:.2e}", flush=True)
     assert e < 2e-5
@@ -150,17 +151,19 @@ def test_split_gemv_partials(gpu, B):
     assert np.array_equal(rb.download(np.float32).reshape(B, ne1), (r + ps).astype(np.float32))
 
 
+@pytest.mark.parametrize("tp", [23, 14])                 # producer format
+@pytest.mark.parametrize("tc", [23, 13, 8])              # consumer format (deferred row factor in the epilogue)
 @pytest.mark.parametrize("B", [1, 4, 7])
-def test_rmsnorm_consumes_partials(gpu, B):
+def test_rmsnorm_consumes_partials(gpu, tp, tc, B):
     """The residual's pending partial planes are added by the next RMSNorm preparation (written back in
     place) and the GEMV that follows sees rmsnorm(R + sum of planes)."""
-    print(f"\n[rms-partials] B={B}", flush=True)
+    print(f"\n[rms-partials] producer={tp} consumer={tc} B={B}", flush=True)
     host = host_lib()
     E, n_out = 1024, 384
-    Wd = host.synth_matrix(23, 4096, E, 31, 5, 0.02)          # narrow producer: 4096 -> 1024 (64 tiles)
-    Td = gpu.tensor(Wd, 23, 4096, E)
-    Wn = host.synth_matrix(23, E, n_out, 32, 6, 0.02)          # consumer: 1024 -> 384
-    Tn = gpu.tensor(Wn, 23, E, n_out)
+    Wd = host.synth_matrix(tp, 4096, E, 31, 5, 0.02)          # narrow producer: 4096 -> 1024 (64 tiles)
+    Td = gpu.tensor(Wd, tp, 4096, E)
+    Wn = host.synth_matrix(tc, E, n_out, 32, 6, 0.02)          # consumer: 1024 -> 384
+    Tn = gpu.tensor(Wn, tc, E, n_out)
     rng = np.random.default_rng(100 + B)
     h = rng.standard_normal((B, 4096)).astype(np.float32)
     R = (3 * rng.standard_normal((B, E))).astype(np.float32)
@@ -185,7 +188,7 @@ def test_rmsnorm_consumes_partials(gpu, B):
     gpu.ok(gpu.L.qgpu_gemv_act_batch(Ws, 1, ctypes.byref(an), B, outs, lds, 0))
     assert np.array_equal(Rb.download(np.float32).reshape(B, E), R_new)
     xin = np.stack([o_rmsnorm(R_new[b], w) for b in range(B)])
-    e = rel_err(ob.download(np.float32).reshape(B, n_out), O.gemv(23, Wn, E, n_out, xin, B))
+    e = rel_err(ob.download(np.float32).reshape(B, n_out), O.gemv(tc, Wn, E, n_out, xin, B))
     print(f"  ks={ks} gemv rel err {e:.2e}", flush=True)
     assert e < 1e-4
     # partial planes are rejected by every transform but single-segment RMSNorm
