@@ -84,8 +84,9 @@ int  qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
  * Replaces gemv_multi_batch / gemv_multi (reference kernels.c:666-736). */
 int  qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx,
                            int n, float *const *outs, const uint64_t *ldos, int flags);
-/* Split form of the IQ4_XS path: qgpu_gemv_prepare converts the activations
- * once (x: n rows of ne0 floats) and qgpu_gemv_prepared runs an IQ4_XS matrix
+/* Split form of the matrix-core path: qgpu_gemv_prepare converts the activations
+ * once (x: n rows of ne0 floats) and qgpu_gemv_prepared runs a packed matrix
+ * (IQ4_XS, Q4_K, Q5_K, Q6_K or Q8_0 with ne0 % 256 == 0; QGPU_E_TYPE otherwise)
  * with ne0 columns on them; several matrices may follow one prepare. */
 int  qgpu_gemv_prepare(const float *x, uint64_t ldx, int n, uint64_t ne0);
 int  qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, int flags);
@@ -138,6 +139,9 @@ int  qgpu_act_prepare(const qgpu_act *act, int n, uint64_t ne0);
 int  qgpu_gemv_act_split(const qgpu_tensor *W, const qgpu_act *act, int n, float *part, uint64_t ldp, int ks);
 /* ks that balances W over the device's compute units (1: no split). */
 int  qgpu_gemv_split_ks(const qgpu_tensor *W);
+/* qgpu_gemv_act_split on the input already prepared by qgpu_gemv_prepare,
+ * qgpu_act_prepare or qgpu_attn_fused_act (packed W only). */
+int  qgpu_gemv_prepared_split(const qgpu_tensor *W, int n, float *part, uint64_t ldp, int ks);
 /* rows x n: y = x + sum_{q < n_part} part[q*rows*ldp + r*ldp + i] (y may equal x). */
 int  qgpu_add_partials(float *y, uint64_t ldy, const float *x, uint64_t ldx, const float *part, uint64_t ldp,
                        int n_part, uint64_t n, int rows);
@@ -206,18 +210,28 @@ int  qgpu_attn_prep(float *q, uint64_t ldq, const float *k, const float *v, uint
                     const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev, int B,
                     int n_head, int n_kv, int head_dim, float eps);
 /* out[b][h*hd+d] = (softmax_{t <= pos+b}(q_bh . k_t / sqrt(hd)) V)[d] * sigmoid(gate_bh[d]);
- * ctx_bound >= pos + B bounds the positions read (chunks beyond *pos_dev+B-1 exit). */
+ * ctx_bound >= pos + B bounds the positions read (spans beyond *pos_dev+B-1 exit).
+ * (n_head/n_kv)*B <= 48. */
 int  qgpu_attn_decode(const float *q, uint64_t ldq, const float *kcache, const float *vcache,
                       const int *pos_dev, int ctx_bound, int B, int n_head, int n_kv, int head_dim,
                       float *out, uint64_t ldo);
 /* qgpu_attn_prep + qgpu_attn_decode in fewer launches: the per-head q/k
  * RMSNorm, RoPE and the cache writes of the B new rows happen inside the
  * attention kernel.  q is not modified.  Same arguments and results as the
- * two calls (model.c:318-406, 760-810). */
+ * two calls (model.c:318-406, 760-810); B <= 8. */
 int  qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
                      const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
                      const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
                      int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out, uint64_t ldo);
+/* qgpu_attn_fused whose output rows are also prepared as the input of the next
+ * GEMV: the digit planes of out (n_head*head_dim columns) are written exactly as
+ * qgpu_act_prepare with QGPU_ACT_COPY would write them from out, so
+ * qgpu_gemv_prepared or qgpu_gemv_prepared_split may follow with no preparation
+ * launch (the o-projection input, model.c:811-816). */
+int  qgpu_attn_fused_act(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                         const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                         const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
+                         int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out, uint64_t ldo);
 /* allocates the attention workspace for ctx_bound positions now (no allocation later) */
 int  qgpu_attn_reserve(int ctx_bound, int n_kv);
 

@@ -5,18 +5,18 @@
 //                     first rope_dim dims (pairs (i, i + rope_dim/2)), k and v
 //                     written to the cache at position pos + b.
 //  qgpu_attn_decode : softmax(q K^T / sqrt(hd)) V over positions t <= pos + b,
-//                     times sigmoid(gate).  Flash-decoding: one block per
-//                     (kv head, 64-position chunk) serves every query head of
-//                     the group and every token of the batch (each K/V row is
-//                     read once per chunk), then a combine pass merges chunks.
+//                     times sigmoid(gate).  Flash-decoding on the matrix cores:
+//                     one block per (kv head, span of 16-position tiles) serves
+//                     every query head of the group and every token of the batch
+//                     (each K/V row is read once per launch), then a combine pass
+//                     merges the spans.
 // Positions come from device memory (*pos_dev) so the launch sequence can be
 // captured in a graph and replayed at any position.
 #include "qgpu_internal.h"
 
 #define ATT_HD   256
-#define ATT_CS   64             // positions per chunk block
-#define ATT_MAXQ 64             // row stride of the chunk partials
-#define ATT_MAXR 48             // query rows (heads per kv head x batch) one chunk block serves
+#define ATT_MAXQ 64             // row stride of the span partials
+#define ATT_MAXR 48             // query rows (heads per kv head x batch) one span block serves
 
 namespace qg {
 void *ws_attn = nullptr;
@@ -61,25 +61,42 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
     }
 }
 
-// Flash-decoding chunk kernel.  Block (g, c): kv head g, positions
-// [c*ATT_CS, c*ATT_CS + ATT_CS), 8 waves.  Serves the QH = (n_head/n_kv) * B
-// query rows of the group (row r = b * per + (h - g*per)); wave w owns rows
-// w, w + 8, ... (<= ATT_RW of them).
+// Span kernel (flash decoding on the matrix cores).  Block (g, s): kv head g,
+// span s of 16-position tiles, 4 waves; wave w owns head dims [64w, 64w + 64).
+// It serves every query row of the group, r = b * per + (h - g*per) < QH =
+// per * B, as NRT row tiles of 16.
+//   * Scores, per tile and row tile: S^T (16 positions x 16 rows) = K Q^T with
+//     v_mfma_f32_16x16x4_f32, lane l supplying K[pos l%16][d] and Q[row l%16][d]
+//     for d = 64w + 16q + 4(l/16) + j (q, j < 4: any order of the d sum is the
+//     same dot product).  Each wave sums its 64 dims; the four partial tiles meet
+//     in LDS and every wave adds them in the same order.
+//   * The score tile's accumulator layout (lane l, register v: position
+//     4(l/16) + v, row l%16) is the A operand of P.V as it stands: MFMA step v
+//     takes positions {v, 4+v, 8+v, 12+v}; lane l supplies V[that position][64w +
+//     4(l%16) + c] for output tile c, so one float4 per step feeds four MFMAs.
+//   * Online softmax per row (running max and sum); rows of a tile meet over
+//     the four 16-lane groups.  O accumulates in fp32 registers (lane l, register
+//     w: row 4(l/16) + w, dim 64w' + 4(l%16) + c).
+//   * The K and V operands of the next tile are loaded while this tile runs.
 //   FUSED = 1: the block also applies the per-head q/k RMSNorm and RoPE
-//              (reference model.c:318-406): q rows are prepared in LDS (each
-//              block recomputes them), the new k/v rows of positions pos..pos+B-1
-//              that fall in this chunk are prepared here and written to the caches
-//              (no other block reads them in this launch).
+//              (reference model.c:318-406) in LDS: q rows, and the new k rows
+//              of positions pos..pos+B-1 when the span reaches them; the block
+//              whose span holds a new position writes its k/v rows to the caches
+//              (no block reads new rows from the caches in this launch).
 //   FUSED = 0: q rows already prepared, caches already hold every position.
-// Every global load is issued first (K and V rows of the chunk, q rows).
-// Scores: lane = position, K rows in LDS, q values broadcast from LDS, one
-// running fp32 sum per row over d = 0..255.  Softmax statistics of a row are a
-// reduction over the 64 lanes of one wave.  P.V: lane = 4 output dims, V rows
-// (written over the K rows once the scores are done) and P from LDS.
-// partials: pml [n_kv][nchunk][ATT_MAXQ][2] (m, l), po [n_kv][nchunk][ATT_MAXQ][ATT_HD]
-#define ATT_KLD  260          // K row stride in LDS (floats)
-#define ATT_NWV  8            // waves per chunk block
-#define ATT_RW   (ATT_MAXR / ATT_NWV)
+// The number of spans follows the live context: ntl tiles hold positions
+// 0..pos+B-1; nsl = ceil(ntl / tps) spans of tps tiles, for at most nspan
+// spans (the launch size); blocks past nsl exit and the combine skips them.
+// partials: pml [n_kv][nspan][ATT_MAXQ][2] (m, l), po [n_kv][nspan][ATT_MAXQ][ATT_HD]
+#define ATT_TP    16          // positions per tile
+#define ATT_NWV   4           // waves per block
+#define ATT_MAXB  8           // new positions per fused call
+#define ATT_NSPAN 64          // spans per kv head at most
+#ifndef ATT_MINTPS
+#define ATT_MINTPS 1          // tiles per span at least
+#endif
+
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 struct AttnArgs {
     const float *q; uint64_t ldq;
@@ -88,13 +105,19 @@ struct AttnArgs {
     float *kc, *vc;
     const int *pos_dev;
     float *pml, *po;
-    int half, B, n_head, n_kv, nchunk;
+    int half, B, n_head, n_kv, nspan;
     float eps;
 };
 
-static __device__ __forceinline__ float4 norm4(float4 v, float4 w, float sc)
+// live tiles ntl, tiles per span tps and spans with work nsl, from the device
+// position (the span kernel and the combine derive the same split)
+static __device__ __forceinline__ void span_split(int pos0, int B, int nspan, int &ntl, int &tps, int &nsl)
 {
-    return make_float4((v.x * sc) * w.x, (v.y * sc) * w.y, (v.z * sc) * w.z, (v.w * sc) * w.w);
+    ntl = (pos0 + B + ATT_TP - 1) / ATT_TP;
+    const int ns = ntl < nspan ? ntl : nspan;
+    tps = (ntl + ns - 1) / ns;
+    if (tps < ATT_MINTPS) tps = ATT_MINTPS;
+    nsl = (ntl + tps - 1) / tps;
 }
 
 static __device__ __forceinline__ float wsum64(float v)
@@ -104,211 +127,363 @@ static __device__ __forceinline__ float wsum64(float v)
     return v;
 }
 
-static __device__ __forceinline__ float wmax64(float v)
+static __device__ __forceinline__ v4f mfma4(float a, float b, v4f c)
 {
-#pragma unroll
-    for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// RW: rows per wave, ceil(QH / 8) (1..ATT_RW): the row loops carry no branches
-template <int FUSED, int RW>
-__global__ __launch_bounds__(ATT_NWV * 64) void k_attn_chunk(const AttnArgs p)
+template <int FUSED, int NRT>
+__global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 {
-    __shared__ float Qs[ATT_MAXR][ATT_HD];       // first: its reads fit the 16-bit LDS offset field
-    __shared__ float Ps[ATT_MAXR][ATT_CS];
-    __shared__ float KV[ATT_CS * ATT_KLD];        // K rows (stride ATT_KLD), then V rows (stride ATT_HD)
-    const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    __shared__ float lds[FUSED ? NRT * 16 * ATT_HD : NRT * 2048];   // q rows (FUSED), then the score exchange
+    __shared__ float Kn[FUSED ? ATT_MAXB : 1][ATT_HD];   // new k rows, normalised and rotated
+    __shared__ float Rc[FUSED ? ATT_MAXB * ATT_HD / 2 : 1], Rs[FUSED ? ATT_MAXB * ATT_HD / 2 : 1];   // RoPE tables
+    const int g = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n = lane & 15, gq = lane >> 4;
     const int per = p.n_head / p.n_kv, QH = per * p.B;
-    const int pos0 = *p.pos_dev, tmax = pos0 + p.B - 1, t0 = c * ATT_CS;
-    float *ml = p.pml + ((uint64_t)g * p.nchunk + c) * ATT_MAXQ * 2;
-    float *o = p.po + ((uint64_t)g * p.nchunk + c) * ATT_MAXQ * ATT_HD;
-    if (t0 > tmax) {                              // chunk beyond the context: empty partial
-        for (int qi = tid; qi < QH; qi += ATT_NWV * 64) { ml[2 * qi] = -INFINITY; ml[2 * qi + 1] = 0.0f; }
-        return;
-    }
-    const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD;
-    const int nt = min(ATT_CS, tmax - t0 + 1);    // positions of this chunk that exist
-    // ---- every global load first: K and V rows pp = wv + 8i (lane = float4), q rows r = wv + 8i
-    float4 kr[ATT_CS / ATT_NWV], vr[ATT_CS / ATT_NWV], qr[RW];
+    const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD, hoff = (uint64_t)g * ATT_HD;
+    const int d0 = 64 * wv;
+
+    // ---- loads that do not depend on the position first: q rows (FUSED: raw rows for the
+    // prologue; else the Q operands, row rt*16 + n, dims d0 + 16q + 4gq .. +3), the new k
+    // rows and the norm weights
+    constexpr int QV = FUSED ? NRT * 16 * 64 / (ATT_NWV * 64) : 1;   // float4 of q rows per thread
+    constexpr int KV = FUSED ? ATT_MAXB * 64 / (ATT_NWV * 64) : 1;
+    float4 qv[QV], knv[KV], qw = make_float4(0.0f, 0.0f, 0.0f, 0.0f), kw = qw;
+    v4f qop[NRT][4];
+    if (FUSED) {
 #pragma unroll
-    for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
-        const int pp = wv + ATT_NWV * i, t = t0 + pp;
-        kr[i] = vr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (pp < nt) {
-            if (FUSED && t >= pos0) {             // new row: raw k/v of token t - pos0
-                const uint64_t off = (uint64_t)(t - pos0) * p.ldkv + (uint64_t)g * ATT_HD + 4 * lane;
-                kr[i] = *(const float4 *)(p.k + off);
-                vr[i] = *(const float4 *)(p.v + off);
-            } else {
-                const uint64_t off = (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * lane;
-                kr[i] = *(const float4 *)(p.kc + off);
-                vr[i] = *(const float4 *)(p.vc + off);
+        for (int u = 0; u < QV; u++) {
+            const int e = tid + u * ATT_NWV * 64, r = e >> 6, d4 = e & 63;
+            qv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (r < QH) {
+                const int b = r / per, h = g * per + r % per;
+                qv[u] = *(const float4 *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + 4 * d4);
             }
         }
-    }
 #pragma unroll
-    for (int i = 0; i < RW; i++) {
-        const int r = wv + ATT_NWV * i;
-        qr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (r < QH) {
-            const int b = r / per, h = g * per + r % per;
-            qr[i] = *(const float4 *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + 4 * lane);
+        for (int u = 0; u < KV; u++) {
+            const int e = tid + u * ATT_NWV * 64, b = e >> 6, d4 = e & 63;
+            knv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (b < p.B) knv[u] = *(const float4 *)(p.k + (uint64_t)b * p.ldkv + hoff + 4 * d4);
         }
-    }
-    float4 qw = make_float4(1.0f, 1.0f, 1.0f, 1.0f), kw = qw;
-    if (FUSED) {
         qw = *(const float4 *)(p.qw + 4 * lane);
         kw = *(const float4 *)(p.kw + 4 * lane);
-    }
-    // ---- to LDS (per-head RMSNorm of q and of the new k rows on the way)
+    } else {
 #pragma unroll
-    for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
-        const int pp = wv + ATT_NWV * i, t = t0 + pp;
-        float4 kv = kr[i];
-        if (FUSED && pp < nt && t >= pos0) {
-            const float ss = wsum64(kv.x * kv.x + kv.y * kv.y + kv.z * kv.z + kv.w * kv.w);
-            kv = norm4(kv, kw, 1.0f / sqrtf(ss / (float)ATT_HD + p.eps));
-        }
-        *(float4 *)&KV[pp * ATT_KLD + 4 * lane] = kv;
-    }
+        for (int rt = 0; rt < NRT; rt++) {
+            const int r = rt * 16 + n;
+            const int b = r / per, h = g * per + r % per;
 #pragma unroll
-    for (int i = 0; i < RW; i++) {                // rows r >= QH hold zeros (their results are not used)
-        const int r = wv + ATT_NWV * i;
-        float4 qv = qr[i];
-        if (FUSED && r < QH) {
-            const float ss = wsum64(qv.x * qv.x + qv.y * qv.y + qv.z * qv.z + qv.w * qv.w);
-            qv = norm4(qv, qw, 1.0f / sqrtf(ss / (float)ATT_HD + p.eps));
+            for (int q = 0; q < 4; q++)
+                qop[rt][q] = r < QH ? *(const v4f *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + d0 + 16 * q + 4 * gq)
+                                    : v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        *(float4 *)&Qs[r][4 * lane] = qv;
     }
-    __syncthreads();
-    if (FUSED) {
-        // NeoX RoPE on (i, i + half) at position pos0 + b: q rows and the new k rows of this chunk
-        for (int e = tid; e < (QH + p.B) * p.half; e += ATT_NWV * 64) {
-            const int r = e / p.half, i = e % p.half;
-            float *x;
-            int t;
-            if (r < QH) { x = Qs[r]; t = pos0 + r / per; }
-            else {
-                t = pos0 + (r - QH);
-                if (t < t0 || t >= t0 + ATT_CS) continue;
-                x = &KV[(t - t0) * ATT_KLD];
+    const int pos0 = *p.pos_dev, tmax = pos0 + p.B - 1;
+    int ntl, tps, nsl;
+    span_split(pos0, p.B, p.nspan, ntl, tps, nsl);
+    if (s >= nsl) return;
+    const int tile0 = s * tps, tile1 = min(tile0 + tps, ntl);
+    const int posA = tile0 * ATT_TP, posB = min(tile1 * ATT_TP, tmax + 1);   // positions of this span
+
+    // ---- operand loads of tile t (positions beyond the live end read as zeros).  K rows of
+    // the new positions (FUSED) come from Kn once the prologue has prepared them:
+    // load_k(t, kr, 0) loads the cached rows only, load_k(t, kr, 1) then fills the new ones.
+    auto load_k = [&](int t, v4f *kr, int new_rows) {
+        const int pp = t * ATT_TP + n;
+        if (FUSED && new_rows) {
+            if (pp >= pos0 && pp <= tmax)
+#pragma unroll
+                for (int q = 0; q < 4; q++) kr[q] = *(const v4f *)&Kn[pp - pos0][d0 + 16 * q + 4 * gq];
+            return;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) kr[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (pp <= tmax && (!FUSED || pp < pos0))
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                kr[q] = *(const v4f *)(p.kc + (uint64_t)pp * kvrow + hoff + d0 + 16 * q + 4 * gq);
+    };
+    auto load_v = [&](int t, v4f *vr) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int pp = t * ATT_TP + 4 * gq + v;
+            vr[v] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (pp <= tmax) {
+                if (FUSED && pp >= pos0) vr[v] = *(const v4f *)(p.v + (uint64_t)(pp - pos0) * p.ldkv + hoff + d0 + 4 * n);
+                else vr[v] = *(const v4f *)(p.vc + (uint64_t)pp * kvrow + hoff + d0 + 4 * n);
             }
-            const float cs = p.rcos[(uint64_t)t * p.half + i], sn = p.rsin[(uint64_t)t * p.half + i];
-            const float v0 = x[i], v1 = x[i + p.half];
-            x[i] = v0 * cs - v1 * sn;
-            x[i + p.half] = v0 * sn + v1 * cs;
+        }
+    };
+    // the first tile's operands are in flight during the q preparation
+    v4f kr[4], vr[4];
+    load_k(tile0, kr, 0);
+    load_v(tile0, vr);
+
+    if (FUSED) {
+        float (*Qs)[ATT_HD] = (float (*)[ATT_HD])lds;
+        const bool has_new = posB > pos0;
+        float cv[ATT_MAXB * ATT_HD / 2 / (ATT_NWV * 64)], sv[ATT_MAXB * ATT_HD / 2 / (ATT_NWV * 64)];
+#pragma unroll
+        for (int u = 0; u < ATT_MAXB * ATT_HD / 2 / (ATT_NWV * 64); u++) {
+            const int e = tid + u * ATT_NWV * 64, b = e / p.half, i = e % p.half;
+            cv[u] = sv[u] = 0.0f;
+            if (b < p.B) {
+                cv[u] = p.rcos[(uint64_t)(pos0 + b) * p.half + i];
+                sv[u] = p.rsin[(uint64_t)(pos0 + b) * p.half + i];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < QV; u++) {
+            const int e = tid + u * ATT_NWV * 64;
+            *(float4 *)&Qs[e >> 6][4 * (e & 63)] = qv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < KV; u++) {
+            const int e = tid + u * ATT_NWV * 64;
+            *(float4 *)&Kn[e >> 6][4 * (e & 63)] = knv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < ATT_MAXB * ATT_HD / 2 / (ATT_NWV * 64); u++) {
+            const int e = tid + u * ATT_NWV * 64;
+            Rc[e] = cv[u];
+            Rs[e] = sv[u];
         }
         __syncthreads();
-        // the new rows go to the caches (no other block of this launch reads them)
-        for (int e = tid; e < p.B * 64; e += ATT_NWV * 64) {
-            const int b = e >> 6, d4 = e & 63, t = pos0 + b;
-            if (t < t0 || t >= t0 + ATT_CS) continue;
-            const uint64_t row = (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * d4;
-            *(float4 *)(p.kc + row) = *(const float4 *)&KV[(t - t0) * ATT_KLD + 4 * d4];
-        }
-#pragma unroll
-        for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
-            const int pp = wv + ATT_NWV * i, t = t0 + pp;
-            if (pp < nt && t >= pos0)
-                *(float4 *)(p.vc + (uint64_t)t * kvrow + (uint64_t)g * ATT_HD + 4 * lane) = vr[i];
-        }
-    }
-    // ---- scores of this wave's rows at position t0 + lane
-    const float scale = 1.0f / sqrtf((float)ATT_HD);
-    {
-        float s[RW];
-#pragma unroll
-        for (int j = 0; j < RW; j++) s[j] = 0.0f;
-        const float *krow = &KV[lane * ATT_KLD];
-#pragma unroll 4
-        for (int d4 = 0; d4 < ATT_HD / 4; d4++) {
-            const float4 kq = *(const float4 *)(krow + 4 * d4);
-            float4 qv[RW];
-#pragma unroll
-            for (int j = 0; j < RW; j++) qv[j] = *(const float4 *)&Qs[wv + ATT_NWV * j][4 * d4];
-#pragma unroll
-            for (int j = 0; j < RW; j++) {
-                s[j] = fmaf(qv[j].x, kq.x, s[j]); s[j] = fmaf(qv[j].y, kq.y, s[j]);
-                s[j] = fmaf(qv[j].z, kq.z, s[j]); s[j] = fmaf(qv[j].w, kq.w, s[j]);
+        // per-head RMSNorm: one wave per row, 4 dims per lane
+        {
+            const int nrow = QH + (has_new ? p.B : 0);
+            for (int r = wv; r < nrow; r += ATT_NWV) {
+                float *x = r < QH ? Qs[r] : Kn[r - QH];
+                const float4 w = r < QH ? qw : kw;
+                float4 v = *(const float4 *)(x + 4 * lane);
+                const float sc = 1.0f / sqrtf(wsum64(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w) / (float)ATT_HD + p.eps);
+                v = make_float4((v.x * sc) * w.x, (v.y * sc) * w.y, (v.z * sc) * w.z, (v.w * sc) * w.w);
+                *(float4 *)(x + 4 * lane) = v;
             }
         }
-        // ---- chunk softmax statistics: a row's 64 scores are the 64 lanes of the wave
-        const int t = t0 + lane;
+        __syncthreads();
+        // NeoX RoPE on (i, i + half) at position pos0 + b (tables of the B positions in LDS)
+        {
+            const int nrow = QH + (has_new ? p.B : 0);
+            for (int e = tid; e < nrow * p.half; e += ATT_NWV * 64) {
+                const int r = e / p.half, i = e % p.half;
+                float *x = r < QH ? Qs[r] : Kn[r - QH];
+                const int b = r < QH ? r / per : r - QH;
+                const float cs = Rc[b * p.half + i], sn = Rs[b * p.half + i];
+                const float v0 = x[i], v1 = x[i + p.half];
+                x[i] = v0 * cs - v1 * sn;
+                x[i + p.half] = v0 * sn + v1 * cs;
+            }
+        }
+        __syncthreads();
+        // cache rows of the new positions this span holds (each position is in exactly one span)
+        if (has_new)
+            for (int e = tid; e < p.B * 64; e += ATT_NWV * 64) {
+                const int b = e >> 6, d4 = e & 63, t = pos0 + b;
+                if (t < posA || t >= posB) continue;
+                const uint64_t row = (uint64_t)t * kvrow + hoff + 4 * d4;
+                *(float4 *)(p.kc + row) = *(const float4 *)&Kn[b][4 * d4];
+                *(float4 *)(p.vc + row) = *(const float4 *)(p.v + (uint64_t)b * p.ldkv + hoff + 4 * d4);
+            }
 #pragma unroll
-        for (int j = 0; j < RW; j++) {
-            const int r = wv + ATT_NWV * j;
-            if (r >= QH) break;                   // wave-uniform
-            const float sv = (lane < nt && t <= pos0 + r / per) ? s[j] * scale : -INFINITY;
-            const float m = wmax64(sv);
-            const float pr = m > -INFINITY ? expf(sv - m) : 0.0f;
-            const float sum = wsum64(pr);
-            Ps[r][lane] = pr;
-            if (lane == 0) { ml[2 * r] = m; ml[2 * r + 1] = sum; }
+        for (int rt = 0; rt < NRT; rt++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) qop[rt][q] = *(const v4f *)&Qs[rt * 16 + n][d0 + 16 * q + 4 * gq];
+        __syncthreads();                          // lds is the score exchange from here on
+    }
+
+    v4f oacc[NRT][4];
+    float mrow[NRT], lrow[NRT];
+    int lim[NRT];                                 // last position row rt*16 + n may see (-1: padding row)
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++) {
+        mrow[rt] = -INFINITY;
+        lrow[rt] = 0.0f;
+        const int r = rt * 16 + n;
+        lim[rt] = r < QH ? pos0 + r / per : -1;
+#pragma unroll
+        for (int c = 0; c < 4; c++) oacc[rt][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const float scale = 1.0f / sqrtf((float)ATT_HD);
+    v4f *Sx = (v4f *)lds;                         // [2][ATT_NWV][NRT][64]
+    if (FUSED) load_k(tile0, kr, 1);
+    for (int t = tile0; t < tile1; t++) {
+        const int buf = (t - tile0) & 1;
+        v4f kn[4], vn[4];
+        if (t + 1 < tile1) {
+            load_k(t + 1, kn, 0);
+            if (FUSED) load_k(t + 1, kn, 1);
+            load_v(t + 1, vn);
+        }
+        // partial score tiles over this wave's dims
+#pragma unroll
+        for (int rt = 0; rt < NRT; rt++) {
+            v4f sp = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) sp = mfma4(kr[q][j], qop[rt][q][j], sp);
+            Sx[((buf * ATT_NWV + wv) * NRT + rt) * 64 + lane] = sp;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rt = 0; rt < NRT; rt++) {
+            const v4f st = ((Sx[((buf * ATT_NWV + 0) * NRT + rt) * 64 + lane] +
+                             Sx[((buf * ATT_NWV + 1) * NRT + rt) * 64 + lane]) +
+                            Sx[((buf * ATT_NWV + 2) * NRT + rt) * 64 + lane]) +
+                           Sx[((buf * ATT_NWV + 3) * NRT + rt) * 64 + lane];
+            float sv[4];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int pp = t * ATT_TP + 4 * gq + v;
+                sv[v] = pp <= lim[rt] ? st[v] * scale : -INFINITY;
+                mx = fmaxf(mx, sv[v]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mnew = fmaxf(mrow[rt], mx);
+            float alpha = 1.0f, pv[4], ps = 0.0f;
+            if (mnew > -INFINITY) alpha = expf(mrow[rt] - mnew);     // exp(-inf) = 0 for the first live tile
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                pv[v] = sv[v] > -INFINITY ? expf(sv[v] - mnew) : 0.0f;
+                ps += pv[v];
+            }
+            ps += __shfl_xor(ps, 16);
+            ps += __shfl_xor(ps, 32);
+            lrow[rt] = lrow[rt] * alpha + ps;
+            mrow[rt] = mnew;
+            // rescale the O rows 4gq + w by their rows' factor (held by lane 4gq + w)
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float aw = __shfl(alpha, 4 * gq + w);
+#pragma unroll
+                for (int c = 0; c < 4; c++) oacc[rt][c][w] *= aw;
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) oacc[rt][c] = mfma4(pv[v], vr[v][c], oacc[rt][c]);
+        }
+        if (t + 1 < tile1) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) { kr[q] = kn[q]; vr[q] = vn[q]; }
         }
     }
-    __syncthreads();                              // scores done: the K rows may be overwritten
+    // ---- partials of this span
+    float *ml = p.pml + ((uint64_t)g * p.nspan + s) * ATT_MAXQ * 2;
+    float *o = p.po + ((uint64_t)g * p.nspan + s) * ATT_MAXQ * ATT_HD;
 #pragma unroll
-    for (int i = 0; i < ATT_CS / ATT_NWV; i++) {
-        const int pp = wv + ATT_NWV * i;
-        *(float4 *)&KV[pp * ATT_HD + 4 * lane] = vr[i];
-    }
-    __syncthreads();
-    // ---- P.V: lane = output dims 4*lane .. 4*lane+3 of this wave's rows
-    float4 acc[RW];
-#pragma unroll
-    for (int j = 0; j < RW; j++) acc[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    // positions beyond nt have P = 0 and V rows of zeros
-#pragma unroll 4
-    for (int pp = 0; pp < ATT_CS; pp++) {
-        const float4 vv = *(const float4 *)&KV[pp * ATT_HD + 4 * lane];
-        float pr[RW];
-#pragma unroll
-        for (int j = 0; j < RW; j++) pr[j] = Ps[wv + ATT_NWV * j][pp];
-#pragma unroll
-        for (int j = 0; j < RW; j++) {
-            acc[j].x = fmaf(pr[j], vv.x, acc[j].x); acc[j].y = fmaf(pr[j], vv.y, acc[j].y);
-            acc[j].z = fmaf(pr[j], vv.z, acc[j].z); acc[j].w = fmaf(pr[j], vv.w, acc[j].w);
+    for (int rt = 0; rt < NRT; rt++) {
+        if (wv == 0 && gq == 0 && rt * 16 + n < QH) {
+            ml[2 * (rt * 16 + n)] = mrow[rt];
+            ml[2 * (rt * 16 + n) + 1] = lrow[rt];
         }
-    }
 #pragma unroll
-    for (int j = 0; j < RW; j++) {
-        const int r = wv + ATT_NWV * j;
-        if (r < QH) *(float4 *)(o + (uint64_t)r * ATT_HD + 4 * lane) = acc[j];
+        for (int w = 0; w < 4; w++) {
+            const int r = rt * 16 + 4 * gq + w;
+            if (r < QH)
+                *(v4f *)(o + (uint64_t)r * ATT_HD + d0 + 4 * n) =
+                    v4f{oacc[rt][0][w], oacc[rt][1][w], oacc[rt][2][w], oacc[rt][3][w]};
+        }
     }
 }
 
-// out[b][h*hd + d] = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) * sigmoid(gate); chunks past
-// the last position (m = -inf) are skipped by the bound taken from *pos_dev
+// out[b][h*hd + d] = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) * sigmoid(gate) over the
+// nc <= 64 spans with work (rows with no position in a span have m = -inf there and are
+// skipped).  One wave per call: lane c holds span c's (m, l), the max and the weighted sum
+// of l are wave reductions, and the o loads are independent of them and of each other.
+static __device__ __forceinline__ float combine_one(const float *q, uint64_t ldq, const float *pml, const float *po,
+                                                    int nspan, int nc, int per, int h, int b, int d)
+{
+    const int lane = threadIdx.x & 63;
+    const int g = h / per, qi = b * per + (h % per);
+    const float *mlg = pml + (uint64_t)g * nspan * ATT_MAXQ * 2 + 2 * qi;
+    const float *pog = po + (uint64_t)g * nspan * ATT_MAXQ * ATT_HD + (uint64_t)qi * ATT_HD + d;
+    const float gate = q[(uint64_t)b * ldq + (uint64_t)h * 2 * ATT_HD + ATT_HD + d];
+    float mc = -INFINITY, lc = 0.0f;
+    if (lane < nc) {
+        mc = mlg[(uint64_t)lane * ATT_MAXQ * 2];
+        lc = mlg[(uint64_t)lane * ATT_MAXQ * 2 + 1];
+    }
+    float m = mc;
+#pragma unroll
+    for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float f = mc > -INFINITY ? expf(mc - m) : 0.0f;
+    float l = lc * f;
+#pragma unroll
+    for (int o = 32; o; o >>= 1) l += __shfl_xor(l, o);
+    // 16 spans per step: their o loads are issued together.  Past nc the load repeats span
+    // nc - 1 (finite) and lane c0 + j holds f = 0, so the padding terms add 0.
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < nc; c0 += 16) {
+        float ov[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) ov[j] = pog[(uint64_t)(c0 + j < nc ? c0 + j : nc - 1) * ATT_MAXQ * ATT_HD];
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            acc = fmaf(ov[j], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), c0 + j)),
+                       acc);
+    }
+    return (acc / l) * (1.0f / (1.0f + expf(-gate)));
+}
+
+// block (h, b): head h of token b, thread = dim
 __global__ __launch_bounds__(ATT_HD) void k_attn_combine(const float *q, uint64_t ldq, const float *pml,
                                                          const float *po, const int *pos_dev, int B, int n_head,
-                                                         int n_kv, int nchunk, float *out, uint64_t ldo)
+                                                         int n_kv, int nspan, float *out, uint64_t ldo)
 {
     const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    const int per = n_head / n_kv, g = h / per, qi = b * per + (h % per);
-    const int nc = min(nchunk, (*pos_dev + B - 1) / ATT_CS + 1);
-    const float *mlg = pml + (uint64_t)g * nchunk * ATT_MAXQ * 2 + 2 * qi;
-    const float *pog = po + (uint64_t)g * nchunk * ATT_MAXQ * ATT_HD + (uint64_t)qi * ATT_HD + d;
-    float m = -INFINITY;
-#pragma unroll 8
-    for (int c = 0; c < nc; c++) m = fmaxf(m, mlg[(uint64_t)c * ATT_MAXQ * 2]);
-    float l = 0.0f, acc = 0.0f;
-#pragma unroll 8
-    for (int c = 0; c < nc; c++) {
-        const float mc = mlg[(uint64_t)c * ATT_MAXQ * 2];
-        const float f = mc > -INFINITY ? expf(mc - m) : 0.0f;
-        l = fmaf(mlg[(uint64_t)c * ATT_MAXQ * 2 + 1], f, l);
-        acc = fmaf(pog[(uint64_t)c * ATT_MAXQ * ATT_HD], f, acc);
-    }
-    const float gate = q[(uint64_t)b * ldq + (uint64_t)h * 2 * ATT_HD + ATT_HD + d];
-    out[(uint64_t)b * ldo + (uint64_t)h * ATT_HD + d] = (acc / l) * (1.0f / (1.0f + expf(-gate)));
+    int ntl, tps, nc;
+    span_split(*pos_dev, B, nspan, ntl, tps, nc);
+    out[(uint64_t)b * ldo + (uint64_t)h * ATT_HD + d] = combine_one(q, ldq, pml, po, nspan, nc, n_head / n_kv, h, b, d);
 }
 
-static int attn_ws(int ctx_bound, int n_kv, int *nchunk)
+// The combine with the output rows also written as the GEMV input digit planes
+// (what the COPY preparation would write from them): block (h, a), 4 x 256
+// threads, merges head h of tokens 4a..4a+3 (thread 256i + d: token 4a+i, dim d),
+// whose 256 outputs are super-block h of each row.
+__global__ __launch_bounds__(4 * ATT_HD) void k_attn_combine_act(const float *q, uint64_t ldq, const float *pml,
+                                                                 const float *po, const int *pos_dev, int B,
+                                                                 int n_head, int n_kv, int nspan, float *out,
+                                                                 uint64_t ldo, uint8_t *A, float *xs)
 {
-    *nchunk = (ctx_bound + ATT_CS - 1) / ATT_CS;
-    const size_t need = (size_t)n_kv * *nchunk * ATT_MAXQ * (2 + ATT_HD) * sizeof(float);
+    __shared__ ActDigitLds dl;
+    __shared__ float vb[4][ATT_HD];
+    const int h = blockIdx.x, a = blockIdx.y, i = threadIdx.x >> 8, d = threadIdx.x & (ATT_HD - 1);
+    const int b = 4 * a + i;
+    int ntl, tps, nc;
+    span_split(*pos_dev, B, nspan, ntl, tps, nc);
+    float val = 0.0f;
+    if (b < B) {                                  // wave-uniform
+        val = combine_one(q, ldq, pml, po, nspan, nc, n_head / n_kv, h, b, d);
+        out[(uint64_t)b * ldo + (uint64_t)h * ATT_HD + d] = val;
+    }
+    vb[i][d] = val;
+    __syncthreads();
+    // the digit stage runs on threads 0..255 (the others take part in its barriers)
+    const bool active = threadIdx.x < ATT_HD;     // wave-uniform
+    float v[4], m[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) { v[t] = vb[t][d]; m[t] = fabsf(v[t]); }
+    if (active)
+#pragma unroll
+        for (int o = 32; o; o >>= 1)
+#pragma unroll
+            for (int t = 0; t < 4; t++) m[t] = fmaxf(m[t], __shfl_xor(m[t], o));
+    act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)h * 4096,
+               xs + (uint64_t)a * XS_FLOATS + (uint64_t)h * 16, active);
+}
+
+static int attn_ws(int ctx_bound, int n_kv, int *nspan)
+{
+    const int nt = (ctx_bound + ATT_TP - 1) / ATT_TP;
+    *nspan = nt < ATT_NSPAN ? nt : ATT_NSPAN;
+    const size_t need = (size_t)n_kv * *nspan * ATT_MAXQ * (2 + ATT_HD) * sizeof(float);
     if (need > qg::ws_attn_bytes) {
         if (qg::ws_attn) {
             QG_CHECK(hipStreamSynchronize(qg::stream));
@@ -340,25 +515,29 @@ extern "C" int qgpu_attn_prep(float *q, uint64_t ldq, const float *k, const floa
     return QGPU_OK;
 }
 
-static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out, uint64_t ldo)
+static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out, uint64_t ldo, int act = 0)
 {
     AttnArgs a = a0;
-    int rc = attn_ws(ctx_bound, a.n_kv, &a.nchunk);
+    int rc = attn_ws(ctx_bound, a.n_kv, &a.nspan);
     if (rc) return rc;
     a.pml = (float *)qg::ws_attn;
-    a.po = a.pml + (size_t)a.n_kv * a.nchunk * ATT_MAXQ * 2;
-    const int rw = ((a.n_head / a.n_kv) * a.B + ATT_NWV - 1) / ATT_NWV;
-    const dim3 grid(a.n_kv, a.nchunk), blk(ATT_NWV * 64);
-#define ATT_GO(F_, R_) hipLaunchKernelGGL((k_attn_chunk<F_, R_>), grid, blk, 0, qg::stream, a)
-#define ATT_RWS(F_) do { switch (rw) { case 1: ATT_GO(F_, 1); break; case 2: ATT_GO(F_, 2); break; \
-                         case 3: ATT_GO(F_, 3); break; case 4: ATT_GO(F_, 4); break; case 5: ATT_GO(F_, 5); break; \
-                         default: ATT_GO(F_, 6); break; } } while (0)
-    if (fused) ATT_RWS(1); else ATT_RWS(0);
-#undef ATT_RWS
+    a.po = a.pml + (size_t)a.n_kv * a.nspan * ATT_MAXQ * 2;
+    const int nrt = ((a.n_head / a.n_kv) * a.B + 15) / 16;
+    const dim3 grid(a.n_kv, a.nspan), blk(ATT_NWV * 64);
+#define ATT_GO(F_, R_) hipLaunchKernelGGL((k_attn_span<F_, R_>), grid, blk, 0, qg::stream, a)
+#define ATT_RTS(F_) do { switch (nrt) { case 1: ATT_GO(F_, 1); break; case 2: ATT_GO(F_, 2); break; \
+                         default: ATT_GO(F_, 3); break; } } while (0)
+    if (fused) ATT_RTS(1); else ATT_RTS(0);
+#undef ATT_RTS
 #undef ATT_GO
     QG_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_attn_combine, dim3(a.n_head, a.B), dim3(ATT_HD), 0, qg::stream, a.q, a.ldq, a.pml, a.po,
-                       a.pos_dev, a.B, a.n_head, a.n_kv, a.nchunk, out, ldo);
+    if (act)
+        hipLaunchKernelGGL(k_attn_combine_act, dim3(a.n_head, (a.B + 3) / 4), dim3(4 * ATT_HD), 0, qg::stream, a.q,
+                           a.ldq, a.pml, a.po, a.pos_dev, a.B, a.n_head, a.n_kv, a.nspan, out, ldo, (uint8_t *)qg::ws,
+                           (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES));
+    else
+        hipLaunchKernelGGL(k_attn_combine, dim3(a.n_head, a.B), dim3(ATT_HD), 0, qg::stream, a.q, a.ldq, a.pml,
+                           a.po, a.pos_dev, a.B, a.n_head, a.n_kv, a.nspan, out, ldo);
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }
@@ -380,11 +559,10 @@ extern "C" int qgpu_attn_decode(const float *q, uint64_t ldq, const float *kcach
     return attn_launch(a, 0, ctx_bound, out, ldo);
 }
 
-extern "C" int qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
-                               const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
-                               const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
-                               int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out,
-                               uint64_t ldo)
+static int attn_fused(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                      const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                      const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev, int ctx_bound,
+                      int B, int n_head, int n_kv, int head_dim, float eps, float *out, uint64_t ldo, int act)
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
@@ -395,12 +573,33 @@ extern "C" int qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, con
         ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15) || ((uintptr_t)q_norm_w & 15) ||
         ((uintptr_t)k_norm_w & 15))
         return QGPU_E_ARG;
-    if ((n_head / n_kv) * B > ATT_MAXR) return QGPU_E_RANGE;
+    if ((n_head / n_kv) * B > ATT_MAXR || B > ATT_MAXB || (act && (uint64_t)n_head * ATT_HD > MAX_K))
+        return QGPU_E_RANGE;
     AttnArgs a = {};
     a.q = q; a.ldq = ldq; a.k = k; a.v = v; a.ldkv = ldkv; a.qw = q_norm_w; a.kw = k_norm_w;
     a.rcos = rope_cos; a.rsin = rope_sin; a.kc = kcache; a.vc = vcache; a.pos_dev = pos_dev;
     a.half = rope_dim / 2; a.B = B; a.n_head = n_head; a.n_kv = n_kv; a.eps = eps;
-    return attn_launch(a, 1, ctx_bound, out, ldo);
+    return attn_launch(a, 1, ctx_bound, out, ldo, act);
+}
+
+extern "C" int qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                               const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                               const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
+                               int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out,
+                               uint64_t ldo)
+{
+    return attn_fused(q, ldq, k, v, ldkv, q_norm_w, k_norm_w, kcache, vcache, rope_cos, rope_sin, rope_dim, pos_dev,
+                      ctx_bound, B, n_head, n_kv, head_dim, eps, out, ldo, 0);
+}
+
+extern "C" int qgpu_attn_fused_act(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                                   const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                                   const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
+                                   int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out,
+                                   uint64_t ldo)
+{
+    return attn_fused(q, ldq, k, v, ldkv, q_norm_w, k_norm_w, kcache, vcache, rope_cos, rope_sin, rope_dim, pos_dev,
+                      ctx_bound, B, n_head, n_kv, head_dim, eps, out, ldo, 1);
 }
 
 // Reserve the attention workspace up front (so later calls never allocate,
@@ -410,6 +609,6 @@ extern "C" int qgpu_attn_reserve(int ctx_bound, int n_kv)
     int rc = qg::ensure_init();
     if (rc) return rc;
     if (ctx_bound < 1 || n_kv < 1) return QGPU_E_ARG;
-    int nchunk;
-    return attn_ws(ctx_bound, n_kv, &nchunk);
+    int nspan;
+    return attn_ws(ctx_bound, n_kv, &nspan);
 }

@@ -24,10 +24,6 @@
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-#define MAX_K       65536
-#define MAX_NSB     (MAX_K / 256)
-#define PLANE_BYTES ((size_t)MAX_NSB * 4096)
-#define XS_FLOATS   ((size_t)MAX_NSB * 16)
 #define RSS_FLOATS  ((size_t)QGPU_MAX_B * MAX_NSB)
 #define ACT_RMS_DEFER 4      // internal prep kind: RMSNORM with the 1/rms factor applied by the GEMV
 
@@ -344,14 +340,9 @@ int qg_repack(int type, const void *raw, uint64_t ne0, uint64_t ne1, void *packe
 }
 
 // ---------------------------------------------------------------- activation prep
-// A operand of K-step (sb, ib) for plane a (tokens 4a..4a+3): 64 lanes x 8 bytes;
-// lane l = g*16 + m holds, for A row m = dgt*4 + t, the digit dgt of token t at
-// the 8 elements of sub-block ib that K-slots 8g..8g+7 stand for:
-//   slot 8g+c, c<4  -> element 4g+c        (low nibble of qs byte 4g+c)
-//   slot 8g+4+c     -> element 16+4g+c     (high nibble of qs byte 4g+c)
-// Two consecutive sub-blocks are interleaved so a lane fetches 16 bytes:
-//   byte offset ((sb*4 + ib/2)*64 + l)*16 + (ib%2)*8 + (slot%8).
-// xs[sb*16 + m] = 2^(8*dgt - s_t) converts the integer result of row m.
+// Digit planes: plane a holds tokens 4a..4a+3; the A tile of super-block sb is
+// at A + a*PLANE_BYTES + sb*4096 and its factors at xs + a*XS_FLOATS + sb*16
+// (layout: act_digits in qgpu_internal.h).
 struct ActDev {
     const float *x, *y, *w, *w2;
     float *xout;
@@ -384,8 +375,8 @@ static __device__ __forceinline__ float wave_sum(float v)
 template <int KIND>
 __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict__ A, float *__restrict__ xs)
 {
-    __shared__ uint8_t stage[4096];
-    __shared__ float red[2][4][4];       // [sum of squares | max |v|][token][wave]
+    __shared__ ActDigitLds dl;
+    __shared__ float red[4][4];          // sums of squares [token][wave]
     const int e = threadIdx.x, sb = blockIdx.x, a = blockIdx.y;
     const int lane = e & 63, wv = e >> 6;
     const uint64_t k = (uint64_t)sb * 256 + e;
@@ -436,7 +427,7 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
             }
         if (lane == 0)
 #pragma unroll
-            for (int i = 0; i < 4; i++) red[0][i][wv] = ss[i];
+            for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
         have_max = true;
     } else if (KIND == QGPU_ACT_RMSNORM) {
         // row RMS over the segment holding this super-block (each block recomputes it: same order, same value)
@@ -474,11 +465,11 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
             for (int i = 0; i < 4; i++) ss[i] += __shfl_xor(ss[i], o);
         if (lane == 0)
 #pragma unroll
-            for (int i = 0; i < 4; i++) red[0][i][wv] = ss[i];
+            for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float tot = (red[0][i][0] + red[0][i][1]) + (red[0][i][2] + red[0][i][3]);
+            const float tot = (red[i][0] + red[i][1]) + (red[i][2] + red[i][3]);
             const float sc = 1.0f / sqrtf(tot / (float)segl + p.eps);
             v[i] = i < nt ? (own[i] * sc) * wk : 0.0f;
         }
@@ -501,12 +492,12 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
             for (int i = 0; i < 4; i++) ss[i] += __shfl_xor(ss[i], o);
         if (lane == 0)
 #pragma unroll
-            for (int i = 0; i < 4; i++) red[0][i][wv] = ss[i];
+            for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            float tot = red[0][i][h0];
-            for (int q = 1; q < hw; q++) tot += red[0][i][h0 + q];
+            float tot = red[i][h0];
+            for (int q = 1; q < hw; q++) tot += red[i][h0 + q];
             const float sc = 1.0f / sqrtf(tot / (float)p.seg + p.eps);
             v[i] = i < nt ? ((raw[i] * sc) * wk) * silu_dev(gy[i]) : 0.0f;
         }
@@ -530,8 +521,7 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
         if (KIND == ACT_RMS_DEFER) {
             __syncthreads();
             if (e < nt)
-                p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] =
-                    (red[0][e][0] + red[0][e][1]) + (red[0][e][2] + red[0][e][3]);
+                p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[e][0] + red[e][1]) + (red[e][2] + red[e][3]);
         }
         return;
     }
@@ -543,40 +533,9 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
 #pragma unroll
             for (int i = 0; i < 4; i++) m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
     }
-    if (lane == 0)
-#pragma unroll
-        for (int i = 0; i < 4; i++) red[1][i][wv] = m[i];
-    __syncthreads();
-    if (KIND == ACT_RMS_DEFER && e < nt)
-        p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[0][e][0] + red[0][e][1]) + (red[0][e][2] + red[0][e][3]);
-    int shift[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float mx = fmaxf(fmaxf(red[1][i][0], red[1][i][1]), fmaxf(red[1][i][2], red[1][i][3]));
-        int E = 0;
-        if (mx > 0.0f && isfinite(mx)) { frexpf(mx, &E); shift[i] = 30 - E; }
-        else shift[i] = 0;
-    }
-    const int ib = e >> 5, w = e & 31, up = w >> 4, jj = w & 15, gg = jj >> 2, c = jj & 3;
-    const int boff = ((ib >> 1) * 64) * 16 + (ib & 1) * 8 + up * 4 + c;   // + lane*16
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float sv = ldexpf(v[i], shift[i]);
-        int X = isfinite(sv) ? (int)rintf(sv) : 0;
-#pragma unroll
-        for (int dg = 0; dg < 4; dg++) {
-            const int d = (dg < 3) ? (int)(int8_t)(X & 0xFF) : X;     // balanced base-256 digit
-            X = (X - d) >> 8;
-            stage[boff + (gg * 16 + dg * 4 + i) * 16] = (uint8_t)d;
-        }
-    }
-    __syncthreads();
-    uint8_t *dst = A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * 4096;
-    ((uint4 *)dst)[e] = ((const uint4 *)stage)[e];
-    if (e < 16) {
-        const int dg = e >> 2, t = e & 3;
-        xs[(uint64_t)a * XS_FLOATS + (uint64_t)sb * 16 + e] = ldexpf(1.0f, 8 * dg - shift[t]);
-    }
+    act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * 4096, xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16);
+    if (KIND == ACT_RMS_DEFER && e < nt)     // red[] was written before the barriers of act_digits
+        p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[e][0] + red[e][1]) + (red[e][2] + red[e][3]);
 }
 
 // ---------------------------------------------------------------- IQ4_XS MFMA GEMV
@@ -1447,6 +1406,14 @@ extern "C" int qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint6
 {
     if (!W || !W->packed) return QGPU_E_TYPE;
     return gemv_multi(&W, 1, nullptr, n, &out, &ldo, flags, nullptr, nullptr);
+}
+
+extern "C" int qgpu_gemv_prepared_split(const qgpu_tensor *W, int n, float *part, uint64_t ldp, int ks)
+{
+    if (!W || !part) return QGPU_E_ARG;
+    if (!W->packed) return QGPU_E_TYPE;
+    if (n > 1 && ldp < W->ne1) return QGPU_E_ARG;
+    return gemv_multi(&W, 1, nullptr, n, &part, &ldp, 0, nullptr, nullptr, ks);
 }
 
 extern "C" int qgpu_gemv_rows_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,

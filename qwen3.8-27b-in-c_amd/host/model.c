@@ -487,6 +487,32 @@ static void residual_gemv(qwen_model_t *m, const qgpu_tensor *W, const qgpu_act 
     }
 }
 
+/* residual_gemv on the input the previous kernel prepared (packed matrices only) */
+static void residual_gemv_prepared(qwen_model_t *m, const qgpu_tensor *W, uint32_t B, float *R)
+{
+    qwen_gpu_t *g = m->gpu;
+    const uint64_t E = m->dims.n_embd;
+    materialize(m);
+    const int ks = qgpu_gemv_split_ks(W);
+    if (ks > 1) {
+        K(qgpu_gemv_prepared_split(W, (int)B, g->part, E, ks));
+        g->pend = R; g->pend_ks = ks; g->pend_B = B;
+    } else {
+        K(qgpu_gemv_prepared(W, (int)B, R, E, QGPU_GEMV_ACCUM));
+    }
+}
+
+/* matrices that run on the matrix cores (packed tile records): the formats with
+ * an MFMA kernel and whole 256-column super-blocks */
+static int mat_packed(const qgpu_tensor *W)
+{
+    int t;
+    uint64_t ne0, ne1;
+    if (qgpu_tensor_shape(W, &t, &ne0, &ne1)) return 0;
+    return (t == GGML_IQ4_XS || t == GGML_Q4_K || t == GGML_Q5_K || t == GGML_Q6_K ||
+            t == GGML_Q8_0) && ne0 % 256 == 0;
+}
+
 static void ffn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B)
 {
     qwen_gpu_t *g = m->gpu;
@@ -518,15 +544,22 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     float *outs[3] = { g->bqkv, g->bk, g->bv };
     const uint64_t ld[3] = { g->SQ, g->kvrow, g->kvrow };
     K(qgpu_gemv_act_batch(W, 3, &an, (int)B, outs, ld, 0));
-    /* q/k norm + RoPE + cache write + attention in one kernel, then the chunk merge */
-    (void)pos;   /* positions come from g->d_pos; the grid covers n_ctx (chunks past the live end exit) */
-    K(qgpu_attn_fused(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos,
-                      g->rope_sin, (int)m->cfg.rope_dim_count, g->d_pos, (int)m->n_ctx, (int)B, (int)d->n_head,
-                      (int)d->n_kv_head, (int)d->head_dim, eps, g->battn, g->A));
-    qgpu_act oc;
-    memset(&oc, 0, sizeof oc);
-    oc.kind = QGPU_ACT_COPY; oc.x = g->battn; oc.ldx = g->A;
-    residual_gemv(m, D->o, &oc, B, R);
+    /* q/k norm + RoPE + cache write + attention in one kernel, then the span merge, which also
+     * prepares the o-projection input when the matrix runs on the matrix cores */
+    (void)pos;   /* positions come from g->d_pos; the grid covers n_ctx (spans past the live end exit) */
+    const int prep = mat_packed(D->o);
+    K((prep ? qgpu_attn_fused_act : qgpu_attn_fused)(
+        g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos, g->rope_sin,
+        (int)m->cfg.rope_dim_count, g->d_pos, (int)m->n_ctx, (int)B, (int)d->n_head, (int)d->n_kv_head,
+        (int)d->head_dim, eps, g->battn, g->A));
+    if (prep) {
+        residual_gemv_prepared(m, D->o, B, R);
+    } else {
+        qgpu_act oc;
+        memset(&oc, 0, sizeof oc);
+        oc.kind = QGPU_ACT_COPY; oc.x = g->battn; oc.ldx = g->A;
+        residual_gemv(m, D->o, &oc, B, R);
+    }
     ffn_dev(m, D, R, B);
 }
 

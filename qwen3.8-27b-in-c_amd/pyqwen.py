@@ -274,6 +274,8 @@ class GpuLib:
             "qgpu_attn_decode": [F32P, u64, F32P, F32P, ctypes.POINTER(i32), i32, i32, i32, i32, i32, F32P, u64],
             "qgpu_attn_fused": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
                                 ctypes.POINTER(i32), i32, i32, i32, i32, i32, f32, F32P, u64],
+            "qgpu_attn_fused_act": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
+                                    ctypes.POINTER(i32), i32, i32, i32, i32, i32, f32, F32P, u64],
             "qgpu_attn_reserve": [i32, i32],
             "qgpu_set_i32": [ctypes.POINTER(i32), i32],
             "qgpu_gemv_act_batch": [ctypes.POINTER(vp), i32, ctypes.POINTER(Act), i32, ctypes.POINTER(F32P),
@@ -281,6 +283,7 @@ class GpuLib:
             "qgpu_act_prepare": [ctypes.POINTER(Act), i32, u64],
             "qgpu_gemv_act_split": [vp, ctypes.POINTER(Act), i32, F32P, u64, i32],
             "qgpu_gemv_split_ks": [vp],
+            "qgpu_gemv_prepared_split": [vp, i32, F32P, u64, i32],
             "qgpu_add_partials": [F32P, u64, F32P, u64, F32P, u64, i32, u64, i32],
             "qgpu_spec_accept": [U32P, U32P, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), i32, U32P],
         }

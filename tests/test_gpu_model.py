@@ -155,10 +155,11 @@ def attn_fp64(q, k, v, qw, kw, kc, vc, pos, B, nh, nkv, hd, rope_dim, theta, eps
     return out, kc, vc
 
 
-@pytest.mark.parametrize("pos,B", [(0, 1), (37, 4), (300, 8), (95, 3), (31, 2), (504, 8)])
-def test_attention_vs_fp64(gpu, pos, B):
-    print(f"\n[attn] pos={pos} B={B}", flush=True)
-    nh, nkv, hd, rope_dim, theta, eps, n_ctx = 24, 4, 256, 64, 1e7, 1e-6, 512
+ATT_DIMS = (24, 4, 256, 64, 1e7, 1e-6, 512)      # n_head, n_kv, head_dim, rope_dim, theta, eps, n_ctx
+
+
+def _attn_inputs(pos, B):
+    nh, nkv, hd, rope_dim, theta, eps, n_ctx = ATT_DIMS
     rng = np.random.default_rng(pos + B)
     q = rng.standard_normal((B, nh * 2 * hd)).astype(np.float32)
     k = rng.standard_normal((B, nkv * hd)).astype(np.float32)
@@ -173,6 +174,14 @@ def test_attention_vs_fp64(gpu, pos, B):
     i = np.arange(half)
     ang = np.arange(n_ctx, dtype=np.float32)[:, None] * np.power(np.float32(theta), (-2.0 * i / rope_dim).astype(np.float32))[None]
     rc, rs = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    return q, k, v, qw, kw, kc, vc, rc, rs
+
+
+@pytest.mark.parametrize("pos,B", [(0, 1), (37, 4), (300, 8), (95, 3), (31, 2), (504, 8), (17, 6), (497, 8)])
+def test_attention_vs_fp64(gpu, pos, B):
+    print(f"\n[attn] pos={pos} B={B}", flush=True)
+    nh, nkv, hd, rope_dim, theta, eps, n_ctx = ATT_DIMS
+    q, k, v, qw, kw, kc, vc, rc, rs = _attn_inputs(pos, B)
     ref, kref, vref = attn_fp64(q, k, v, qw, kw, kc, vc, pos, B, nh, nkv, hd, rope_dim, theta, eps)
     qb, kb, vb = gpu.put(q), gpu.put(k), gpu.put(v)
     kcb, vcb = gpu.put(kc), gpu.put(vc)
@@ -202,6 +211,58 @@ def test_attention_vs_fp64(gpu, pos, B):
     assert rel_err(kcg2[pos:pos + B], kref[pos:pos + B]) < 1e-5
     assert np.array_equal(kcg2[:pos], kc[:pos]) and np.array_equal(kcg2[pos + B:], kc[pos + B:])
     assert np.array_equal(vcb2.download(np.float32).reshape(n_ctx, nkv, hd)[pos:pos + B], v.reshape(B, nkv, hd))
+
+
+@pytest.mark.parametrize("t", [23, 14])
+@pytest.mark.parametrize("pos,B", [(0, 1), (300, 4), (95, 7), (504, 8)])
+def test_attention_prepares_o_projection(gpu, t, pos, B):
+    """qgpu_attn_fused_act writes the rows of qgpu_attn_fused and the digit planes the COPY preparation
+    writes from them: the o-projection through qgpu_gemv_prepared(_split) equals qgpu_gemv_act_split /
+    qgpu_gemv_act_batch on the rows, bit for bit."""
+    import ctypes
+    print(f"\n[attn-act] type={t} pos={pos} B={B}", flush=True)
+    nh, nkv, hd, rope_dim, theta, eps, n_ctx = ATT_DIMS
+    q, k, v, qw, kw, kc, vc, rc, rs = _attn_inputs(pos, B)
+    host = host_lib()
+    ne0, ne1 = nh * hd, 320
+    W = host.synth_matrix(t, ne0, ne1, 41, 7, 0.02)
+    T = gpu.tensor(W, t, ne0, ne1)
+    ks = gpu.L.qgpu_gemv_split_ks(T.h)
+    assert ks > 1
+    qb, kb, vb = gpu.put(q), gpu.put(k), gpu.put(v)
+    posb = gpu.put(np.array([pos], np.int32))
+    qwb, kwb, rcb, rsb = gpu.put(qw), gpu.put(kw), gpu.put(rc), gpu.put(rs)
+
+    def attn(fn):
+        kcb, vcb, ob = gpu.put(kc), gpu.put(vc), gpu.buf(B * ne0 * 4)
+        gpu.ok(fn(qb.f32(), nh * 2 * hd, kb.f32(), vb.f32(), nkv * hd, qwb.f32(), kwb.f32(), kcb.f32(), vcb.f32(),
+                  rcb.f32(), rsb.f32(), rope_dim, posb.i32(), n_ctx, B, nh, nkv, hd, eps, ob.f32(), ne0))
+        return ob, kcb.download(np.float32), vcb.download(np.float32)
+
+    pa, pb = gpu.buf(ks * B * ne1 * 4), gpu.buf(ks * B * ne1 * 4)
+    ya, yb = gpu.buf(B * ne1 * 4), gpu.buf(B * ne1 * 4)
+    # the reference sequence: attention rows, then the COPY preparation inside the GEMV calls
+    oa, kca, vca = attn(gpu.L.qgpu_attn_fused)
+    a = pyqwen.Act()
+    a.kind, a.x, a.ldx = pyqwen.ACT_COPY, oa.f32(), ne0
+    gpu.ok(gpu.L.qgpu_gemv_act_split(T.h, ctypes.byref(a), B, pa.f32(), ne1, ks))
+    Ws = (ctypes.c_void_p * 1)(T.h)
+    gpu.ok(gpu.L.qgpu_gemv_act_batch(Ws, 1, ctypes.byref(a), B, (pyqwen.F32P * 1)(ya.f32()),
+                                     (ctypes.c_uint64 * 1)(ne1), 0))
+    # the prepared sequence
+    ob1, kcb1, vcb1 = attn(gpu.L.qgpu_attn_fused_act)
+    gpu.ok(gpu.L.qgpu_gemv_prepared_split(T.h, B, pb.f32(), ne1, ks))
+    ob2, _, _ = attn(gpu.L.qgpu_attn_fused_act)
+    gpu.ok(gpu.L.qgpu_gemv_prepared(T.h, B, yb.f32(), ne1, 0))
+    rows = oa.download(np.float32)
+    assert np.array_equal(ob1.download(np.float32), rows) and np.array_equal(ob2.download(np.float32), rows)
+    assert np.array_equal(kcb1, kca) and np.array_equal(vcb1, vca)
+    assert np.array_equal(pb.download(np.float32), pa.download(np.float32))
+    assert np.array_equal(yb.download(np.float32), ya.download(np.float32))
+    ref = O.gemv(t, W, ne0, ne1, rows.reshape(B, ne0), B)
+    e = rel_err(ya.download(np.float32).reshape(B, ne1), ref)
+    print(f"  ks={ks} prepared == act path; gemv rel err {e:.2e}", flush=True)
+    assert e < 2e-5
 
 
 def test_spec_accept_kernel(gpu):
