@@ -285,8 +285,8 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 const int b = e >> 6, d4 = e & 63, t = pos0 + b;
                 if (t < posA || t >= posB) continue;
                 const uint64_t row = (uint64_t)t * kvrow + hoff + 4 * d4;
-                *(float4 *)(p.kc + row) = *(const float4 *)&Kn[b][4 * d4];
-                *(float4 *)(p.vc + row) = *(const float4 *)(p.v + (uint64_t)b * p.ldkv + hoff + 4 * d4);
+                st_stream4(p.kc + row, *(const float4 *)&Kn[b][4 * d4]);
+                st_stream4(p.vc + row, *(const float4 *)(p.v + (uint64_t)b * p.ldkv + hoff + 4 * d4));
             }
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++)

@@ -15,6 +15,13 @@
 
 static __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
 
+// state rows after each token: written once, read only by a later launch (rollback or the next verify)
+static __device__ __forceinline__ void store_state8(float *p, const float (&S)[8])
+{
+    st_stream4(p, S[0], S[1], S[2], S[3]);
+    st_stream4(p + 4, S[4], S[5], S[6], S[7]);
+}
+
 // one thread per channel: 4-tap causal conv over the sliding window, SiLU, snapshots
 __global__ __launch_bounds__(256) void k_gdn_conv(const float *__restrict__ x, uint64_t ldx, int B, int conv_dim,
                                                   const float *__restrict__ w, float *__restrict__ ring,
@@ -129,9 +136,7 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float *__restrict__ xq,
         if (cc == 0) out[(uint64_t)b * ldo + (uint64_t)h * GDN_HK + j] = (decay * sq + dj * kq) * qscale;
 #pragma unroll
         for (int i = 0; i < 8; i++) S[i] = fmaf(dj, k[i], decay * S[i]);
-        float *Sn = ring + (uint64_t)((cur + 1 + b) % nslot) * stride + hoff;
-        *(float4 *)Sn = make_float4(S[0], S[1], S[2], S[3]);
-        *(float4 *)(Sn + 4) = make_float4(S[4], S[5], S[6], S[7]);
+        store_state8(ring + (uint64_t)((cur + 1 + b) % nslot) * stride + hoff, S);
     }
 }
 
@@ -210,7 +215,7 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
             dA[b * GDN_HK] = silu_f(((a0 * wA.x + a1 * wA.y) + a2 * wA.z) + a3 * wA.w);
             if (own_qk) {
                 const int slot = (cur + 1 + b) % nslot;
-                *(float4 *)(cring + (uint64_t)slot * cstride + (uint64_t)cA * 4) = make_float4(a0, a1, a2, a3);
+                st_stream4(cring + (uint64_t)slot * cstride + (uint64_t)cA * 4, a0, a1, a2, a3);
             }
         }
     }
@@ -224,7 +229,7 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
             const float a0 = win[b + 1], a1 = win[b + 2], a2 = win[b + 3], a3 = win[b + 4];
             Yv[b][tid] = silu_f(((a0 * wB.x + a1 * wB.y) + a2 * wB.z) + a3 * wB.w);
             const int slot = (cur + 1 + b) % nslot;
-            *(float4 *)(cring + (uint64_t)slot * cstride + (uint64_t)cB * 4) = make_float4(a0, a1, a2, a3);
+            st_stream4(cring + (uint64_t)slot * cstride + (uint64_t)cB * 4, a0, a1, a2, a3);
         }
     }
     __syncthreads();
@@ -274,9 +279,7 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
         if (cc == 0) out[(uint64_t)b * ldo + (uint64_t)h * GDN_HK + j] = (decay * sq + dj * kq) * qscale;
 #pragma unroll
         for (int i = 0; i < 8; i++) S[i] = fmaf(dj, k[i], decay * S[i]);
-        float *Sn = sring + (uint64_t)((cur + 1 + b) % nslot) * sstride + hoff;
-        *(float4 *)Sn = make_float4(S[0], S[1], S[2], S[3]);
-        *(float4 *)(Sn + 4) = make_float4(S[4], S[5], S[6], S[7]);
+        store_state8(sring + (uint64_t)((cur + 1 + b) % nslot) * sstride + hoff, S);
     }
 }
 

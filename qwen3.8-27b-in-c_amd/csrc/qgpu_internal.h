@@ -38,6 +38,18 @@ struct qgpu_tensor {
     int      packed;      // 1: tile records (IQ4_XS, Q4_K, Q5_K, Q6_K, Q8_0 with ne0 % 256 == 0)
 };
 
+// State that only a later step reads (GDN state and conv snapshots, new KV
+// cache rows) goes out with non-temporal stores: it leaves this XCD's L2 as it
+// is written instead of in the write-back at the end of the kernel, which
+// otherwise holds up the next launch.  Results the next launch reads stay
+// plain stores (non-temporal ones made those reads slower).
+typedef float qg_v4f __attribute__((ext_vector_type(4)));
+static __device__ __forceinline__ void st_stream4(float *p, float a, float b, float c, float d)
+{
+    __builtin_nontemporal_store(qg_v4f{a, b, c, d}, (qg_v4f *)p);
+}
+static __device__ __forceinline__ void st_stream4(float *p, float4 v) { st_stream4(p, v.x, v.y, v.z, v.w); }
+
 // GEMV activation workspace (qg::ws): two digit planes of 4 tokens each, then
 // their conversion factors, then the deferred-RMSNorm sums (gemv.hip).
 #define MAX_K       65536
