@@ -27,10 +27,12 @@ mode sweep -- gemv_batch over every weight format of the path (IQ4_XS, Q4_K,
 
 roofline (every mode): the dominant kernel, k_gemv_mfma (IQ4_XS), on the gemv workload
 (17408 x 5120 IQ4_XS, B = 4), run first in the process: W + K gemv_batch calls,
-then W + K launches of the GEMV kernel alone on prepared activations, the last
-K bracketed by HIP events on the library stream.  achieved = algorithmic bytes
-per launch (47,349,760 weight + 4 x (5120 + 17408) x 4 activation/output =
-47,710,208 B) / average launch duration.  Weights rotate over 12 copies
+then the GEMV kernel alone on prepared activations.  Each timed series of K
+calls is captured in a HIP graph, replayed once untimed and once bracketed by
+HIP events on the library stream (the replay issues the K kernels back to back,
+so the host loop's per-call cost does not enter the kernel time).  achieved =
+algorithmic bytes per launch (47,349,760 weight + 4 x (5120 + 17408) x 4
+activation/output = 47,710,208 B) / average launch duration.  Weights rotate over 12 copies
 (568 MB) so the 256 MB MALL cannot serve repeats.
 
 cpu_baseline: the reference engine itself (oracle/_ref, compiled from the
@@ -145,6 +147,26 @@ def cpu_baseline_spec(path, prompt, k, seconds):
 
 
 # ---------------------------------------------------------------------------------- roofline microbench
+def graph_ms(gpu, calls, e0, e1):
+    """Captures the stream work of calls() in a HIP graph, replays it once untimed and once
+    between HIP events; returns the timed replay's milliseconds.  The replay issues the
+    captured kernels back to back, so the host's per-call cost is not in the figure."""
+    L = gpu.L
+    gpu.sync()
+    gpu.ok(L.qgpu_graph_begin())
+    calls()
+    gexec = ctypes.c_void_p()
+    gpu.ok(L.qgpu_graph_end(ctypes.byref(gexec)))
+    gpu.ok(L.qgpu_graph_launch(gexec))
+    gpu.record(e0)
+    gpu.ok(L.qgpu_graph_launch(gexec))
+    gpu.record(e1)
+    ms = gpu.elapsed_ms(e0, e1)
+    gpu.sync()
+    gpu.ok(L.qgpu_graph_destroy(gexec))
+    return ms
+
+
 def gemv_roofline(gpu, host, steps, warmup):
     """config-1 GEMV: gemv_batch calls, then the GEMV kernel alone (roofline)."""
     ne0, ne1, B = 5120, 17408, 4
@@ -159,21 +181,18 @@ def gemv_roofline(gpu, host, steps, warmup):
     # gemv_batch calls (activation prep + GEMV kernel), the library entry point
     for i in range(warmup):
         gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
-    gpu.record(e0)
-    for i in range(steps):
-        gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
-    gpu.record(e1)
-    ms_call = gpu.elapsed_ms(e0, e1) / steps
+
+    def batch_calls():
+        for i in range(steps):
+            gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
+    ms_call = graph_ms(gpu, batch_calls, e0, e1) / steps
     # the GEMV kernel alone: activations prepared once
     gpu.ok(L.qgpu_gemv_prepare(xb.f32(), ne0, B, ne0))
-    for i in range(warmup):
-        gpu.ok(L.qgpu_gemv_prepared(Ts[i % R].h, B, ob.f32(), ne1, 0))
-    gpu.record(e0)
-    for i in range(steps):
-        gpu.ok(L.qgpu_gemv_prepared(Ts[i % R].h, B, ob.f32(), ne1, 0))
-    gpu.record(e1)
-    ms_kernel = gpu.elapsed_ms(e0, e1) / steps
-    gpu.sync()
+
+    def kernel_calls():
+        for i in range(steps):
+            gpu.ok(L.qgpu_gemv_prepared(Ts[i % R].h, B, ob.f32(), ne1, 0))
+    ms_kernel = graph_ms(gpu, kernel_calls, e0, e1) / steps
     for T in Ts:
         T.close()
     achieved = algo / (ms_kernel * 1e-3) / 1e9
@@ -182,7 +201,7 @@ def gemv_roofline(gpu, host, steps, warmup):
             "kernel": ROOF_KERNEL, "workload": "IQ4_XS 17408x5120, B=4", "kernel_us": round(ms_kernel * 1e3, 3),
             "algo_bytes": algo,
             # dispatch ordinals of this kernel (0-based, in launch order) that the events bracket
-            "dispatches": {"first": 2 * warmup + steps, "count": steps}}
+            "dispatches": {"first": warmup + 3 * steps, "count": steps}}
     gemv_call_gbs = algo / (ms_call * 1e-3) / 1e9
     return roof, gemv_call_gbs, ms_call, (W, x, ne0, ne1, B)
 
@@ -206,11 +225,11 @@ def bench_sweep(gpu, host, steps, warmup):
             for B in (1, 2, 4, 8):
                 for i in range(warmup):
                     gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
-                gpu.record(e0)
-                for i in range(steps):
-                    gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
-                gpu.record(e1)
-                us = gpu.elapsed_ms(e0, e1) / steps * 1e3
+
+                def calls():
+                    for i in range(steps):
+                        gpu.ok(L.qgpu_gemv_batch(Ts[i % R].h, xb.f32(), ne0, B, ob.f32(), ne1, 0))
+                us = graph_ms(gpu, calls, e0, e1) / steps * 1e3
                 algo = W.nbytes + B * (ne0 + ne1) * 4
                 rows.append({"format": fname, "rows": ne1, "cols": ne0, "B": B, "us": round(us, 2),
                              "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 4),

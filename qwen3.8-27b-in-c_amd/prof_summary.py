@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """Short text summaries of rocprofv3 results (SQLite *_results.db, ROCm 7).
 
-    prof_summary.py stats   DB_OR_DIR --cmd "<command that made it>" [--bench-json FILE] [--top N]
+    prof_summary.py stats   DB_OR_DIR --cmd "<command that made it>" [--bench-json FILE] [--plain-json FILE] [--top N]
     prof_summary.py traffic FETCH_DB WRITE_DB --bench-json FILE [--calib-bytes N]
 
 stats   : per-kernel calls / total / average duration of a --kernel-trace run,
@@ -9,7 +9,8 @@ stats   : per-kernel calls / total / average duration of a --kernel-trace run,
           roofline kernel over exactly the dispatches the benchmark's events
           bracketed (roofline.dispatches: ordinal of the first one among that
           kernel's dispatches, and their count), next to the benchmark's own
-          event-timed figure.
+          event-timed figure, in the traced run and (--plain-json) in a run of
+          the same command without the tracer.
 traffic : HBM bytes per launch of the roofline kernel from two --pmc runs
           (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by what the
           same counter reads for the k_copy kernel of known size (the
@@ -82,15 +83,24 @@ def cmd_stats(a):
             out += ["", f"## Roofline kernel `{r['kernel']}` ({r.get('workload', '')})", "",
                     f"Dispatches {first}..{first + count - 1} of this kernel (the ones the benchmark's events "
                     f"bracket): average {avg:.3f} us, median {statistics.median(sel) / 1e3:.3f} us.",
-                    f"Benchmark's event-timed average over the same launches: {r['kernel_us']:.3f} us "
-                    f"(ratio {r['kernel_us'] / avg:.3f}).",
+                    f"Benchmark's event-timed average over the same launches in the traced run: {r['kernel_us']:.3f} us "
+                    f"(ratio {r['kernel_us'] / avg:.3f}; the tracer's per-dispatch cost is inside this figure when the "
+                    f"launches are graph replays)."]
+            if a.plain_json:
+                rp = bench_line(a.plain_json)["roofline"]
+                out += [f"Same command without the tracer: event-timed average {rp['kernel_us']:.3f} us "
+                        f"(ratio {rp['kernel_us'] / avg:.3f} to the traced kernel durations)."]
+            out += [
                     f"Algorithmic bytes per launch {r['algo_bytes']:,} -> {r['algo_bytes'] / avg / 1e3:.1f} GB/s "
                     f"= {r['algo_bytes'] / avg / 1e3 / r['peak']:.3f} of {r['peak']:.0f} GB/s."]
         else:
             out += ["", f"roofline kernel {r['kernel']}: only {len(durs)} dispatches in the trace"]
         keys = [k for k in ("value", "unit", "ms_per_step", "verify_ms", "decode_ms", "draft_ms",
                             "verify_over_decode", "verify_hbm_gbs", "forced_accept_tok_s") if k in b]
-        out += ["", "Benchmark line of this run: " + ", ".join(f"{k} = {b[k]}" for k in keys) + "."]
+        out += ["", "Benchmark line of the traced run: " + ", ".join(f"{k} = {b[k]}" for k in keys) + "."]
+        if a.plain_json:
+            bp = bench_line(a.plain_json)
+            out += ["", "Benchmark line without the tracer: " + ", ".join(f"{k} = {bp[k]}" for k in keys if k in bp) + "."]
     print("\n".join(out))
 
 
@@ -134,6 +144,7 @@ def main():
     s.add_argument("--cmd", required=True)
     s.add_argument("--title", default=None)
     s.add_argument("--bench-json", default=None)
+    s.add_argument("--plain-json", default=None, help="bench line of the same command run without the tracer")
     s.add_argument("--top", type=int, default=25)
     t = sub.add_parser("traffic")
     t.add_argument("fetch_db")
