@@ -62,7 +62,8 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
 }
 
 // Span kernel (flash decoding on the matrix cores).  Block (g, s): kv head g,
-// span s of 16-position tiles, 4 waves; wave w owns head dims [64w, 64w + 64).
+// span s of 16-position tiles, NW waves; wave w owns head dims [DW w, DW w + DW),
+// DW = 256 / NW (the comments below take NW = 4, DW = 64).
 // It serves every query row of the group, r = b * per + (h - g*per) < QH =
 // per * B, as NRT row tiles of 16.
 //   * Scores, per tile and row tile: S^T (16 positions x 16 rows) = K Q^T with
@@ -89,14 +90,19 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
 // spans (the launch size); blocks past nsl exit and the combine skips them.
 // partials: pml [n_kv][nspan][ATT_MAXQ][2] (m, l), po [n_kv][nspan][ATT_MAXQ][ATT_HD]
 #define ATT_TP    16          // positions per tile
-#define ATT_NWV   4           // waves per block
 #define ATT_MAXB  8           // new positions per fused call
+#ifndef ATT_NSPAN
 #define ATT_NSPAN 64          // spans per kv head at most
+#endif
 #ifndef ATT_MINTPS
 #define ATT_MINTPS 1          // tiles per span at least
 #endif
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+template <int N> struct VSlice;                     // a lane's V slice of N dims
+template <> struct VSlice<4> { typedef v4f T; };
+template <> struct VSlice<2> { typedef v2f T; };
 
 struct AttnArgs {
     const float *q; uint64_t ldq;
@@ -132,10 +138,14 @@ static __device__ __forceinline__ v4f mfma4(float a, float b, v4f c)
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <int FUSED, int NRT>
+template <int FUSED, int NRT, int ATT_NWV>
 __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 {
-    __shared__ float lds[FUSED ? NRT * 16 * ATT_HD : NRT * 2048];   // q rows (FUSED), then the score exchange
+    constexpr int ATT_DW = ATT_HD / ATT_NWV;      // head dims per wave
+    constexpr int ATT_NQ = ATT_DW / 16;           // float4 operand loads per row and 16-dim output tiles per wave
+    typedef typename VSlice<ATT_NQ>::T vqf;
+    constexpr int SXF = 2 * ATT_NWV * NRT * 64 * 4;               // floats of the score exchange
+    __shared__ float lds[FUSED && NRT * 16 * ATT_HD > SXF ? NRT * 16 * ATT_HD : SXF];   // q rows (FUSED), then the score exchange
     __shared__ float Kn[FUSED ? ATT_MAXB : 1][ATT_HD];   // new k rows, normalised and rotated
     __shared__ float Rc[FUSED ? ATT_MAXB * ATT_HD / 2 : 1], Rs[FUSED ? ATT_MAXB * ATT_HD / 2 : 1];   // RoPE tables
     const int g = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
@@ -143,7 +153,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     const int n = lane & 15, gq = lane >> 4;
     const int per = p.n_head / p.n_kv, QH = per * p.B;
     const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD, hoff = (uint64_t)g * ATT_HD;
-    const int d0 = 64 * wv;
+    const int d0 = ATT_DW * wv;
 
     // ---- loads that do not depend on the position first: q rows (FUSED: raw rows for the
     // prologue; else the Q operands, row rt*16 + n, dims d0 + 16q + 4gq .. +3), the new k
@@ -151,7 +161,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     constexpr int QV = FUSED ? NRT * 16 * 64 / (ATT_NWV * 64) : 1;   // float4 of q rows per thread
     constexpr int KV = FUSED ? ATT_MAXB * 64 / (ATT_NWV * 64) : 1;
     float4 qv[QV], knv[KV], qw = make_float4(0.0f, 0.0f, 0.0f, 0.0f), kw = qw;
-    v4f qop[NRT][4];
+    v4f qop[NRT][ATT_NQ];
     if (FUSED) {
 #pragma unroll
         for (int u = 0; u < QV; u++) {
@@ -176,7 +186,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
             const int r = rt * 16 + n;
             const int b = r / per, h = g * per + r % per;
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+            for (int q = 0; q < ATT_NQ; q++)
                 qop[rt][q] = r < QH ? *(const v4f *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + d0 + 16 * q + 4 * gq)
                                     : v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -196,29 +206,30 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         if (FUSED && new_rows) {
             if (pp >= pos0 && pp <= tmax)
 #pragma unroll
-                for (int q = 0; q < 4; q++) kr[q] = *(const v4f *)&Kn[pp - pos0][d0 + 16 * q + 4 * gq];
+                for (int q = 0; q < ATT_NQ; q++) kr[q] = *(const v4f *)&Kn[pp - pos0][d0 + 16 * q + 4 * gq];
             return;
         }
 #pragma unroll
-        for (int q = 0; q < 4; q++) kr[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int q = 0; q < ATT_NQ; q++) kr[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         if (pp <= tmax && (!FUSED || pp < pos0))
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+            for (int q = 0; q < ATT_NQ; q++)
                 kr[q] = *(const v4f *)(p.kc + (uint64_t)pp * kvrow + hoff + d0 + 16 * q + 4 * gq);
     };
-    auto load_v = [&](int t, v4f *vr) {
+    auto load_v = [&](int t, vqf *vr) {
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int pp = t * ATT_TP + 4 * gq + v;
-            vr[v] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            vr[v] = vqf{};
             if (pp <= tmax) {
-                if (FUSED && pp >= pos0) vr[v] = *(const v4f *)(p.v + (uint64_t)(pp - pos0) * p.ldkv + hoff + d0 + 4 * n);
-                else vr[v] = *(const v4f *)(p.vc + (uint64_t)pp * kvrow + hoff + d0 + 4 * n);
+                if (FUSED && pp >= pos0) vr[v] = *(const vqf *)(p.v + (uint64_t)(pp - pos0) * p.ldkv + hoff + d0 + ATT_NQ * n);
+                else vr[v] = *(const vqf *)(p.vc + (uint64_t)pp * kvrow + hoff + d0 + ATT_NQ * n);
             }
         }
     };
     // the first tile's operands are in flight during the q preparation
-    v4f kr[4], vr[4];
+    v4f kr[ATT_NQ];
+    vqf vr[4];
     load_k(tile0, kr, 0);
     load_v(tile0, vr);
 
@@ -291,11 +302,11 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) qop[rt][q] = *(const v4f *)&Qs[rt * 16 + n][d0 + 16 * q + 4 * gq];
+            for (int q = 0; q < ATT_NQ; q++) qop[rt][q] = *(const v4f *)&Qs[rt * 16 + n][d0 + 16 * q + 4 * gq];
         __syncthreads();                          // lds is the score exchange from here on
     }
 
-    v4f oacc[NRT][4];
+    v4f oacc[NRT][ATT_NQ];
     float mrow[NRT], lrow[NRT];
     int lim[NRT];                                 // last position row rt*16 + n may see (-1: padding row)
 #pragma unroll
@@ -305,14 +316,15 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         const int r = rt * 16 + n;
         lim[rt] = r < QH ? pos0 + r / per : -1;
 #pragma unroll
-        for (int c = 0; c < 4; c++) oacc[rt][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < ATT_NQ; c++) oacc[rt][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     }
     const float scale = 1.0f / sqrtf((float)ATT_HD);
     v4f *Sx = (v4f *)lds;                         // [2][ATT_NWV][NRT][64]
     if (FUSED) load_k(tile0, kr, 1);
     for (int t = tile0; t < tile1; t++) {
         const int buf = (t - tile0) & 1;
-        v4f kn[4], vn[4];
+        v4f kn[ATT_NQ];
+        vqf vn[4];
         if (t + 1 < tile1) {
             load_k(t + 1, kn, 0);
             if (FUSED) load_k(t + 1, kn, 1);
@@ -323,7 +335,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         for (int rt = 0; rt < NRT; rt++) {
             v4f sp = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+            for (int q = 0; q < ATT_NQ; q++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) sp = mfma4(kr[q][j], qop[rt][q][j], sp);
             Sx[((buf * ATT_NWV + wv) * NRT + rt) * 64 + lane] = sp;
@@ -331,10 +343,9 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         __syncthreads();
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
-            const v4f st = ((Sx[((buf * ATT_NWV + 0) * NRT + rt) * 64 + lane] +
-                             Sx[((buf * ATT_NWV + 1) * NRT + rt) * 64 + lane]) +
-                            Sx[((buf * ATT_NWV + 2) * NRT + rt) * 64 + lane]) +
-                           Sx[((buf * ATT_NWV + 3) * NRT + rt) * 64 + lane];
+            v4f st = Sx[((buf * ATT_NWV + 0) * NRT + rt) * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < ATT_NWV; w++) st += Sx[((buf * ATT_NWV + w) * NRT + rt) * 64 + lane];
             float sv[4];
             float mx = -INFINITY;
 #pragma unroll
@@ -362,16 +373,18 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
             for (int w = 0; w < 4; w++) {
                 const float aw = __shfl(alpha, 4 * gq + w);
 #pragma unroll
-                for (int c = 0; c < 4; c++) oacc[rt][c][w] *= aw;
+                for (int c = 0; c < ATT_NQ; c++) oacc[rt][c][w] *= aw;
             }
 #pragma unroll
             for (int v = 0; v < 4; v++)
 #pragma unroll
-                for (int c = 0; c < 4; c++) oacc[rt][c] = mfma4(pv[v], vr[v][c], oacc[rt][c]);
+                for (int c = 0; c < ATT_NQ; c++) oacc[rt][c] = mfma4(pv[v], vr[v][c], oacc[rt][c]);
         }
         if (t + 1 < tile1) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) { kr[q] = kn[q]; vr[q] = vn[q]; }
+            for (int q = 0; q < ATT_NQ; q++) kr[q] = kn[q];
+#pragma unroll
+            for (int v = 0; v < 4; v++) vr[v] = vn[v];
         }
     }
     // ---- partials of this span
@@ -386,17 +399,22 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             const int r = rt * 16 + 4 * gq + w;
-            if (r < QH)
-                *(v4f *)(o + (uint64_t)r * ATT_HD + d0 + 4 * n) =
-                    v4f{oacc[rt][0][w], oacc[rt][1][w], oacc[rt][2][w], oacc[rt][3][w]};
+            if (r < QH) {
+                vqf ov;
+#pragma unroll
+                for (int c = 0; c < ATT_NQ; c++) ov[c] = oacc[rt][c][w];
+                *(vqf *)(o + (uint64_t)r * ATT_HD + d0 + ATT_NQ * n) = ov;
+            }
         }
     }
 }
 
 // out[b][h*hd + d] = sum_c o_c exp(m_c - M) / sum_c l_c exp(m_c - M) * sigmoid(gate) over the
-// nc <= 64 spans with work (rows with no position in a span have m = -inf there and are
-// skipped).  One wave per call: lane c holds span c's (m, l), the max and the weighted sum
-// of l are wave reductions, and the o loads are independent of them and of each other.
+// nc <= ATT_NSPAN spans with work (rows with no position in a span have m = -inf there and
+// are skipped).  One wave per call: lane c holds the (m, l) of spans c, c + 64, ...; the max
+// and the weighted sum of l are wave reductions, and the o loads are independent of them
+// and of each other.
+#define ATT_SPL ((ATT_NSPAN + 63) / 64)   // spans per lane in the combine
 static __device__ __forceinline__ float combine_one(const float *q, uint64_t ldq, const float *pml, const float *po,
                                                     int nspan, int nc, int per, int h, int b, int d)
 {
@@ -405,28 +423,43 @@ static __device__ __forceinline__ float combine_one(const float *q, uint64_t ldq
     const float *mlg = pml + (uint64_t)g * nspan * ATT_MAXQ * 2 + 2 * qi;
     const float *pog = po + (uint64_t)g * nspan * ATT_MAXQ * ATT_HD + (uint64_t)qi * ATT_HD + d;
     const float gate = q[(uint64_t)b * ldq + (uint64_t)h * 2 * ATT_HD + ATT_HD + d];
-    float mc = -INFINITY, lc = 0.0f;
-    if (lane < nc) {
-        mc = mlg[(uint64_t)lane * ATT_MAXQ * 2];
-        lc = mlg[(uint64_t)lane * ATT_MAXQ * 2 + 1];
+    float mc[ATT_SPL], lc[ATT_SPL], f[ATT_SPL];
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < ATT_SPL; u++) {
+        const int c = lane + 64 * u;
+        mc[u] = -INFINITY;
+        lc[u] = 0.0f;
+        if (c < nc) {
+            mc[u] = mlg[(uint64_t)c * ATT_MAXQ * 2];
+            lc[u] = mlg[(uint64_t)c * ATT_MAXQ * 2 + 1];
+        }
+        m = fmaxf(m, mc[u]);
     }
-    float m = mc;
 #pragma unroll
     for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    const float f = mc > -INFINITY ? expf(mc - m) : 0.0f;
-    float l = lc * f;
+    float l = 0.0f;
+#pragma unroll
+    for (int u = 0; u < ATT_SPL; u++) {
+        f[u] = mc[u] > -INFINITY ? expf(mc[u] - m) : 0.0f;
+        l += lc[u] * f[u];
+    }
 #pragma unroll
     for (int o = 32; o; o >>= 1) l += __shfl_xor(l, o);
     // 16 spans per step: their o loads are issued together.  Past nc the load repeats span
-    // nc - 1 (finite) and lane c0 + j holds f = 0, so the padding terms add 0.
+    // nc - 1 (finite) and the lane holding span c0 + j has f = 0, so the padding terms add 0.
     float acc = 0.0f;
     for (int c0 = 0; c0 < nc; c0 += 16) {
+        float fu = f[0];                          // spans c0 .. c0 + 15 sit in f[c0 / 64]
+#pragma unroll
+        for (int u = 1; u < ATT_SPL; u++)
+            if ((c0 >> 6) == u) fu = f[u];
         float ov[16];
 #pragma unroll
         for (int j = 0; j < 16; j++) ov[j] = pog[(uint64_t)(c0 + j < nc ? c0 + j : nc - 1) * ATT_MAXQ * ATT_HD];
 #pragma unroll
         for (int j = 0; j < 16; j++)
-            acc = fmaf(ov[j], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), c0 + j)),
+            acc = fmaf(ov[j], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fu), (c0 + j) & 63)),
                        acc);
     }
     return (acc / l) * (1.0f / (1.0f + expf(-gate)));
@@ -523,8 +556,11 @@ static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out,
     a.pml = (float *)qg::ws_attn;
     a.po = a.pml + (size_t)a.n_kv * a.nspan * ATT_MAXQ * 2;
     const int nrt = ((a.n_head / a.n_kv) * a.B + 15) / 16;
-    const dim3 grid(a.n_kv, a.nspan), blk(ATT_NWV * 64);
-#define ATT_GO(F_, R_) hipLaunchKernelGGL((k_attn_span<F_, R_>), grid, blk, 0, qg::stream, a)
+    // 8 waves of 32 dims for one or two row tiles, 4 waves of 64 dims for three (same-box A/B: each
+    // the faster one by ~0.5%)
+    const dim3 grid(a.n_kv, a.nspan);
+#define ATT_GO(F_, R_) hipLaunchKernelGGL((k_attn_span<F_, R_, (R_ < 3 ? 8 : 4)>), grid, dim3((R_ < 3 ? 8 : 4) * 64), 0, \
+                                          qg::stream, a)
 #define ATT_RTS(F_) do { switch (nrt) { case 1: ATT_GO(F_, 1); break; case 2: ATT_GO(F_, 2); break; \
                          default: ATT_GO(F_, 3); break; } } while (0)
     if (fused) ATT_RTS(1); else ATT_RTS(0);

@@ -158,8 +158,8 @@ def attn_fp64(q, k, v, qw, kw, kc, vc, pos, B, nh, nkv, hd, rope_dim, theta, eps
 ATT_DIMS = (24, 4, 256, 64, 1e7, 1e-6, 512)      # n_head, n_kv, head_dim, rope_dim, theta, eps, n_ctx
 
 
-def _attn_inputs(pos, B):
-    nh, nkv, hd, rope_dim, theta, eps, n_ctx = ATT_DIMS
+def _attn_inputs(pos, B, n_ctx=ATT_DIMS[6]):
+    nh, nkv, hd, rope_dim, theta, eps, _ = ATT_DIMS
     rng = np.random.default_rng(pos + B)
     q = rng.standard_normal((B, nh * 2 * hd)).astype(np.float32)
     k = rng.standard_normal((B, nkv * hd)).astype(np.float32)
@@ -177,11 +177,14 @@ def _attn_inputs(pos, B):
     return q, k, v, qw, kw, kc, vc, rc, rs
 
 
-@pytest.mark.parametrize("pos,B", [(0, 1), (37, 4), (300, 8), (95, 3), (31, 2), (504, 8), (17, 6), (497, 8)])
-def test_attention_vs_fp64(gpu, pos, B):
-    print(f"\n[attn] pos={pos} B={B}", flush=True)
-    nh, nkv, hd, rope_dim, theta, eps, n_ctx = ATT_DIMS
-    q, k, v, qw, kw, kc, vc, rc, rs = _attn_inputs(pos, B)
+@pytest.mark.parametrize("pos,B,n_ctx", [(0, 1, 512), (37, 4, 512), (300, 8, 512), (95, 3, 512), (31, 2, 512),
+                                         (504, 8, 512), (17, 6, 512), (497, 8, 512),
+                                         (3000, 8, 4096), (4090, 5, 4096), (2047, 1, 4096)])
+def test_attention_vs_fp64(gpu, pos, B, n_ctx):
+    """Spans of one to several tiles: 512 positions give one tile per span, 4096 up to four."""
+    print(f"\n[attn] pos={pos} B={B} n_ctx={n_ctx}", flush=True)
+    nh, nkv, hd, rope_dim, theta, eps, _ = ATT_DIMS
+    q, k, v, qw, kw, kc, vc, rc, rs = _attn_inputs(pos, B, n_ctx)
     ref, kref, vref = attn_fp64(q, k, v, qw, kw, kc, vc, pos, B, nh, nkv, hd, rope_dim, theta, eps)
     qb, kb, vb = gpu.put(q), gpu.put(k), gpu.put(v)
     kcb, vcb = gpu.put(kc), gpu.put(vc)
