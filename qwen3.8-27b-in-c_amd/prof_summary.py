@@ -3,6 +3,7 @@
 
     prof_summary.py stats   DB_OR_DIR --cmd "<command that made it>" [--bench-json FILE] [--plain-json FILE] [--top N]
     prof_summary.py traffic FETCH_DB WRITE_DB --bench-json FILE [--calib-bytes N]
+    prof_summary.py sweep   BENCH_JSON --cmd "<command that made it>"
 
 stats   : per-kernel calls / total / average duration of a --kernel-trace run,
           and, given the benchmark's JSON line, the average duration of the
@@ -15,6 +16,7 @@ traffic : HBM bytes per launch of the roofline kernel from two --pmc runs
           (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by what the
           same counter reads for the k_copy kernel of known size (the
           benchmark's --copy-calib: 5 copies of 256 MiB).  Prints JSON.
+sweep   : the table of a `bench.py --mode sweep` line (formats x shapes x B).
 """
 import argparse
 import glob
@@ -136,6 +138,35 @@ def cmd_traffic(a):
         indent=1))
 
 
+def cmd_sweep(a):
+    b = bench_line(a.bench_json)
+    rows = b["sweep"]
+    out = ["# gemv_batch sweep over formats, shapes and batch (config 2)", "",
+           "Command (`/root/repo` is the repository root):", "", "```", a.cmd, "```", "",
+           "Each point: warm-up calls, then 40 `qgpu_gemv_batch` calls (activation preparation + GEMV) captured in a",
+           "HIP graph, replayed once untimed and once between HIP events on the library stream; weights rotate over",
+           "enough device copies to exceed the 256 MB MALL.  GB/s = (weight bytes + B x (in + out) x 4) / time;",
+           "% = of 8 TB/s.  Every format runs the int8-MFMA digit GEMV on packed 16-row tile records",
+           "(`k_gemv_mfma<format, ...>`).", ""]
+    bs = sorted({r["B"] for r in rows})
+    out.append("| format | rows x cols | weight MB | " + " | ".join(f"B={B} us | B={B} GB/s" for B in bs) + " |")
+    out.append("|---|---|---:|" + "---:|---:|" * len(bs))
+    seen = []
+    for r in rows:
+        key = (r["format"], r["rows"], r["cols"])
+        if key not in seen:
+            seen.append(key)
+    for f, nr, nc in seen:
+        pts = {r["B"]: r for r in rows if (r["format"], r["rows"], r["cols"]) == (f, nr, nc)}
+        wmb = next(iter(pts.values()))["weight_bytes"] / 1e6
+        cells = []
+        for B in bs:
+            p = pts.get(B)
+            cells.append(f"{p['us']:.1f} | {p['gbs']:.0f} ({100 * p['frac']:.0f}%)" if p else " | ")
+        out.append(f"| {f} | {nr} x {nc} | {wmb:.1f} | " + " | ".join(cells) + " |")
+    print("\n".join(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd_name", required=True)
@@ -151,8 +182,11 @@ def main():
     t.add_argument("write_db")
     t.add_argument("--bench-json", required=True)
     t.add_argument("--calib-bytes", type=int, default=256 << 20)
+    w = sub.add_parser("sweep")
+    w.add_argument("bench_json")
+    w.add_argument("--cmd", required=True)
     a = ap.parse_args()
-    cmd_stats(a) if a.cmd_name == "stats" else cmd_traffic(a)
+    {"stats": cmd_stats, "traffic": cmd_traffic, "sweep": cmd_sweep}[a.cmd_name](a)
 
 
 if __name__ == "__main__":
