@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """Benchmark of the MTP speculative-decode hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode model|gemv|longctx|sweep]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode model|gemv|longctx|sweep|sample]
 
 Prints ONE JSON line on stdout (progress goes to stderr).
 
@@ -24,6 +24,13 @@ mode sweep -- gemv_batch over every weight format of the path (IQ4_XS, Q4_K,
     {1, 2, 4, 8}; HBM GB/s of algorithmic bytes per call (weights rotate over
     enough copies to exceed the 256 MB MALL).  value = the IQ4_XS 17408x5120
     B=4 point.
+mode sample -- the non-speculative sampled decode (main.c:232-248) on the same
+    27B model after a 512-token prompt: every token drawn on the device by the
+    reference sampler (temp 0.8, top-p 0.9, top-k 40, repeat penalty 1.1 over
+    the last 64 tokens), then one model_forward step; K = 128 tokens timed.
+    value = sampled tokens per second; the greedy decode of the same length,
+    and the sampler kernels alone at the 248,320-token vocabulary (graph
+    replays), are reported beside it.
 
 roofline (every mode): the dominant kernel, k_gemv_mfma (IQ4_XS), on the gemv workload
 (17408 x 5120 IQ4_XS, B = 4), run first in the process: W + K gemv_batch calls,
@@ -38,7 +45,8 @@ activation/output = 47,710,208 B) / average launch duration.  Weights rotate ove
 cpu_baseline: the reference engine itself (oracle/_ref, compiled from the
 reference sources; AVX2, its own pinned thread pool) on the host cores:
 model mode runs the reference's speculative cycle on the same 27B model file
-for a bounded sample; gemv mode runs its gemv_batch.
+for a bounded sample; gemv mode runs its gemv_batch; sample mode runs its
+sampled decode loop (sampler_sample + model_forward).
 """
 import argparse
 import ctypes
@@ -144,6 +152,29 @@ def cpu_baseline_spec(path, prompt, k, seconds):
                       f"({int(out[2])} tokens, {int(out[4])} drafts accepted), pool of {cores} pinned threads"
                       + ("; stopped early: a cycle accepted 2 drafts, which the reference cannot roll back"
                          if rc == -2 else "")}
+
+
+def cpu_baseline_sample(path, prompt, cfg, seconds):
+    """The reference's sampled decode (main.c:232-248) on the same model file."""
+    drv = os.path.join(ROOT, "oracle", "_ref", "librefbench.so")
+    if not os.path.exists(drv):
+        return None
+    L = ctypes.CDLL(drv)
+    U = ctypes.POINTER(ctypes.c_uint32)
+    f32, u32 = ctypes.c_float, ctypes.c_uint32
+    L.ref_sample_bench.argtypes = [ctypes.c_char_p, u32, U, u32, f32, f32, u32, f32, ctypes.c_uint64, u32,
+                                   ctypes.c_double, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    p = np.ascontiguousarray(prompt, np.uint32)
+    out = (ctypes.c_double * 5)()
+    cores = host_cores()
+    temp, top_p, top_k, pen, seed = cfg
+    if L.ref_sample_bench(path.encode(), 256, p.ctypes.data_as(U), len(p), temp, top_p, top_k, pen, seed, 1000,
+                          seconds, cores, out) or out[2] < 1:
+        return None
+    return {"value": round(out[2] / out[1], 4), "unit": "tok/s", "cores": cores, "kind": "reference",
+            "sample": f"reference engine, same 27B model file, {len(p)}-token prompt (prefill {out[0]:.1f} s), "
+                      f"then {int(out[2])} sampled tokens over {out[1]:.1f} s; sampler_sample "
+                      f"{1e6 * out[3] / out[4]:.0f} us per call; pool of {cores} pinned threads"}
 
 
 # ---------------------------------------------------------------------------------- roofline microbench
@@ -375,12 +406,75 @@ def bench_longctx(args, gpu, host, roof, gemv_call_gbs):
     }
 
 
+SAMPLE_CFG = (0.8, 0.9, 40, 1.1, 7)        # temp, top_p, top_k, repeat penalty, seed
+
+
+def bench_sample(args, gpu, host, roof, gemv_call_gbs):
+    from qwen_pkg import pyqwen
+    K, W, n_prompt = args.steps, args.warmup, args.prompt
+    path = None
+    if not args.no_cpu:
+        path, spec = model_file(host, args.seed)
+    else:
+        spec = host.spec_27b(args.seed)
+    n_ctx = ((n_prompt + max(K, W) + 64 + 255) // 256) * 256
+    m = pyqwen.Model(path, n_ctx) if path else pyqwen.Model(spec=spec, n_ctx=n_ctx)
+    V = m.V
+    prompt = np.random.default_rng(args.seed + 512).integers(0, V, n_prompt).astype(np.uint32)
+    m.reset()
+    m.generate_sample(prompt, W, *SAMPLE_CFG)                # warm-up (first call allocates the candidates)
+    m.reset()
+    toks, st = m.generate_sample(prompt, K, *SAMPLE_CFG)
+    log(f"sampled decode: {len(toks)} tokens in {st.t_decode_s:.3f} s (prefill {st.t_prefill_s:.2f} s)")
+    m.reset()
+    gtoks, gst = m.generate_greedy(prompt, K)
+    log(f"greedy decode: {len(gtoks)} tokens in {gst.t_decode_s:.3f} s")
+    m.close()
+    # the sampler kernels alone on 27B-vocabulary logits, graph replays of 200 calls
+    L, reps = gpu.L, 200
+    lg = gpu.put((np.random.default_rng(1).standard_normal(V) * 4).astype(np.float32))
+    tk, rng, out = gpu.put(prompt[-64:]), gpu.put(np.array([7], np.uint64)), gpu.buf(4)
+    e0, e1 = gpu.event(), gpu.event()
+    kern = {}
+    for name, (temp, top_p, top_k, pen) in {"sample_us": SAMPLE_CFG[:4], "sample_top256_us": (1.0, 1.0, 256, 1.1),
+                                            "sample_greedy_us": (0.0, 1.0, 40, 1.1)}.items():
+        def call():
+            gpu.ok(L.qgpu_sample(lg.f32(), V, tk.u32(), 64, temp, top_p, top_k, pen, 64, rng.u64(), out.u32()))
+        call()
+        kern[name] = round(graph_ms(gpu, lambda: [call() for _ in range(reps)], e0, e1) * 1e3 / reps, 2)
+    kern["argmax_us"] = round(graph_ms(gpu, lambda: [gpu.ok(L.qgpu_argmax(lg.f32(), V, V, 1, out.u32()))
+                                                     for _ in range(reps)], e0, e1) * 1e3 / reps, 2)
+    log(f"sampler kernels: {kern}")
+    cpu = None
+    if path:
+        try:
+            log("CPU baseline: reference sampled decode on the host cores")
+            cpu = cpu_baseline_sample(path, prompt[:8], SAMPLE_CFG, args.cpu_seconds)
+        finally:
+            os.remove(path)
+    temp, top_p, top_k, pen, seed = SAMPLE_CFG
+    return {
+        "metric": f"sampled decode tok/s, 27B IQ4_XS (temp {temp}, top-p {top_p}, top-k {top_k}, repeat penalty "
+                  f"{pen}) on 1 GPU", "value": round(len(toks) / st.t_decode_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": K, "warmup": W, "ms_per_step": round(st.t_decode_s / len(toks) * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (IQ4_XS weights; int8-MFMA digit GEMV, fp32 accumulate; sampler fp32 / fp64 sum)",
+        "data": "synthetic: seeded random-init 27B hybrid (IQ4_XS), seeded random-id prompt",
+        "config": {"workload": f"27B hybrid sampled decode, {n_prompt}-token prompt, {K} tokens",
+                   "prompt_tokens": n_prompt, "n_ctx": n_ctx, "sampler": {"temp": temp, "top_p": top_p,
+                   "top_k": top_k, "repeat_penalty": pen, "repeat_last_n": 64, "seed": seed}},
+        "greedy_tok_s": round(len(gtoks) / gst.t_decode_s, 2), **kern,
+        "prefill_s": round(st.t_prefill_s, 3), "gemv_batch_gbs": round(gemv_call_gbs, 1), "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (model: cycles; gemv: calls)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["model", "gemv", "longctx", "sweep"], default="model")
+    ap.add_argument("--mode", choices=["model", "gemv", "longctx", "sweep", "sample"], default="model")
     ap.add_argument("--k", type=int, default=3, help="drafts per speculative cycle (model mode)")
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (model 512, longctx 8192)")
     ap.add_argument("--forced-cycles", type=int, default=None)
@@ -397,7 +491,7 @@ def main():
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     dflt = {"model": (256, 8, 512, 64, 15.0), "gemv": (200, 20, 0, 0, 5.0), "longctx": (0, 0, 8192, 16, 0.0),
-            "sweep": (40, 5, 0, 0, 0.0)}
+            "sweep": (40, 5, 0, 0, 0.0), "sample": (128, 8, 512, 0, 15.0)}
     s, w, p, f, c = dflt[args.mode]
     args.steps = s if args.steps is None else args.steps
     args.warmup = w if args.warmup is None else args.warmup
@@ -449,6 +543,8 @@ def main():
         }
     elif args.mode == "model":
         res = bench_model(args, gpu, host, roof, gemv_gbs)
+    elif args.mode == "sample":
+        res = bench_sample(args, gpu, host, roof, gemv_gbs)
     else:
         res = bench_longctx(args, gpu, host, roof, gemv_gbs)
     print(json.dumps(res), flush=True)

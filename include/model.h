@@ -142,6 +142,14 @@ uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n
 int      model_spec_begin(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t k);
 uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_accept, uint32_t max_cycles,
                         uint32_t max_tokens, uint32_t *out, uint32_t *cycle_j, qwen_gen_stats_t *st);
+/* Sampled decode (main.c:232-248): prefill, then every token drawn by the
+ * reference sampler (sampler_init(temp, top_p, top_k, repeat_penalty, seed) +
+ * sampler_sample over the prompt and the tokens generated so far), here on the
+ * device (qgpu_sample), then a model_forward step.  Stops after n_predict tokens,
+ * at eos (written) or at n_ctx.  Returns the number of tokens written to out. */
+uint32_t model_generate_sample(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                               float temp, float top_p, uint32_t top_k, float repeat_penalty, uint64_t seed,
+                               uint32_t eos, uint32_t *out, qwen_gen_stats_t *st);
 /* Plain greedy decode with model_forward steps (the lossless reference stream). */
 uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
                                uint32_t eos, uint32_t *out, qwen_gen_stats_t *st);

@@ -235,6 +235,22 @@ int  qgpu_attn_fused_act(const float *q, uint64_t ldq, const float *k, const flo
 /* allocates the attention workspace for ctx_bound positions now (no allocation later) */
 int  qgpu_attn_reserve(int ctx_bound, int n_kv);
 
+/* ------------------------------------------------------------ sampling (sampler.c:62-162) */
+/* sampler_sample on device data: logits[vocab] (the repeat penalty is applied in
+ * place, as the reference does), tokens[n_tokens] the prompt and generated
+ * tokens (the last repeat_last_n are penalised), *rng_state the xorshift64 state
+ * (advanced once per non-greedy call), *out_token the chosen id.  temp, top_p,
+ * top_k, repeat_penalty, repeat_last_n: the fields of an initialised sampler_t
+ * (top_k >= 1; top_k > 256 takes 256).  temp <= 0 or top_k == 1: the first
+ * maximum, and rng_state may be NULL.  QGPU_E_RANGE for vocab > 2^24 or a
+ * penalty window of more than 4096 tokens.  Stream-ordered; the first call for
+ * a larger vocabulary or top_k allocates the candidate buffers.  Logits of
+ * exactly equal value are taken in index order (the reference's order among
+ * them follows its heap and qsort). */
+int  qgpu_sample(float *logits, uint32_t vocab, const uint32_t *tokens, uint32_t n_tokens, float temp,
+                 float top_p, uint32_t top_k, float repeat_penalty, uint32_t repeat_last_n,
+                 uint64_t *rng_state, uint32_t *out_token);
+
 /* ------------------------------------------------------------ driver helpers */
 /* *dst = value, stream-ordered (graph-capturable) */
 int  qgpu_set_i32(int *dst, int value);

@@ -780,6 +780,32 @@ uint32_t or_generate_spec(or_model_t *m, const uint32_t *prompt, uint32_t n_prom
 /* Plain greedy stream used as the lossless-spec oracle: argmax of model_forward
  * logits each step (debug_spec2.c:60-85 pattern; main.c:232-248 with temp <= 0
  * and no repeat penalty). */
+/* main.c:232-248: prefill, then sample from the last logits, forward the sampled token,
+ * sample again; the repeat penalty sees the prompt and every generated token
+ * (all_tokens).  The sampler state advances in place. */
+uint32_t or_generate_sample(or_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                            uint32_t eos, or_sampler_t *s, uint32_t *out)
+{
+    const uint32_t V = m->cfg.vocab_size;
+    uint32_t *all = malloc(sizeof(uint32_t) * ((size_t)n_prompt + n_predict + 1));
+    if (!all) return 0;
+    memcpy(all, prompt, sizeof(uint32_t) * n_prompt);
+    size_t n_all = n_prompt;
+    prefill(m, prompt, n_prompt, 0);
+    uint32_t cur = or_sampler_sample(s, m->logits, V, all, n_all), gen = 0;
+    all[n_all++] = cur;
+    out[gen++] = cur;
+    for (uint32_t i = 1; i < n_predict; i++) {
+        if (cur == eos || m->pos >= m->n_ctx) break;
+        or_model_forward(m, cur, m->pos);
+        cur = or_sampler_sample(s, m->logits, V, all, n_all);
+        all[n_all++] = cur;
+        out[gen++] = cur;
+    }
+    free(all);
+    return gen;
+}
+
 uint32_t or_generate_greedy(or_model_t *m, const uint32_t *prompt, uint32_t n_prompt,
                             uint32_t n_predict, uint32_t eos, uint32_t *out)
 {

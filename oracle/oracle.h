@@ -131,9 +131,26 @@ typedef struct {
 uint32_t or_generate_spec(or_model_t *m, const uint32_t *prompt, uint32_t n_prompt,
                           uint32_t n_predict, uint32_t k, uint32_t eos,
                           uint32_t *out, or_spec_stats_t *st, uint32_t *cycle_j);
+/* ---------------- sampler (reference sampler.c, main.c:232-248) ---------------- */
+typedef struct {
+    float    temp;
+    float    top_p;
+    uint32_t top_k;
+    float    repeat_penalty;
+    uint32_t repeat_last_n;
+    uint64_t rng_state;
+} or_sampler_t;                                                   /* sampler.h:7-14  */
+void     or_sampler_init(or_sampler_t *s, float temp, float top_p, uint32_t top_k, float repeat_penalty,
+                         uint64_t seed);                          /* sampler.c:46-56 */
+uint32_t or_sampler_sample(or_sampler_t *s, float *logits, uint32_t vocab, const uint32_t *tokens,
+                           size_t n_tokens);                      /* sampler.c:62-162 */
+
 /* Prefill then plain greedy decode with model_forward (main.c:232-248 with temp<=0). */
 uint32_t or_generate_greedy(or_model_t *m, const uint32_t *prompt, uint32_t n_prompt,
                             uint32_t n_predict, uint32_t eos, uint32_t *out);
+/* Prefill then the sampled decode of main.c:232-248 (sampler s advances in place). */
+uint32_t or_generate_sample(or_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                            uint32_t eos, or_sampler_t *s, uint32_t *out);
 
 #ifdef __cplusplus
 }

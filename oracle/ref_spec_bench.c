@@ -10,9 +10,13 @@
  * keeps SPEC_MAX_B-1 = 2 state checkpoints (include/model.h:113), so with k = 3
  * a cycle that accepts exactly 2 drafts cannot be rolled back by the reference;
  * the run then stops and reports -2 (random-init weights accept ~0 drafts).
+ *
+ * ref_sample_bench times the reference's sampled decode (src/main.c:232-248):
+ * sampler_sample over the prompt and the generated tokens, then model_forward.
  */
 #define _POSIX_C_SOURCE 200809L
 #include "model.h"
+#include "sampler.h"
 #include "threadpool.h"
 
 #include <stdint.h>
@@ -84,4 +88,50 @@ int ref_spec_bench(const char *gguf, uint32_t n_ctx, const uint32_t *prompt, uin
     model_free(m);
     free(m);
     return rc;
+}
+
+/* out[0] = prefill seconds, out[1] = timed decode seconds, out[2] = tokens sampled in it,
+ * out[3] = seconds inside sampler_sample, out[4] = sampler_sample calls.  Returns 0 or -1. */
+int ref_sample_bench(const char *gguf, uint32_t n_ctx, const uint32_t *prompt, uint32_t n_prompt, float temp,
+                     float top_p, uint32_t top_k, float repeat_penalty, uint64_t seed, uint32_t max_tokens,
+                     double max_secs, int threads, double *out)
+{
+    qwen_model_t *m = calloc(1, sizeof *m);
+    if (!m || model_init(m, gguf, n_ctx)) { free(m); return -1; }
+    pool_t *pool = pool_create(threads, 1);
+    sampler_t *smp = sampler_init(temp, top_p, top_k, repeat_penalty, seed);
+    uint32_t *all = malloc(sizeof(uint32_t) * ((size_t)n_prompt + max_tokens + 1));
+    const uint32_t V = m->cfg.vocab_size;
+    double t = wall();
+    for (uint32_t p = 0, B; p < n_prompt; p += B) {
+        B = n_prompt - p < PREFILL_MAX_B ? n_prompt - p : PREFILL_MAX_B;
+        model_forward_batch(m, pool, prompt + p, p, B, 0);
+    }
+    float *lg = m->logits_b + (size_t)((n_prompt - 1) % PREFILL_MAX_B) * V;
+    out[0] = wall() - t;
+    memcpy(all, prompt, sizeof(uint32_t) * n_prompt);
+    size_t n_all = n_prompt;
+    double t_smp = 0.0;
+    uint32_t gen = 0;
+    const double t_start = wall();
+    for (;;) {
+        const double t1 = wall();
+        const uint32_t cur = sampler_sample(smp, lg, V, all, n_all);
+        t_smp += wall() - t1;
+        all[n_all++] = cur;
+        gen++;
+        if (gen >= max_tokens || m->pos >= n_ctx || wall() - t_start > max_secs) break;
+        model_forward(m, pool, cur, m->pos);
+        lg = m->logits;
+    }
+    out[1] = wall() - t_start;
+    out[2] = (double)gen;
+    out[3] = t_smp;
+    out[4] = (double)gen;
+    free(all);
+    sampler_free(smp);
+    pool_destroy(pool);
+    model_free(m);
+    free(m);
+    return 0;
 }

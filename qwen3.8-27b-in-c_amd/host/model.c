@@ -813,7 +813,8 @@ void gdn_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool)
 }
 
 /* ------------------------------------------------------------------ device-resident generation */
-static void prefill_dev(qwen_model_t *m, const uint32_t *prompt, uint32_t n, int with_mtp)
+/* returns the rows of the last chunk: the prompt's last logits row is logits_b[last - 1] */
+static uint32_t prefill_dev(qwen_model_t *m, const uint32_t *prompt, uint32_t n, int with_mtp)
 {
     qwen_gpu_t *g = m->gpu;
     uint32_t pos = 0, last = 0;
@@ -829,6 +830,7 @@ static void prefill_dev(qwen_model_t *m, const uint32_t *prompt, uint32_t n, int
     /* next token = argmax of the last prompt row (main.c:148-151, 175) */
     K(qgpu_argmax(g->logits_b + (size_t)(last - 1) * m->cfg.vocab_size, m->cfg.vocab_size, m->cfg.vocab_size, 1,
                   g->d_cand));
+    return last;
 }
 
 int model_spec_begin(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t k)
@@ -930,6 +932,55 @@ uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t
     }
     K(qgpu_sync());
     s.t_decode_s = now_s() - t0;
+    if (st) *st = s;
+    return gen;
+}
+
+uint32_t model_generate_sample(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
+                               float temp, float top_p, uint32_t top_k, float repeat_penalty, uint64_t seed,
+                               uint32_t eos, uint32_t *out, qwen_gen_stats_t *st)
+{
+    qwen_gpu_t *g = m ? m->gpu : NULL;
+    qwen_gen_stats_t s;
+    memset(&s, 0, sizeof s);
+    if (!g || !prompt || !out || n_prompt < 1 || n_prompt >= m->n_ctx || n_predict < 1) return 0;
+    const uint32_t V = m->cfg.vocab_size;
+    /* the fields sampler_init sets (sampler.c:46-56) */
+    if (!top_k) top_k = 40;
+    if (repeat_penalty <= 0.0f) repeat_penalty = 1.0f;
+    uint64_t rng = seed ? seed : 0x123456789abcdefULL;
+    const uint32_t last_n = 64;
+    /* all_tokens of main.c: the prompt, then every sampled token, on the device */
+    uint32_t *d_all = NULL;
+    uint64_t *d_rng = NULL;
+    K(qgpu_malloc((void **)&d_all, ((size_t)n_prompt + n_predict) * sizeof(uint32_t)));
+    K(qgpu_malloc((void **)&d_rng, sizeof(uint64_t)));
+    K(qgpu_memcpy_h2d(d_all, prompt, (size_t)n_prompt * sizeof(uint32_t)));
+    K(qgpu_memcpy_h2d(d_rng, &rng, sizeof rng));
+    uint32_t n_all = n_prompt;
+    double t0 = now_s();
+    const uint32_t last = prefill_dev(m, prompt, n_prompt, 0);
+    K(qgpu_sync());
+    s.t_prefill_s = now_s() - t0;
+    t0 = now_s();
+    /* main.c:233-246: sample from the last logits, forward the token, sample again */
+    float *lg = g->logits_b + (size_t)(last - 1) * V;
+    uint32_t gen = 0, cur = 0;
+    for (;;) {
+        K(qgpu_sample(lg, V, d_all, n_all, temp, top_p, top_k, repeat_penalty, last_n, d_rng, d_all + n_all));
+        K(qgpu_memcpy_d2h(&cur, d_all + n_all, sizeof cur));
+        n_all++;
+        out[gen++] = cur;
+        if (gen >= n_predict || cur == eos || m->pos >= m->n_ctx) break;
+        forward_dev(m, d_all + n_all - 1, 1, m->pos, g->logits1, 0);
+        m->pos++;
+        lg = g->logits1;
+        s.n_cycles++;
+    }
+    K(qgpu_sync());
+    s.t_decode_s = now_s() - t0;
+    K(qgpu_free(d_all));
+    K(qgpu_free(d_rng));
     if (st) *st = s;
     return gen;
 }

@@ -199,6 +199,9 @@ class DevBuf:
     def u32(self, offset_elems=0):
         return self._ptr(offset_elems, U32P)
 
+    def u64(self, offset_elems=0):
+        return self._ptr(offset_elems, ctypes.POINTER(ctypes.c_uint64))
+
     def i32(self, offset_elems=0):
         return self._ptr(offset_elems, ctypes.POINTER(ctypes.c_int))
 
@@ -261,6 +264,8 @@ class GpuLib:
             "qgpu_silu_mul": [F32P, u64, F32P, u64, u64, i32],
             "qgpu_add": [F32P, u64, F32P, u64, u64, i32],
             "qgpu_argmax": [F32P, u64, ctypes.c_uint32, i32, U32P],
+            "qgpu_sample": [F32P, ctypes.c_uint32, U32P, ctypes.c_uint32, f32, f32, ctypes.c_uint32, f32,
+                            ctypes.c_uint32, ctypes.POINTER(u64), U32P],
             "qgpu_gemv_prepare": [F32P, u64, i32, u64], "qgpu_gemv_prepared": [vp, i32, F32P, u64, i32],
             "qgpu_copy": [vp, vp, ctypes.c_size_t],
             "qgpu_gdn_conv": [F32P, u64, i32, i32, F32P, F32P, u64, i32, ctypes.POINTER(i32), F32P, u64],
@@ -390,6 +395,9 @@ def _model_lib():
     L.model_spec_run.restype = u32
     L.model_generate_greedy.argtypes = [vp, U32P, u32, u32, u32, U32P, ctypes.POINTER(GenStats)]
     L.model_generate_greedy.restype = u32
+    L.model_generate_sample.argtypes = [vp, U32P, u32, u32, ctypes.c_float, ctypes.c_float, u32, ctypes.c_float,
+                                        ctypes.c_uint64, u32, U32P, ctypes.POINTER(GenStats)]
+    L.model_generate_sample.restype = u32
     L.model_time_steps.argtypes = [vp, u32, i32, F32P, F32P, F32P]
     L._model_sigs = True
     return L
@@ -498,6 +506,15 @@ class Model:
         out = np.zeros(n_predict, np.uint32)
         st = GenStats()
         n = self.L.model_generate_greedy(self.h, uptr(p), len(p), n_predict, eos, uptr(out), ctypes.byref(st))
+        return out[:n], st
+
+    def generate_sample(self, prompt, n_predict, temp, top_p, top_k, repeat_penalty, seed, eos=0xFFFFFFFF):
+        """Prefill, then the sampled decode of main.c:232-248 with the sampler on the device."""
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(n_predict, np.uint32)
+        st = GenStats()
+        n = self.L.model_generate_sample(self.h, uptr(p), len(p), n_predict, temp, top_p, top_k, repeat_penalty,
+                                         seed, eos, uptr(out), ctypes.byref(st))
         return out[:n], st
 
     def time_steps(self, B, reps):

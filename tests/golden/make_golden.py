@@ -13,6 +13,8 @@ to the inputs and the reference outputs:
                                deq [ne1][ne0] (dequant_row of every row)
   ops.npz                    : test_ops.c:171-240 random-dimension cases
   model_<variant>.npz        : tiny hybrid model scenarios (ref_harness.c)
+  sampler.npz                : sampler_sample on seeded logits (3 calls per case): tokens, generator
+                               state after each call, penalised logits
   model_27b.npz              : full-size 27B greedy stream + top-2 gaps
                                (`python tests/golden/make_golden.py 27b`, ~10 min)
 """
@@ -127,6 +129,50 @@ def ops_fixtures(ref):
     print("ops fixtures", len(out))
 
 
+class Sampler(ctypes.Structure):
+    """Layout of sampler_t (sampler.h:7-14)."""
+    _fields_ = [("temp", ctypes.c_float), ("top_p", ctypes.c_float), ("top_k", ctypes.c_uint32),
+                ("repeat_penalty", ctypes.c_float), ("repeat_last_n", ctypes.c_uint32), ("rng_state", ctypes.c_uint64)]
+
+
+# (vocab, temp, top_p, top_k, repeat_penalty, seed, window tokens): greedy, top-k / top-p edges, K > 256,
+# K > vocab, penalties with repeated tokens
+SAMPLER_CASES = [
+    (1000, 0.0, 1.0, 40, 1.1, 5, 80), (1000, 0.8, 0.9, 40, 1.1, 7, 80), (1000, 1.0, 1.0, 1, 1.0, 9, 0),
+    (17, 1.0, 1.0, 40, 1.0, 11, 30), (4103, 0.5, 0.5, 5, 1.3, 12345, 120), (4103, 1.5, 0.05, 256, 1.0, 3, 0),
+    (40000, 1.2, 0.95, 300, 1.05, 42, 64), (40000, 0.7, 1.0, 2, 0.9, 0, 200), (9000, 1.0, 0.99, 128, 2.0, 77, 65),
+]
+
+
+def sampler_fixtures(ref):
+    ref.sampler_init.restype = ctypes.POINTER(Sampler)
+    ref.sampler_init.argtypes = [ctypes.c_float, ctypes.c_float, ctypes.c_uint32, ctypes.c_float, ctypes.c_uint64]
+    ref.sampler_sample.restype = ctypes.c_uint32
+    ref.sampler_sample.argtypes = [ctypes.POINTER(Sampler), ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p,
+                                   ctypes.c_size_t]
+    ref.sampler_free.argtypes = [ctypes.POINTER(Sampler)]
+    out = {}
+    for c, (V, temp, top_p, top_k, pen, seed, W) in enumerate(SAMPLER_CASES):
+        rng = np.random.default_rng(1000 + c)
+        logits = (rng.standard_normal(V) * 3).astype(np.float32)
+        toks = rng.integers(0, min(V, 50), W).astype(np.uint32)        # repeats inside the window
+        s = ref.sampler_init(temp, top_p, top_k, pen, seed)
+        tok, st, lg = [], [], []
+        for step in range(3):
+            l = logits.copy()
+            tok.append(ref.sampler_sample(s, l.ctypes.data, V, toks.ctypes.data, len(toks)))
+            st.append(s.contents.rng_state)
+            lg.append(l)
+        ref.sampler_free(s)
+        out[f"logits_{c}"] = logits
+        out[f"tokens_{c}"] = toks
+        out[f"sampled_{c}"] = np.array(tok, np.uint32)
+        out[f"state_{c}"] = np.array(st, np.uint64)
+        out[f"penalised_{c}"] = lg[0]
+    np.savez(os.path.join(HERE, "sampler.npz"), cases=np.array(SAMPLER_CASES, np.float64), **out)
+    print("sampler", {c: out[f"sampled_{c}"].tolist() for c in range(len(SAMPLER_CASES))})
+
+
 def model_fixtures(host):
     with tempfile.TemporaryDirectory() as td:
         exe = os.path.join(td, "ref_harness")
@@ -142,7 +188,7 @@ def model_fixtures(host):
             arrs = {}
             for fn in sorted(os.listdir(outd)):
                 base, ext = fn.rsplit(".", 1)
-                arrs[base] = np.fromfile(os.path.join(outd, fn), np.float32 if ext == "f32" else np.uint32)
+                arrs[base] = np.fromfile(os.path.join(outd, fn), {"f32": np.float32, "f64": np.float64}.get(ext, np.uint32))
             np.savez(os.path.join(HERE, f"model_{variant}.npz"), gguf_sha256=np.array(sha), seed=np.uint64(seed),
                      mixed=np.int32(mixed), n_ctx=np.int32(256), **arrs)
             print(variant, sha[:16], {k: v.shape for k, v in arrs.items()})
@@ -190,13 +236,15 @@ def main():
         sys.exit("build the reference first: make -C oracle")
     ref = ctypes.CDLL(REF_LIB)
     host = qwen_pkg.host_lib()
-    which = sys.argv[1:] or ["gemv", "ops", "model"]
+    which = sys.argv[1:] or ["gemv", "ops", "model", "sampler"]
     if "gemv" in which:
         gemv_fixtures(ref, host)
     if "ops" in which:
         ops_fixtures(ref)
     if "model" in which:
         model_fixtures(host)
+    if "sampler" in which:
+        sampler_fixtures(ref)
     if "27b" in which:
         model27b_fixture(host)
 

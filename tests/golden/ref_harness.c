@@ -21,9 +21,13 @@
  *   spec_seq_k{K}.u32   same streams with sequential verification (any K)
  *   spec_j_k{K}.u32     accepted index j per cycle
  *   greedy.u32          plain greedy stream (argmax of model_forward)
+ *   sample_cfg.f64      [4][5] sampler configurations: temp, top_p, top_k, repeat_penalty, seed
+ *   sample_c{C}.u32     sampled streams (main.c:232-248: sampler_init + sampler_sample over the prompt
+ *                       and the generated tokens), sampler configuration C of SAMPLE_CFG
  */
 #define _POSIX_C_SOURCE 200809L
 #include "model.h"
+#include "sampler.h"
 #include "threadpool.h"
 #include <stdio.h>
 #include <stdlib.h>
@@ -252,6 +256,40 @@ int main(int argc, char **argv)
     }
     dump(dir, "greedy.u32", out, n_predict * 4);
     model_free(m);
+    /* sampled streams: temp, top_p, top_k, repeat_penalty, seed (main.c:108, 232-248) */
+    static const struct { float temp, top_p; uint32_t top_k; float pen; uint64_t seed; } SAMPLE_CFG[4] = {
+        { 0.8f, 0.9f, 40, 1.1f, 7 }, { 1.0f, 1.0f, 0, 1.0f, 99 }, { 0.5f, 0.5f, 5, 1.3f, 12345 },
+        { 1.2f, 0.95f, 300, 1.05f, 42 } };
+    double cfg[4][5];
+    for (uint32_t c = 0; c < 4; c++) {
+        cfg[c][0] = SAMPLE_CFG[c].temp; cfg[c][1] = SAMPLE_CFG[c].top_p; cfg[c][2] = SAMPLE_CFG[c].top_k;
+        cfg[c][3] = SAMPLE_CFG[c].pen; cfg[c][4] = (double)SAMPLE_CFG[c].seed;
+    }
+    dump(dir, "sample_cfg.f64", cfg, sizeof cfg);
+    for (uint32_t c = 0; c < 4; c++) {
+        if (model_init(m, path, n_ctx)) return 1;
+        prefill(m, prompt, n_prompt, 0);
+        sampler_t *smp = sampler_init(SAMPLE_CFG[c].temp, SAMPLE_CFG[c].top_p, SAMPLE_CFG[c].top_k, SAMPLE_CFG[c].pen,
+                                      SAMPLE_CFG[c].seed);
+        uint32_t all[256];
+        memcpy(all, prompt, n_prompt * sizeof(uint32_t));
+        size_t n_all = n_prompt;
+        uint32_t gen = 0;
+        cur = sampler_sample(smp, m->logits, V, all, n_all);
+        all[n_all++] = cur;
+        out[gen++] = cur;
+        for (uint32_t i = 1; i < n_predict; i++) {
+            if (m->pos >= n_ctx) break;
+            model_forward(m, NULL, cur, m->pos);
+            cur = sampler_sample(smp, m->logits, V, all, n_all);
+            all[n_all++] = cur;
+            out[gen++] = cur;
+        }
+        snprintf(name, sizeof name, "sample_c%u.u32", c);
+        dump(dir, name, out, gen * 4);
+        sampler_free(smp);
+        model_free(m);
+    }
     free(m); free(seq);
     return 0;
 }

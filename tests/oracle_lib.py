@@ -28,6 +28,12 @@ class SpecStats(ctypes.Structure):
     _fields_ = [("n_cycles", ctypes.c_uint64), ("n_accepted", ctypes.c_uint64), ("n_drafts", ctypes.c_uint64)]
 
 
+class Sampler(ctypes.Structure):
+    """or_sampler_t (the layout of the reference's sampler_t, sampler.h:7-14)."""
+    _fields_ = [("temp", ctypes.c_float), ("top_p", ctypes.c_float), ("top_k", ctypes.c_uint32),
+                ("repeat_penalty", ctypes.c_float), ("repeat_last_n", ctypes.c_uint32), ("rng_state", ctypes.c_uint64)]
+
+
 _lib = None
 
 
@@ -86,8 +92,26 @@ def lib():
     L.or_generate_spec_ex.restype = ctypes.c_uint32
     L.or_generate_greedy.argtypes = [vp, U32P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, U32P]
     L.or_generate_greedy.restype = ctypes.c_uint32
+    SP = ctypes.POINTER(Sampler)
+    L.or_sampler_init.argtypes = [SP, f32, f32, ctypes.c_uint32, f32, u64]
+    L.or_sampler_sample.argtypes = [SP, F32P, ctypes.c_uint32, U32P, ctypes.c_size_t]
+    L.or_sampler_sample.restype = ctypes.c_uint32
+    L.or_generate_sample.argtypes = [vp, U32P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, SP, U32P]
+    L.or_generate_sample.restype = ctypes.c_uint32
     _lib = L
     return L
+
+
+def sampler(temp, top_p, top_k, repeat_penalty, seed):
+    s = Sampler()
+    lib().or_sampler_init(ctypes.byref(s), temp, top_p, top_k, repeat_penalty, seed)
+    return s
+
+
+def sample(s, logits, tokens):
+    """one sampler_sample call; `logits` (float32) receives the repeat penalty in place"""
+    t = np.ascontiguousarray(tokens, np.uint32)
+    return lib().or_sampler_sample(ctypes.byref(s), fptr(logits), len(logits), uptr(t) if len(t) else None, len(t))
 
 
 def gemv(t, W, ne0, ne1, x, n, threads=8):
@@ -136,6 +160,12 @@ class Model:
         t = np.ascontiguousarray(toks, np.uint32)
         self.L.or_model_forward_batch(self.h, uptr(t), pos, len(t), ckpt)
         return self.arr(self.L.or_model_logits_b, len(t) * self.V).reshape(len(t), self.V)
+
+    def generate_sample(self, prompt, n_predict, s, eos=0xFFFFFFFF):
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(n_predict, np.uint32)
+        n = self.L.or_generate_sample(self.h, uptr(p), len(p), n_predict, eos, ctypes.byref(s), uptr(out))
+        return out[:n]
 
     def h_save(self, B):
         return self.arr(self.L.or_model_h_save, B * self.E).reshape(B, self.E)

@@ -285,3 +285,81 @@ def test_oracle_greedy_stream_bitexact(tiny_model):
     path, z = tiny_model
     m = O.Model(path, int(z["n_ctx"]))
     assert np.array_equal(m.generate_greedy(z["prompt"][:20], 40), z["greedy"])
+
+
+# ---------------------------------------------------------------- sampler (sampler.c:46-162)
+def test_oracle_sampler_bitexact_vs_reference():
+    """Three sampler_sample calls per case against the compiled reference: tokens, the generator
+    state after each call and the penalised logits (greedy, top-k 1/2/5/40/128/256/300, K > vocab,
+    nucleus 0.05..0.99, penalties 0.9..2.0 with repeated window tokens, seed 0)."""
+    z = load("sampler.npz")
+    for c, (V, temp, top_p, top_k, pen, seed, W) in enumerate(z["cases"]):
+        s = O.sampler(temp, top_p, int(top_k), pen, int(seed))
+        for step in range(3):
+            lg = z[f"logits_{c}"].copy()
+            tok = O.sample(s, lg, z[f"tokens_{c}"])
+            assert tok == z[f"sampled_{c}"][step], (c, step)
+            assert s.rng_state == z[f"state_{c}"][step], (c, step)
+            if step == 0:
+                assert np.array_equal(lg.view(np.uint32), z[f"penalised_{c}"].view(np.uint32)), c
+
+
+def test_oracle_sampler_defaults_and_greedy():
+    """sampler_init's defaults (sampler.c:46-56), and greedy = the first maximum of the penalised logits."""
+    s = O.sampler(0.7, 0.9, 0, -1.0, 0)
+    assert (s.top_k, s.repeat_penalty, s.repeat_last_n, s.rng_state) == (40, 1.0, 64, 0x123456789abcdef)
+    rng = np.random.default_rng(5)
+    lg = rng.standard_normal(300).astype(np.float32)
+    lg[[17, 200]] = 9.0                                  # tie: the earlier index wins
+    for temp, k in ((0.0, 40), (1.0, 1), (-2.0, 7)):
+        s = O.sampler(temp, 1.0, k, 1.0, 3)
+        st0 = s.rng_state
+        assert O.sample(s, lg.copy(), []) == 17
+        assert s.rng_state == st0, "greedy draws no random number"
+    # penalty: 17 occurs twice in the window (9 / 1.5 / 1.5 = 4), 200 once (9 / 1.5 = 6)
+    s = O.sampler(0.0, 1.0, 40, 1.5, 3)
+    l2 = lg.copy()
+    assert O.sample(s, l2, [17, 5, 17, 200]) == 200
+    assert l2[17] == np.float32(np.float32(9.0 / 1.5) / np.float32(1.5)) and l2[200] == np.float32(9.0 / 1.5)
+    neg = l2[5]
+    assert neg == (lg[5] / np.float32(1.5) if lg[5] > 0 else lg[5] * np.float32(1.5))
+    # only the last repeat_last_n = 64 tokens count
+    l3 = lg.copy()
+    O.sample(O.sampler(0.0, 1.0, 40, 1.5, 3), l3, [17] + [1] * 64)
+    assert l3[17] == lg[17]
+
+
+def _draws(temp, top_p, top_k, lg, n, seed=11):
+    s = O.sampler(temp, top_p, top_k, 1.0, seed)
+    return np.bincount([O.sample(s, lg.copy(), []) for _ in range(n)], minlength=len(lg))
+
+
+def test_oracle_sampler_distribution():
+    """Draw frequencies against the closed form: softmax(l / temp) restricted to the top-k largest logits
+    and to the shortest descending prefix whose mass reaches top_p, renormalised (5-sigma bands)."""
+    lg = np.array([2.0, 0.5, 1.5, -1.0, 1.0, 0.0, 2.5, -0.5], np.float32)
+    order = np.argsort(-lg, kind="stable")
+    n = 40000
+    for temp, top_p, top_k in ((1.0, 1.0, 8), (0.5, 1.0, 8), (2.0, 1.0, 3), (1.0, 0.7, 8), (0.7, 0.8, 5)):
+        z = lg[order[:top_k]].astype(np.float64) / temp
+        p = np.exp(z - z.max())
+        p /= p.sum()
+        m = len(p)
+        if top_p < 1.0:
+            m = int(np.searchsorted(np.cumsum(p), top_p) + 1)
+        q = np.zeros(len(lg))
+        q[order[:m]] = p[:m] / p[:m].sum()
+        f = _draws(temp, top_p, top_k, lg, n)
+        assert np.all(f[q == 0] == 0), (temp, top_p, top_k)
+        sig = np.sqrt(n * q * (1 - q)) + 1
+        assert np.all(np.abs(f - n * q) < 5 * sig), (temp, top_p, top_k, f, n * q)
+
+
+def test_oracle_sample_stream_bitexact(tiny_model):
+    """The sampled decode of main.c:232-248 (prefill, then sample / forward) on the tiny models."""
+    path, z = tiny_model
+    for c, (temp, top_p, top_k, pen, seed) in enumerate(z["sample_cfg"].reshape(4, 5)):
+        m = O.Model(path, int(z["n_ctx"]))
+        s = O.sampler(temp, top_p, int(top_k), pen, int(seed))
+        assert np.array_equal(m.generate_sample(z["prompt"][:20], 40, s), z[f"sample_c{c}"]), c
+        m.close()
