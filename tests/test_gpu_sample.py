@@ -140,6 +140,53 @@ def test_sample_ties_at_the_cut(gpu):
         assert all(t in set(top[:K].tolist()) for t in got[0]), (K, got[0])
 
 
+def test_sample_graph_replays_match_eager(gpu):
+    """Three sampler calls captured in a HIP graph (the sampler issues kernels only, no memset): every
+    replay, with eager sampler calls and host copies between replays, gives the eager tokens, generator
+    state and penalised logits (after the first call, which allocated the candidate buffers)."""
+    V = VOCAB_27B
+    rng0 = np.random.default_rng(41)
+    logits = (rng0.standard_normal(V) * 4).astype(np.float32)
+    toks = rng0.integers(0, 200, 100).astype(np.uint32)
+    L = gpu.L
+    lg, tk = gpu.put(logits), gpu.put(toks)
+    st, out = gpu.put(np.array([99], np.uint64)), gpu.buf(3 * 4)
+    cfgs = [(0.8, 0.9, 40, 1.1), (1.0, 1.0, 256, 1.0), (0.0, 1.0, 40, 1.3)]
+
+    def calls():
+        for i, (temp, top_p, top_k, pen) in enumerate(cfgs):
+            gpu.ok(L.qgpu_sample(lg.f32(), V, tk.u32(), len(toks), temp, top_p, top_k, pen, 64, st.u64(),
+                                 out.u32(i)))
+
+    def reset():
+        lg.upload(logits)
+        st.upload(np.array([99], np.uint64))
+
+    reset()
+    calls()
+    want = (out.download(np.uint32).tolist(), int(st.download(np.uint64)[0]), lg.download(np.float32))
+    gpu.sync()
+    gpu.ok(L.qgpu_graph_begin())
+    calls()
+    g = ctypes.c_void_p()
+    gpu.ok(L.qgpu_graph_end(ctypes.byref(g)))
+    try:
+        for rep in range(4):
+            reset()
+            out.upload(np.zeros(3, np.uint32))
+            gpu.ok(L.qgpu_graph_launch(g))
+            gpu.sync()
+            got = (out.download(np.uint32).tolist(), int(st.download(np.uint64)[0]), lg.download(np.float32))
+            assert got[0] == want[0] and got[1] == want[1], rep
+            assert np.array_equal(got[2].view(np.uint32), want[2].view(np.uint32)), rep
+            reset()
+            calls()                                     # eager work between replays
+            gpu.sync()
+            assert out.download(np.uint32).tolist() == want[0], rep
+    finally:
+        gpu.ok(L.qgpu_graph_destroy(g))
+
+
 def test_sample_rejects_bad_arguments(gpu):
     lg = gpu.put(np.zeros(8, np.float32))
     out = gpu.buf(4)
