@@ -630,23 +630,41 @@ struct IQ4A {
 };
 
 // rec, Ab, xsb are wave-uniform (scalar) addresses of this super-block's weight
-// record, digit plane 0 and digit scales; lanes add their own offsets.  The
-// digit scale of lane group g (digit g) and token t is 2^(8 g) xs[t]: only the
-// four token scales are loaded (scalar loads), 2^(8 g) is a lane constant.
+// record, digit plane 0 and digit scales; lanes add their own offsets.  The A
+// operand of lane l is digit l%4 of token (l%16)/4; lanes of tokens past ntok
+// load nothing (zero), and since each token's lanes read one 256-byte run per
+// kilobyte, a GEMV of B < 4 tokens reads B/4 of the digit lines.  Result row
+// 4 g + v of the matrix product (lane group g, register v) is digit v of token
+// g: its scale is 2^(8 v) xs[g], from the four token scales (scalar loads).
+// The digit loads are raw buffer loads over this super-block's tile: a lane of a
+// token past ntok gets an offset beyond the record count, which reads zero and
+// fetches nothing (no branch around the loads).
+#define DIGIT_OOB 0x80000000u
+#define DIGIT_RECORDS 0x40000000          // > NA planes of the workspace; < DIGIT_OOB
 template <int NA>
-static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab, const float *xsb, int lane)
+static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab, const float *xsb, int lane,
+                                                  int ntok)
 {
+    const int tk = (lane & 15) >> 2;
+    const uint32_t off = (uint32_t)(tk * 16 + (lane >> 4) * 4 + (lane & 3)) * 16;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)Ab, 0, DIGIT_RECORDS, 0x00020000);
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        const uint8_t *Aa = Ab + (uint64_t)a * PLANE_BYTES;
+        const uint32_t vo = 4 * a + tk < ntok ? (uint32_t)(a * PLANE_BYTES) + off : DIGIT_OOB;
 #pragma unroll
-        for (int p = 0; p < 4; p++) x.av[a][p] = *(const uint4 *)(Aa + p * 1024 + lane * 16);
+        for (int p = 0; p < 4; p++)
+            x.av[a][p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo + p * 1024, 0, 0));
         x.xt[a] = *(const float4 *)(xsb + (uint64_t)a * XS_FLOATS);
     }
 }
 
+// 2^(8 v): the weight of digit v
+static __device__ __forceinline__ float p8(int v) { return __builtin_bit_cast(float, (uint32_t)(127 + 8 * v) << 23); }
+// scale of token g (this lane group's) from the four token scales
+static __device__ __forceinline__ float tok_scale(float4 xt, int g) { return g == 0 ? xt.x : g == 1 ? xt.y : g == 2 ? xt.z : xt.w; }
+
 template <int NA>
-static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, const IQ4A<NA> &x, float p8g, float (&accf)[NA][4])
+static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, const IQ4A<NA> &x, int g, float (&accf)[NA][4])
 {
     const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
     v4i acci[NA];
@@ -670,13 +688,12 @@ static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, cons
             for (int i = 0; i < 4; i++) acci[a][i] = mad24(D[i], wsc, acci[a][i]);
         }
     }
-    const float dg = h2f(w.hdr.x & 0xFFFFu) * p8g;             // d 2^(8 g): exact
+    const float d = h2f(w.hdr.x & 0xFFFFu);
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        accf[a][0] += (float)acci[a][0] * (dg * x.xt[a].x);
-        accf[a][1] += (float)acci[a][1] * (dg * x.xt[a].y);
-        accf[a][2] += (float)acci[a][2] * (dg * x.xt[a].z);
-        accf[a][3] += (float)acci[a][3] * (dg * x.xt[a].w);
+        const float xg = tok_scale(x.xt[a], g);
+#pragma unroll
+        for (int v = 0; v < 4; v++) accf[a][v] += (float)acci[a][v] * ((d * p8(v)) * xg);   // d 2^(8 v): exact
     }
 }
 
@@ -736,7 +753,7 @@ static __device__ __forceinline__ long kq_aop(const IQ4A<NA> &x, int a, int ib)
 static __device__ __forceinline__ long kq_b(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
 template <int FMT, int NA>
-static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A<NA> &x, float p8g, float (&accf)[NA][4])
+static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A<NA> &x, int g, float (&accf)[NA][4])
 {
     const v4i z4 = (v4i){0, 0, 0, 0};
     if constexpr (FMT == T_Q8_0) {
@@ -759,10 +776,9 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
         }
 #pragma unroll
         for (int a = 0; a < NA; a++) {
-            accf[a][0] += accs[a][0] * (p8g * x.xt[a].x);
-            accf[a][1] += accs[a][1] * (p8g * x.xt[a].y);
-            accf[a][2] += accs[a][2] * (p8g * x.xt[a].z);
-            accf[a][3] += accs[a][3] * (p8g * x.xt[a].w);
+            const float xg = tok_scale(x.xt[a], g);
+#pragma unroll
+            for (int v = 0; v < 4; v++) accf[a][v] += accs[a][v] * (p8(v) * xg);
         }
     } else if constexpr (FMT == T_Q6_K) {
         const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
@@ -788,13 +804,12 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
                 for (int i = 0; i < 4; i++) acc[a][i] = mad24(DA[i], sa, mad24(DB[i], sb2, acc[a][i]));
             }
         }
-        const float dg = h2f(w.d & 0xFFFFu) * p8g;
+        const float d = h2f(w.d & 0xFFFFu);
 #pragma unroll
         for (int a = 0; a < NA; a++) {
-            accf[a][0] += (float)acc[a][0] * (dg * x.xt[a].x);
-            accf[a][1] += (float)acc[a][1] * (dg * x.xt[a].y);
-            accf[a][2] += (float)acc[a][2] * (dg * x.xt[a].z);
-            accf[a][3] += (float)acc[a][3] * (dg * x.xt[a].w);
+            const float xg = tok_scale(x.xt[a], g);
+#pragma unroll
+            for (int v = 0; v < 4; v++) accf[a][v] += (float)acc[a][v] * ((d * p8(v)) * xg);
         }
     } else {                                                   // Q4_K, Q5_K
         const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
@@ -820,13 +835,13 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
                 for (int i = 0; i < 4; i++) acq[a][i] = mad24(D[i], sc, acq[a][i]);
             }
         }
-        const float dg = h2f(w.hdr.x & 0xFFFFu) * p8g, mg = h2f(w.hdr.x >> 16) * p8g;
+        const float d = h2f(w.hdr.x & 0xFFFFu), dm = h2f(w.hdr.x >> 16);
 #pragma unroll
         for (int a = 0; a < NA; a++) {
-            const float xt[4] = { x.xt[a].x, x.xt[a].y, x.xt[a].z, x.xt[a].w };
+            const float xg = tok_scale(x.xt[a], g);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                accf[a][i] += (float)acq[a][i] * (dg * xt[i]) - (float)acm[a][i] * (mg * xt[i]);
+            for (int v = 0; v < 4; v++)
+                accf[a][v] += (float)acq[a][v] * ((d * p8(v)) * xg) - (float)acm[a][v] * ((dm * p8(v)) * xg);
         }
     }
 }
@@ -868,7 +883,6 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
     const int sb0 = kb0 + wv * nkb / NW, sb1 = kb0 + (wv + 1) * nkb / NW;
     RmsPart rp;
     if (MODE & IQ4_RMS) rms_load(args, wv, NW, lane, rp);
-    const float p8g = __builtin_bit_cast(float, (uint32_t)(127 + 8 * g) << 23);   // 2^(8 g)
 
     float accf[NA][4];
 #pragma unroll
@@ -884,7 +898,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
     WRec<FMT> wr[IQ4_WDEPTH];
     IQ4A<NA> ar[IQ4_ADEPTH];
 #define LOAD_W(slot, sbx) kq_load_w<FMT>(wr[slot], rec0 + (uint64_t)(sbx) * REC, lane, n)
-#define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * 4096, args.xs + (uint64_t)(sbx) * 16, lane)
+#define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * 4096, args.xs + (uint64_t)(sbx) * 16, lane, args.ntok)
 #pragma unroll
     for (int d = 0; d < IQ4_WDEPTH - 1 || d < IQ4_ADEPTH - 1; d++) {
         if (d < IQ4_ADEPTH - 1 && sb0 + d < sb1) LOAD_A(d, sb0 + d);
@@ -897,24 +911,17 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
                 const int pw = sb + d + IQ4_WDEPTH - 1, pa = sb + d + IQ4_ADEPTH - 1;
                 if (pa < sb1) LOAD_A((d + IQ4_ADEPTH - 1) % IQ4_ADEPTH, pa);
                 if (pw < sb1) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
-                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], p8g, accf);
-                else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], p8g, accf);
+                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], g, accf);
+                else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], g, accf);
             }
         }
     }
 #undef LOAD_W
 #undef LOAD_A
     if (MODE & IQ4_RMS) rms_reduce(args, wv, NW, lane, rp, rsc);
-    // lanes n, n+16, n+32, n+48 hold digits 0..3 of the same (token, row): sum them
+    // registers 0..3 of lane (g, n) hold digits 0..3 of token g, row n: sum them
 #pragma unroll
-    for (int a = 0; a < NA; a++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float v = accf[a][i];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            if (g == 0) red[wv][a][i][n] = v;
-        }
+    for (int a = 0; a < NA; a++) red[wv][a][g][n] = (accf[a][0] + accf[a][1]) + (accf[a][2] + accf[a][3]);
     __syncthreads();
     for (int e = tid; e < NA * 64; e += NW * 64) {     // (plane, token, row) entries of the tile
         const int a = e >> 6, i = (e >> 4) & 3, nn = e & 15;

@@ -64,12 +64,14 @@ static __device__ __forceinline__ void st_stream4(float *p, float4 v) { st_strea
 // 2^30 (s_t = 30 - exponent of the max; 0 for an all-zero or non-finite max);
 // x 2^s_t rounds to an integer X split into balanced base-256 digits d0..d3 (X =
 // d0 + 2^8 d1 + 2^16 d2 + 2^24 d3, d0..d2 in [-128, 127]).  A tile layout (4096
-// bytes): lane l = g*16 + m of the GEMV wave holds, for A row m = dgt*4 + t,
-// digit dgt of token t at the 8 elements of sub-block ib that K-slots 8g..8g+7
-// stand for (slot 8g+c, c < 4 -> element 4g+c; slot 8g+4+c -> element 16+4g+c);
-// two sub-blocks interleave so a lane fetches 16 bytes: byte ((ib/2)*64 + l)*16
-// + (ib%2)*8 + slot%8.  xs_tile[dgt*4 + t] = 2^(8 dgt - s_t) converts the
-// integer result of A row dgt*4 + t.  Every thread of the block calls it (two
+// bytes): lane l = g*16 + m of the GEMV wave holds, for A row m = t*4 + dgt
+// (token-major), digit dgt of token t at the 8 elements of sub-block ib that
+// K-slots 8g..8g+7 stand for (slot 8g+c, c < 4 -> element 4g+c; slot 8g+4+c ->
+// element 16+4g+c); two sub-blocks interleave so a lane fetches 16 bytes, and
+// each token's lanes come first to last in one 256-byte run: byte
+// (ib/2)*1024 + (t*16 + g*4 + dgt)*16 + (ib%2)*8 + slot%8.  A GEMV of fewer than
+// 4 tokens reads only the runs of its tokens.  xs_tile[dgt*4 + t] =
+// 2^(8 dgt - s_t) converts the integer result of A row t*4 + dgt.  Every thread of the block calls it (two
 // barriers); in blocks of more than 256 threads, threads 0..255 pass active =
 // true and the others false (they only take part in the barriers).
 struct ActDigitLds {
@@ -104,7 +106,7 @@ static __device__ __forceinline__ void act_digits(const float v[4], const float 
             for (int dg = 0; dg < 4; dg++) {
                 const int d = (dg < 3) ? (int)(int8_t)(X & 0xFF) : X;     // balanced base-256 digit
                 X = (X - d) >> 8;
-                L.stage[boff + (gg * 16 + dg * 4 + i) * 16] = (uint8_t)d;
+                L.stage[boff + (i * 16 + gg * 4 + dg) * 16] = (uint8_t)d;
             }
         }
     }
