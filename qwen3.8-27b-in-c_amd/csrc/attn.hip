@@ -508,7 +508,7 @@ __global__ __launch_bounds__(4 * ATT_HD) void k_attn_combine_act(const float *q,
         for (int o = 32; o; o >>= 1)
 #pragma unroll
             for (int t = 0; t < 4; t++) m[t] = fmaxf(m[t], __shfl_xor(m[t], o));
-    act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)h * 4096,
+    act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)h * DIGIT_TILE,
                xs + (uint64_t)a * XS_FLOATS + (uint64_t)h * 16, active);
 }
 

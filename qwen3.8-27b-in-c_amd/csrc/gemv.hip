@@ -7,18 +7,18 @@
 //     a wave loads its MFMA B operand for 4 sub-blocks with one 16-byte load;
 //   * a nibble dword decodes with 4 v_perm_b32 into two int8 halves of the
 //     codebook values, which two chained MFMAs multiply by the same operand;
-//   * the activations are turned once per call into 4 balanced int8 "digits"
-//     of a 30-bit fixed-point value per (token, super-block):
-//       x = 2^-s * (d0 + 2^8 d1 + 2^16 d2 + 2^24 d3),  |x| 2^s < 2^30,
+//   * the activations are turned once per call into 3 balanced int8 "digits"
+//     of a 22-bit fixed-point value per (token, super-block):
+//       x = 2^-s * (d0 + 2^8 d1 + 2^16 d2),  |x| 2^s < 2^22,
 //     so v_mfma_i32_16x16x32_i8 computes exact integer sub-block dot products
-//     for 4 tokens x 4 digits (rows of the A tile) against 16 weight rows;
+//     for 4 tokens x 4 digit rows (rows of the A tile; the fourth digit row is
+//     zero and is not stored or loaded) against 16 weight rows;
 //   * the 6-bit sub-block scale (ls - 32) is applied in int32 (exact: |acc| <
 //     2^27 per super-block), then (d * 2^(8 dgt - s)) once per super-block in
-//     fp32.  The only roundings are the x quantisation (2^-31 of the block max)
-//     and the fp32 super-block accumulation, below the fp32 FMA rounding of the
-//     reference's own accumulation.
-// Other formats (Q4_K/Q5_K/Q6_K/Q8_0/F32: embeddings, lm_head, eh_proj of the
-// real checkpoint) use a VALU kernel on the GGUF layout.
+//     fp32.  The roundings are the x quantisation (2^-23 of the super-block
+//     max) and the fp32 super-block accumulation.
+// Q4_K/Q5_K/Q6_K/Q8_0 run on the same matrix-core path; F32 (and Q8_0 rows
+// that are not a multiple of 256) use a VALU kernel on the GGUF layout.
 #include "qgpu_internal.h"
 #include <stdlib.h>
 
@@ -341,7 +341,7 @@ int qg_repack(int type, const void *raw, uint64_t ne0, uint64_t ne1, void *packe
 
 // ---------------------------------------------------------------- activation prep
 // Digit planes: plane a holds tokens 4a..4a+3; the A tile of super-block sb is
-// at A + a*PLANE_BYTES + sb*4096 and its factors at xs + a*XS_FLOATS + sb*16
+// at A + a*PLANE_BYTES + sb*DIGIT_TILE and its factors at xs + a*XS_FLOATS + sb*16
 // (layout: act_digits in qgpu_internal.h).
 struct ActDev {
     const float *x, *y, *w, *w2;
@@ -533,7 +533,7 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
 #pragma unroll
             for (int i = 0; i < 4; i++) m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
     }
-    act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * 4096, xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16);
+    act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * DIGIT_TILE, xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16);
     if (KIND == ACT_RMS_DEFER && e < nt)     // red[] was written before the barriers of act_digits
         p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[e][0] + red[e][1]) + (red[e][2] + red[e][3]);
 }
@@ -631,9 +631,10 @@ struct IQ4A {
 
 // rec, Ab, xsb are wave-uniform (scalar) addresses of this super-block's weight
 // record, digit plane 0 and digit scales; lanes add their own offsets.  The A
-// operand of lane l is digit l%4 of token (l%16)/4; lanes of tokens past ntok
-// load nothing (zero), and since each token's lanes read one 256-byte run per
-// kilobyte, a GEMV of B < 4 tokens reads B/4 of the digit lines.  Result row
+// operand of lane l is digit l%4 of token (l%16)/4; lanes of digit 3 and of
+// tokens past ntok load nothing (zero), and since each token's lanes read one
+// 192-byte run per 768 bytes, a GEMV of B < 4 tokens reads about B/4 of the
+// digit lines.  Result row
 // 4 g + v of the matrix product (lane group g, register v) is digit v of token
 // g: its scale is 2^(8 v) xs[g], from the four token scales (scalar loads).
 // The digit loads are raw buffer loads over this super-block's tile: a lane of a
@@ -645,15 +646,15 @@ template <int NA>
 static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab, const float *xsb, int lane,
                                                   int ntok)
 {
-    const int tk = (lane & 15) >> 2;
-    const uint32_t off = (uint32_t)(tk * 16 + (lane >> 4) * 4 + (lane & 3)) * 16;
+    const int tk = (lane & 15) >> 2, dg = lane & 3;
+    const uint32_t off = (uint32_t)(tk * 12 + (lane >> 4) * 3 + dg) * 16;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)Ab, 0, DIGIT_RECORDS, 0x00020000);
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        const uint32_t vo = 4 * a + tk < ntok ? (uint32_t)(a * PLANE_BYTES) + off : DIGIT_OOB;
+        const uint32_t vo = dg < 3 && 4 * a + tk < ntok ? (uint32_t)(a * PLANE_BYTES) + off : DIGIT_OOB;
 #pragma unroll
         for (int p = 0; p < 4; p++)
-            x.av[a][p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo + p * 1024, 0, 0));
+            x.av[a][p] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, vo + p * DIGIT_SUB, 0, 0));
         x.xt[a] = *(const float4 *)(xsb + (uint64_t)a * XS_FLOATS);
     }
 }
@@ -898,7 +899,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
     WRec<FMT> wr[IQ4_WDEPTH];
     IQ4A<NA> ar[IQ4_ADEPTH];
 #define LOAD_W(slot, sbx) kq_load_w<FMT>(wr[slot], rec0 + (uint64_t)(sbx) * REC, lane, n)
-#define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * 4096, args.xs + (uint64_t)(sbx) * 16, lane, args.ntok)
+#define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * DIGIT_TILE, args.xs + (uint64_t)(sbx) * 16, lane, args.ntok)
 #pragma unroll
     for (int d = 0; d < IQ4_WDEPTH - 1 || d < IQ4_ADEPTH - 1; d++) {
         if (d < IQ4_ADEPTH - 1 && sb0 + d < sb1) LOAD_A(d, sb0 + d);

@@ -54,28 +54,31 @@ static __device__ __forceinline__ void st_stream4(float *p, float4 v) { st_strea
 // their conversion factors, then the deferred-RMSNorm sums (gemv.hip).
 #define MAX_K       65536
 #define MAX_NSB     (MAX_K / 256)
-#define PLANE_BYTES ((size_t)MAX_NSB * 4096)
+#define DIGIT_TILE  3072     // digit bytes of one (4-token plane, super-block): 4 tokens x 3 digits x 256
+#define DIGIT_SUB   768      // of one pair of sub-blocks
+#define PLANE_BYTES ((size_t)MAX_NSB * DIGIT_TILE)
 #define XS_FLOATS   ((size_t)MAX_NSB * 16)
 
 // Digit planes of one (4-token plane, 256-element super-block), written by a
 // block of 256 threads: thread e holds element e of the super-block for the 4
 // tokens (v[i]; tokens past the batch hold 0) and m[i], the largest |v[i]| of
 // its wave.  Per token t the shift s_t puts the super-block maximum just under
-// 2^30 (s_t = 30 - exponent of the max; 0 for an all-zero or non-finite max);
-// x 2^s_t rounds to an integer X split into balanced base-256 digits d0..d3 (X =
-// d0 + 2^8 d1 + 2^16 d2 + 2^24 d3, d0..d2 in [-128, 127]).  A tile layout (4096
-// bytes): lane l = g*16 + m of the GEMV wave holds, for A row m = t*4 + dgt
-// (token-major), digit dgt of token t at the 8 elements of sub-block ib that
-// K-slots 8g..8g+7 stand for (slot 8g+c, c < 4 -> element 4g+c; slot 8g+4+c ->
-// element 16+4g+c); two sub-blocks interleave so a lane fetches 16 bytes, and
-// each token's lanes come first to last in one 256-byte run: byte
-// (ib/2)*1024 + (t*16 + g*4 + dgt)*16 + (ib%2)*8 + slot%8.  A GEMV of fewer than
+// 2^22 (s_t = 22 - exponent of the max; 0 for an all-zero or non-finite max);
+// x 2^s_t rounds to an integer X split into three balanced base-256 digits (X =
+// d0 + 2^8 d1 + 2^16 d2, d0, d1 in [-128, 127], |d2| <= 64): x to 2^-23 of the
+// super-block maximum.  A tile layout (3072 bytes): lane l = g*16 + m of the
+// GEMV wave holds, for A row m = t*4 + dgt (token-major; rows with dgt = 3 are
+// zero), digit dgt of token t at the 8 elements of sub-block ib that K-slots
+// 8g..8g+7 stand for (slot 8g+c, c < 4 -> element 4g+c; slot 8g+4+c -> element
+// 16+4g+c); two sub-blocks interleave so a lane fetches 16 bytes, and each
+// token's lanes come first to last in one 192-byte run: byte
+// (ib/2)*768 + (t*12 + g*3 + dgt)*16 + (ib%2)*8 + slot%8.  A GEMV of fewer than
 // 4 tokens reads only the runs of its tokens.  xs_tile[dgt*4 + t] =
 // 2^(8 dgt - s_t) converts the integer result of A row t*4 + dgt.  Every thread of the block calls it (two
 // barriers); in blocks of more than 256 threads, threads 0..255 pass active =
 // true and the others false (they only take part in the barriers).
 struct ActDigitLds {
-    uint8_t stage[4096];
+    uint8_t stage[DIGIT_TILE];
     float mx[4][4];          // [token][wave]
 };
 static __device__ __forceinline__ void act_digits(const float v[4], const float m[4], ActDigitLds &L,
@@ -92,27 +95,27 @@ static __device__ __forceinline__ void act_digits(const float v[4], const float 
     for (int i = 0; i < 4; i++) {
         const float mx = fmaxf(fmaxf(L.mx[i][0], L.mx[i][1]), fmaxf(L.mx[i][2], L.mx[i][3]));
         int E = 0;
-        if (mx > 0.0f && isfinite(mx)) { frexpf(mx, &E); shift[i] = 30 - E; }
+        if (mx > 0.0f && isfinite(mx)) { frexpf(mx, &E); shift[i] = 22 - E; }
         else shift[i] = 0;
     }
     if (active) {
         const int ib = e >> 5, w = e & 31, up = w >> 4, jj = w & 15, gg = jj >> 2, c = jj & 3;
-        const int boff = ((ib >> 1) * 64) * 16 + (ib & 1) * 8 + up * 4 + c;   // + lane*16
+        const int boff = (ib >> 1) * DIGIT_SUB + (ib & 1) * 8 + up * 4 + c;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float sv = ldexpf(v[i], shift[i]);
             int X = isfinite(sv) ? (int)rintf(sv) : 0;
 #pragma unroll
-            for (int dg = 0; dg < 4; dg++) {
-                const int d = (dg < 3) ? (int)(int8_t)(X & 0xFF) : X;     // balanced base-256 digit
+            for (int dg = 0; dg < 3; dg++) {
+                const int d = (dg < 2) ? (int)(int8_t)(X & 0xFF) : X;     // balanced base-256 digit
                 X = (X - d) >> 8;
-                L.stage[boff + (i * 16 + gg * 4 + dg) * 16] = (uint8_t)d;
+                L.stage[boff + (i * 12 + gg * 3 + dg) * 16] = (uint8_t)d;
             }
         }
     }
     __syncthreads();
     if (active) {
-        ((uint4 *)A_tile)[e] = ((const uint4 *)L.stage)[e];
+        if (e < DIGIT_TILE / 16) ((uint4 *)A_tile)[e] = ((const uint4 *)L.stage)[e];
         if (e < 16) xs_tile[e] = ldexpf(1.0f, 8 * (e >> 2) - shift[e & 3]);
     }
 }
