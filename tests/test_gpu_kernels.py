@@ -120,6 +120,34 @@ def test_gemv_multi_accum_rows(gpu):
     assert rel_err(got[:, 17:70], ref[:, 17:70]) < GEMV_TIGHT
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 6, 8])
+def test_gemv_wide_grids(gpu, n):
+    """Wide IQ4_XS grids against the oracle: a single 32768-row matrix (2048 row tiles), a multi-GEMV of
+    two 16400-row matrices (1025 tiles each, an odd count per matrix), and an accumulate into the
+    outputs."""
+    print(f"\n[gemv] wide grids, B={n}", flush=True)
+    host = host_lib()
+    ne0 = 512
+    x = host.synth_normal(8 * ne0, 13, 2).reshape(8, ne0)
+    W = host.synth_matrix(23, ne0, 32768, 5, 1, 0.02)
+    T = gpu.tensor(W, 23, ne0, 32768)
+    got = run_gemv(gpu, T, x, n)
+    assert rel_err(got, O.gemv(23, W, ne0, 32768, x, n)) < GEMV_TIGHT
+    Ws = [host.synth_matrix(23, ne0, 16400, 6, k, 0.02) for k in range(2)]
+    Ts = [gpu.tensor(Wk, 23, ne0, 16400) for Wk in Ws]
+    xb = gpu.put(np.ascontiguousarray(x[:n]))
+    outs = [gpu.put(np.zeros((n, 16400), np.float32)) for _ in range(2)]
+    gpu.ok(gpu.L.qgpu_gemv_multi_batch((ctypes.c_void_p * 2)(*[t.h for t in Ts]), 2, xb.f32(), ne0, n,
+                                       (pyqwen.F32P * 2)(*[o.f32() for o in outs]),
+                                       (ctypes.c_uint64 * 2)(16400, 16400), 0))
+    for k in range(2):
+        ref = O.gemv(23, Ws[k], ne0, 16400, x, n)
+        assert rel_err(outs[k].download(np.float32).reshape(n, 16400), ref) < GEMV_TIGHT, k
+    base = np.arange(n * 32768, dtype=np.float32).reshape(n, 32768) * 1e-3
+    got = run_gemv(gpu, T, x, n, pyqwen_accum(), out_init=base)
+    assert rel_err(got - base, O.gemv(23, W, ne0, 32768, x, n)) < 1e-4
+
+
 def pyqwen_accum():
     return 1   # QGPU_GEMV_ACCUM
 
