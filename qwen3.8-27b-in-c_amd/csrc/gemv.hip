@@ -618,9 +618,9 @@ static __device__ __forceinline__ void iq4_decode8(uint32_t q, uint32_t &x_lo, u
 // Weight records come from HBM and activation digits from L2, so the two are
 // prefetched to different depths: weights IQ4_WDEPTH super-blocks ahead
 // (10 VGPRs each), digits IQ4_ADEPTH ahead (16 * NA + 4 * NA VGPRs each).
-// Measured on MI355X (rings of 2..5 x 1..2, with and without tail loads that
-// keep the wait counts exact): all within +-3%, deeper rings slightly slower;
-// 3 / 1 keeps the plain kernel at 93 VGPRs (5 waves per SIMD).
+// Measured on MI355X over the whole 27B step with 3-digit tiles: weights 2 ahead
+// is 0.7% faster than 3 (decode 5.55 -> 5.49 ms), 4 ahead 5% slower, digits 2
+// ahead 3% slower.
 template <int FMT> struct WRec;                              // a lane's slice of one record
 template <> struct WRec<T_IQ4_XS> { uint2 hdr; uint4 qa, qb; };
 template <int NA>
@@ -848,7 +848,7 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
 }
 
 #ifndef IQ4_WDEPTH
-#define IQ4_WDEPTH 3    // weight records in flight per wave
+#define IQ4_WDEPTH 2    // weight records in flight per wave
 #endif
 #ifndef IQ4_ADEPTH
 #define IQ4_ADEPTH 1    // digit super-blocks in flight per wave
