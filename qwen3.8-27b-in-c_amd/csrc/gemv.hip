@@ -1357,12 +1357,16 @@ extern "C" int qgpu_gemv_act_split(const qgpu_tensor *W, const qgpu_act *act, in
 // cover the compute units about 4-5 times; measured on MI355X: 5120 x 17408
 // runs best at ks 4, 5120 x 6144 at ks 2..4 (a single-pass grid of 320 tiles
 // leaves 1.6x more work on the CUs that get two tiles).
+#ifndef SPLIT_TARGET
+#define SPLIT_TARGET 1280   // blocks a K-split GEMV of a narrow output aims at (5 per CU); measured over the
+                            // 27B step: 640 (ks 2) 2% and 2560 (ks 8) 1% slower
+#endif
 extern "C" int qgpu_gemv_split_ks(const qgpu_tensor *W)
 {
     if (!W || !W->packed) return 1;
     const uint64_t tiles = (W->ne1 + IQ4_TILE_ROWS - 1) / IQ4_TILE_ROWS, nsb = W->ne0 / 256;
     if (tiles > 640) return 1;
-    int ks = (int)(1280 / tiles);
+    int ks = (int)(SPLIT_TARGET / tiles);
     if (ks > 8) ks = 8;
     while (ks > 1 && (uint64_t)ks * 4 > nsb) ks--;          // at least 4 super-blocks per block
     return ks < 1 ? 1 : ks;
