@@ -1178,6 +1178,11 @@ static void launch_mfma(const GemvArgs &A, uint32_t blocks, int na, int nw, int 
 #undef MF_GO
 }
 
+#ifndef NW8_TILES
+#define NW8_TILES 512       // grids of at most this many tiles (no K split) run 8 waves per tile; with 1100
+                            // or 1280 the plain 17408x5120 B=4 GEMV alone is 3% faster, but the 27B step
+                            // (896..1088-tile GEMVs with row factors) 1.6% slower
+#endif
 static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x, uint64_t ldx,
                         int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
                         const uint64_t *r1s, int ks, float eps, bool deferred)
@@ -1224,7 +1229,7 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
             const char *e = getenv("QGPU_GEMV_NW");
             force_nw = e ? atoi(e) : 0;
         }
-        int nw = (ks == 1 && tiles <= 512) ? 8 : 4;
+        int nw = (ks == 1 && tiles <= NW8_TILES) ? 8 : 4;
         if (force_nw == 1 || force_nw == 2 || force_nw == 4 || force_nw == 8) nw = force_nw;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
         if (A.rss && nw < 4) nw = 4;                        // row factors: <= 2 tokens per wave
