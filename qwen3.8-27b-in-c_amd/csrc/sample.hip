@@ -8,16 +8,21 @@
 //      order, written back to the logits: the reference changes them in place)
 //      and finds its K largest keys by radix select (8-bit digits from the top,
 //      a 256-bin LDS histogram per digit, stopping as soon as the digit's bin
-//      holds exactly the keys still needed).  The K keys leave unsorted.  When
-//      the lists of all blocks exceed what the final block holds, the same
-//      kernel selects again over the keys (groups of 4096).
-//   2. k_smp_final: one block selects the K largest of the lists the same way,
-//      orders them by rank, computes the K exponentials in parallel, then one
-//      thread runs the order-dependent rest of the reference's arithmetic in
-//      its order: the double sum, the float scaling, the nucleus cut, the
-//      xorshift64 draw (state in device memory) and the running-sum selection.
-//      Greedy (temp <= 0 or top_k == 1) is the same pipeline with K = 1: the
-//      first maximum under strict > (-0.0 and +0.0 compare equal, as there).
+//      holds exactly the keys still needed).  The K keys leave unsorted, with
+//      the smallest of them (the block's K-th).  When the lists of all blocks
+//      exceed what the final block holds, the same kernel selects again over
+//      the keys (groups of 4096).
+//   2. k_smp_final: one block drops the keys below the largest block K-th
+//      (the global K-th is at least that), selects the K largest the same way,
+//      orders them by rank and runs the reference's arithmetic with its
+//      results: K exponentials in parallel; the double sum (a tree when every
+//      term is at least 2^-21, where every partial sum is exact, else in order
+//      on one thread); the float scaling; the one float sequence of cumulative
+//      sums that the nucleus cut, the total and the draw all use (one thread),
+//      with the cut and the draw as first-index searches over it; the
+//      xorshift64 draw (state in device memory).  Greedy (temp <= 0 or
+//      top_k == 1) is the same pipeline with K = 1: the first maximum under
+//      strict > (-0.0 and +0.0 compare equal, as there).
 // The candidates are the reference's: the K largest logits in descending order.
 // Where logits are exactly equal, the reference's order (and, at the K-th place,
 // which of them it keeps) follows its heap and the C library's qsort; here equal
