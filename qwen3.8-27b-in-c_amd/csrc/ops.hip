@@ -6,7 +6,7 @@
 #include "qgpu_internal.h"
 
 namespace qg {
-void *ws_small = nullptr;     // 64 KiB: argmax partials
+void *ws_small = nullptr;     // 128 KiB: argmax partials (64 rows x AMAX_CHUNKS keys)
 }
 
 static __device__ __forceinline__ float block_sum(float v, float *sh)
@@ -109,6 +109,7 @@ __global__ void k_add(float *y, uint64_t ldy, const float *x, uint64_t ldx, uint
 }
 
 // ---------------------------------------------------------------- argmax
+#define AMAX_CHUNKS 256
 // key = order-preserving float bits << 32 | ~index : the max key is the max
 // value with the lowest index (model.c:750 strict '>').
 static __device__ __forceinline__ uint64_t akey(float v, uint32_t i)
@@ -118,7 +119,8 @@ static __device__ __forceinline__ uint64_t akey(float v, uint32_t i)
     return ((uint64_t)u << 32) | (0xFFFFFFFFu - i);
 }
 
-#define AMAX_CHUNKS 64
+// AMAX_CHUNKS blocks per row; a thread issues its (up to 4) loads of a pass before
+// comparing, so a 248,320-logit row costs one load latency.
 __global__ __launch_bounds__(256) void k_argmax_part(const float *logits, uint64_t ld, uint32_t n, uint64_t *part)
 {
     __shared__ uint64_t sh[4];
@@ -126,9 +128,16 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float *logits, uint64
     const uint32_t per = (n + AMAX_CHUNKS - 1) / AMAX_CHUNKS;
     const uint32_t lo = blockIdx.x * per, hi = min(n, lo + per);
     uint64_t best = 0;
-    for (uint32_t i = lo + threadIdx.x; i < hi; i += blockDim.x) {
-        const uint64_t k = akey(r[i], i);
-        best = k > best ? k : best;
+    for (uint32_t i0 = lo + threadIdx.x; i0 < hi; i0 += 4 * 256) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = i0 + j * 256 < hi ? r[i0 + j * 256] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (i0 + j * 256 < hi) {
+                const uint64_t k = akey(v[j], i0 + j * 256);
+                best = k > best ? k : best;
+            }
     }
 #pragma unroll
     for (int o = 32; o; o >>= 1) {
@@ -146,7 +155,12 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float *logits, uint64
 
 __global__ void k_argmax_final(const uint64_t *part, uint32_t *out)
 {
-    uint64_t b = part[(uint64_t)blockIdx.x * AMAX_CHUNKS + threadIdx.x];
+    uint64_t b = 0;
+#pragma unroll
+    for (int j = 0; j < AMAX_CHUNKS / 64; j++) {
+        const uint64_t k = part[(uint64_t)blockIdx.x * AMAX_CHUNKS + threadIdx.x + 64 * j];
+        b = k > b ? k : b;
+    }
 #pragma unroll
     for (int o = 32; o; o >>= 1) {
         const uint64_t k = __shfl_xor(b, o);
@@ -219,7 +233,7 @@ static int ensure_small()
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
-    if (!qg::ws_small) QG_CHECK(hipMalloc(&qg::ws_small, 65536));
+    if (!qg::ws_small) QG_CHECK(hipMalloc(&qg::ws_small, 64 * AMAX_CHUNKS * sizeof(uint64_t)));
     return QGPU_OK;
 }
 
