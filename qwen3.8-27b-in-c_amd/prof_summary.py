@@ -4,6 +4,7 @@
     prof_summary.py stats   DB_OR_DIR --cmd "<command that made it>" [--bench-json FILE] [--plain-json FILE] [--top N]
     prof_summary.py traffic FETCH_DB WRITE_DB --bench-json FILE [--calib-bytes N]
     prof_summary.py sweep   BENCH_JSON --cmd "<command that made it>"
+    prof_summary.py steps   DB_OR_DIR --cmd "<command that made it>" [--rows 4] [--title T]
 
 stats   : per-kernel calls / total / average duration of a --kernel-trace run,
           and, given the benchmark's JSON line, the average duration of the
@@ -17,6 +18,12 @@ traffic : HBM bytes per launch of the roofline kernel from two --pmc runs
           same counter reads for the k_copy kernel of known size (the
           benchmark's --copy-calib: 5 copies of 256 MiB).  Prints JSON.
 sweep   : the table of a `bench.py --mode sweep` line (formats x shapes x B).
+steps   : per-kernel time of one verify step of a --kernel-trace run of the model
+          benchmark.  The trace is cut after every k_argmax_final; a verify step
+          is a piece that ends in the argmax of --rows rows (drafts and decode
+          steps end in a one-row argmax).  Durations are averaged over all verify
+          steps of the run (the timed spec cycles, forced acceptance and the
+          step timings).
 """
 import argparse
 import glob
@@ -167,6 +174,40 @@ def cmd_sweep(a):
     print("\n".join(out))
 
 
+def cmd_steps(a):
+    rows = kernel_rows(a.db)
+    segs, cur = [], []
+    for r in rows:
+        cur.append(r)
+        if short(r[0]).startswith("k_argmax_final"):
+            segs.append(cur)
+            cur = []
+    steps = [g for g in segs if g[-1][3] // max(g[-1][4], 1) == a.rows]
+    if not steps:
+        sys.exit(f"no step ending in a {a.rows}-row argmax")
+    agg = {}
+    for g in steps:
+        for name, _, dur, gx, wx in g:
+            key = (short(name), gx // max(wx, 1), wx)
+            c = agg.setdefault(key, [0, 0])
+            c[0] += 1
+            c[1] += dur
+    n = len(steps)
+    busy = sum(c[1] for c in agg.values()) / n
+    out = [f"# rocprofv3 kernel trace: one verify step (B = {a.rows}){' -- ' + a.title if a.title else ''}", "",
+           "Command (`/root/repo` is the repository root):", "", "```", a.cmd, "```", "",
+           f"{n} verify steps in the trace; {statistics.median(len(g) for g in steps):.0f} dispatches and "
+           f"{busy / 1e3:.1f} us of kernel time per step (sum of kernel durations).", "",
+           "| kernel | grid x block | launches per step | avg us | us per step | % |",
+           "|---|---|---:|---:|---:|---:|"]
+    for (name, gb, wx), (cnt, tot) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        if tot / n / 1e3 < a.min_us:
+            continue
+        out.append(f"| `{name}` | {gb} x {wx} | {cnt / n:.1f} | {tot / cnt / 1e3:.2f} | {tot / n / 1e3:.1f} | "
+                   f"{100 * tot / n / busy:.1f} |")
+    print("\n".join(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd_name", required=True)
@@ -185,8 +226,14 @@ def main():
     w = sub.add_parser("sweep")
     w.add_argument("bench_json")
     w.add_argument("--cmd", required=True)
+    st = sub.add_parser("steps")
+    st.add_argument("db")
+    st.add_argument("--cmd", required=True)
+    st.add_argument("--rows", type=int, default=4)
+    st.add_argument("--title", default=None)
+    st.add_argument("--min-us", type=float, default=1.0, help="omit kernels below this many us per step")
     a = ap.parse_args()
-    {"stats": cmd_stats, "traffic": cmd_traffic, "sweep": cmd_sweep}[a.cmd_name](a)
+    {"stats": cmd_stats, "traffic": cmd_traffic, "sweep": cmd_sweep, "steps": cmd_steps}[a.cmd_name](a)
 
 
 if __name__ == "__main__":
