@@ -6,7 +6,7 @@
  * contract, so names and layouts match the reference; the implementation
  * (host/gguf.c) is this library's own.
  */
-#ifndef QWEN_GGUF_H
+#if !defined(QWEN_GGUF_H) && !defined(GGUF_H)   /* either header, whichever came first */
 #define QWEN_GGUF_H
 /* the reference header of the same name is superseded by this one when both
    are on the include path (reference drivers compiled against this library) */

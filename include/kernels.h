@@ -9,7 +9,7 @@
  * tensor is uploaded (and, for IQ4_XS, repacked) the first time it is used and
  * cached by its data address until kernels_release_weights().
  */
-#ifndef QWEN_KERNELS_H
+#if !defined(QWEN_KERNELS_H) && !defined(KERNELS_H)   /* either header, whichever came first */
 #define QWEN_KERNELS_H
 /* the reference header of the same name is superseded by this one when both
    are on the include path (reference drivers compiled against this library) */
@@ -48,6 +48,11 @@ void softmax_inplace(float *x, uint64_t n);
 
 /* frees the device copies of weights uploaded by the calls above */
 void kernels_release_weights(void);
+/* first failure of the calls above (0 = none): an unsupported weight type,
+ * a batch above 8, rows past the matrix, or a device error.  The failing call
+ * wrote zeros to its outputs, as the reference does for unsupported types
+ * (kernels.c:596).  No reference counterpart. */
+int kernels_status(void);
 
 #ifdef __cplusplus
 }

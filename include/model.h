@@ -17,8 +17,14 @@
  *   - SPEC_MAX_B is 8 (drafts k <= 7); the reference caps k at 2.
  *   - Recurrent-state checkpoints are a ring of state slots on the device;
  *     model_rollback_to() moves the ring index (no copy).
+ *   - Calls whose positions run past n_ctx (pos + B > n_ctx) are rejected on
+ *     the host with a message, before any device work; the reference writes
+ *     past its KV arrays.  After a rejected call or a device error,
+ *     qwen_model_status() returns nonzero (the reference API has no error
+ *     channel on the compute path); a device error is sticky: every later call
+ *     does nothing.
  */
-#ifndef QWEN_MODEL_H
+#if !defined(QWEN_MODEL_H) && !defined(MODEL_H)   /* either header, whichever came first */
 #define QWEN_MODEL_H
 /* the reference header of the same name is superseded by this one when both
    are on the include path (reference drivers compiled against this library) */
@@ -40,34 +46,66 @@ typedef struct {            /* reference model.h:10-31 */
     uint32_t n_v_heads, n_k_heads, head_k_dim, head_v_dim, d_inner, conv_dim, d_conv, d_state;
 } qwen_dims_t;
 
-typedef struct {            /* reference model.h:33-57 (host descriptors) */
+typedef struct {            /* reference model.h:33-57 */
     bool is_recurrent;
     const gguf_tensor_info_t *attn_norm, *post_attn_norm, *ffn_gate, *ffn_up, *ffn_down;
     const gguf_tensor_info_t *attn_q, *attn_k, *attn_v, *attn_q_norm, *attn_k_norm, *attn_out;
     const gguf_tensor_info_t *wqkv, *wqkv_gate, *ssm_conv1d, *ssm_dt_bias, *ssm_a, *ssm_beta, *ssm_alpha,
                              *ssm_norm, *ssm_out;
+    /* States (reference model.h:53-56).  Here the KV caches and recurrent states
+     * live in GPU memory (a ring of state slots per GDN layer), so these host
+     * pointers stay NULL. */
+    float *kv_k, *kv_v;
+    float *conv_state;
+    float *ssm_state;
 } qwen_layer_t;
 
 typedef struct qwen_gpu qwen_gpu_t;   /* device-side state (host/model.c) */
 
+/* Field order and names of reference model.h:59-111, then this build's own
+ * fields.  The host buffers are laid out as the reference lays them out
+ * (model.c:166-230): one activation arena x | xb | qkv | kv_small | z | ffn_buf |
+ * attn_out | logits | scores and one batch arena bx | bxb | bqkv | bkv | bz |
+ * bffn | battn_out | h_save.  The device path writes the result fields (mtp_h,
+ * x, logits, logits_b, h_save) when host_sync is on; the other buffers are host
+ * scratch that reference callers may use (test_kernels.c passes xb to gemv). */
 typedef struct {
     gguf_context_t gguf;          /* file metadata / tensor table (synthetic models: generated table) */
     qwen_config_t  cfg;
     qwen_dims_t    dims;
     qwen_layer_t  *layers;
     const gguf_tensor_info_t *tok_embd, *output_norm, *output;
+
+    float *mtp_h;      /* [n_embd]        MTP hidden (input of the next mtp_forward)  */
+
+    float *x;          /* [n_embd]        residual after the last single-token pass   */
+    float *xb;         /* [n_embd]        host scratch                                */
+    float *qkv;        /* [max(conv_dim, 2*n_head*head_dim, n_ff)] host scratch       */
+    float *kv_small;   /* [2*n_kv_head*head_dim] host scratch                         */
+    float *z;          /* [d_inner]       host scratch                                */
+    float *ffn_buf;    /* [n_ff]          host scratch                                */
+    float *attn_out;   /* [n_head*head_dim] host scratch                              */
+    float *logits;     /* [vocab]         last single-token / MTP logits              */
+    float *scores;     /* [n_head][n_ctx] host scratch                                */
+
+    float *rope_cos, *rope_sin;   /* [n_ctx][rope_dim/2], host copies of the device tables */
+    void  *arena;
+
+    float *bx, *bxb, *bqkv, *bkv, *bz, *bffn, *battn_out;   /* [8][...] host scratch */
+    float *h_save;     /* [8][n_embd]     pre-norm hidden per token of the last batch */
+    float *logits_b;   /* [8][vocab]      logits of the last batched forward          */
+    void  *arena_b;
+
+    /* rollback checkpoints: a ring of state slots in GPU memory here, NULL */
+    float *ckpt_conv;
+    float *ckpt_ssm;
+
     qwen_layer_t   mtp_layer;
     const gguf_tensor_info_t *mtp_eh_proj, *mtp_enorm, *mtp_hnorm, *mtp_shnorm;
 
-    /* host-side results (reference model.h:62-104 field names) */
-    float *mtp_h;      /* [n_embd]        MTP hidden (input of the next mtp_forward)  */
-    float *x;          /* [n_embd]        residual after the last single-token pass   */
-    float *logits;     /* [vocab]         last single-token / MTP logits              */
-    float *logits_b;   /* [8][vocab]      logits of the last batched forward          */
-    float *h_save;     /* [8][n_embd]     pre-norm hidden per token of that batch     */
-
     uint32_t n_ctx;
     uint32_t pos;
+
     int      host_sync;    /* 1: copy results into the fields above after each call */
     qwen_gpu_t *gpu;
 } qwen_model_t;
@@ -138,7 +176,10 @@ uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n
 /* The same loop in two parts, for callers that time or pace the cycles:
  * model_spec_begin prefills the prompt (0, or -1 on bad arguments);
  * model_spec_run continues from the current state for at most max_cycles
- * cycles / max_tokens tokens and may be called again to go on. */
+ * cycles / max_tokens tokens and may be called again to go on.  It stops as
+ * main.c:210 does once the verified positions reach n_ctx.  With host_sync on,
+ * it leaves logits_b / h_save (the last verify's rows; row cycle_j[last] is
+ * the logits the next cycle starts from) and mtp_h in the host fields. */
 int      model_spec_begin(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t k);
 uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_accept, uint32_t max_cycles,
                         uint32_t max_tokens, uint32_t *out, uint32_t *cycle_j, qwen_gen_stats_t *st);
@@ -156,6 +197,12 @@ uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t
 /* One timed verify step (B tokens at the current position) and one timed decode
  * step, on device buffers (benchmark support); the model state is restored. */
 int  model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, float *ms_decode, float *ms_draft);
+
+/* Status of the last model call: 0 = done, -1 = rejected on the host (bad
+ * arguments, positions past n_ctx), -2 = a device error (sticky: from then on
+ * every call does nothing and returns -1 / leaves the results untouched).
+ * No reference counterpart. */
+int qwen_model_status(const qwen_model_t *m);
 
 /* FFI helpers (no reference counterpart; for callers that do not mirror the
  * struct layout, e.g. ctypes): allocation and field access. */

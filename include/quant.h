@@ -4,7 +4,7 @@
  * The block layouts are the ggml on-disk format and are reproduced field for
  * field (sizes asserted below); host/quant.c is this library's own code.
  */
-#ifndef QWEN_QUANT_H
+#if !defined(QWEN_QUANT_H) && !defined(QUANT_H)   /* either header, whichever came first */
 #define QWEN_QUANT_H
 /* the reference header of the same name is superseded by this one when both
    are on the include path (reference drivers compiled against this library) */

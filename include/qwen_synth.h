@@ -30,12 +30,27 @@ typedef struct {
     int32_t  type_embd, type_output, type_qkv, type_eh_proj;   /* ... unless overridden (<0 = default) */
     float    gain_output;                    /* output-RMS gain of the lm_head            */
     uint64_t seed;
+    /* structure knobs (all zero = plain random init) */
+    float    gain_embd;                      /* token-embedding RMS gain (0 = 1)          */
+    float    gain_resid;                     /* gain of ffn_down, ssm_out, attn_output (0 = 0.5) */
+    int32_t  mtp_diag;                       /* 1: the token half of nextn.eh_proj is a scaled
+                                                identity plus weak noise, the hidden half weak
+                                                noise (IQ4_XS only)                      */
+    float    norm_sigma;                     /* spread of the RMSNorm weights around 1 (0 = 0.1) */
+    int32_t  tie_shift;                      /* 1: output.weight row v = token_embd row v-1 (mod
+                                                vocab), so the greedy next token of t is t+1
+                                                unless the layers outweigh the embedding  */
 } qwen_synth_spec_t;
 
 /* The 27B hybrid: 48 GDN + 16 GQA layers + MTP, H=5120, F=17408, V=248320, all IQ4_XS. */
 void qwen_synth_spec_27b(qwen_synth_spec_t *s, uint64_t seed);
-/* Small hybrid of the same structure for parity tests (dims in the body). */
-void qwen_synth_spec_tiny(qwen_synth_spec_t *s, uint64_t seed, int mixed_types);
+/* Small hybrid of the same structure for parity tests (dims in the body).
+ * variant 0: every 2-D weight IQ4_XS; 1: the real checkpoint's format mix;
+ * 2: a model whose MTP drafts agree with the backbone most of the time
+ *    (output rows = embedding rows shifted by one, identity-like eh_proj,
+ *    embeddings a little weaker than the layers' sum), so greedy speculative
+ *    decoding accepts anywhere from 0 to k drafts per cycle. */
+void qwen_synth_spec_tiny(qwen_synth_spec_t *s, uint64_t seed, int variant);
 
 typedef struct {
     char     name[GGUF_MAX_NAME];

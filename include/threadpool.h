@@ -4,7 +4,7 @@
  * threads; the pool is kept so reference callers compile and link unchanged,
  * and pool_run still runs fn on n_threads host threads for host-side work.
  */
-#ifndef QWEN_THREADPOOL_H
+#if !defined(QWEN_THREADPOOL_H) && !defined(THREADPOOL_H)   /* either header, whichever came first */
 #define QWEN_THREADPOOL_H
 /* the reference header of the same name is superseded by this one when both
    are on the include path (reference drivers compiled against this library) */

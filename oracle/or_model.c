@@ -757,7 +757,9 @@ uint32_t or_generate_spec_ex(or_model_t *m, const uint32_t *prompt, uint32_t n_p
         if (cycle_j) cycle_j[s.n_cycles] = j;
         s.n_accepted += j;
         s.n_drafts += k;
-        if (m->pos >= m->n_ctx) break;
+        /* n_cycles counts every cycle run, also the one that reaches the context
+         * end (main.c's printed counter skips that one) */
+        if (m->pos >= m->n_ctx) { s.n_cycles++; break; }
         if (j < k) {
             or_model_rollback_to(m, j);
             m->pos = P + j + 2;

@@ -512,19 +512,26 @@ __global__ __launch_bounds__(4 * ATT_HD) void k_attn_combine_act(const float *q,
                xs + (uint64_t)a * XS_FLOATS + (uint64_t)h * 16, active);
 }
 
+// The span-partial workspace is sized for the largest span count (ATT_NSPAN), so
+// one reservation serves every later context length of that head count.  A
+// larger head count (another model) takes a new buffer; the old one is kept,
+// not freed, because HIP graphs captured earlier hold its address.
+static void *ws_attn_retired[16];
+static int n_ws_attn_retired = 0;
+
 static int attn_ws(int ctx_bound, int n_kv, int *nspan)
 {
     const int nt = (ctx_bound + ATT_TP - 1) / ATT_TP;
     *nspan = nt < ATT_NSPAN ? nt : ATT_NSPAN;
-    const size_t need = (size_t)n_kv * *nspan * ATT_MAXQ * (2 + ATT_HD) * sizeof(float);
+    const size_t need = (size_t)n_kv * ATT_NSPAN * ATT_MAXQ * (2 + ATT_HD) * sizeof(float);
     if (need > qg::ws_attn_bytes) {
+        void *p = nullptr;
+        QG_CHECK(hipMalloc(&p, need));
         if (qg::ws_attn) {
-            QG_CHECK(hipStreamSynchronize(qg::stream));
-            QG_CHECK(hipFree(qg::ws_attn));
+            if (n_ws_attn_retired < 16) ws_attn_retired[n_ws_attn_retired++] = qg::ws_attn;
+            // (beyond 16 retired buffers the oldest addresses are simply kept allocated)
         }
-        qg::ws_attn = nullptr;
-        qg::ws_attn_bytes = 0;
-        QG_CHECK(hipMalloc(&qg::ws_attn, need));
+        qg::ws_attn = p;
         qg::ws_attn_bytes = need;
     }
     return QGPU_OK;

@@ -167,7 +167,7 @@ extern "C" int qgpu_graph_end(void **exec)
     QG_CHECK(hipStreamEndCapture(qg::stream, &g));
     hipGraphExec_t e;
     hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     QG_CHECK(err);
     *exec = (void *)e;
     return QGPU_OK;
@@ -192,12 +192,12 @@ static int make_tensor(const void *dev_raw, int type, uint64_t ne0, uint64_t ne1
         hipError_t e = hipMalloc(&t->data, t->bytes);
         if (e != hipSuccess) { delete t; return (int)e; }
         int rc = qg_repack(type, dev_raw, ne0, ne1, t->data, 0);
-        if (rc) { hipFree(t->data); delete t; return rc; }
+        if (rc) { (void)hipFree(t->data); delete t; return rc; }
     } else {
         t->bytes = t->algo_bytes;
         hipError_t e = hipMalloc(&t->data, t->bytes);
         if (e == hipSuccess) e = hipMemcpyAsync(t->data, dev_raw, t->bytes, hipMemcpyDeviceToDevice, qg::stream);
-        if (e != hipSuccess) { hipFree(t->data); delete t; return (int)e; }
+        if (e != hipSuccess) { (void)hipFree(t->data); delete t; return (int)e; }
     }
     *out = t;
     return QGPU_OK;
@@ -221,10 +221,10 @@ extern "C" int qgpu_tensor_upload(const void *host, int type, uint64_t ne0, uint
     void *tmp = nullptr;
     QG_CHECK(hipMalloc(&tmp, n));
     hipError_t e = hipMemcpyAsync(tmp, host, n, hipMemcpyHostToDevice, qg::stream);
-    if (e != hipSuccess) { hipFree(tmp); return (int)e; }
+    if (e != hipSuccess) { (void)hipFree(tmp); return (int)e; }
     rc = make_tensor(tmp, type, ne0, ne1, out);
     hipError_t s = hipStreamSynchronize(qg::stream);
-    hipFree(tmp);
+    (void)hipFree(tmp);
     if (rc) return rc;
     return qg::check(s);
 }
@@ -247,7 +247,7 @@ extern "C" int qgpu_tensor_download(const qgpu_tensor *t, void *host)
     QG_CHECK(hipMalloc(&tmp, t->algo_bytes));
     rc = qg_repack(t->type, tmp, t->ne0, t->ne1, t->data, 1);
     if (!rc) rc = qgpu_memcpy_d2h(host, tmp, t->algo_bytes);
-    hipFree(tmp);
+    (void)hipFree(tmp);
     return rc;
 }
 

@@ -2,11 +2,12 @@
  * gguf.c -- GGUF v2/v3 reader (mmap, zero copy) filling qwen_config_t from
  * "<arch>.*" keys.  Implements include/gguf.h; replaces the reference
  * gguf.c:84-317 with the same acceptance rules (magic, version 2..3,
- * tensor_count in 1..100000, n_dims <= 4, exact key types, tensor offsets
- * inside the file, vocab fallback from token_embd).
+ * tensor_count in 1..100000, n_dims <= 4, exact key types, vocab fallback
+ * from token_embd), and checks that every tensor's bytes lie inside the file.
  */
 #define _POSIX_C_SOURCE 200809L
 #include "gguf.h"
+#include "quant.h"
 #include <fcntl.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -203,9 +204,19 @@ int gguf_open(gguf_context_t *g, const char *path)
     why = "data section outside file";
     if (base >= g->file_size) goto fail;
     g->data_base = (const uint8_t *)map + base;
+    const uint64_t avail = g->file_size - base;
     for (uint64_t i = 0; i < g->tensor_count; i++) {
         gguf_tensor_info_t *t = &g->tensors[i];
-        if (t->offset >= g->file_size - base) goto fail;
+        if (t->offset >= avail) goto fail;
+        /* the whole tensor must lie in the file (types without a known row size
+         * are only checked for their start; nothing here can compute on them) */
+        const uint64_t rb = quant_row_bytes(t->type, t->ne[0]);
+        uint64_t rows = 1;
+        for (uint32_t d = 1; d < t->n_dims; d++) {
+            if (t->ne[d] && rows > UINT64_MAX / t->ne[d]) goto fail;
+            rows *= t->ne[d];
+        }
+        if (rb && (rows > (avail - t->offset) / rb)) goto fail;
         t->data = (const uint8_t *)g->data_base + t->offset;
     }
     if (!g->config.vocab_size) {

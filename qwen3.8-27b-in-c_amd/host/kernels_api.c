@@ -13,11 +13,20 @@ typedef struct { const void *key; uint64_t ne0, ne1; int type; qgpu_tensor *t; }
 static wentry *g_w;
 static size_t g_nw, g_cap;
 
-static void die(const char *what, int rc)
+/* The reference functions return nothing and write zeros for a weight type
+ * they do not support (kernels.c:596).  Here any failure (unsupported type,
+ * allocation, device error) is reported once on stderr, leaves zeros in the
+ * requested outputs, and is kept for kernels_status(). */
+static int g_status;
+
+static int fail(const char *what, int rc)
 {
-    fprintf(stderr, "qwen gpu: %s failed: %s\n", what, qgpu_strerror(rc));
-    abort();
+    if (!g_status) fprintf(stderr, "qwen gpu: %s failed: %s\n", what, qgpu_strerror(rc));
+    g_status = rc ? rc : QGPU_E_ARG;
+    return -1;
 }
+
+int kernels_status(void) { return g_status; }
 
 static qgpu_tensor *weight(const gguf_tensor_info_t *W)
 {
@@ -27,10 +36,12 @@ static qgpu_tensor *weight(const gguf_tensor_info_t *W)
     qgpu_tensor *t = NULL;
     const uint64_t rows = W->n_dims >= 2 ? W->ne[1] : 1;
     int rc = qgpu_tensor_upload(W->data, (int)W->type, W->ne[0], rows, &t);
-    if (rc) die("weight upload", rc);
+    if (rc) { fail("weight upload", rc); return NULL; }
     if (g_nw == g_cap) {
+        wentry *nw = realloc(g_w, (g_cap ? 2 * g_cap : 64) * sizeof *g_w);
+        if (!nw) { qgpu_tensor_free(t); fail("host allocation", QGPU_E_ARG); return NULL; }
+        g_w = nw;
         g_cap = g_cap ? 2 * g_cap : 64;
-        g_w = realloc(g_w, g_cap * sizeof *g_w);
     }
     g_w[g_nw++] = (wentry){ W->data, W->ne[0], rows, (int)W->type, t };
     return t;
@@ -51,8 +62,10 @@ static float *dev_buf(int slot, size_t bytes)
     static size_t cap[4];
     if (bytes > cap[slot]) {
         if (p[slot]) qgpu_free(p[slot]);
+        p[slot] = NULL;
+        cap[slot] = 0;
         int rc = qgpu_malloc((void **)&p[slot], bytes);
-        if (rc) die("device allocation", rc);
+        if (rc) { p[slot] = NULL; fail("device allocation", rc); return NULL; }
         cap[slot] = bytes;
     }
     return p[slot];
@@ -63,38 +76,47 @@ static float *stage_x(const float *x, uint64_t ldx, int n, uint64_t ne0, uint64_
 {
     const uint64_t ld = (ne0 + 3) & ~(uint64_t)3;
     float *d = dev_buf(0, (size_t)n * ld * sizeof(float));
+    if (!d) return NULL;
     if (ld == ldx && ld == ne0) {
         int rc = qgpu_memcpy_h2d(d, x, (size_t)n * ld * sizeof(float));
-        if (rc) die("copy to device", rc);
+        if (rc) { fail("copy to device", rc); return NULL; }
     } else {
         for (int t = 0; t < n; t++) {
             int rc = qgpu_memcpy_h2d(d + (size_t)t * ld, x + (size_t)t * ldx, ne0 * sizeof(float));
-            if (rc) die("copy to device", rc);
+            if (rc) { fail("copy to device", rc); return NULL; }
         }
     }
     *ld_dev = ld;
     return d;
 }
 
+static void zero_out(float *out, uint64_t ldo, int n, uint64_t r0, uint64_t r1)
+{
+    for (int t = 0; t < n; t++) memset(out + (size_t)t * ldo + r0, 0, (r1 - r0) * sizeof(float));
+}
+
 static void fetch_out(float *out, uint64_t ldo, const float *dout, uint64_t rows, int n, uint64_t r0, uint64_t r1)
 {
     for (int t = 0; t < n; t++) {
         int rc = qgpu_memcpy_d2h(out + (size_t)t * ldo + r0, dout + (size_t)t * rows + r0, (r1 - r0) * sizeof(float));
-        if (rc) die("copy to host", rc);
+        if (rc) { fail("copy to host", rc); zero_out(out, ldo, n, r0, r1); return; }
     }
 }
 
 void gemv_rows_batch(const gguf_tensor_info_t *W, const float *x, uint64_t ldx, int n, float *out, uint64_t ldo,
                      uint64_t r0, uint64_t r1)
 {
-    if (r1 <= r0 || n < 1) return;
+    const uint64_t rows = W && W->n_dims >= 2 ? W->ne[1] : 1;
+    if (!W || r1 <= r0 || n < 1) return;
+    if (n > GEMV_MAX_B || r1 > rows) { fail("gemv (batch above 8 or rows past the matrix)", QGPU_E_ARG); return; }
     qgpu_tensor *T = weight(W);
-    uint64_t ld;
+    if (!T) { zero_out(out, ldo, n, r0, r1); return; }
+    uint64_t ld = 0;
     const float *dx = stage_x(x, ldx, n, W->ne[0], &ld);
-    float *dout = dev_buf(1, (size_t)n * W->ne[1] * sizeof(float));
-    int rc = qgpu_gemv_rows_batch(T, dx, ld, n, dout, W->ne[1], r0, r1);
-    if (rc) die("gemv", rc);
-    fetch_out(out, ldo, dout, W->ne[1], n, r0, r1);
+    float *dout = dx ? dev_buf(1, (size_t)n * rows * sizeof(float)) : NULL;
+    int rc = dout ? qgpu_gemv_rows_batch(T, dx, ld, n, dout, rows, r0, r1) : QGPU_E_ARG;
+    if (rc) { if (dout) fail("gemv", rc); zero_out(out, ldo, n, r0, r1); return; }
+    fetch_out(out, ldo, dout, rows, n, r0, r1);
 }
 
 void gemv_rows(const gguf_tensor_info_t *W, const float *x, float *out, uint64_t r0, uint64_t r1)
@@ -133,10 +155,11 @@ static void run_rows(int op, float *out, const float *x, const float *w, uint64_
 {
     if (!n) return;
     float *d = dev_buf(2, n * sizeof(float) * 2);
+    if (!d) return;
     float *dw = d + n;
     int rc = qgpu_memcpy_h2d(d, x, n * sizeof(float));
     if (!rc && w) rc = qgpu_memcpy_h2d(dw, w, n * sizeof(float));
-    if (rc) die("copy to device", rc);
+    if (rc) { fail("copy to device", rc); return; }
     switch (op) {
     case 0: rc = qgpu_rmsnorm(d, n, d, n, w ? dw : NULL, n, 1, eps); break;
     case 1: rc = qgpu_l2norm(d, n, d, n, n, 1, eps); break;
@@ -145,9 +168,9 @@ static void run_rows(int op, float *out, const float *x, const float *w, uint64_
     case 4: rc = qgpu_softplus(d, n); break;
     default: rc = qgpu_softmax(d, n, n, 1); break;
     }
-    if (rc) die("op", rc);
+    if (rc) { fail("op", rc); return; }
     rc = qgpu_memcpy_d2h(out, d, n * sizeof(float));
-    if (rc) die("copy to host", rc);
+    if (rc) fail("copy to host", rc);
 }
 
 void rmsnorm(float *out, const float *x, const float *weight, uint64_t n, float eps) { run_rows(0, out, x, weight, n, eps); }

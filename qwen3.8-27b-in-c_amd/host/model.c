@@ -56,6 +56,7 @@ struct qwen_gpu {
      * (kind, token pointer, hidden-state pointer, logits pointer, B, flag) */
     int use_graphs, n_graphs;
     struct { int kind, flag; uint32_t B; const void *tok, *h, *lg; void *exec; } graphs[48];
+    int status;               /* of the last call: 0, -1 rejected on the host, -2 device error */
     void **allocs;
     size_t n_allocs, cap_allocs;
     qgpu_tensor **tensors;
@@ -69,12 +70,43 @@ static double now_s(void)
     return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
 }
 
+/* The first device error is sticky: it is reported once, every later device
+ * call is skipped, and the public entry points then do nothing (status -2).
+ * A failed launch or a device fault leaves the HIP context unusable, so the
+ * model stops rather than compute on it; the caller's process goes on. */
+static int qwen_dev_err;
+
 static void fail_rc(const char *what, int rc)
 {
-    fprintf(stderr, "qwen gpu: %s failed: %s\n", what, qgpu_strerror(rc));
-    abort();
+    if (!qwen_dev_err)
+        fprintf(stderr, "qwen gpu: %s failed: %s (the model accepts no further calls)\n", what, qgpu_strerror(rc));
+    qwen_dev_err = rc ? rc : -1;
 }
-#define K(call) do { int _rc = (call); if (_rc) fail_rc(#call, _rc); } while (0)
+#define K(call) do { if (!qwen_dev_err) { int _rc = (call); if (_rc) fail_rc(#call, _rc); } } while (0)
+
+/* entry and exit of every public call: status 0 / -1 (rejected) / -2 (device error) */
+static int call_begin(qwen_model_t *m)
+{
+    if (!m || !m->gpu) return -1;
+    m->gpu->status = qwen_dev_err ? -2 : 0;
+    return qwen_dev_err ? -1 : 0;
+}
+static void call_end(qwen_model_t *m)
+{
+    if (qwen_dev_err) m->gpu->status = -2;
+}
+static int reject(qwen_model_t *m, const char *fn, uint32_t pos, uint32_t B)
+{
+    fprintf(stderr, "%s: positions %u..%u outside the context (n_ctx = %u) or batch %u outside 1..%d; call ignored\n",
+            fn, pos, pos + B - 1, m->n_ctx, B, SPEC_MAX_B);
+    m->gpu->status = -1;
+    return -1;
+}
+/* pos .. pos+B-1 must be KV rows of the cache (the device writes row pos+b) */
+static int bad_span(const qwen_model_t *m, uint32_t pos, uint32_t B)
+{
+    return B < 1 || B > SPEC_MAX_B || pos >= m->n_ctx || B > m->n_ctx - pos;
+}
 
 /* ------------------------------------------------------------------ allocation */
 static void *dalloc(qwen_gpu_t *g, size_t bytes)
@@ -256,7 +288,7 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     /* shapes the GPU kernels are written for */
     if (d->head_k_dim != 128 || d->head_dim != 256 || d->d_conv != 4 || c->rope_dim_count > d->head_dim ||
         d->n_embd % 256 || d->n_ff % 256 || !d->n_kv_head || d->n_head % d->n_kv_head ||
-        (d->n_head / d->n_kv_head) * MAXB > 64 || d->d_inner > d->n_ff) {
+        (d->n_head / d->n_kv_head) * MAXB > 48 || d->d_inner > d->n_ff) {
         fprintf(stderr, "model_init: dimensions outside what the GPU kernels support\n");
         return -1;
     }
@@ -291,9 +323,11 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
             bad1(m->mtp_hnorm, d->n_embd, "nextn.hnorm") || bad1(m->mtp_shnorm, d->n_embd, "nextn.shared_head_norm"))
             return -1;
     }
+    if (n_ctx < 2) { fprintf(stderr, "model_init: n_ctx must be at least 2\n"); return -1; }
     m->n_ctx = n_ctx;
     m->pos = 0;
 
+    if (qwen_dev_err) { fprintf(stderr, "model_init: an earlier device error is pending\n"); return -1; }
     if (qgpu_init(0)) { fprintf(stderr, "model_init: no GPU\n"); return -1; }
     qwen_gpu_t *g = calloc(1, sizeof *g);
     m->gpu = g;
@@ -350,6 +384,7 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     /* RoPE tables with the reference's own expressions (model.c:186-201) */
     const uint32_t half = c->rope_dim_count / 2;
     float *cs = malloc((size_t)n_ctx * half * sizeof(float)), *sn = malloc((size_t)n_ctx * half * sizeof(float));
+    if (!cs || !sn) { free(cs); free(sn); return -1; }
     for (uint32_t p = 0; p < n_ctx; p++)
         for (uint32_t i = 0; i < half; i++) {
             const float angle = (float)p * powf(c->rope_theta, -2.0f * (float)i / (float)c->rope_dim_count);
@@ -361,16 +396,39 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     int rc = (!g->rope_cos || !g->rope_sin) ? -1 :
              (qgpu_memcpy_h2d(g->rope_cos, cs, (size_t)n_ctx * half * sizeof(float)) ||
               qgpu_memcpy_h2d(g->rope_sin, sn, (size_t)n_ctx * half * sizeof(float)));
-    free(cs);
-    free(sn);
+    m->rope_cos = cs;                          /* host copies (reference field names) */
+    m->rope_sin = sn;
     if (rc || qgpu_attn_reserve((int)n_ctx, (int)d->n_kv_head)) return -1;
-    /* host-side result fields */
-    m->mtp_h = calloc(E, sizeof(float));
-    m->x = calloc(E, sizeof(float));
-    m->logits = calloc(V, sizeof(float));
-    m->logits_b = calloc(MAXB * V, sizeof(float));
-    m->h_save = calloc(MAXB * E, sizeof(float));
-    if (!m->mtp_h || !m->x || !m->logits || !m->logits_b || !m->h_save) return -1;
+    /* host-side fields, laid out as the reference's arenas (model.c:166-230) */
+    {
+        const uint64_t sq = g->SQ > F ? g->SQ : F, kvs = 2ull * d->n_kv_head * d->head_dim;
+        const uint64_t hd = (uint64_t)d->n_head * d->head_dim;
+        float *p = m->arena = calloc(2 * E + sq + kvs + d->d_inner + F + hd + V + (uint64_t)d->n_head * n_ctx,
+                                     sizeof(float));
+        if (!p) return -1;
+        m->x = p; p += E;
+        m->xb = p; p += E;
+        m->qkv = p; p += sq;
+        m->kv_small = p; p += kvs;
+        m->z = p; p += d->d_inner;
+        m->ffn_buf = p; p += F;
+        m->attn_out = p; p += hd;
+        m->logits = p; p += V;
+        m->scores = p;
+        p = m->arena_b = calloc(MAXB * (2 * E + F + kvs + d->d_inner + F + hd + E), sizeof(float));
+        if (!p) return -1;
+        m->bx = p; p += MAXB * E;
+        m->bxb = p; p += MAXB * E;
+        m->bqkv = p; p += MAXB * F;
+        m->bkv = p; p += MAXB * kvs;
+        m->bz = p; p += MAXB * (uint64_t)d->d_inner;
+        m->bffn = p; p += MAXB * F;
+        m->battn_out = p; p += MAXB * hd;
+        m->h_save = p;
+        m->logits_b = calloc(MAXB * V, sizeof(float));
+        m->mtp_h = calloc(E, sizeof(float));
+        if (!m->logits_b || !m->mtp_h) return -1;
+    }
     m->host_sync = 1;
     g->cur = g->cur_base = 0;
     if (qgpu_sync()) return -1;
@@ -428,7 +486,7 @@ void model_free(qwen_model_t *m)
     if (!m) return;
     gpu_free(m->gpu);
     free(m->layers);
-    free(m->mtp_h); free(m->x); free(m->logits); free(m->logits_b); free(m->h_save);
+    free(m->arena); free(m->arena_b); free(m->logits_b); free(m->mtp_h); free(m->rope_cos); free(m->rope_sin);
     if (m->gguf.fd >= 0 || m->gguf.mmap_data) gguf_close(&m->gguf);
     else free(m->gguf.tensors);
     memset(m, 0, sizeof *m);
@@ -680,6 +738,13 @@ static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, 
 }
 
 /* ------------------------------------------------------------------ reference API */
+static int bad_tokens(const qwen_model_t *m, const uint32_t *tokens, uint32_t B)
+{
+    for (uint32_t b = 0; b < B; b++)
+        if (tokens[b] >= m->cfg.vocab_size) return 1;
+    return 0;
+}
+
 static void put_tokens(qwen_model_t *m, const uint32_t *tokens, uint32_t B)
 {
     K(qgpu_memcpy_h2d(m->gpu->d_tok, tokens, B * sizeof(uint32_t)));
@@ -688,6 +753,8 @@ static void put_tokens(qwen_model_t *m, const uint32_t *tokens, uint32_t B)
 void model_forward(qwen_model_t *m, pool_t *pool, uint32_t token, uint32_t pos)
 {
     (void)pool;
+    if (call_begin(m)) return;
+    if (bad_span(m, pos, 1) || token >= m->cfg.vocab_size) { reject(m, "model_forward", pos, 1); return; }
     const double t0 = now_s();
     put_tokens(m, &token, 1);
     forward_dev(m, m->gpu->d_tok, 1, pos, m->gpu->logits1, 0);
@@ -698,13 +765,15 @@ void model_forward(qwen_model_t *m, pool_t *pool, uint32_t token, uint32_t pos)
     qwen_prof_head += now_s() - t0;
     qwen_prof_calls++;
     m->pos = pos + 1;
+    call_end(m);
 }
 
 void model_forward_batch(qwen_model_t *m, pool_t *pool, const uint32_t *tokens, uint32_t pos, uint32_t B, int ckpt)
 {
     (void)pool;
     (void)ckpt;
-    if (B < 1 || B > MAXB) { fprintf(stderr, "model_forward_batch: B=%u outside 1..%d\n", B, MAXB); abort(); }
+    if (call_begin(m)) return;
+    if (!tokens || bad_span(m, pos, B) || bad_tokens(m, tokens, B)) { reject(m, "model_forward_batch", pos, B); return; }
     put_tokens(m, tokens, B);
     forward_dev(m, m->gpu->d_tok, B, pos, m->gpu->logits_b, 1);
     if (m->host_sync) {
@@ -712,10 +781,12 @@ void model_forward_batch(qwen_model_t *m, pool_t *pool, const uint32_t *tokens, 
         K(qgpu_memcpy_d2h(m->h_save, m->gpu->h_save, (size_t)B * m->dims.n_embd * sizeof(float)));
     }
     m->pos = pos + B;
+    call_end(m);
 }
 
 void model_reset(qwen_model_t *m)
 {
+    if (call_begin(m)) return;
     qwen_gpu_t *g = m->gpu;
     for (uint32_t il = 0; il < m->dims.n_layer; il++) {
         const glayer_t *D = &g->L[il];
@@ -730,6 +801,7 @@ void model_reset(qwen_model_t *m)
     K(qgpu_set_i32(g->d_pos, 0));
     K(qgpu_sync());
     m->pos = 0;
+    call_end(m);
 }
 
 int model_snapshot_states(qwen_model_t *m) { (void)m; return 0; }
@@ -737,14 +809,19 @@ void model_rollback_states(qwen_model_t *m) { (void)m; }
 
 void model_rollback_to(qwen_model_t *m, uint32_t b)
 {
+    if (call_begin(m)) return;
+    if (b >= SPEC_MAX_B) { reject(m, "model_rollback_to", b, 1); return; }
     qwen_gpu_t *g = m->gpu;
     g->cur = (g->cur_base + 1 + (int)b) % NSLOT;
     K(qgpu_set_i32(g->d_cur, g->cur));
+    call_end(m);
 }
 
 int mtp_forward(qwen_model_t *m, pool_t *pool, uint32_t token, uint32_t pos, int want_logits)
 {
     (void)pool;
+    if (call_begin(m)) return -1;
+    if (bad_span(m, pos, 1) || token >= m->cfg.vocab_size) return reject(m, "mtp_forward", pos, 1);
     qwen_gpu_t *g = m->gpu;
     const uint64_t E = m->dims.n_embd;
     if (m->host_sync) K(qgpu_memcpy_h2d(g->mtp_h, m->mtp_h, E * sizeof(float)));
@@ -754,15 +831,17 @@ int mtp_forward(qwen_model_t *m, pool_t *pool, uint32_t token, uint32_t pos, int
         K(qgpu_memcpy_d2h(m->mtp_h, g->mtp_h, E * sizeof(float)));
         if (want_logits) K(qgpu_memcpy_d2h(m->logits, g->logits1, (size_t)m->cfg.vocab_size * sizeof(float)));
     }
-    return 0;
+    call_end(m);
+    return g->status;
 }
 
 int mtp_forward_batch(qwen_model_t *m, pool_t *pool, const uint32_t *tokens, uint32_t pos, uint32_t B,
                       int want_logits)
 {
     (void)pool;
+    if (call_begin(m)) return -1;
+    if (!tokens || bad_span(m, pos, B) || bad_tokens(m, tokens, B)) return reject(m, "mtp_forward_batch", pos, B);
     qwen_gpu_t *g = m->gpu;
-    if (B < 1 || B > MAXB) return -1;
     put_tokens(m, tokens, B);
     mtp_dev(m, g->d_tok, g->h_save, B, pos, want_logits ? g->logits_b : NULL);
     if (m->host_sync) {
@@ -770,7 +849,8 @@ int mtp_forward_batch(qwen_model_t *m, pool_t *pool, const uint32_t *tokens, uin
         if (want_logits)
             K(qgpu_memcpy_d2h(m->logits_b, g->logits_b, (size_t)B * m->cfg.vocab_size * sizeof(float)));
     }
-    return 0;
+    call_end(m);
+    return g->status;
 }
 
 uint32_t model_sample_greedy(const float *logits, uint32_t vocab_size)
@@ -785,6 +865,8 @@ uint32_t model_sample_greedy(const float *logits, uint32_t vocab_size)
 void attention_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool, uint32_t pos)
 {
     (void)pool;
+    if (call_begin(m)) return;
+    if (bad_span(m, pos, 1) || !L || L->is_recurrent) { reject(m, "attention_layer", pos, 1); return; }
     qwen_gpu_t *g = m->gpu;
     glayer_t *D = (L == &m->mtp_layer) ? &g->mtp : &g->L[L - m->layers];
     K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
@@ -792,11 +874,17 @@ void attention_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool, uint32_t po
     attn_dev(m, D, g->bx, 1, pos);
     materialize(m);
     K(qgpu_memcpy_d2h(m->x, g->bx, m->dims.n_embd * sizeof(float)));
+    call_end(m);
 }
 
 void gdn_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool)
 {
     (void)pool;
+    if (call_begin(m)) return;
+    if (!L || !L->is_recurrent || L < m->layers || L >= m->layers + m->dims.n_layer) {
+        reject(m, "gdn_layer", 0, 1);
+        return;
+    }
     qwen_gpu_t *g = m->gpu;
     K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
     glayer_t *D = &g->L[L - m->layers];
@@ -810,6 +898,7 @@ void gdn_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool)
     K(qgpu_copy(D->ssm_ring + (size_t)g->cur * g->ssm_elems, D->ssm_ring + (size_t)nxt * g->ssm_elems,
                 g->ssm_elems * sizeof(float)));
     K(qgpu_memcpy_d2h(m->x, g->bx, m->dims.n_embd * sizeof(float)));
+    call_end(m);
 }
 
 /* ------------------------------------------------------------------ device-resident generation */
@@ -835,35 +924,40 @@ static uint32_t prefill_dev(qwen_model_t *m, const uint32_t *prompt, uint32_t n,
 
 int model_spec_begin(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t k)
 {
-    if (!m || !m->gpu || !prompt || n_prompt < 1 || n_prompt >= m->n_ctx) return -1;
+    if (call_begin(m)) return -1;
+    if (!prompt || n_prompt < 1 || n_prompt >= m->n_ctx || bad_tokens(m, prompt, n_prompt))
+        return reject(m, "model_spec_begin", 0, n_prompt);
     prefill_dev(m, prompt, n_prompt, k > 0);
     K(qgpu_sync());
-    return 0;
+    call_end(m);
+    return m->gpu->status;
 }
 
 uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_accept, uint32_t max_cycles,
                         uint32_t max_tokens, uint32_t *out, uint32_t *cycle_j, qwen_gen_stats_t *st)
 {
+    qwen_gen_stats_t s;
+    memset(&s, 0, sizeof s);
+    if (st) *st = s;
+    if (call_begin(m)) return 0;
+    if (!out && max_tokens) { reject(m, "model_spec_run", m->pos, 1); return 0; }
     qwen_gpu_t *g = m->gpu;
     const uint32_t V = m->cfg.vocab_size;
     const uint64_t E = m->dims.n_embd;
-    qwen_gen_stats_t s;
-    memset(&s, 0, sizeof s);
     if (k > SPEC_MAX_B - 1) k = SPEC_MAX_B - 1;
     const double t0 = now_s();
-    uint32_t gen = 0;
-    uint32_t acc[24], next0;
+    uint32_t gen = 0, kk = 0, j = 0;
+    uint32_t acc[24] = { 0 }, next0 = 0;
     K(qgpu_memcpy_d2h(&next0, g->d_cand, sizeof next0));          /* argmax of the last verified row */
-    while (gen < max_tokens && s.n_cycles < max_cycles && m->pos >= 1) {
+    while (!qwen_dev_err && gen < max_tokens && s.n_cycles < max_cycles && m->pos >= 1 && m->pos < m->n_ctx) {
         const uint32_t P = m->pos - 1;
-        const uint32_t room = m->n_ctx - 1 - P;
-        if (room < 1) break;
-        const uint32_t kk = k < room - 1 ? k : room - 1;
+        const uint32_t room = m->n_ctx - 1 - P;                    /* >= 1: pos < n_ctx */
+        kk = k < room - 1 ? k : room - 1;
         if (next0 == eos) break;                                   /* main.c:179 */
         /* drafts: cand[s] = argmax MTP(cand[s-1], P+s) (main.c:182-185) */
-        for (uint32_t j = 1; j <= kk; j++) {
-            mtp_dev(m, g->d_cand + (j - 1), g->mtp_h, 1, P + j, g->logits1);
-            K(qgpu_argmax(g->logits1, V, V, 1, g->d_cand + j));
+        for (uint32_t d = 1; d <= kk; d++) {
+            mtp_dev(m, g->d_cand + (d - 1), g->mtp_h, 1, P + d, g->logits1);
+            K(qgpu_argmax(g->logits1, V, V, 1, g->d_cand + d));
         }
         /* batched verification (main.c:189) and argmax of every row */
         forward_dev(m, g->d_cand, kk + 1, P + 1, g->logits_b, 1);
@@ -874,23 +968,33 @@ uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_acc
         const int force_j = force_accept == 1 ? (int)kk : force_accept == 2 ? (int)(s.n_cycles % (kk + 1)) : -1;
         K(qgpu_spec_accept(g->d_cand, g->d_vtok, (int)kk, force_j, g->d_pos, g->d_cur, NSLOT, g->d_acc));
         K(qgpu_memcpy_d2h(acc, g->d_acc, (kk + 3) * sizeof(uint32_t)));
-        const uint32_t j = acc[0];
+        if (qwen_dev_err) break;
+        j = acc[0] <= kk ? acc[0] : kk;
         g->cur = (g->cur_base + 1 + (int)j) % NSLOT;
         if (cycle_j) cycle_j[s.n_cycles] = j;
         for (uint32_t i = 0; i <= j && gen < max_tokens; i++) out[gen++] = acc[1 + i];
         s.n_accepted += j;
         s.n_drafts += kk;
         s.n_cycles++;
+        /* the verify left the position at P+kk+2: the reference stops there once it
+         * reaches the context end, before any rollback (main.c:210) */
+        if (P + kk + 2 >= m->n_ctx) { m->pos = P + kk + 2; break; }
         m->pos = P + j + 2;
-        if (m->pos >= m->n_ctx) break;
         /* MTP re-anchor on the backbone hidden state of the last accepted token (main.c:220-222) */
         if (k > 0) mtp_dev(m, g->d_cand + j, g->h_save + (size_t)j * E, 1, P + j + 1, NULL);
         K(qgpu_memcpy_d2d(g->d_cand, g->d_acc + j + 2, sizeof(uint32_t)));   /* next cand[0] = argmax logits_b[j] */
         next0 = acc[j + 2];
     }
     K(qgpu_sync());
+    if (m->host_sync && s.n_cycles) {
+        /* the last verify's rows (row j starts the next cycle) and the MTP state */
+        K(qgpu_memcpy_d2h(m->logits_b, g->logits_b, (size_t)(kk + 1) * V * sizeof(float)));
+        K(qgpu_memcpy_d2h(m->h_save, g->h_save, (size_t)(kk + 1) * E * sizeof(float)));
+        K(qgpu_memcpy_d2h(m->mtp_h, g->mtp_h, E * sizeof(float)));
+    }
     s.t_decode_s = now_s() - t0;
     if (st) *st = s;
+    call_end(m);
     return gen;
 }
 
@@ -899,6 +1003,7 @@ uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n
                              qwen_gen_stats_t *st)
 {
     const double t0 = now_s();
+    if (st) memset(st, 0, sizeof *st);
     if (model_spec_begin(m, prompt, n_prompt, k)) return 0;
     const double t_prefill = now_s() - t0;
     const uint32_t n = model_spec_run(m, k, eos, force_accept, UINT32_MAX, n_predict, out, cycle_j, st);
@@ -909,20 +1014,25 @@ uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n
 uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
                                uint32_t eos, uint32_t *out, qwen_gen_stats_t *st)
 {
-    qwen_gpu_t *g = m->gpu;
-    const uint32_t V = m->cfg.vocab_size;
     qwen_gen_stats_t s;
     memset(&s, 0, sizeof s);
-    if (n_prompt < 1 || n_prompt >= m->n_ctx) return 0;
+    if (st) *st = s;
+    if (call_begin(m)) return 0;
+    if (!prompt || !out || n_prompt < 1 || n_prompt >= m->n_ctx || n_predict < 1 || bad_tokens(m, prompt, n_prompt)) {
+        reject(m, "model_generate_greedy", 0, n_prompt);
+        return 0;
+    }
+    qwen_gpu_t *g = m->gpu;
+    const uint32_t V = m->cfg.vocab_size;
     double t0 = now_s();
     prefill_dev(m, prompt, n_prompt, 0);
     K(qgpu_sync());
     s.t_prefill_s = now_s() - t0;
     t0 = now_s();
-    uint32_t gen = 0, cur;
+    uint32_t gen = 0, cur = 0;
     K(qgpu_memcpy_d2h(&cur, g->d_cand, sizeof cur));
     out[gen++] = cur;
-    while (gen < n_predict && cur != eos && m->pos < m->n_ctx) {
+    while (!qwen_dev_err && gen < n_predict && cur != eos && m->pos < m->n_ctx) {
         forward_dev(m, g->d_cand, 1, m->pos, g->logits1, 0);
         K(qgpu_argmax(g->logits1, V, V, 1, g->d_cand));
         K(qgpu_memcpy_d2h(&cur, g->d_cand, sizeof cur));
@@ -933,6 +1043,7 @@ uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t
     K(qgpu_sync());
     s.t_decode_s = now_s() - t0;
     if (st) *st = s;
+    call_end(m);
     return gen;
 }
 
@@ -940,10 +1051,15 @@ uint32_t model_generate_sample(qwen_model_t *m, const uint32_t *prompt, uint32_t
                                float temp, float top_p, uint32_t top_k, float repeat_penalty, uint64_t seed,
                                uint32_t eos, uint32_t *out, qwen_gen_stats_t *st)
 {
-    qwen_gpu_t *g = m ? m->gpu : NULL;
     qwen_gen_stats_t s;
     memset(&s, 0, sizeof s);
-    if (!g || !prompt || !out || n_prompt < 1 || n_prompt >= m->n_ctx || n_predict < 1) return 0;
+    if (st) *st = s;
+    if (call_begin(m)) return 0;
+    if (!prompt || !out || n_prompt < 1 || n_prompt >= m->n_ctx || n_predict < 1 || bad_tokens(m, prompt, n_prompt)) {
+        reject(m, "model_generate_sample", 0, n_prompt);
+        return 0;
+    }
+    qwen_gpu_t *g = m->gpu;
     const uint32_t V = m->cfg.vocab_size;
     /* the fields sampler_init sets (sampler.c:46-56) */
     if (!top_k) top_k = 40;
@@ -966,7 +1082,7 @@ uint32_t model_generate_sample(qwen_model_t *m, const uint32_t *prompt, uint32_t
     /* main.c:233-246: sample from the last logits, forward the token, sample again */
     float *lg = g->logits_b + (size_t)(last - 1) * V;
     uint32_t gen = 0, cur = 0;
-    for (;;) {
+    while (!qwen_dev_err) {
         K(qgpu_sample(lg, V, d_all, n_all, temp, top_p, top_k, repeat_penalty, last_n, d_rng, d_all + n_all));
         K(qgpu_memcpy_d2h(&cur, d_all + n_all, sizeof cur));
         n_all++;
@@ -982,13 +1098,15 @@ uint32_t model_generate_sample(qwen_model_t *m, const uint32_t *prompt, uint32_t
     K(qgpu_free(d_all));
     K(qgpu_free(d_rng));
     if (st) *st = s;
+    call_end(m);
     return gen;
 }
 
 int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, float *ms_decode, float *ms_draft)
 {
+    if (call_begin(m)) return -1;
+    if (bad_span(m, m->pos, B) || reps < 1 || !ms_verify || !ms_decode) return reject(m, "model_time_steps", m->pos, B);
     qwen_gpu_t *g = m->gpu;
-    if (B < 1 || B > MAXB || reps < 1 || m->pos + B >= m->n_ctx) return -1;
     const int cur0 = g->cur, base0 = g->cur_base;
     const uint32_t pos = m->pos;
     void *e0, *e1;
@@ -1034,7 +1152,8 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
     K(qgpu_sync());
     qgpu_event_destroy(e0);
     qgpu_event_destroy(e1);
-    return 0;
+    call_end(m);
+    return m->gpu->status;
 }
 
 /* ------------------------------------------------------------------ FFI helpers */
@@ -1059,5 +1178,6 @@ uint32_t qwen_model_get(const qwen_model_t *m, const char *name)
     return 0;
 }
 void qwen_model_set_pos(qwen_model_t *m, uint32_t pos) { m->pos = pos; }
+int qwen_model_status(const qwen_model_t *m) { return (m && m->gpu) ? m->gpu->status : -1; }
 void qwen_model_set_host_sync(qwen_model_t *m, int on) { m->host_sync = on; }
 void qwen_model_set_graphs(qwen_model_t *m, int on) { if (m && m->gpu) m->gpu->use_graphs = on ? 1 : 0; }

@@ -183,8 +183,9 @@ void qwen_synth_spec_27b(qwen_synth_spec_t *s, uint64_t seed)
     s->seed = seed;
 }
 
-void qwen_synth_spec_tiny(qwen_synth_spec_t *s, uint64_t seed, int mixed)
+void qwen_synth_spec_tiny(qwen_synth_spec_t *s, uint64_t seed, int variant)
 {
+    const int mixed = variant == 1;
     memset(s, 0, sizeof *s);
     s->n_embd = 256; s->n_ff = 2048; s->n_layer = 8;   /* n_ff >= max(conv_dim, 2*n_head*head_dim, 2*n_embd): the reference batch arenas use stride n_ff (model.c:207) */
     s->n_head = 4; s->n_kv_head = 2; s->head_dim = 256;
@@ -199,6 +200,11 @@ void qwen_synth_spec_tiny(qwen_synth_spec_t *s, uint64_t seed, int mixed)
     }
     s->gain_output = 4.0f;
     s->seed = seed;
+    if (variant == 2) {                  /* drafts that the backbone mostly accepts */
+        s->gain_embd = 5.0f;
+        s->mtp_diag = 1;
+        s->tie_shift = 1;
+    }
 }
 
 /* RMS of one decoded weight per unit d, per format (uniform random codes):
@@ -232,7 +238,9 @@ static uint32_t enumerate(const qwen_synth_spec_t *s, tdesc *d)
 #define ADD(NAME_FMT, IDX, ND, A, B, TY, KIND, GAIN) do { \
         if (d) { snprintf(d[n].name, GGUF_MAX_NAME, NAME_FMT, IDX); d[n].nd = ND; d[n].ne0 = A; \
                  d[n].ne1 = B; d[n].type = TY; d[n].kind = KIND; d[n].gain = GAIN; } n++; } while (0)
-    ADD("token_embd.weight%.0u", 0u, 2, E, V, pick(s->type_embd, T), K_MAT, 1.0f);
+    const float ge = s->gain_embd > 0.0f ? s->gain_embd : 1.0f;
+    const float gr = s->gain_resid > 0.0f ? s->gain_resid : 0.5f;
+    ADD("token_embd.weight%.0u", 0u, 2, E, V, pick(s->type_embd, T), K_MAT, ge);
     ADD("output_norm.weight%.0u", 0u, 1, E, 1, GGML_F32, K_NORM, 1.0f);
     ADD("output.weight%.0u", 0u, 2, E, V, pick(s->type_output, T), K_MAT, s->gain_output);
     for (uint32_t il = 0; il <= s->n_layer; il++) {
@@ -242,7 +250,7 @@ static uint32_t enumerate(const qwen_synth_spec_t *s, tdesc *d)
         ADD("blk.%u.post_attention_norm.weight", il, 1, E, 1, GGML_F32, K_NORM, 1.0f);
         ADD("blk.%u.ffn_gate.weight", il, 2, E, F, T, K_MAT, 1.0f);
         ADD("blk.%u.ffn_up.weight", il, 2, E, F, T, K_MAT, 1.0f);
-        ADD("blk.%u.ffn_down.weight", il, 2, F, E, T, K_MAT, 0.5f);
+        ADD("blk.%u.ffn_down.weight", il, 2, F, E, T, K_MAT, gr);
         if (rec) {
             ADD("blk.%u.attn_qkv.weight", il, 2, E, cd, pick(s->type_qkv, T), K_MAT, 1.0f);
             ADD("blk.%u.attn_gate.weight", il, 2, E, di, T, K_MAT, 1.0f);
@@ -252,14 +260,14 @@ static uint32_t enumerate(const qwen_synth_spec_t *s, tdesc *d)
             ADD("blk.%u.ssm_beta.weight", il, 2, E, s->n_v_heads, T, K_MAT, 1.0f);
             ADD("blk.%u.ssm_alpha.weight", il, 2, E, s->n_v_heads, T, K_MAT, 1.0f);
             ADD("blk.%u.ssm_norm.weight", il, 1, s->state, 1, GGML_F32, K_NORM, 1.0f);
-            ADD("blk.%u.ssm_out.weight", il, 2, di, E, T, K_MAT, 0.5f);
+            ADD("blk.%u.ssm_out.weight", il, 2, di, E, T, K_MAT, gr);
         } else {
             ADD("blk.%u.attn_q.weight", il, 2, E, 2ull * s->n_head * s->head_dim, T, K_MAT, 1.0f);
             ADD("blk.%u.attn_k.weight", il, 2, E, (uint64_t)s->n_kv_head * s->head_dim, T, K_MAT, 1.0f);
             ADD("blk.%u.attn_v.weight", il, 2, E, (uint64_t)s->n_kv_head * s->head_dim, T, K_MAT, 1.0f);
             ADD("blk.%u.attn_q_norm.weight", il, 1, s->head_dim, 1, GGML_F32, K_NORM, 1.0f);
             ADD("blk.%u.attn_k_norm.weight", il, 1, s->head_dim, 1, GGML_F32, K_NORM, 1.0f);
-            ADD("blk.%u.attn_output.weight", il, 2, (uint64_t)s->n_head * s->head_dim, E, T, K_MAT, 0.5f);
+            ADD("blk.%u.attn_output.weight", il, 2, (uint64_t)s->n_head * s->head_dim, E, T, K_MAT, gr);
         }
         if (mtp) {
             ADD("blk.%u.nextn.eh_proj.weight", il, 2, 2 * E, E, pick(s->type_eh_proj, T), K_MAT, 1.0f);
@@ -288,7 +296,7 @@ int qwen_synth_describe(const qwen_synth_spec_t *s, uint32_t i, qwen_synth_tenso
     o->type = d[i].type;
     o->nbytes = quant_row_bytes((ggml_type_t)d[i].type, d[i].ne0) * d[i].ne1;
     switch (d[i].kind) {
-    case K_NORM: o->mu = 1.0f; o->sigma = 0.1f; break;
+    case K_NORM: o->mu = 1.0f; o->sigma = s->norm_sigma > 0.0f ? s->norm_sigma : 0.1f; break;
     case K_CONV: o->mu = 0.0f; o->sigma = 0.5f; break;
     case K_DTB:  o->mu = 0.0f; o->sigma = 0.5f; break;
     case K_SSMA: o->mu = 0.5f; o->sigma = 0.5f; o->neg_abs = 1; break;
@@ -299,10 +307,84 @@ int qwen_synth_describe(const qwen_synth_spec_t *s, uint32_t i, qwen_synth_tenso
     return 0;
 }
 
+/* IQ4_XS eh_proj [2E -> E] whose token half is ~identity: in row r every
+ * 32-element sub-block of the first E columns has scale code 32 (weights 0)
+ * except the one holding column r, code 63, with nibble 15 (codebook 113) at
+ * column r and nibble 8 (codebook 1) elsewhere; d = 1/(31*113), so W[r][r] ~ 1
+ * and its 31 neighbours ~ 0.009.  The hidden half keeps the random codes with
+ * scale codes drawn from 31..33 and d/8, i.e. weights of at most 127 d/8 ~ 0.0045. */
+static int diag_eh_proj(const qwen_synth_tensor_t *t, uint64_t seed, uint32_t id, uint8_t *out)
+{
+    if (t->type != GGML_IQ4_XS || t->ne[0] % 512 || t->ne[1] * 2 != t->ne[0]) return -1;
+    const uint64_t E = t->ne[1], nsb = t->ne[0] / 256;
+    const uint64_t base = stream_base(seed, (uint64_t)id ^ 0x5EEDull);
+    const uint16_t d = qwen_f32_to_f16(1.0f / (31.0f * 113.0f)), dh = qwen_f32_to_f16(1.0f / (8.0f * 31.0f * 113.0f));
+    for (uint64_t r = 0; r < E; r++)
+        for (uint64_t sb = 0; sb < nsb; sb++) {
+            uint8_t *b = out + (r * nsb + sb) * 136;
+            uint16_t sh = 0;
+            uint8_t sl[4] = { 0, 0, 0, 0 };
+            if (sb * 256 < E) {                       /* token half */
+                const int hit = r / 256 == sb;
+                const uint32_t ib_r = (uint32_t)(r % 256) / 32, jj = (uint32_t)(r % 32);
+                for (uint32_t ib = 0; ib < 8; ib++) {
+                    const uint32_t ls = (hit && ib == ib_r) ? 63u : 32u;
+                    sl[ib / 2] |= (uint8_t)((ls & 15u) << (4 * (ib % 2)));
+                    sh |= (uint16_t)(((ls >> 4) & 3u) << (2 * ib));
+                }
+                memset(b + 8, 0x88, 128);
+                if (hit) {
+                    uint8_t *q = b + 8 + 16 * ib_r + (jj % 16);
+                    *q = jj < 16 ? (uint8_t)((*q & 0xF0) | 0x0F) : (uint8_t)((*q & 0x0F) | 0xF0);
+                }
+                put16(b, d);
+            } else {                                  /* hidden half: weak random */
+                const uint64_t key = block_key(base, r * nsb + sb);
+                for (uint32_t ib = 0; ib < 8; ib++) {
+                    const uint32_t ls = 31u + (uint32_t)(word(key, 40 + ib) % 3u);
+                    sl[ib / 2] |= (uint8_t)((ls & 15u) << (4 * (ib % 2)));
+                    sh |= (uint16_t)(((ls >> 4) & 3u) << (2 * ib));
+                }
+                put_words(b + 8, key, 4, 128);
+                put16(b, dh);
+            }
+            put16(b + 2, sh);
+            memcpy(b + 4, sl, 4);
+        }
+    return 0;
+}
+
+/* token_embd of a tie_shift model (IQ4_XS): random codes with one super-block
+ * scale d for every block, so all rows have about the same norm and no output
+ * row outweighs the others for every input */
+static int tied_embd(const qwen_synth_spec_t *s, void *out)
+{
+    qwen_synth_tensor_t e;
+    if (qwen_synth_describe(s, 0, &e) || e.type != GGML_IQ4_XS) return -1;
+    if (qwen_synth_matrix(e.type, e.ne[0], e.ne[1], s->seed, 0, e.sigma, out, 0)) return -1;
+    const uint16_t d = qwen_f32_to_f16(e.sigma);
+    for (uint64_t b = 0; b < e.nbytes / 136; b++) put16((uint8_t *)out + b * 136, d);
+    return 0;
+}
+
 int qwen_synth_fill(const qwen_synth_spec_t *s, uint32_t i, void *out)
 {
     qwen_synth_tensor_t t;
     if (qwen_synth_describe(s, i, &t)) return -1;
+    if (s->mtp_diag && strstr(t.name, ".nextn.eh_proj.weight"))
+        return diag_eh_proj(&t, s->seed, i, out);
+    if (s->tie_shift && i == 0) return tied_embd(s, out);
+    if (s->tie_shift && !strcmp(t.name, "output.weight")) {
+        qwen_synth_tensor_t e;                    /* token_embd is tensor 0 */
+        if (qwen_synth_describe(s, 0, &e) || e.type != t.type || e.nbytes != t.nbytes || e.ne[1] < 2) return -1;
+        uint8_t *emb = malloc(e.nbytes);
+        if (!emb || tied_embd(s, emb)) { free(emb); return -1; }
+        const size_t rb = e.nbytes / e.ne[1];
+        memcpy(out, emb + (e.ne[1] - 1) * rb, rb);
+        memcpy((uint8_t *)out + rb, emb, (e.ne[1] - 1) * rb);
+        free(emb);
+        return 0;
+    }
     if (t.type != GGML_F32)
         return qwen_synth_matrix(t.type, t.ne[0], t.ne[1], s->seed, i, t.sigma, out, 0);
     const uint64_t n = t.ne[0] * t.ne[1];

@@ -49,7 +49,9 @@ class SynthSpec(ctypes.Structure):
         "rope_dim full_attn_interval context_len").split()]
         + [("rope_theta", ctypes.c_float), ("eps", ctypes.c_float)]
         + [(n, ctypes.c_int32) for n in "type_default type_embd type_output type_qkv type_eh_proj".split()]
-        + [("gain_output", ctypes.c_float), ("seed", ctypes.c_uint64)])
+        + [("gain_output", ctypes.c_float), ("seed", ctypes.c_uint64)]
+        + [("gain_embd", ctypes.c_float), ("gain_resid", ctypes.c_float), ("mtp_diag", ctypes.c_int32),
+           ("norm_sigma", ctypes.c_float), ("tie_shift", ctypes.c_int32)])
 
 
 class SynthTensor(ctypes.Structure):
@@ -399,6 +401,8 @@ def _model_lib():
                                         ctypes.c_uint64, u32, U32P, ctypes.POINTER(GenStats)]
     L.model_generate_sample.restype = u32
     L.model_time_steps.argtypes = [vp, u32, i32, F32P, F32P, F32P]
+    L.qwen_model_status.argtypes = [vp]
+    L.qwen_model_status.restype = i32
     L._model_sigs = True
     return L
 
@@ -423,6 +427,10 @@ class Model:
             raise QgpuError(f"model_init failed ({path or 'synthetic'})")
         self.V = self.L.qwen_model_get(self.h, b"vocab")
         self.E = self.L.qwen_model_get(self.h, b"n_embd")
+
+    def status(self):
+        """0 = last call done, -1 = rejected on the host, -2 = device error (include/model.h)"""
+        return self.L.qwen_model_status(self.h)
 
     def set_graphs(self, on):
         """replay captured launch sequences (HIP graphs) of the forward / MTP bodies (default off)"""

@@ -13,6 +13,10 @@ to the inputs and the reference outputs:
                                deq [ne1][ne0] (dequant_row of every row)
   ops.npz                    : test_ops.c:171-240 random-dimension cases
   model_<variant>.npz        : tiny hybrid model scenarios (ref_harness.c)
+  model_tiny_accept.npz      : speculative scenarios (ref_harness.c spec mode) on the tiny model whose
+                               drafts are mostly accepted (synth variant 2): natural streams and j for
+                               k = 1..7, forced-acceptance streams, final logits / MTP state; keys
+                               prefixed end_ come from a run that stops at the end of a short context
   sampler.npz                : sampler_sample on seeded logits (3 calls per case): tokens, generator
                                state after each call, penalised logits
   model_27b.npz              : full-size 27B greedy stream + top-2 gaps
@@ -194,6 +198,36 @@ def model_fixtures(host):
             print(variant, sha[:16], {k: v.shape for k, v in arrs.items()})
 
 
+ACCEPT_SEED = 1234
+ACCEPT_RUNS = (("", 256, 20, 160), ("end_", 57, 20, 200))   # key prefix, n_ctx, n_prompt, n_predict
+
+
+def accept_fixtures(host):
+    """Speculative decode with drafts the backbone accepts (j over 0..k)."""
+    with tempfile.TemporaryDirectory() as td:
+        exe = os.path.join(td, "ref_harness")
+        subprocess.check_call(["gcc", "-O2", "-std=c11", f"-I{REF_INC}", os.path.join(HERE, "ref_harness.c"),
+                               REF_LIB, f"-Wl,-rpath,{os.path.dirname(REF_LIB)}", "-lm", "-lpthread", "-o", exe])
+        path = os.path.join(td, "accept.gguf")
+        host.write_tiny_gguf(path, ACCEPT_SEED, 2)
+        sha = hashlib.sha256(open(path, "rb").read()).hexdigest()
+        arrs = {}
+        for pre, n_ctx, n_prompt, n_predict in ACCEPT_RUNS:
+            outd = os.path.join(td, "out" + pre)
+            os.makedirs(outd)
+            subprocess.check_call([exe, path, outd, str(n_ctx), "spec", str(n_prompt), str(n_predict)])
+            for fn in sorted(os.listdir(outd)):
+                base, ext = fn.rsplit(".", 1)
+                arrs[pre + base] = np.fromfile(os.path.join(outd, fn), {"f32": np.float32}.get(ext, np.uint32))
+            arrs[pre + "n_ctx"] = np.int32(n_ctx)
+            arrs[pre + "n_predict"] = np.int32(n_predict)
+        np.savez(os.path.join(HERE, "model_tiny_accept.npz"), gguf_sha256=np.array(sha), seed=np.uint64(ACCEPT_SEED),
+                 variant=np.int32(2), **arrs)
+        for k in range(1, 8):
+            print("k", k, "j histogram", np.bincount(arrs[f"spec_seq_k{k}_j"], minlength=k + 1).tolist(),
+                  "| end", np.bincount(arrs[f"end_spec_seq_k{k}_j"], minlength=k + 1).tolist())
+
+
 SEED_27B = 27            # the benchmark's model seed
 PROMPT_SEED_27B = 20251201
 
@@ -236,7 +270,7 @@ def main():
         sys.exit("build the reference first: make -C oracle")
     ref = ctypes.CDLL(REF_LIB)
     host = qwen_pkg.host_lib()
-    which = sys.argv[1:] or ["gemv", "ops", "model", "sampler"]
+    which = sys.argv[1:] or ["gemv", "ops", "model", "sampler", "accept"]
     if "gemv" in which:
         gemv_fixtures(ref, host)
     if "ops" in which:
@@ -245,6 +279,8 @@ def main():
         model_fixtures(host)
     if "sampler" in which:
         sampler_fixtures(ref)
+    if "accept" in which:
+        accept_fixtures(host)
     if "27b" in which:
         model27b_fixture(host)
 

@@ -6,6 +6,14 @@
  *
  * usage: ref_harness <model.gguf> <out_dir> <n_ctx>
  *        ref_harness <model.gguf> <out_dir> <n_ctx> greedy <prompt.u32> <n_gen>
+ *        ref_harness <model.gguf> <out_dir> <n_ctx> spec <n_prompt> <n_predict>
+ * The spec form runs every speculative scenario from a prefill of n_prompt ids
+ * and writes, per scenario, the stream (.u32), j per cycle (_j.u32), the logits
+ * the next cycle would start from (_last.f32) and the final MTP hidden state
+ * (_mtph.f32): spec_k{1,2} (main.c's batched loop), spec_seq_k{1..7}
+ * (sequential verification, any k), spec_f{1,2}_k{1..7} (forced acceptance,
+ * sequential verification), and greedy.u32 (n_predict + 8 tokens: the tokens a
+ * cycle cut by n_predict verified and kept are on it too).
  * The second form (full-size model) prefills the prompt in chunks of 8 and
  * decodes n_gen tokens greedily with model_forward, writing
  *   stream.u32        the greedy tokens
@@ -143,9 +151,15 @@ static uint32_t spec_batch(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t
 
 /* Same stream for any k: drafts as main.c:182-185, verification by single-token
  * forwards that stop at the first mismatch (no rollback needed), MTP anchored on
- * the backbone hidden state after the last accepted token (debug_spec.c:26). */
-static uint32_t spec_seq(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n_predict,
-                         uint32_t *out, uint32_t *js, uint32_t *ncyc)
+ * the backbone hidden state after the last accepted token (debug_spec.c:26).
+ * The context-end test is main.c's: after a batched verify of kk+1 tokens the
+ * position is P+kk+2, and the loop stops once that reaches n_ctx (main.c:210).
+ * force (no reference counterpart; the device loop's benchmark modes): 1 = every
+ * draft accepted (j = kk), 2 = j = cycle mod (kk+1); verification then forwards
+ * cand[0..j] whatever the backbone predicts.  last/mtph (optional) receive the
+ * logits the next cycle would start from and the MTP hidden state at the end. */
+static uint32_t spec_seq(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n_predict, int force,
+                         uint32_t *out, uint32_t *js, uint32_t *ncyc, float *last_out, float *mtph_out)
 {
     const uint32_t V = m->cfg.vocab_size, E = m->dims.n_embd;
     float *last = malloc(V * sizeof(float)), *h = malloc(E * sizeof(float));
@@ -160,23 +174,78 @@ static uint32_t spec_seq(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n
             mtp_forward(m, NULL, cand[s - 1], P + s, 1);
             cand[s] = model_sample_greedy(m->logits, V);
         }
-        uint32_t j = kk;
-        for (uint32_t i = 0; i <= kk; i++) {
+        const uint32_t jf = force == 1 ? kk : force == 2 ? cyc % (kk + 1) : kk;
+        uint32_t j = jf;
+        for (uint32_t i = 0; i <= jf; i++) {
             model_forward(m, NULL, cand[i], P + 1 + i);
             memcpy(last, m->logits, V * sizeof(float));
             memcpy(h, m->x, E * sizeof(float));
-            if (i < kk && model_sample_greedy(last, V) != cand[i + 1]) { j = i; break; }
+            if (!force && i < kk && model_sample_greedy(last, V) != cand[i + 1]) { j = i; break; }
         }
         for (uint32_t i = 0; i <= j && gen < n_predict; i++) out[gen++] = cand[i];
         js[cyc] = j;
-        if (m->pos >= n_ctx) { cyc++; break; }
+        if (P + kk + 2 >= n_ctx) { cyc++; break; }
         memcpy(m->mtp_h, h, E * sizeof(float));
         mtp_forward(m, NULL, cand[j], P + j + 1, 0);
         cyc++;
     }
+    if (last_out) memcpy(last_out, last, V * sizeof(float));
+    if (mtph_out) memcpy(mtph_out, m->mtp_h, E * sizeof(float));
     free(last); free(h);
     *ncyc = cyc;
     return gen;
+}
+
+/* spec mode: every speculative scenario on one model, prompt of n_prompt ids */
+static int spec_mode(const char *path, const char *dir, uint32_t n_ctx, uint32_t n_prompt, uint32_t n_predict)
+{
+    qwen_model_t *m = calloc(1, sizeof *m);
+    if (!m || model_init(m, path, n_ctx)) return 1;
+    const uint32_t V = m->cfg.vocab_size, E = m->dims.n_embd;
+    uint32_t prompt[256], *out = calloc(n_predict + 16, 4), *js = calloc(n_predict + 16, 4), nc, ng;
+    if (n_prompt > 256) return 1;
+    float *last = malloc((size_t)V * 4), *mtph = malloc((size_t)E * 4);
+    for (uint32_t i = 0; i < n_prompt; i++) prompt[i] = prompt_tok(i, V);
+    dump(dir, "prompt.u32", prompt, n_prompt * 4);
+    char name[96];
+#define DUMP4(FMT, ...) do { snprintf(name, sizeof name, FMT ".u32", __VA_ARGS__); dump(dir, name, out, ng * 4); \
+        snprintf(name, sizeof name, FMT "_j.u32", __VA_ARGS__); dump(dir, name, js, nc * 4); \
+        snprintf(name, sizeof name, FMT "_last.f32", __VA_ARGS__); dump(dir, name, last, (size_t)V * 4); \
+        snprintf(name, sizeof name, FMT "_mtph.f32", __VA_ARGS__); dump(dir, name, mtph, (size_t)E * 4); } while (0)
+    for (uint32_t k = 1; k <= 2; k++) {               /* main.c's own loop */
+        model_free(m);
+        if (model_init(m, path, n_ctx)) return 1;
+        prefill(m, prompt, n_prompt, 1);
+        ng = spec_batch(m, k, n_ctx, n_predict, out, js, &nc);
+        memcpy(last, m->logits_b + (size_t)js[nc - 1] * V, (size_t)V * 4);
+        memcpy(mtph, m->mtp_h, (size_t)E * 4);
+        DUMP4("spec_k%u", k);
+    }
+    for (int force = 0; force <= 2; force++)
+        for (uint32_t k = 1; k <= 7; k++) {
+            model_free(m);
+            if (model_init(m, path, n_ctx)) return 1;
+            prefill(m, prompt, n_prompt, 1);
+            ng = spec_seq(m, k, n_ctx, n_predict, force, out, js, &nc, last, mtph);
+            if (force) DUMP4("spec_f%d_k%u", force, k);
+            else DUMP4("spec_seq_k%u", k);
+        }
+#undef DUMP4
+    model_free(m);
+    if (model_init(m, path, n_ctx)) return 1;          /* plain greedy stream, k tokens past n_predict */
+    prefill(m, prompt, n_prompt, 0);
+    uint32_t cur = model_sample_greedy(m->logits, V);
+    ng = 0;
+    out[ng++] = cur;
+    while (ng < n_predict + 8 && m->pos < n_ctx) {
+        model_forward(m, NULL, cur, m->pos);
+        cur = model_sample_greedy(m->logits, V);
+        out[ng++] = cur;
+    }
+    dump(dir, "greedy.u32", out, ng * 4);
+    model_free(m);
+    free(m); free(out); free(js); free(last); free(mtph);
+    return 0;
 }
 
 int main(int argc, char **argv)
@@ -184,6 +253,8 @@ int main(int argc, char **argv)
     if (argc < 4) { fprintf(stderr, "usage: %s model.gguf outdir n_ctx\n", argv[0]); return 1; }
     if (argc >= 7 && !strcmp(argv[4], "greedy")) return greedy_mode(argv[1], argv[2], (uint32_t)atoi(argv[3]), argv[5],
                                                                   (uint32_t)atoi(argv[6]));
+    if (argc >= 7 && !strcmp(argv[4], "spec")) return spec_mode(argv[1], argv[2], (uint32_t)atoi(argv[3]),
+                                                               (uint32_t)atoi(argv[5]), (uint32_t)atoi(argv[6]));
     const char *path = argv[1], *dir = argv[2];
     const uint32_t n_ctx = (uint32_t)atoi(argv[3]);
     qwen_model_t *m = calloc(1, sizeof *m);
@@ -239,7 +310,7 @@ int main(int argc, char **argv)
         if (model_init(m, path, n_ctx)) return 1;
         prefill(m, prompt, n_prompt, 1);
         memset(out, 0, sizeof out); memset(js, 0, sizeof js);
-        ng = spec_seq(m, k, n_ctx, n_predict, out, js, &nc);
+        ng = spec_seq(m, k, n_ctx, n_predict, 0, out, js, &nc, NULL, NULL);
         snprintf(name, sizeof name, "spec_seq_k%u.u32", k); dump(dir, name, out, ng * 4);
         snprintf(name, sizeof name, "spec_seq_j_k%u.u32", k); dump(dir, name, js, nc * 4);
         model_free(m);

@@ -65,3 +65,25 @@ def test_error_strings_without_gpu(name):
     f.restype = ctypes.c_char_p
     f.argtypes = [ctypes.c_int]
     assert f(0) and f(-1) and f(-12345)
+
+
+def test_gguf_open_rejects_truncated_tensor_data(tmp_path):
+    """A GGUF whose last tensor runs past the end of the file is refused by gguf_open (not read
+    past the mapping later)."""
+    from qwen_pkg import host_lib
+    host = host_lib()
+    path = str(tmp_path / "t.gguf")
+    host.write_tiny_gguf(path, 1, 0)
+    L = host.L
+
+    class Ctx(ctypes.Structure):
+        _fields_ = [("pad", ctypes.c_uint8 * 65536)]
+    L.gguf_open.argtypes = [ctypes.c_void_p, ctypes.c_char_p]
+    L.gguf_close.argtypes = [ctypes.c_void_p]
+    ctx = Ctx()
+    assert L.gguf_open(ctypes.byref(ctx), path.encode()) == 0
+    L.gguf_close(ctypes.byref(ctx))
+    data = open(path, "rb").read()
+    bad = str(tmp_path / "cut.gguf")
+    open(bad, "wb").write(data[:-1000])
+    assert L.gguf_open(ctypes.byref(ctx), bad.encode()) == -1

@@ -420,3 +420,86 @@ def test_model_graphs_match_eager(gpu, tiny, mode):
         m.close()
     assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1])
     assert np.array_equal(res[0][2], res[1][2])
+
+
+# ---------------------------------------------------------------- accepted drafts (j > 0)
+@pytest.fixture(scope="module")
+def accept():
+    """The tiny model whose MTP drafts the backbone mostly accepts (synth variant 2); the
+    fixture holds the reference's streams for every j in 0..k."""
+    z = load("model_tiny_accept.npz")
+    td = tempfile.mkdtemp()
+    path = os.path.join(td, "accept.gguf")
+    host_lib().write_tiny_gguf(path, int(z["seed"]), int(z["variant"]))
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == str(z["gguf_sha256"])
+    yield path, z
+    os.remove(path)
+
+
+def accept_key(pre, force, k):
+    if force:
+        return f"{pre}spec_f{force}_k{k}"
+    return f"{pre}spec_k{k}" if k <= 2 else f"{pre}spec_seq_k{k}"
+
+
+@pytest.mark.parametrize("pre", ["", "end_"])
+@pytest.mark.parametrize("force", [0, 1, 2])
+@pytest.mark.parametrize("k", range(1, 8))
+def test_model_spec_accept_vs_reference(gpu, accept, pre, force, k):
+    """The device loop against the reference with drafts accepted (j over 0..k): tokens and j of
+    every cycle identical; the logits the next cycle starts from (logits_b row j of the last cycle)
+    and the MTP state within 1e-3.  force 1/2 are the forced-acceptance modes, pinned by the
+    reference's sequential-verify harness; end_ runs into the end of a 57-position context."""
+    path, z = accept
+    print(f"\n[accept] n_ctx={int(z[pre + 'n_ctx'])} force={force} k={k}", flush=True)
+    key = accept_key(pre, force, k)
+    m = pyqwen.Model(path, int(z[pre + "n_ctx"]))
+    toks, js, st = m.generate_spec(z["prompt"], int(z[pre + "n_predict"]), k, force_accept=force)
+    assert m.status() == 0
+    assert np.array_equal(toks, z[key])
+    assert np.array_equal(js, z[key + "_j"])
+    jl = int(js[-1])
+    last = m.field("logits_b", (jl + 1) * m.V).reshape(jl + 1, m.V)[jl]
+    ref = z[key + "_last"]
+    assert rel_err(last, ref) < 1e-3 and last.argmax() == ref.argmax()
+    assert rel_err(m.field("mtp_h", m.E), z[key + "_mtph"]) < 1e-3
+    m.close()
+
+
+def test_model_rejects_positions_past_the_context(gpu, tiny):
+    """Calls whose KV rows would fall past n_ctx are refused on the host (status -1) before any
+    device work; the model stays usable and later valid calls match a fresh model."""
+    path, z = tiny
+    n_ctx = 16
+    m = pyqwen.Model(path, n_ctx)
+    p = z["prompt"]
+    m.forward_batch(p[:8], 0)
+    assert m.status() == 0 and m.pos == 8
+    before = m.field("logits_b", m.V).copy()
+    m.forward_batch(p[:8], 12)                       # rows 12..19 > 15
+    assert m.status() == -1 and m.pos == 8
+    assert np.array_equal(m.field("logits_b", m.V), before)
+    m.forward(int(p[0]), n_ctx)
+    assert m.status() == -1
+    m.L.mtp_forward(m.h, None, int(p[0]), n_ctx, 1)
+    assert m.status() == -1
+    m.forward_batch(np.array([m.V + 3], np.uint32), 8)   # token id past the vocabulary
+    assert m.status() == -1
+    m.forward_batch(p[8:16], 8)                      # rows 8..15: the last valid span
+    assert m.status() == 0 and m.pos == 16
+    got = m.field("logits_b", 8 * m.V).reshape(8, m.V)
+    m.close()
+    f = pyqwen.Model(path, n_ctx)
+    f.forward_batch(p[:8], 0)
+    want = f.forward_batch(p[8:16], 8)
+    assert np.array_equal(got, want)
+    f.close()
+
+
+def test_model_init_rejects_unsupported_head_ratio(gpu):
+    """More than 48 query rows per KV head at the largest batch (attention kernel limit) fails at
+    model_init, not at the first verify."""
+    spec = host_lib().spec_tiny(5, 0)
+    spec.n_head, spec.n_kv_head = 14, 2              # 7 x 8 = 56 > 48
+    with pytest.raises(pyqwen.QgpuError):
+        pyqwen.Model(spec=spec, n_ctx=64)

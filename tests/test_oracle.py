@@ -363,3 +363,81 @@ def test_oracle_sample_stream_bitexact(tiny_model):
         s = O.sampler(temp, top_p, int(top_k), pen, int(seed))
         assert np.array_equal(m.generate_sample(z["prompt"][:20], 40, s), z[f"sample_c{c}"]), c
         m.close()
+
+
+# ---------------------------------------------------------------- accepted drafts (j > 0)
+@pytest.fixture(scope="module")
+def accept_model():
+    """The tiny model whose MTP drafts the backbone mostly accepts (synth variant 2)."""
+    z = load("model_tiny_accept.npz")
+    td = tempfile.mkdtemp()
+    path = os.path.join(td, "accept.gguf")
+    host_lib().write_tiny_gguf(path, int(z["seed"]), int(z["variant"]))
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == str(z["gguf_sha256"]), \
+        "generator no longer reproduces the fixture's GGUF"
+    yield path, z
+    os.remove(path)
+
+
+def accept_key(pre, force, k):
+    if force:
+        return f"{pre}spec_f{force}_k{k}"
+    return f"{pre}spec_k{k}" if k <= 2 else f"{pre}spec_seq_k{k}"
+
+
+def test_accept_fixture_spans_every_j():
+    """The reference's own loops accept every number of drafts 0..k on this model (k = 1..7), the
+    batched loop of main.c and the sequential-verify harness agree exactly (k <= 2), and every
+    natural stream is the greedy stream (lossless speculation)."""
+    z = load("model_tiny_accept.npz")
+    for k in range(1, 8):
+        assert set(np.unique(z[f"spec_seq_k{k}_j"]).tolist()) == set(range(k + 1)), k
+    for pre in ("", "end_"):
+        for k in (1, 2):
+            for suf in ("", "_j", "_last", "_mtph"):
+                assert np.array_equal(z[f"{pre}spec_k{k}{suf}"], z[f"{pre}spec_seq_k{k}{suf}"]), (pre, k, suf)
+        g = z[f"{pre}greedy"]
+        for k in range(1, 8):
+            s = z[accept_key(pre, 0, k)]
+            assert np.array_equal(s, g[:len(s)]), (pre, k)
+
+
+@pytest.mark.parametrize("pre", ["", "end_"])
+@pytest.mark.parametrize("force", [0, 1, 2])
+@pytest.mark.parametrize("k", range(1, 8))
+def test_oracle_spec_accept_bitexact(accept_model, pre, force, k):
+    """The oracle's batched speculative loop (verify of k+1 tokens, rollback to j, re-anchor) against
+    the reference: tokens, j of every cycle, the logits the next cycle starts from and the MTP state,
+    bit for bit.  end_: a 57-position context that the loop runs into (main.c:210 stop)."""
+    path, z = accept_model
+    m = O.Model(path, int(z[pre + "n_ctx"]), k_max=7)
+    toks, js, st = m.generate_spec(z["prompt"], int(z[pre + "n_predict"]), k, force_accept=force)
+    key = accept_key(pre, force, k)
+    assert np.array_equal(toks, z[key])
+    assert np.array_equal(js, z[key + "_j"])
+    last = m.arr(m.L.or_model_logits_b, (k + 1) * m.V).reshape(k + 1, m.V)[js[-1]]
+    assert np.array_equal(last.view(np.uint32), z[key + "_last"].view(np.uint32))
+    assert np.array_equal(m.arr(m.L.or_model_mtp_h, m.E).view(np.uint32), z[key + "_mtph"].view(np.uint32))
+    if force == 1:
+        assert np.all(js[:-1] == k)
+
+
+@pytest.mark.parametrize("force,k", [(0, 3), (0, 7), (1, 3), (1, 7), (2, 3), (2, 4)])
+def test_oracle_spec_state_equals_sequential_forward(accept_model, force, k):
+    """What the mathematics fixes: after the cycles, the logits the loop continues from are the
+    logits of a plain sequential model_forward over the prompt and every token the cycles verified
+    and kept (cand[0..j] of each cycle), whatever the acceptance rule.  In the natural mode the kept
+    tokens are the greedy stream (also past the emission cut of n_predict)."""
+    path, z = accept_model
+    key = accept_key("", force, k)
+    toks, js = z[key], z[key + "_j"]
+    kept = int(np.sum(js + 1))
+    if force == 0:
+        assert kept <= len(z["greedy"])
+        toks = z["greedy"][:kept]
+    assert kept == len(toks), "forced cases chosen where n_predict does not cut the last cycle"
+    m = O.Model(path, int(z["n_ctx"]))
+    seq = np.concatenate([z["prompt"], toks]).astype(np.uint32)
+    for i, t in enumerate(seq):
+        lg = m.forward(int(t), i)
+    assert np.array_equal(lg.view(np.uint32), z[key + "_last"].view(np.uint32))
