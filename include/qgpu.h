@@ -80,6 +80,16 @@ uint64_t qgpu_tensor_bytes(const qgpu_tensor *t);
  * with n = 1, gemv (kernels.c:615-621). */
 int  qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
                      float *out, uint64_t ldo, int flags);
+/* qgpu_gemv_batch without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as qgpu_gemv_batch (bit-identical), plus the HIP stream
+ * to launch on (NULL: the default stream); it neither initialises the library
+ * nor allocates: the activation workspace is a static device array of
+ * 1,613,824 bytes per GPU (ne0 <= 65536, else QGPU_E_RANGE).  Calls that
+ * overlap on one GPU share that array and race. */
+int  qgpu_gemv_batch_noalloc(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
+                             uint64_t ldo, int flags, void *stream);
 /* Several matrices sharing x, one launch per format group.
  * Replaces gemv_multi_batch / gemv_multi (reference kernels.c:666-736). */
 int  qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx,

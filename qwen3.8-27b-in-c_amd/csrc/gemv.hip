@@ -27,8 +27,19 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 #define RSS_FLOATS  ((size_t)QGPU_MAX_B * MAX_NSB)
 #define ACT_RMS_DEFER 4      // internal prep kind: RMSNORM with the 1/rms factor applied by the GEMV
 
-size_t qg_gemv_workspace_bytes() { return 2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float) + RSS_FLOATS * sizeof(float); }
-static float *ws_rss() { return (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float)); }
+#define GEMV_WS_BYTES (2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float) + RSS_FLOATS * sizeof(float))
+size_t qg_gemv_workspace_bytes() { return GEMV_WS_BYTES; }
+
+// Where a GEMV runs: its stream and its activation workspace (two digit planes,
+// their conversion factors, the deferred-RMSNorm sums).  The library entry
+// points use the library stream and workspace; qgpu_gemv_batch_noalloc the
+// caller's stream and a static device array.
+struct GemvExec {
+    hipStream_t st;
+    uint8_t *ws;
+};
+static GemvExec lib_exec() { return GemvExec{ qg::stream, (uint8_t *)qg::ws }; }
+static float *ws_rss(const GemvExec &ex) { return (float *)(ex.ws + 2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float)); }
 
 static __device__ __forceinline__ float h2f(uint32_t h16) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h16); }
 
@@ -1097,7 +1108,7 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
 // kernel: digit planes into the workspace when `digits`, fp32 rows into xout.
 // defer: single-segment RMSNORM is prepared as x*w plus per-super-block sums of
 // squares (ws_rss) for the GEMV to apply the row factor; *deferred tells the caller.
-static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits, bool defer = false,
+static int prep_act(const GemvExec &ex, const qgpu_act *act, int n, uint64_t ne0, int digits, bool defer = false,
                     bool *deferred = nullptr)
 {
     if (deferred) *deferred = false;
@@ -1115,10 +1126,10 @@ static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits, bool d
     if (single && defer) {
         if (!act->w || (rows && act->ldx < ne0) || (act->xout && rows && act->ldxo < ne0)) return QGPU_E_ARG;
         d.part = act->part; d.ldp = act->ldp; d.pstride = (uint64_t)n * act->ldp; d.n_part = act->n_part;
-        d.xnew = act->xnew; d.ldxn = act->ldxn; d.rss = ws_rss(); d.nsb = (int)(ne0 / 256);
+        d.xnew = act->xnew; d.ldxn = act->ldxn; d.rss = ws_rss(ex); d.nsb = (int)(ne0 / 256);
         const dim3 grid((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1));
-        hipLaunchKernelGGL(k_prep_act<ACT_RMS_DEFER>, grid, dim3(256), 0, qg::stream, d, (uint8_t *)qg::ws,
-                           (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES));
+        hipLaunchKernelGGL(k_prep_act<ACT_RMS_DEFER>, grid, dim3(256), 0, ex.st, d, ex.ws,
+                           (float *)(ex.ws + 2 * PLANE_BYTES));
         QG_LAUNCH_CHECK();
         if (deferred) *deferred = true;
         return QGPU_OK;
@@ -1149,13 +1160,13 @@ static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits, bool d
     }
     if (rows && act->ldx < wx) return QGPU_E_ARG;
     const dim3 grid((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1));
-    uint8_t *A = (uint8_t *)qg::ws;
-    float *xs = (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES);
+    uint8_t *A = ex.ws;
+    float *xs = (float *)(ex.ws + 2 * PLANE_BYTES);
     switch (act->kind) {
-    case QGPU_ACT_COPY: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_COPY>, grid, dim3(256), 0, qg::stream, d, A, xs); break;
-    case QGPU_ACT_RMSNORM: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_RMSNORM>, grid, dim3(256), 0, qg::stream, d, A, xs); break;
-    case QGPU_ACT_SILU_MUL: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_SILU_MUL>, grid, dim3(256), 0, qg::stream, d, A, xs); break;
-    default: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_GATED_NORM>, grid, dim3(256), 0, qg::stream, d, A, xs); break;
+    case QGPU_ACT_COPY: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_COPY>, grid, dim3(256), 0, ex.st, d, A, xs); break;
+    case QGPU_ACT_RMSNORM: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_RMSNORM>, grid, dim3(256), 0, ex.st, d, A, xs); break;
+    case QGPU_ACT_SILU_MUL: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_SILU_MUL>, grid, dim3(256), 0, ex.st, d, A, xs); break;
+    default: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_GATED_NORM>, grid, dim3(256), 0, ex.st, d, A, xs); break;
     }
     QG_LAUNCH_CHECK();
     return QGPU_OK;
@@ -1165,9 +1176,9 @@ static int prep_act(const qgpu_act *act, int n, uint64_t ne0, int digits, bool d
 // digit planes already in the workspace; the other formats read fp32 rows x.
 // one matrix-core GEMV launch: format FMT, NA digit planes, nw waves per tile, MODE bits
 template <int FMT>
-static void launch_mfma(const GemvArgs &A, uint32_t blocks, int na, int nw, int mode)
+static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, int na, int nw, int mode)
 {
-#define MF_GO(NA_, NW_, M_) hipLaunchKernelGGL((k_gemv_mfma<FMT, NA_, NW_, M_>), dim3(blocks), dim3(64 * NW_), 0, qg::stream, A)
+#define MF_GO(NA_, NW_, M_) hipLaunchKernelGGL((k_gemv_mfma<FMT, NA_, NW_, M_>), dim3(blocks), dim3(64 * NW_), 0, ex.st, A)
 #define MF_NW(NA_, M_) do { if (nw == 1) MF_GO(NA_, 1, M_); else if (nw == 2) MF_GO(NA_, 2, M_); \
                             else if (nw == 4) MF_GO(NA_, 4, M_); else MF_GO(NA_, 8, M_); } while (0)
 #define MF_MODE(NA_) do { if (mode == 0) MF_NW(NA_, 0); else if (mode == IQ4_RMS) MF_NW(NA_, IQ4_RMS); \
@@ -1183,8 +1194,8 @@ static void launch_mfma(const GemvArgs &A, uint32_t blocks, int na, int nw, int 
                             // or 1280 the plain 17408x5120 B=4 GEMV alone is 3% faster, but the 27B step
                             // (896..1088-tile GEMVs with row factors) 1.6% slower
 #endif
-static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x, uint64_t ldx,
-                        int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
+static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x,
+                        uint64_t ldx, int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
                         const uint64_t *r1s, int ks, float eps, bool deferred)
 {
     const qgpu_tensor *W0 = Ws[idx[0]];
@@ -1193,7 +1204,7 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
     A.ks = ks;
     A.pstride = (uint64_t)n * ldos[idx[0]];
     if (deferred) {
-        A.rss = ws_rss(); A.rss_nsb = (int)(W0->ne0 / 256); A.rss_inv_n = 1.0f / (float)W0->ne0; A.eps = eps;
+        A.rss = ws_rss(ex); A.rss_nsb = (int)(W0->ne0 / 256); A.rss_inv_n = 1.0f / (float)W0->ne0; A.eps = eps;
     }
     A.nsb = (int)(W0->ne0 / 256);
     const bool mfma = W0->packed;
@@ -1217,8 +1228,8 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
     if (mfma) {
         if (W0->ne0 > MAX_K) return QGPU_E_RANGE;
         const int na = n > 4 ? 2 : 1;
-        A.A = (const uint8_t *)qg::ws;
-        A.xs = (const float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES);
+        A.A = ex.ws;
+        A.xs = (const float *)(ex.ws + 2 * PLANE_BYTES);
         // waves per tile (K split inside the block).  Measured on MI355X over the
         // model's shapes with the 3/1 prefetch rings: 4 waves is best or within
         // noise everywhere except narrow outputs (<= 512 tiles, e.g. 5120 rows,
@@ -1235,11 +1246,11 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
         if (A.rss && nw < 4) nw = 4;                        // row factors: <= 2 tokens per wave
         const int mode = (A.rss ? IQ4_RMS : 0) | (ks > 1 ? IQ4_SPLIT : 0);
         switch (W0->type) {
-        case T_IQ4_XS: launch_mfma<T_IQ4_XS>(A, tiles * ks, na, nw, mode); break;
-        case T_Q4_K: launch_mfma<T_Q4_K>(A, tiles * ks, na, nw, mode); break;
-        case T_Q5_K: launch_mfma<T_Q5_K>(A, tiles * ks, na, nw, mode); break;
-        case T_Q6_K: launch_mfma<T_Q6_K>(A, tiles * ks, na, nw, mode); break;
-        case T_Q8_0: launch_mfma<T_Q8_0>(A, tiles * ks, na, nw, mode); break;
+        case T_IQ4_XS: launch_mfma<T_IQ4_XS>(ex, A, tiles * ks, na, nw, mode); break;
+        case T_Q4_K: launch_mfma<T_Q4_K>(ex, A, tiles * ks, na, nw, mode); break;
+        case T_Q5_K: launch_mfma<T_Q5_K>(ex, A, tiles * ks, na, nw, mode); break;
+        case T_Q6_K: launch_mfma<T_Q6_K>(ex, A, tiles * ks, na, nw, mode); break;
+        case T_Q8_0: launch_mfma<T_Q8_0>(ex, A, tiles * ks, na, nw, mode); break;
         default: return QGPU_E_TYPE;
         }
         QG_LAUNCH_CHECK();
@@ -1248,10 +1259,10 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
 #define VALU_CASE(F)                                                                                              \
     case F:                                                                                                       \
         switch (n) {                                                                                              \
-        case 1: hipLaunchKernelGGL((k_gemv_valu<F, 1>), dim3(tiles), dim3(256), 0, qg::stream, A); break;        \
-        case 2: hipLaunchKernelGGL((k_gemv_valu<F, 2>), dim3(tiles), dim3(256), 0, qg::stream, A); break;        \
-        case 3: case 4: hipLaunchKernelGGL((k_gemv_valu<F, 4>), dim3(tiles), dim3(256), 0, qg::stream, A); break; \
-        default: hipLaunchKernelGGL((k_gemv_valu<F, 8>), dim3(tiles), dim3(256), 0, qg::stream, A); break;      \
+        case 1: hipLaunchKernelGGL((k_gemv_valu<F, 1>), dim3(tiles), dim3(256), 0, ex.st, A); break;        \
+        case 2: hipLaunchKernelGGL((k_gemv_valu<F, 2>), dim3(tiles), dim3(256), 0, ex.st, A); break;        \
+        case 3: case 4: hipLaunchKernelGGL((k_gemv_valu<F, 4>), dim3(tiles), dim3(256), 0, ex.st, A); break; \
+        default: hipLaunchKernelGGL((k_gemv_valu<F, 8>), dim3(tiles), dim3(256), 0, ex.st, A); break;      \
         }                                                                                                         \
         break;
     switch (W0->type) {
@@ -1268,11 +1279,11 @@ static int launch_group(const qgpu_tensor *const *Ws, const int *idx, int cnt, c
 }
 
 // act == NULL: packed matrices only, on the digit planes of the last prepare.
-static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n, float *const *outs,
-                      const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s, int ks = 1)
+static int gemv_multi_on(const GemvExec &ex, const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,
+                         float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
+                         const uint64_t *r1s, int ks = 1)
 {
-    int rc = qg::ensure_init();
-    if (rc) return rc;
+    int rc = QGPU_OK;
     if (!Ws || !outs || !ldos || n_mat < 1 || n_mat > QGPU_MAX_MULTI || n < 1 || n > QGPU_MAX_B || !Ws[0])
         return QGPU_E_ARG;
     const uint64_t ne0 = Ws[0]->ne0;
@@ -1299,7 +1310,7 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *a
         }
         if (any_mfma || xform) {
             if (!any_mfma && ne0 % 256) return QGPU_E_RANGE;
-            rc = prep_act(act, n, ne0, any_mfma ? 1 : 0, ne0 <= 64 * 256, &deferred);   // row factors: <= 64 sums
+            rc = prep_act(ex, act, n, ne0, any_mfma ? 1 : 0, ne0 <= 64 * 256, &deferred);   // row factors: <= 64 sums
             if (rc) return rc;
         }
     }
@@ -1311,10 +1322,19 @@ static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *a
         int idx[QGPU_MAX_MULTI], cnt = 0;
         for (int i = j; i < n_mat; i++)
             if (!done[i] && Ws[i]->type == Ws[j]->type) { idx[cnt++] = i; done[i] = 1; }
-        rc = launch_group(Ws, idx, cnt, xv, ldxv, n, outs, ldos, flags, r0s, r1s, ks, eps, deferred);
+        rc = launch_group(ex, Ws, idx, cnt, xv, ldxv, n, outs, ldos, flags, r0s, r1s, ks, eps, deferred);
         if (rc) return rc;
     }
     return QGPU_OK;
+}
+
+// the library entry points: library stream and workspace
+static int gemv_multi(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n, float *const *outs,
+                      const uint64_t *ldos, int flags, const uint64_t *r0s, const uint64_t *r1s, int ks = 1)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    return gemv_multi_on(lib_exec(), Ws, n_mat, act, n, outs, ldos, flags, r0s, r1s, ks);
 }
 
 static qgpu_act copy_act(const float *x, uint64_t ldx)
@@ -1332,6 +1352,41 @@ extern "C" int qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ld
     if (!x || !W || (n > 1 && ldx < W->ne0)) return QGPU_E_ARG;
     const qgpu_act a = copy_act(x, ldx);
     return gemv_multi(&W, 1, &a, n, &out, &ldo, flags, nullptr, nullptr);
+}
+
+// ---------------------------------------------------------------- allocation-free gemv_batch
+// For callers that cannot allocate device memory (code under HIP graph capture,
+// tight serving loops, harnesses that forbid hipMalloc): the workspace of the
+// batched GEMV (two 4-token digit planes for up to MAX_K = 65536 columns, their
+// conversion factors and the deferred-RMSNorm sums: 1,613,824 bytes) lives in
+// this file-scope device array, one copy per GPU, held until the process ends.
+// Its device address is looked up once per device with hipGetSymbolAddress; the
+// host-side name is never passed to a kernel.  Every call on a GPU shares that
+// GPU's copy, so calls that overlap on one GPU (two streams, two threads) race.
+// Nothing in it has to start at zero: each call writes the digit tiles and
+// factors of every super-block it reads before the GEMV reads them.
+static __device__ __align__(256) uint8_t scratch[GEMV_WS_BYTES];
+#define SCRATCH_MAX_DEV 64
+static uint8_t *scratch_ptr[SCRATCH_MAX_DEV];
+
+extern "C" int qgpu_gemv_batch_noalloc(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
+                                       uint64_t ldo, int flags, void *stream)
+{
+    if (!x || !W || !out || n < 1 || n > QGPU_MAX_B || (n > 1 && (ldx < W->ne0 || ldo < W->ne1)))
+        return QGPU_E_ARG;
+    if (W->ne0 > MAX_K) return QGPU_E_RANGE;              // the digit planes hold MAX_K columns
+    int dev = -1;
+    QG_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= SCRATCH_MAX_DEV) return QGPU_E_RANGE;
+    if (!scratch_ptr[dev]) {                              // first call on this device: its copy's address
+        void *p = nullptr;
+        QG_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return QGPU_E_INIT;
+        scratch_ptr[dev] = (uint8_t *)p;
+    }
+    const GemvExec ex{ (hipStream_t)stream, scratch_ptr[dev] };
+    const qgpu_act a = copy_act(x, ldx);
+    return gemv_multi_on(ex, &W, 1, &a, n, &out, &ldo, flags, nullptr, nullptr);
 }
 
 extern "C" int qgpu_gemv_multi_batch(const qgpu_tensor *const *Ws, int n_mat, const float *x, uint64_t ldx, int n,
@@ -1408,7 +1463,7 @@ extern "C" int qgpu_gemv_prepare(const float *x, uint64_t ldx, int n, uint64_t n
     if (rc) return rc;
     if (!x || (n > 1 && ldx < ne0)) return QGPU_E_ARG;
     const qgpu_act a = copy_act(x, ldx);
-    return prep_act(&a, n, ne0, 1);
+    return prep_act(lib_exec(), &a, n, ne0, 1);
 }
 
 extern "C" int qgpu_act_prepare(const qgpu_act *act, int n, uint64_t ne0)
@@ -1416,7 +1471,7 @@ extern "C" int qgpu_act_prepare(const qgpu_act *act, int n, uint64_t ne0)
     int rc = qg::ensure_init();
     if (rc) return rc;
     if (!act || !act->xout) return QGPU_E_ARG;
-    return prep_act(act, n, ne0, ne0 <= MAX_K ? 1 : 0);
+    return prep_act(lib_exec(), act, n, ne0, ne0 <= MAX_K ? 1 : 0);
 }
 
 extern "C" int qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, int flags)

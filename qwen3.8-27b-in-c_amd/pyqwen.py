@@ -255,6 +255,7 @@ class GpuLib:
             "qgpu_tensor_from_device": [vp, i32, u64, u64, ctypes.POINTER(vp)],
             "qgpu_tensor_free": [vp], "qgpu_tensor_download": [vp, vp],
             "qgpu_gemv_batch": [vp, F32P, u64, i32, F32P, u64, i32],
+            "qgpu_gemv_batch_noalloc": [vp, F32P, u64, i32, F32P, u64, i32, vp],
             "qgpu_gemv_multi_batch": [ctypes.POINTER(vp), i32, F32P, u64, i32, ctypes.POINTER(F32P),
                                       ctypes.POINTER(u64), i32],
             "qgpu_gemv_rows_batch": [vp, F32P, u64, i32, F32P, u64, u64, u64],
