@@ -174,7 +174,8 @@ uint32_t model_generate_spec(qwen_model_t *m, const uint32_t *prompt, uint32_t n
                              uint32_t k, uint32_t eos, int force_accept, uint32_t *out, uint32_t *cycle_j,
                              qwen_gen_stats_t *st);
 /* The same loop in two parts, for callers that time or pace the cycles:
- * model_spec_begin prefills the prompt (0, or -1 on bad arguments);
+ * model_spec_begin prefills the prompt (0, or -1 on bad arguments) and, with
+ * host_sync on, leaves the last prompt row's logits in m->logits (main.c:146-150);
  * model_spec_run continues from the current state for at most max_cycles
  * cycles / max_tokens tokens and may be called again to go on.  It stops as
  * main.c:210 does once the verified positions reach n_ctx.  With host_sync on,

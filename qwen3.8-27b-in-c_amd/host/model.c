@@ -927,7 +927,10 @@ int model_spec_begin(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt,
     if (call_begin(m)) return -1;
     if (!prompt || n_prompt < 1 || n_prompt >= m->n_ctx || bad_tokens(m, prompt, n_prompt))
         return reject(m, "model_spec_begin", 0, n_prompt);
-    prefill_dev(m, prompt, n_prompt, k > 0);
+    const uint32_t last = prefill_dev(m, prompt, n_prompt, k > 0);
+    if (m->host_sync)             /* the last prompt row, where main.c:146-150 leaves it */
+        K(qgpu_memcpy_d2h(m->logits, m->gpu->logits_b + (size_t)(last - 1) * m->cfg.vocab_size,
+                          (size_t)m->cfg.vocab_size * sizeof(float)));
     K(qgpu_sync());
     call_end(m);
     return m->gpu->status;

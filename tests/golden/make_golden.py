@@ -17,6 +17,9 @@ to the inputs and the reference outputs:
                                drafts are mostly accepted (synth variant 2): natural streams and j for
                                k = 1..7, forced-acceptance streams, final logits / MTP state; keys
                                prefixed end_ come from a run that stops at the end of a short context
+  model_tiny_accept_long.npz : the same model at n_ctx 8192 after an 8176-token prompt (ref_harness.c long
+                               mode): prefill logits, natural and all-accepted streams for k = 1, 3, 5, 7
+                               (`python tests/golden/make_golden.py long`, ~5 min)
   sampler.npz                : sampler_sample on seeded logits (3 calls per case): tokens, generator
                                state after each call, penalised logits
   model_27b.npz              : full-size 27B greedy stream + top-2 gaps
@@ -228,6 +231,34 @@ def accept_fixtures(host):
                   "| end", np.bincount(arrs[f"end_spec_seq_k{k}_j"], minlength=k + 1).tolist())
 
 
+LONG_RUN = (8192, 8176, 12)      # n_ctx, n_prompt, n_predict
+
+
+def long_fixtures(host):
+    """Long context (8192 positions) on the draft-accepting tiny model."""
+    with tempfile.TemporaryDirectory() as td:
+        exe = os.path.join(td, "ref_harness")
+        subprocess.check_call(["gcc", "-O2", "-std=c11", f"-I{REF_INC}", os.path.join(HERE, "ref_harness.c"),
+                               REF_LIB, f"-Wl,-rpath,{os.path.dirname(REF_LIB)}", "-lm", "-lpthread", "-o", exe])
+        path = os.path.join(td, "accept.gguf")
+        host.write_tiny_gguf(path, ACCEPT_SEED, 2)
+        sha = hashlib.sha256(open(path, "rb").read()).hexdigest()
+        n_ctx, n_prompt, n_predict = LONG_RUN
+        outd = os.path.join(td, "out")
+        os.makedirs(outd)
+        subprocess.check_call([exe, path, outd, str(n_ctx), "long", str(n_prompt), str(n_predict)])
+        arrs = {}
+        for fn in sorted(os.listdir(outd)):
+            base, ext = fn.rsplit(".", 1)
+            if base == "prompt":
+                continue                                  # prompt_tok(i): regenerated by the tests
+            arrs[base] = np.fromfile(os.path.join(outd, fn), {"f32": np.float32}.get(ext, np.uint32))
+        np.savez(os.path.join(HERE, "model_tiny_accept_long.npz"), gguf_sha256=np.array(sha),
+                 seed=np.uint64(ACCEPT_SEED), variant=np.int32(2), n_ctx=np.int32(n_ctx), n_prompt=np.int32(n_prompt),
+                 n_predict=np.int32(n_predict), **arrs)
+        print("long", {k: v.tolist() for k, v in arrs.items() if k.endswith("_j")})
+
+
 SEED_27B = 27            # the benchmark's model seed
 PROMPT_SEED_27B = 20251201
 
@@ -281,6 +312,8 @@ def main():
         sampler_fixtures(ref)
     if "accept" in which:
         accept_fixtures(host)
+    if "long" in which:
+        long_fixtures(host)
     if "27b" in which:
         model27b_fixture(host)
 

@@ -7,13 +7,16 @@
  * usage: ref_harness <model.gguf> <out_dir> <n_ctx>
  *        ref_harness <model.gguf> <out_dir> <n_ctx> greedy <prompt.u32> <n_gen>
  *        ref_harness <model.gguf> <out_dir> <n_ctx> spec <n_prompt> <n_predict>
+ *        ref_harness <model.gguf> <out_dir> <n_ctx> long <n_prompt> <n_predict>
  * The spec form runs every speculative scenario from a prefill of n_prompt ids
  * and writes, per scenario, the stream (.u32), j per cycle (_j.u32), the logits
  * the next cycle would start from (_last.f32) and the final MTP hidden state
  * (_mtph.f32): spec_k{1,2} (main.c's batched loop), spec_seq_k{1..7}
  * (sequential verification, any k), spec_f{1,2}_k{1..7} (forced acceptance,
  * sequential verification), and greedy.u32 (n_predict + 8 tokens: the tokens a
- * cycle cut by n_predict verified and kept are on it too).
+ * cycle cut by n_predict verified and kept are on it too).  The long form
+ * (a prompt that fills most of n_ctx) writes prefill_last.f32 and only
+ * spec_seq_k / spec_f1_k for k = 1, 3, 5, 7.
  * The second form (full-size model) prefills the prompt in chunks of 8 and
  * decodes n_gen tokens greedily with model_forward, writing
  *   stream.u32        the greedy tokens
@@ -53,14 +56,18 @@ static void dump(const char *dir, const char *name, const void *p, size_t bytes)
 
 static uint32_t prompt_tok(uint32_t i, uint32_t V) { return (uint32_t)((i * 2654435761u + 12345u) % V); }
 
+/* worker pool of the reference calls (NULL = serial; the long form uses every core:
+ * the reference's row and head partitions do not change any result bit) */
+static pool_t *g_pool;
+
 /* prefill exactly as main.c:133-152 */
 static void prefill(qwen_model_t *m, const uint32_t *p, uint32_t n, int mtp)
 {
     uint32_t pos = 0, last = 0;
     while (pos < n) {
         uint32_t B = n - pos > PREFILL_MAX_B ? PREFILL_MAX_B : n - pos;
-        model_forward_batch(m, NULL, p + pos, pos, B, 0);
-        if (mtp) mtp_forward_batch(m, NULL, p + pos, pos, B, 0);
+        model_forward_batch(m, g_pool, p + pos, pos, B, 0);
+        if (mtp) mtp_forward_batch(m, g_pool, p + pos, pos, B, 0);
         pos += B;
         last = B;
     }
@@ -129,10 +136,10 @@ static uint32_t spec_batch(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t
         uint32_t cand[SPEC_MAX_B];
         cand[0] = model_sample_greedy(last, V);
         for (uint32_t s = 1; s <= kk; s++) {
-            mtp_forward(m, NULL, cand[s - 1], P + s, 1);
+            mtp_forward(m, g_pool, cand[s - 1], P + s, 1);
             cand[s] = model_sample_greedy(m->logits, V);
         }
-        model_forward_batch(m, NULL, cand, P + 1, kk + 1, 1);
+        model_forward_batch(m, g_pool, cand, P + 1, kk + 1, 1);
         uint32_t j = kk;
         for (uint32_t i = 0; i < kk; i++)
             if (model_sample_greedy(m->logits_b + (size_t)i * V, V) != cand[i + 1]) { j = i; break; }
@@ -141,7 +148,7 @@ static uint32_t spec_batch(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t
         if (m->pos >= n_ctx) { cyc++; break; }
         if (j < kk) { model_rollback_to(m, j); m->pos = P + j + 2; }
         memcpy(m->mtp_h, m->h_save + (size_t)j * m->dims.n_embd, m->dims.n_embd * sizeof(float));
-        mtp_forward(m, NULL, cand[j], P + j + 1, 0);
+        mtp_forward(m, g_pool, cand[j], P + j + 1, 0);
         last = m->logits_b + (size_t)j * V;
         cyc++;
     }
@@ -171,13 +178,13 @@ static uint32_t spec_seq(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n
         const uint32_t kk = k < room - 1 ? k : room - 1;
         cand[0] = model_sample_greedy(last, V);
         for (uint32_t s = 1; s <= kk; s++) {
-            mtp_forward(m, NULL, cand[s - 1], P + s, 1);
+            mtp_forward(m, g_pool, cand[s - 1], P + s, 1);
             cand[s] = model_sample_greedy(m->logits, V);
         }
         const uint32_t jf = force == 1 ? kk : force == 2 ? cyc % (kk + 1) : kk;
         uint32_t j = jf;
         for (uint32_t i = 0; i <= jf; i++) {
-            model_forward(m, NULL, cand[i], P + 1 + i);
+            model_forward(m, g_pool, cand[i], P + 1 + i);
             memcpy(last, m->logits, V * sizeof(float));
             memcpy(h, m->x, E * sizeof(float));
             if (!force && i < kk && model_sample_greedy(last, V) != cand[i + 1]) { j = i; break; }
@@ -186,7 +193,7 @@ static uint32_t spec_seq(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n
         js[cyc] = j;
         if (P + kk + 2 >= n_ctx) { cyc++; break; }
         memcpy(m->mtp_h, h, E * sizeof(float));
-        mtp_forward(m, NULL, cand[j], P + j + 1, 0);
+        mtp_forward(m, g_pool, cand[j], P + j + 1, 0);
         cyc++;
     }
     if (last_out) memcpy(last_out, last, V * sizeof(float));
@@ -196,14 +203,21 @@ static uint32_t spec_seq(qwen_model_t *m, uint32_t k, uint32_t n_ctx, uint32_t n
     return gen;
 }
 
-/* spec mode: every speculative scenario on one model, prompt of n_prompt ids */
-static int spec_mode(const char *path, const char *dir, uint32_t n_ctx, uint32_t n_prompt, uint32_t n_predict)
+/* spec mode: every speculative scenario on one model, prompt of n_prompt ids.
+ * long_form (an n_ctx-sized prompt): the prefill's last logits, then natural
+ * and all-accepted streams for k = 1, 3, 5, 7 only, with sequential verification. */
+static int spec_mode(const char *path, const char *dir, uint32_t n_ctx, uint32_t n_prompt, uint32_t n_predict,
+                     int long_form)
 {
     qwen_model_t *m = calloc(1, sizeof *m);
     if (!m || model_init(m, path, n_ctx)) return 1;
+    if (long_form) {
+        const long ncpu = sysconf(_SC_NPROCESSORS_ONLN);
+        g_pool = pool_create(ncpu > 0 ? (int)ncpu : 1, 1);
+    }
     const uint32_t V = m->cfg.vocab_size, E = m->dims.n_embd;
-    uint32_t prompt[256], *out = calloc(n_predict + 16, 4), *js = calloc(n_predict + 16, 4), nc, ng;
-    if (n_prompt > 256) return 1;
+    uint32_t *prompt = malloc((size_t)n_prompt * 4), *out = calloc(n_predict + 16, 4), *js = calloc(n_predict + 16, 4);
+    uint32_t nc, ng;
     float *last = malloc((size_t)V * 4), *mtph = malloc((size_t)E * 4);
     for (uint32_t i = 0; i < n_prompt; i++) prompt[i] = prompt_tok(i, V);
     dump(dir, "prompt.u32", prompt, n_prompt * 4);
@@ -212,7 +226,11 @@ static int spec_mode(const char *path, const char *dir, uint32_t n_ctx, uint32_t
         snprintf(name, sizeof name, FMT "_j.u32", __VA_ARGS__); dump(dir, name, js, nc * 4); \
         snprintf(name, sizeof name, FMT "_last.f32", __VA_ARGS__); dump(dir, name, last, (size_t)V * 4); \
         snprintf(name, sizeof name, FMT "_mtph.f32", __VA_ARGS__); dump(dir, name, mtph, (size_t)E * 4); } while (0)
-    for (uint32_t k = 1; k <= 2; k++) {               /* main.c's own loop */
+    if (long_form) {
+        prefill(m, prompt, n_prompt, 1);
+        dump(dir, "prefill_last.f32", m->logits, (size_t)V * 4);
+    }
+    for (uint32_t k = 1; k <= 2 && !long_form; k++) {               /* main.c's own loop */
         model_free(m);
         if (model_init(m, path, n_ctx)) return 1;
         prefill(m, prompt, n_prompt, 1);
@@ -223,6 +241,7 @@ static int spec_mode(const char *path, const char *dir, uint32_t n_ctx, uint32_t
     }
     for (int force = 0; force <= 2; force++)
         for (uint32_t k = 1; k <= 7; k++) {
+            if (long_form && (force == 2 || !(k & 1))) continue;
             model_free(m);
             if (model_init(m, path, n_ctx)) return 1;
             prefill(m, prompt, n_prompt, 1);
@@ -238,13 +257,13 @@ static int spec_mode(const char *path, const char *dir, uint32_t n_ctx, uint32_t
     ng = 0;
     out[ng++] = cur;
     while (ng < n_predict + 8 && m->pos < n_ctx) {
-        model_forward(m, NULL, cur, m->pos);
+        model_forward(m, g_pool, cur, m->pos);
         cur = model_sample_greedy(m->logits, V);
         out[ng++] = cur;
     }
     dump(dir, "greedy.u32", out, ng * 4);
     model_free(m);
-    free(m); free(out); free(js); free(last); free(mtph);
+    free(m); free(prompt); free(out); free(js); free(last); free(mtph);
     return 0;
 }
 
@@ -253,8 +272,9 @@ int main(int argc, char **argv)
     if (argc < 4) { fprintf(stderr, "usage: %s model.gguf outdir n_ctx\n", argv[0]); return 1; }
     if (argc >= 7 && !strcmp(argv[4], "greedy")) return greedy_mode(argv[1], argv[2], (uint32_t)atoi(argv[3]), argv[5],
                                                                   (uint32_t)atoi(argv[6]));
-    if (argc >= 7 && !strcmp(argv[4], "spec")) return spec_mode(argv[1], argv[2], (uint32_t)atoi(argv[3]),
-                                                               (uint32_t)atoi(argv[5]), (uint32_t)atoi(argv[6]));
+    if (argc >= 7 && (!strcmp(argv[4], "spec") || !strcmp(argv[4], "long")))
+        return spec_mode(argv[1], argv[2], (uint32_t)atoi(argv[3]), (uint32_t)atoi(argv[5]), (uint32_t)atoi(argv[6]),
+                         !strcmp(argv[4], "long"));
     const char *path = argv[1], *dir = argv[2];
     const uint32_t n_ctx = (uint32_t)atoi(argv[3]);
     qwen_model_t *m = calloc(1, sizeof *m);
@@ -267,30 +287,30 @@ int main(int argc, char **argv)
     /* sequential vs batched forward of prompt[0..7] */
     float *seq = malloc((size_t)8 * V * sizeof(float));
     for (uint32_t i = 0; i < 8; i++) {
-        model_forward(m, NULL, prompt[i], i);
+        model_forward(m, g_pool, prompt[i], i);
         memcpy(seq + (size_t)i * V, m->logits, V * sizeof(float));
     }
     dump(dir, "seq_logits.f32", seq, (size_t)8 * V * sizeof(float));
     model_free(m);
     if (model_init(m, path, n_ctx)) return 1;
-    model_forward_batch(m, NULL, prompt, 0, 8, 0);
+    model_forward_batch(m, g_pool, prompt, 0, 8, 0);
     dump(dir, "batch_logits.f32", m->logits_b, (size_t)8 * V * sizeof(float));
     dump(dir, "batch_hsave.f32", m->h_save, (size_t)8 * E * sizeof(float));
     /* MTP: prefill the MTP KV for prompt[0..7] then one draft with logits */
-    mtp_forward_batch(m, NULL, prompt, 0, 8, 0);
-    mtp_forward(m, NULL, prompt[8], 8, 1);
+    mtp_forward_batch(m, g_pool, prompt, 0, 8, 0);
+    mtp_forward(m, g_pool, prompt[8], 8, 1);
     dump(dir, "mtp_logits.f32", m->logits, V * sizeof(float));
     dump(dir, "mtp_h.f32", m->mtp_h, E * sizeof(float));
     model_free(m);
 
     /* rollback (debug_rollback.c:25-57 pattern) on prompt[0..4] */
     if (model_init(m, path, n_ctx)) return 1;
-    for (uint32_t i = 0; i < 5; i++) model_forward(m, NULL, prompt[i], i);
+    for (uint32_t i = 0; i < 5; i++) model_forward(m, g_pool, prompt[i], i);
     uint32_t c1[3] = { prompt[10], prompt[11], prompt[12] }, c2[3] = { prompt[13], prompt[14], prompt[15] };
-    model_forward_batch(m, NULL, c1, 5, 3, 1);
+    model_forward_batch(m, g_pool, c1, 5, 3, 1);
     model_rollback_to(m, 1);
     m->pos = 5 + 1 + 2;
-    model_forward_batch(m, NULL, c2, 7, 3, 1);
+    model_forward_batch(m, g_pool, c2, 7, 3, 1);
     dump(dir, "rollback_logits.f32", m->logits_b, (size_t)3 * V * sizeof(float));
     model_free(m);
 
@@ -321,7 +341,7 @@ int main(int argc, char **argv)
     uint32_t cur = model_sample_greedy(m->logits, V);
     out[0] = cur;
     for (uint32_t i = 1; i < n_predict; i++) {
-        model_forward(m, NULL, cur, m->pos);
+        model_forward(m, g_pool, cur, m->pos);
         cur = model_sample_greedy(m->logits, V);
         out[i] = cur;
     }
@@ -351,7 +371,7 @@ int main(int argc, char **argv)
         out[gen++] = cur;
         for (uint32_t i = 1; i < n_predict; i++) {
             if (m->pos >= n_ctx) break;
-            model_forward(m, NULL, cur, m->pos);
+            model_forward(m, g_pool, cur, m->pos);
             cur = sampler_sample(smp, m->logits, V, all, n_all);
             all[n_all++] = cur;
             out[gen++] = cur;

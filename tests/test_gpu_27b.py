@@ -75,3 +75,33 @@ def test_27b_spec_stream(gpu, m27, k):
     n = agreeing_prefix(z["gap"])
     toks, js, st = m.generate_spec(z["prompt"], len(z["stream"]), k)
     assert np.array_equal(toks[:n], z["stream"][:n])
+
+
+def test_27b_verify_equals_sequential_past_8192(gpu):
+    """Long context at full size: after an 8192-token prompt, a verify of B = 2, 4, 6, 8 tokens at
+    positions 8192.. gives the logits of B single-token decode steps on the same prefix, within 1e-3
+    (two models, one per path, stepped over the same tokens)."""
+    host = host_lib()
+    spec = host.spec_27b(27)
+    n_ctx, n_prompt = 8224, 8192
+    print("\n[27b-long] two models, 8192-token prefill each", flush=True)
+    ms, mb = pyqwen.Model(spec=spec, n_ctx=n_ctx), pyqwen.Model(spec=spec, n_ctx=n_ctx)
+    rng = np.random.default_rng(8192)
+    prompt = rng.integers(0, spec.vocab, n_prompt).astype(np.uint32)
+    for m in (ms, mb):
+        m.spec_begin(prompt, 0)
+        assert m.status() == 0 and m.pos == n_prompt
+    pos = n_prompt
+    for B in (2, 4, 6, 8):
+        toks = rng.integers(0, spec.vocab, B).astype(np.uint32)
+        seq = np.array([ms.forward(int(t), pos + i) for i, t in enumerate(toks)])
+        bat = mb.forward_batch(toks, pos, 1)
+        for b in range(B):
+            e = rel_err(bat[b], seq[b])
+            assert e < 1e-3, (B, b, e)
+            assert bat[b].argmax() == seq[b].argmax() or np.sort(seq[b])[-1] - np.sort(seq[b])[-2] < 1e-2
+        print(f"  B={B} at positions {pos}..{pos + B - 1}: max rel err "
+              f"{max(rel_err(bat[b], seq[b]) for b in range(B)):.2e}", flush=True)
+        pos += B
+    ms.close()
+    mb.close()

@@ -503,3 +503,48 @@ def test_model_init_rejects_unsupported_head_ratio(gpu):
     spec.n_head, spec.n_kv_head = 14, 2              # 7 x 8 = 56 > 48
     with pytest.raises(pyqwen.QgpuError):
         pyqwen.Model(spec=spec, n_ctx=64)
+
+
+# ---------------------------------------------------------------- long context (8192 positions)
+def prompt_ids(n, V):
+    """the reference harness's prompt: id i = (i * 2654435761 + 12345) mod 2^32 mod V"""
+    i = np.arange(n, dtype=np.uint64)
+    return (((i * np.uint64(2654435761) + np.uint64(12345)) & np.uint64(0xFFFFFFFF)) % np.uint64(V)).astype(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def accept_long():
+    z = load("model_tiny_accept_long.npz")
+    td = tempfile.mkdtemp()
+    path = os.path.join(td, "accept.gguf")
+    host_lib().write_tiny_gguf(path, int(z["seed"]), int(z["variant"]))
+    assert hashlib.sha256(open(path, "rb").read()).hexdigest() == str(z["gguf_sha256"])
+    yield path, z
+    os.remove(path)
+
+
+@pytest.mark.parametrize("force", [0, 1])
+@pytest.mark.parametrize("k", [1, 3, 5, 7])
+def test_model_long_context_vs_reference(gpu, accept_long, force, k):
+    """An 8176-token prompt in an 8192-position context (attention over the whole KV cache, RoPE tables
+    to n_ctx), then speculative decode at k = 1, 3, 5, 7, natural and all-accepted: the prefill
+    logits, tokens, j of every cycle, final logits and MTP state against the reference's own run."""
+    path, z = accept_long
+    n_ctx, n_prompt, n_predict = int(z["n_ctx"]), int(z["n_prompt"]), int(z["n_predict"])
+    print(f"\n[long] n_ctx={n_ctx} prompt={n_prompt} k={k} force={force}", flush=True)
+    m = pyqwen.Model(path, n_ctx)
+    prompt = prompt_ids(n_prompt, m.V)
+    key = f"spec_f1_k{k}" if force else f"spec_seq_k{k}"
+    m.spec_begin(prompt, k)
+    first = m.field("logits", m.V)
+    assert rel_err(first, z["prefill_last"]) < 1e-3 and first.argmax() == z["prefill_last"].argmax()
+    toks, js, st = m.spec_run(k, 10**6, n_predict, force_accept=force)
+    assert m.status() == 0
+    assert np.array_equal(toks, z[key]) and np.array_equal(js, z[key + "_j"])
+    jl = int(js[-1])
+    last = m.field("logits_b", (jl + 1) * m.V).reshape(jl + 1, m.V)[jl]
+    assert rel_err(last, z[key + "_last"]) < 1e-3 and last.argmax() == z[key + "_last"].argmax()
+    assert rel_err(m.field("mtp_h", m.E), z[key + "_mtph"]) < 1e-3
+    if not force:
+        assert np.array_equal(toks, z["greedy"][:len(toks)])
+    m.close()
