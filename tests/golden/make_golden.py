@@ -22,7 +22,7 @@ to the inputs and the reference outputs:
                                (`python tests/golden/make_golden.py long`, ~5 min)
   sampler.npz                : sampler_sample on seeded logits (3 calls per case): tokens, generator
                                state after each call, penalised logits
-  model_27b.npz              : full-size 27B greedy stream + top-2 gaps
+  model_27b.npz              : full-size 27B greedy stream of 256 tokens + top-2 gaps
                                (`python tests/golden/make_golden.py 27b`, ~10 min)
 """
 import ctypes
@@ -263,7 +263,7 @@ SEED_27B = 27            # the benchmark's model seed
 PROMPT_SEED_27B = 20251201
 
 
-def model27b_fixture(host, n_prompt=512, n_gen=48, n_ctx=1024):
+def model27b_fixture(host, n_prompt=512, n_gen=256, n_ctx=1024):
     """Full-size random-init 27B: reference greedy stream after a seeded
     random-id prompt, with the top-2 gap of every step (the streams must agree
     wherever the gap exceeds 1e-2), plus the prefill logits."""

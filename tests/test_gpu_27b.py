@@ -3,9 +3,10 @@ IQ4_XS, generated on the box from the same seed as the fixture) against the
 reference engine's own run on the same weights (tests/golden/model_27b.npz,
 made by make_golden.py from the compiled reference):
   * the logits of the last prompt token after a 512-token prefill, within 1e-3;
-  * the greedy stream (device greedy decode, and the device MTP speculative
-    loop at k = 3) identical to the reference's wherever the reference top-2
-    gap exceeds 1e-2, up to the first step at or below that gap."""
+  * the 256-token greedy stream (device greedy decode, and the device MTP
+    speculative loop at k = 3) identical to the reference's wherever the
+    reference top-2 gap exceeds 1e-2 (a difference may only start at a step
+    whose gap is at most 1e-2)."""
 import hashlib
 import json
 import os
@@ -40,10 +41,17 @@ def m27():
     m.close()
 
 
-def agreeing_prefix(gap):
-    """steps up to (excluding) the first whose reference top-2 gap is <= 1e-2"""
-    low = np.nonzero(gap <= 1e-2)[0]
-    return int(low[0]) if len(low) else len(gap)
+def check_stream(toks, z):
+    """the streams agree wherever the reference top-2 gap exceeds 1e-2: identical up to the end,
+    or up to a first difference at a step whose reference gap is at most 1e-2 (after which the two
+    continue from different tokens)"""
+    ref, gap = z["stream"], z["gap"]
+    n = min(len(toks), len(ref))
+    diff = np.nonzero(toks[:n] != ref[:n])[0]
+    if len(diff):
+        assert gap[diff[0]] <= 1e-2, f"stream differs at step {diff[0]} where the reference gap is {gap[diff[0]]}"
+    assert len(toks) == len(ref)
+    return int(diff[0]) if len(diff) else n
 
 
 def test_27b_prefill_logits(gpu, m27):
@@ -62,19 +70,20 @@ def test_27b_prefill_logits(gpu, m27):
 def test_27b_greedy_stream(gpu, m27):
     m, z = m27
     m.reset()
-    n = agreeing_prefix(z["gap"])
     toks, st = m.generate_greedy(z["prompt"], len(z["stream"]))
-    print(f"  greedy: {n} steps with gap > 1e-2", flush=True)
-    assert np.array_equal(toks[:n], z["stream"][:n])
+    n = check_stream(toks, z)
+    print(f"  greedy: {n} of {len(z['stream'])} tokens identical", flush=True)
 
 
 @pytest.mark.parametrize("k", [3])
 def test_27b_spec_stream(gpu, m27, k):
+    """config 4: 512-token prompt, 256 generated tokens, greedy MTP speculation at k = 3"""
     m, z = m27
     m.reset()
-    n = agreeing_prefix(z["gap"])
     toks, js, st = m.generate_spec(z["prompt"], len(z["stream"]), k)
-    assert np.array_equal(toks[:n], z["stream"][:n])
+    n = check_stream(toks, z)
+    print(f"  spec k={k}: {n} of {len(z['stream'])} tokens identical, {st.n_accepted}/{st.n_drafts} drafts accepted",
+          flush=True)
 
 
 def test_27b_verify_equals_sequential_past_8192(gpu):
