@@ -40,19 +40,25 @@ HIP events on the library stream (the replay issues the K kernels back to back,
 so the host loop's per-call cost does not enter the kernel time).  achieved =
 algorithmic bytes per launch (47,349,760 weight + 4 x (5120 + 17408) x 4
 activation/output = 47,710,208 B) / average launch duration.  Weights rotate over 12 copies
-(568 MB) so the 256 MB MALL cannot serve repeats.
+(568 MB) so the 256 MB MALL cannot serve repeats.  read_floor_us: the same
+47,349,760 weight bytes of each copy read by a plain XOR-reduction kernel
+(qgpu_tensor_checksum, 8192 blocks x 256 threads, 4 x 16 B loads in flight per
+thread, one 4-byte store per block), timed the same way: the read bandwidth a
+kernel of this size reaches.
 
 cpu_baseline: the reference engine itself (oracle/_ref, compiled from the
 reference sources; AVX2, its own pinned thread pool) on the host cores:
 model mode runs the reference's speculative cycle on the same 27B model file
-for a bounded sample; gemv mode runs its gemv_batch; sample mode runs its
-sampled decode loop (sampler_sample + model_forward).
+after the same 512-token prompt (its batched prefill, then a bounded sample of
+cycles); gemv mode runs its gemv_batch; sample mode runs its sampled decode
+loop (sampler_sample + model_forward) after the same prompt.
 """
 import argparse
 import ctypes
 import json
 import os
 import shutil
+import subprocess
 import sys
 import tempfile
 import time
@@ -66,6 +72,7 @@ HBM_PEAK_GBS = 8000.0
 IQ4 = 23
 METRIC = "accepted tok/s, 27B IQ4_XS MTP k=3 on 1 GPU; gemv_batch HBM GB/s (% peak)"
 ROOF_KERNEL = "k_gemv_mfma<23, 1, 4, 0>"
+READ_BLOCKS = 8192      # plain-read floor launch: 8192 blocks x 256 threads (best of 1024..8192 at 47.7 MB)
 
 
 def log(*a):
@@ -82,8 +89,26 @@ def traffic_for(kernel):
         return None
 
 
+def host_info():
+    """The host as lscpu reports it, and the threads the CPU baselines use: the physical cores
+    of one NUMA node, capped by the CPUs this process may run on."""
+    info = {"affinity_cpus": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        kv = dict((k.strip(), v.strip()) for k, v in (ln.split(":", 1) for ln in out.splitlines() if ":" in ln))
+        info.update({"model": kv.get("Model name"), "sockets": int(kv.get("Socket(s)", 1)),
+                     "cores_per_socket": int(kv.get("Core(s) per socket", 0)),
+                     "threads_per_core": int(kv.get("Thread(s) per core", 1)),
+                     "numa_nodes": int(kv.get("NUMA node(s)", 1))})
+        node_cores = info["sockets"] * info["cores_per_socket"] // max(1, info["numa_nodes"])
+        info["threads_used"] = max(1, min(info["affinity_cpus"], node_cores or info["affinity_cpus"]))
+    except (OSError, ValueError, subprocess.SubprocessError):
+        info["threads_used"] = info["affinity_cpus"]
+    return info
+
+
 def host_cores():
-    return len(os.sched_getaffinity(0))
+    return host_info()["threads_used"]
 
 
 # ---------------------------------------------------------------------------------- CPU baselines
@@ -126,10 +151,10 @@ def cpu_baseline_gemv(W, x, ne0, ne1, n, seconds):
     algo = W.nbytes + n * (ne0 + ne1) * 4
     return {"value": round(algo * calls / el / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "reference",
             "sample": f"{calls} calls of the reference gemv_batch (IQ4_XS 17408x5120, B=4) over {el:.1f} s, "
-                      f"4 rotating weight copies, pool of {cores} pinned threads"}
+                      f"4 rotating weight copies, pool of {cores} pinned threads", "host": host_info()}
 
 
-def cpu_baseline_spec(path, prompt, k, seconds):
+def cpu_baseline_spec(path, prompt, k, seconds, gpu_prompt, kv_note):
     """The reference's greedy MTP speculative cycle (main.c:158-231) on the same model file."""
     drv = os.path.join(ROOT, "oracle", "_ref", "librefbench.so")
     if not os.path.exists(drv):
@@ -142,7 +167,8 @@ def cpu_baseline_spec(path, prompt, k, seconds):
     p = np.ascontiguousarray(prompt, np.uint32)
     out = (ctypes.c_double * 5)()
     cores = host_cores()
-    rc = L.ref_spec_bench(path.encode(), 256, p.ctypes.data_as(U), len(p), k, 1, 1000, seconds, cores, out)
+    n_ctx = len(p) + 1024                   # the loop stops before a cycle would pass n_ctx
+    rc = L.ref_spec_bench(path.encode(), n_ctx, p.ctypes.data_as(U), len(p), k, 1, 1000, seconds, cores, out)
     if rc == -1 or out[3] < 1:
         return None
     tps = out[2] / out[1]
@@ -151,10 +177,15 @@ def cpu_baseline_spec(path, prompt, k, seconds):
                       f"then {int(out[3])} greedy speculative cycles with k={k} over {out[1]:.1f} s "
                       f"({int(out[2])} tokens, {int(out[4])} drafts accepted), pool of {cores} pinned threads"
                       + ("; stopped early: a cycle accepted 2 drafts, which the reference cannot roll back"
-                         if rc == -2 else "")}
+                         if rc == -2 else ""),
+            "prompt_as_gpu_run": len(p) == gpu_prompt,
+            **({} if len(p) == gpu_prompt else {
+                "differs_from_gpu_run": f"prompt of {len(p)} tokens, not {gpu_prompt}: the cycles' attention spans "
+                                        f"{len(p)}+ instead of {gpu_prompt}+ positions ({kv_note})"}),
+            "host": host_info()}
 
 
-def cpu_baseline_sample(path, prompt, cfg, seconds):
+def cpu_baseline_sample(path, prompt, cfg, seconds, gpu_prompt):
     """The reference's sampled decode (main.c:232-248) on the same model file."""
     drv = os.path.join(ROOT, "oracle", "_ref", "librefbench.so")
     if not os.path.exists(drv):
@@ -168,13 +199,15 @@ def cpu_baseline_sample(path, prompt, cfg, seconds):
     out = (ctypes.c_double * 5)()
     cores = host_cores()
     temp, top_p, top_k, pen, seed = cfg
-    if L.ref_sample_bench(path.encode(), 256, p.ctypes.data_as(U), len(p), temp, top_p, top_k, pen, seed, 1000,
-                          seconds, cores, out) or out[2] < 1:
+    if L.ref_sample_bench(path.encode(), len(p) + 1024, p.ctypes.data_as(U), len(p), temp, top_p, top_k, pen, seed,
+                          1000, seconds, cores, out) or out[2] < 1:
         return None
     return {"value": round(out[2] / out[1], 4), "unit": "tok/s", "cores": cores, "kind": "reference",
             "sample": f"reference engine, same 27B model file, {len(p)}-token prompt (prefill {out[0]:.1f} s), "
                       f"then {int(out[2])} sampled tokens over {out[1]:.1f} s; sampler_sample "
-                      f"{1e6 * out[3] / out[4]:.0f} us per call; pool of {cores} pinned threads"}
+                      f"{1e6 * out[3] / out[4]:.0f} us per call; pool of {cores} pinned threads",
+            "prompt_as_gpu_run": len(p) == gpu_prompt,
+            "host": host_info()}
 
 
 # ---------------------------------------------------------------------------------- roofline microbench
@@ -224,6 +257,14 @@ def gemv_roofline(gpu, host, steps, warmup):
         for i in range(steps):
             gpu.ok(L.qgpu_gemv_prepared(Ts[i % R].h, B, ob.f32(), ne1, 0))
     ms_kernel = graph_ms(gpu, kernel_calls, e0, e1) / steps
+    # plain-read floor over the same device bytes: k_checksum over each rotating copy's records
+    dev_bytes = int(L.qgpu_tensor_device_bytes(Ts[0].h))
+    cs = gpu.buf(READ_BLOCKS * 4)
+
+    def read_calls():
+        for i in range(steps):
+            gpu.ok(L.qgpu_tensor_checksum(Ts[i % R].h, cs.u32(), READ_BLOCKS))
+    ms_read = graph_ms(gpu, read_calls, e0, e1) / steps
     for T in Ts:
         T.close()
     achieved = algo / (ms_kernel * 1e-3) / 1e9
@@ -231,6 +272,9 @@ def gemv_roofline(gpu, host, steps, warmup):
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(ROOF_KERNEL.split("<")[0]),
             "kernel": ROOF_KERNEL, "workload": "IQ4_XS 17408x5120, B=4", "kernel_us": round(ms_kernel * 1e3, 3),
             "algo_bytes": algo,
+            # the same weight bytes read by a plain XOR-reduction kernel (k_checksum), same rotation
+            "read_floor_us": round(ms_read * 1e3, 3), "read_floor_gbs": round(dev_bytes / (ms_read * 1e-3) / 1e9, 1),
+            "kernel_over_read_floor": round(ms_kernel / ms_read, 3),
             # dispatch ordinals of this kernel (0-based, in launch order) that the events bracket
             "dispatches": {"first": warmup + 3 * steps, "count": steps}}
     gemv_call_gbs = algo / (ms_call * 1e-3) / 1e9
@@ -345,7 +389,10 @@ def bench_model(args, gpu, host, roof, gemv_call_gbs):
     if path:
         try:
             log("CPU baseline: reference speculative loop on the host cores")
-            cpu = cpu_baseline_spec(path, prompt[:8], k, args.cpu_seconds)
+            kv = 2 * spec.n_kv_head * spec.head_dim * 4 * (spec.n_layer // spec.full_attn_interval)
+            kv_note = (f"the KV bytes a cycle reads at {n_prompt} positions are {kv * n_prompt / 1e6:.0f} MB, "
+                       f"{100 * kv * n_prompt / vbytes:.2f}% of the verify step's {vbytes / 1e9:.2f} GB")
+            cpu = cpu_baseline_spec(path, prompt, k, args.cpu_seconds, n_prompt, kv_note)
         finally:
             os.remove(path)
     value = len(toks) / t_dec
@@ -358,6 +405,8 @@ def bench_model(args, gpu, host, roof, gemv_call_gbs):
                                f"{K} cycles", "k": k, "prompt_tokens": n_prompt, "n_ctx": n_ctx,
                    "layers": "48 GDN + 16 GQA + MTP", "device": gpu.device_info()[0]},
         "tokens": int(len(toks)), "drafts_accepted": int(st.n_accepted), "drafts": int(st.n_drafts),
+        # accepted drafts per timed cycle: j_hist[j] = cycles that accepted j of the k drafts
+        "j_hist": [int(c) for c in np.bincount(np.asarray(js, np.int64), minlength=k + 1)[:k + 1]],
         "forced_accept_tok_s": round(len(ftoks) / fst.t_decode_s, 2),
         "verify_ms": round(ms_verify, 4), "decode_ms": round(ms_decode, 4), "draft_ms": round(ms_draft, 4),
         "verify_over_decode": round(ms_verify / ms_decode, 4),
@@ -449,7 +498,7 @@ def bench_sample(args, gpu, host, roof, gemv_call_gbs):
     if path:
         try:
             log("CPU baseline: reference sampled decode on the host cores")
-            cpu = cpu_baseline_sample(path, prompt[:8], SAMPLE_CFG, args.cpu_seconds)
+            cpu = cpu_baseline_sample(path, prompt, SAMPLE_CFG, args.cpu_seconds, n_prompt)
         finally:
             os.remove(path)
     temp, top_p, top_k, pen, seed = SAMPLE_CFG

@@ -217,7 +217,17 @@ void          qwen_model_set_host_sync(qwen_model_t *m, int on);
  * HIP graphs and replayed (default 0; environment QWEN_GRAPHS=1 sets 1) */
 void          qwen_model_set_graphs(qwen_model_t *m, int on);
 
-/* Profiling counters (reference model.h:151-152): seconds per section. */
+/* 1: model_forward times its sections on the device (below).  Default: on when
+ * QWEN_PROFILE is set (not "0") in the environment at model_init, the run-time
+ * form of the reference's compile-time QWEN_PROFILE (model.c:701-712). */
+void          qwen_model_set_profile(qwen_model_t *m, int on);
+
+/* Profiling counters (reference model.h:151-152, accumulated by model_forward as
+ * in model.c:714-742): seconds of device time per section -- the embedding row,
+ * the GDN layers, the attention layers, the output norm + lm_head -- between HIP
+ * events recorded on the library stream.  qwen_prof_calls counts model_forward
+ * calls; the sections stay 0 while profiling is off, as in a reference build
+ * without QWEN_PROFILE. */
 extern double qwen_prof_embed, qwen_prof_gdn, qwen_prof_attn, qwen_prof_head;
 extern uint64_t qwen_prof_calls;
 

@@ -183,6 +183,17 @@ int  qgpu_silu_mul(float *a, uint64_t lda, const float *b, uint64_t ldb, uint64_
 int  qgpu_add(float *y, uint64_t ldy, const float *x, uint64_t ldx, uint64_t n, int rows);
 /* device copy kernel (16-byte aligned, multiple of 16 bytes); graph-capturable */
 int  qgpu_copy(void *dst, const void *src, size_t bytes);
+/* Plain read of src (16-byte aligned, a multiple of 16 bytes) by n blocks
+ * (1..65536): block b writes to partials[b] (device) the XOR of the 32-bit words
+ * of its share, so the XOR of partials[0..n) is the XOR of every word of src.
+ * Stream-ordered, graph-capturable.  For device-memory integrity checks against
+ * a host XOR, and as the read-bandwidth floor the GEMV kernels are measured
+ * against (n = 2048).  No counterpart in the reference (no device memory there). */
+int  qgpu_checksum(const void *src, size_t bytes, uint32_t *partials, int n);
+/* qgpu_checksum over a tensor's device bytes: the tile records of the matrix-core
+ * formats, the GGUF rows of the others (qgpu_tensor_device_bytes of them) */
+int  qgpu_tensor_checksum(const qgpu_tensor *t, uint32_t *partials, int n);
+uint64_t qgpu_tensor_device_bytes(const qgpu_tensor *t);
 /* argmax of each of `rows` rows (lowest index wins ties; model.c:746-756) into out[r] */
 int  qgpu_argmax(const float *logits, uint64_t ld, uint32_t n, int rows, uint32_t *out);
 

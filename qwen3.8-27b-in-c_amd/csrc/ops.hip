@@ -177,6 +177,31 @@ __global__ void k_copy(uint4 *__restrict__ d, const uint4 *__restrict__ s, uint6
 
 __global__ void k_set_i32(int *dst, int v) { *dst = v; }
 
+// XOR of the 32-bit words of block b's grid-stride share of n16 16-byte words
+// into part[b]: 4 loads in flight per thread, one plain store per block (no
+// atomics: one address hit by every block serialises across the XCDs).
+#define CSUM_UNROLL 4
+__global__ __launch_bounds__(256) void k_checksum(const uint4 *__restrict__ s, uint64_t n16, uint32_t *part)
+{
+    const uint64_t nth = (uint64_t)gridDim.x * blockDim.x;
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + (CSUM_UNROLL - 1) * nth < n16; i += CSUM_UNROLL * nth) {
+        uint4 v[CSUM_UNROLL];
+#pragma unroll
+        for (int u = 0; u < CSUM_UNROLL; u++) v[u] = s[i + u * nth];
+#pragma unroll
+        for (int u = 0; u < CSUM_UNROLL; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += nth) { const uint4 v = s[i]; acc ^= v.x ^ v.y ^ v.z ^ v.w; }
+#pragma unroll
+    for (int o = 32; o; o >>= 1) acc ^= __shfl_xor(acc, o);
+    __shared__ uint32_t wsum[4];
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = wsum[0] ^ wsum[1] ^ wsum[2] ^ wsum[3];
+}
+
 __global__ void k_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int *pos, int *cur,
                               int nslot, uint32_t *out)
 {
@@ -228,6 +253,28 @@ extern "C" int qgpu_copy(void *dst, const void *src, size_t bytes)
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }
+
+// n blocks of 256 threads.  Measured on MI355X (graph replays, 12 rotating
+// 47.7 MB buffers): n = 8192 reads 47.7 MB in 8.7 us, n = 2048 in 9.6 us.
+extern "C" int qgpu_checksum(const void *src, size_t bytes, uint32_t *partials, int n)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!src || !partials || bytes % 16 || ((uintptr_t)src & 15) || n < 1 || n > 65536) return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_checksum, dim3((unsigned)n), dim3(256), 0, qg::stream, (const uint4 *)src,
+                       (uint64_t)(bytes / 16), partials);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_tensor_checksum(const qgpu_tensor *t, uint32_t *partials, int n)
+{
+    if (!t) return QGPU_E_ARG;
+    if (t->bytes % 16) return QGPU_E_RANGE;
+    return qgpu_checksum(t->data, t->bytes, partials, n);
+}
+
+extern "C" uint64_t qgpu_tensor_device_bytes(const qgpu_tensor *t) { return t ? t->bytes : 0; }
 
 static int ensure_small()
 {

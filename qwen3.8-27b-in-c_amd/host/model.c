@@ -57,6 +57,10 @@ struct qwen_gpu {
     int use_graphs, n_graphs;
     struct { int kind, flag; uint32_t B; const void *tok, *h, *lg; void *exec; } graphs[48];
     int status;               /* of the last call: 0, -1 rejected on the host, -2 device error */
+    /* section timing of model_forward: events before the embedding, after it, after each layer
+     * and after the head (n_layer + 3), recorded while prof_active */
+    int prof, prof_active, n_pev;
+    void **pev;
     void **allocs;
     size_t n_allocs, cap_allocs;
     qgpu_tensor **tensors;
@@ -127,6 +131,11 @@ static void gpu_free(qwen_gpu_t *g)
     if (!g) return;
     qgpu_sync();
     for (int i = 0; i < g->n_graphs; i++) qgpu_graph_destroy(g->graphs[i].exec);
+    if (g->pev) {
+        for (int i = 0; i < g->n_pev; i++)
+            if (g->pev[i]) qgpu_event_destroy(g->pev[i]);
+        free(g->pev);
+    }
     for (size_t i = 0; i < g->n_tensors; i++) qgpu_tensor_free(g->tensors[i]);
     for (size_t i = 0; i < g->n_allocs; i++) qgpu_free(g->allocs[i]);
     free(g->tensors);
@@ -337,6 +346,8 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
          * kernels, not the dispatch), so kernels are launched from the host by default. */
         const char *ge = getenv("QWEN_GRAPHS");
         g->use_graphs = ge && ge[0] == '1';
+        const char *pe = getenv("QWEN_PROFILE");
+        g->prof = pe && pe[0] && pe[0] != '0';
     }
     g->L = calloc(d->n_layer, sizeof *g->L);
     for (uint32_t il = 0; il < d->n_layer; il++)
@@ -574,10 +585,8 @@ static int mat_packed(const qgpu_tensor *W)
 static void ffn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B)
 {
     qwen_gpu_t *g = m->gpu;
-    const uint64_t E = m->dims.n_embd, F = m->dims.n_ff;
-    const float eps = m->cfg.rms_norm_eps;
+    const uint64_t F = m->dims.n_ff;
     /* post-attention RMSNorm -> gate/up (model.c:469-476) */
-    (void)eps;
     const qgpu_act an = act_norm_res(m, R, D->post_norm, g->bxb);
     const qgpu_tensor *W[2] = { D->ffn_gate, D->ffn_up };
     float *outs[2] = { g->bffn, g->bqkv };
@@ -595,7 +604,6 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
 {
     qwen_gpu_t *g = m->gpu;
     const qwen_dims_t *d = &m->dims;
-    const uint64_t E = d->n_embd;
     const float eps = m->cfg.rms_norm_eps;
     const qgpu_act an = act_norm_res(m, R, D->attn_norm, g->bxb);
     const qgpu_tensor *W[3] = { D->q, D->k, D->v };
@@ -625,7 +633,7 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
 {
     qwen_gpu_t *g = m->gpu;
     const qwen_dims_t *d = &m->dims;
-    const uint64_t E = d->n_embd, di = d->d_inner;
+    const uint64_t di = d->d_inner;
     const float eps = m->cfg.rms_norm_eps;
     const qgpu_act an = act_norm_res(m, g->bx, D->attn_norm, g->bxb);
     const qgpu_tensor *W[4] = { D->wqkv, D->wgate, D->beta, D->alpha };
@@ -645,6 +653,49 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     ffn_dev(m, D, g->bx, B);
 }
 
+/* Section timing of model_forward (reference model.c:697-742, printed by main.c
+ * --profile): while prof_active, forward_body records an event before the
+ * embedding, after it, after every layer and after the head; prof_collect then
+ * adds the device time between consecutive events to qwen_prof_embed,
+ * qwen_prof_gdn / qwen_prof_attn (by layer kind) and qwen_prof_head.  It is on
+ * when QWEN_PROFILE is set in the environment at model_init (the reference's
+ * compile-time switch of that name) or after qwen_model_set_profile(m, 1). */
+static void prof_mark(qwen_gpu_t *g, uint32_t i)
+{
+    if (g->prof_active) K(qgpu_event_record(g->pev[i]));
+}
+
+static int prof_begin(qwen_model_t *m)
+{
+    qwen_gpu_t *g = m->gpu;
+    if (!g->prof || qwen_dev_err) return 0;
+    if (!g->pev) {
+        g->pev = calloc(m->dims.n_layer + 3, sizeof *g->pev);
+        if (!g->pev) return 0;
+        g->n_pev = (int)m->dims.n_layer + 3;
+        for (uint32_t i = 0; i < m->dims.n_layer + 3; i++) K(qgpu_event_create(&g->pev[i]));
+        if (qwen_dev_err) return 0;
+    }
+    g->prof_active = 1;
+    return 1;
+}
+
+static void prof_collect(qwen_model_t *m)
+{
+    qwen_gpu_t *g = m->gpu;
+    const uint32_t nl = m->dims.n_layer;
+    g->prof_active = 0;
+    for (uint32_t i = 0; i <= nl + 1 && !qwen_dev_err; i++) {
+        float ms = 0.0f;
+        K(qgpu_event_elapsed_ms(g->pev[i], g->pev[i + 1], &ms));
+        const double sec = 1e-3 * (double)ms;
+        if (i == 0) qwen_prof_embed += sec;
+        else if (i == nl + 1) qwen_prof_head += sec;
+        else if (g->L[i - 1].rec) qwen_prof_gdn += sec;
+        else qwen_prof_attn += sec;
+    }
+}
+
 /* Graph cache: the launch sequence of a body depends only on its pointers, B
  * and flag (positions and the GDN ring index are read from device memory), so
  * it is captured once and replayed; replay cuts the per-kernel launch gap. */
@@ -655,7 +706,7 @@ static void run_body(qwen_model_t *m, int kind, body_fn fn, const uint32_t *tok,
                      float *lg, int flag)
 {
     qwen_gpu_t *g = m->gpu;
-    if (!g->use_graphs) { fn(m, tok, h, B, lg, flag); return; }
+    if (!g->use_graphs || g->prof_active) { fn(m, tok, h, B, lg, flag); return; }
     for (int i = 0; i < g->n_graphs; i++)
         if (g->graphs[i].kind == kind && g->graphs[i].tok == tok && g->graphs[i].h == h && g->graphs[i].lg == lg &&
             g->graphs[i].B == B && g->graphs[i].flag == flag) {
@@ -680,13 +731,17 @@ static void forward_body(qwen_model_t *m, const uint32_t *d_tokens, const float 
     qwen_gpu_t *g = m->gpu;
     const qwen_dims_t *d = &m->dims;
     const uint64_t E = d->n_embd, V = m->cfg.vocab_size;
+    prof_mark(g, 0);
     K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bx, E));
+    prof_mark(g, 1);
     for (uint32_t il = 0; il < d->n_layer; il++) {
         if (g->L[il].rec) gdn_dev(m, &g->L[il], B);
         else attn_dev(m, &g->L[il], g->bx, B, 0);
+        prof_mark(g, 2 + il);
     }
     const qgpu_act an = act_norm_res(m, g->bx, g->out_norm, g->bxb);
     K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
+    prof_mark(g, 2 + d->n_layer);
     if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
 }
 
@@ -755,14 +810,14 @@ void model_forward(qwen_model_t *m, pool_t *pool, uint32_t token, uint32_t pos)
     (void)pool;
     if (call_begin(m)) return;
     if (bad_span(m, pos, 1) || token >= m->cfg.vocab_size) { reject(m, "model_forward", pos, 1); return; }
-    const double t0 = now_s();
     put_tokens(m, &token, 1);
+    const int prof = prof_begin(m);
     forward_dev(m, m->gpu->d_tok, 1, pos, m->gpu->logits1, 0);
+    if (prof) prof_collect(m);
     if (m->host_sync) {
         K(qgpu_memcpy_d2h(m->logits, m->gpu->logits1, (size_t)m->cfg.vocab_size * sizeof(float)));
         K(qgpu_memcpy_d2h(m->x, m->gpu->bx, m->dims.n_embd * sizeof(float)));
     }
-    qwen_prof_head += now_s() - t0;
     qwen_prof_calls++;
     m->pos = pos + 1;
     call_end(m);
@@ -1184,3 +1239,4 @@ void qwen_model_set_pos(qwen_model_t *m, uint32_t pos) { m->pos = pos; }
 int qwen_model_status(const qwen_model_t *m) { return (m && m->gpu) ? m->gpu->status : -1; }
 void qwen_model_set_host_sync(qwen_model_t *m, int on) { m->host_sync = on; }
 void qwen_model_set_graphs(qwen_model_t *m, int on) { if (m && m->gpu) m->gpu->use_graphs = on ? 1 : 0; }
+void qwen_model_set_profile(qwen_model_t *m, int on) { if (m && m->gpu) m->gpu->prof = on ? 1 : 0; }

@@ -5,6 +5,7 @@
     prof_summary.py traffic FETCH_DB WRITE_DB --bench-json FILE [--calib-bytes N]
     prof_summary.py sweep   BENCH_JSON --cmd "<command that made it>"
     prof_summary.py steps   DB_OR_DIR --cmd "<command that made it>" [--rows 4] [--title T]
+    prof_summary.py counters DB [DB ...] --bench-json FILE --cmd "<commands that made them>"
 
 stats   : per-kernel calls / total / average duration of a --kernel-trace run,
           and, given the benchmark's JSON line, the average duration of the
@@ -18,12 +19,20 @@ traffic : HBM bytes per launch of the roofline kernel from two --pmc runs
           same counter reads for the k_copy kernel of known size (the
           benchmark's --copy-calib: 5 copies of 256 MiB).  Prints JSON.
 sweep   : the table of a `bench.py --mode sweep` line (formats x shapes x B).
+counters: every PMC counter of one or more --pmc runs of `bench.py --mode gemv`,
+          averaged per launch over the roofline kernel's bracketed dispatches
+          and over the plain-read kernel (k_checksum) of the read floor, side
+          by side: the GEMV's instruction mix and vector-memory path against a
+          kernel that only reads the same bytes.
 steps   : per-kernel time of one verify step of a --kernel-trace run of the model
           benchmark.  The trace is cut after every k_argmax_final; a verify step
           is a piece that ends in the argmax of --rows rows (drafts and decode
           steps end in a one-row argmax).  Durations are averaged over all verify
           steps of the run (the timed spec cycles, forced acceptance and the
-          step timings).
+          step timings).  A second table gives each kernel's role in the step
+          (from its place in the launch order), its algorithmic HBM bytes per
+          launch (27B hybrid dimensions, --pos KV positions) and the achieved
+          fraction of 8 TB/s.
 """
 import argparse
 import glob
@@ -145,6 +154,48 @@ def cmd_traffic(a):
         indent=1))
 
 
+def counter_table(db):
+    """{counter: {kernel: [per-dispatch value in dispatch order]}} of one --pmc run"""
+    c = sqlite3.connect(find_db(db))
+    rows = c.execute("select kernel_name, dispatch_id, counter_name, value from counters_collection "
+                     "order by dispatch_id").fetchall()
+    acc = {}
+    for name, did, cn, v in rows:
+        acc.setdefault(cn, {}).setdefault(short(name), {}).setdefault(did, 0.0)
+        acc[cn][short(name)][did] += v
+    return {cn: {k: [d[i] for i in sorted(d)] for k, d in per.items()} for cn, per in acc.items()}
+
+
+def cmd_counters(a):
+    b = bench_line(a.bench_json)
+    r = b["roofline"]
+    first, count = r["dispatches"]["first"], r["dispatches"]["count"]
+    out = ["# PMC counters: the roofline GEMV against a plain read of the same bytes", "",
+           "Commands (`/root/repo` is the repository root; one rocprofv3 --pmc pass per line):", "", "```",
+           *a.cmd.split(" ;; "), "```", "",
+           f"Per launch, averaged over the {count} bracketed dispatches of `{r['kernel']}` ({r.get('workload', '')}, "
+           f"{r['algo_bytes']:,} algorithmic bytes) and over the last {count} dispatches of `k_checksum` (the read "
+           f"floor: the same {r['algo_bytes'] - 4 * (5120 + 17408) * 4:,} weight bytes, XOR-reduced).  Values are summed over the "
+           "counter's instances (XCDs, SEs, channels) of one dispatch.", "",
+           "| counter | GEMV per launch | read kernel per launch | GEMV / read |", "|---|---:|---:|---:|"]
+    seen = {}
+    for db in a.dbs:
+        for cn, per in counter_table(db).items():
+            g = per.get(r["kernel"], [])[first:first + count]
+            rd = per.get("k_checksum", [])[-count:]
+            if len(g) == count and rd:
+                seen[cn] = (statistics.fmean(g), statistics.fmean(rd))
+    for cn in sorted(seen):
+        gv, rv = seen[cn]
+        out.append(f"| {cn} | {gv:,.0f} | {rv:,.0f} | {gv / rv:.2f} |" if rv else f"| {cn} | {gv:,.0f} | {rv:,.0f} | - |")
+    if "TCP_TCC_READ_REQ_sum" in seen:
+        gv, rv = seen["TCP_TCC_READ_REQ_sum"]
+        out += ["", f"L2 read requests from the CUs (TCP_TCC_READ_REQ): GEMV {gv:,.0f} per launch, read kernel "
+                    f"{rv:,.0f} ({gv / rv:.2f}x) for the same weight bytes; the excess is the activation digit "
+                    "tiles every row tile reads again from L2."]
+    print("\n".join(out))
+
+
 def cmd_sweep(a):
     b = bench_line(a.bench_json)
     rows = b["sweep"]
@@ -172,6 +223,63 @@ def cmd_sweep(a):
             cells.append(f"{p['us']:.1f} | {p['gbs']:.0f} ({100 * p['frac']:.0f}%)" if p else " | ")
         out.append(f"| {f} | {nr} x {nc} | {wmb:.1f} | " + " | ".join(cells) + " |")
     print("\n".join(out))
+
+
+# The 27B hybrid's dimensions (hidden 5120, FFN 17408, vocab 248320; GDN: 16 key heads and
+# 48 value heads of 128, conv kernel 4; attention: 24 query / 4 KV heads of 256, q||gate)
+D27 = dict(E=5120, F=17408, V=248320, KD=2048, VD=6144, VH=48, HS=128, CONV=10240, QD=6144, KV=1024)
+IQ4_ROW = lambda cols: cols // 256 * 136        # bytes of one IQ4_XS row
+DIGITS = 3                                      # activation digit bytes per element (int8 x 3)
+
+
+def step_roles(step, B, P):
+    """(role, bytes) of each dispatch of one verify step, by kernel name, grid and what came before"""
+    d, f4 = D27, 4
+    out, prev, n_part = [], "", 0
+    for name, _, dur, gx, wx in step:
+        k, grid = short(name), gx // max(wx, 1)
+        if k.startswith("k_dequant_rows"):
+            role, by = "embedding rows (dequant)", B * IQ4_ROW(d["E"]) + B * d["E"] * f4
+        elif k == "k_prep_act<4>":
+            role = "RMSNorm prep (+ residual partials)"
+            by = (1 + n_part) * B * d["E"] * f4 + d["E"] * f4 + B * d["E"] * (2 * f4 + DIGITS)
+        elif k == "k_prep_act<3>":
+            role, by = "gated-norm prep (GDN out)", 2 * B * d["VD"] * f4 + B * d["VD"] * (f4 + DIGITS)
+        elif k == "k_prep_act<2>":
+            role, by = "SiLU x up prep", 2 * B * d["F"] * f4 + B * d["F"] * (f4 + DIGITS)
+        elif k.startswith("k_gemv_mfma") and (k.endswith(", 2>") or k.endswith(", 3>")):
+            ks = max(1, grid // (d["E"] // 16))
+            cols = {"k_prep_act<3>": d["VD"], "k_attn_combine_act": d["QD"], "k_prep_act<2>": d["F"]}.get(prev, 0)
+            role = {"k_prep_act<3>": "GEMV ssm_out (K-split)", "k_attn_combine_act": "GEMV attn_output (K-split)",
+                    "k_prep_act<2>": "GEMV ffn_down (K-split)"}.get(prev, "GEMV K-split (?)")
+            by = d["E"] * IQ4_ROW(cols) + B * cols * DIGITS + ks * B * d["E"] * f4
+            n_part = ks
+        elif k.startswith("k_gemv_mfma"):
+            rows = {1030: d["CONV"] + d["VD"] + 2 * d["VH"], 896: 2 * d["QD"] + 2 * d["KV"], 2176: 2 * d["F"],
+                    15520: d["V"]}.get(grid, grid * 16)
+            role = {1030: "GEMV GDN in (qkv, z, beta, alpha)", 896: "GEMV attention q||gate, k, v",
+                    2176: "GEMV ffn_gate + ffn_up", 15520: "GEMV lm_head"}.get(grid, f"GEMV {rows} rows")
+            by = rows * IQ4_ROW(d["E"]) + B * d["E"] * DIGITS + B * rows * f4
+            if grid != 15520:
+                n_part = 0
+        elif k == "k_gdn_fused":
+            state = d["VH"] * d["HS"] * d["HS"] * f4
+            role = "GDN conv + recurrence + snapshots"
+            by = (1 + B) * state + (1 + B) * d["CONV"] * 3 * f4 + B * (d["CONV"] + d["VD"] + 2 * d["VH"]) * f4
+        elif k.startswith("k_attn_span"):
+            role = "attention spans (KV read)"
+            by = P * 2 * d["KV"] * f4 + B * (2 * d["QD"] + 2 * d["KV"]) * f4
+        elif k == "k_attn_combine_act":
+            role, by = "attention combine + o-proj prep", B * d["QD"] * (2 * f4 + DIGITS)
+        elif k == "k_copy":
+            role, by = "hidden-state copy (h_save)", 2 * B * d["E"] * f4
+        elif k.startswith("k_argmax"):
+            role, by = "argmax", B * d["V"] * f4 if k == "k_argmax_part" else 0
+        else:
+            role, by = k, 0
+        out.append((role, k, grid, wx, dur, by))
+        prev = k
+    return out
 
 
 def cmd_steps(a):
@@ -205,6 +313,30 @@ def cmd_steps(a):
             continue
         out.append(f"| `{name}` | {gb} x {wx} | {cnt / n:.1f} | {tot / cnt / 1e3:.2f} | {tot / n / 1e3:.1f} | "
                    f"{100 * tot / n / busy:.1f} |")
+    roles = {}
+    for g in steps:
+        for role, k, gb, wx, dur, by in step_roles(g, a.rows, a.pos):
+            r = roles.setdefault((role, k), [0, 0.0, 0.0])
+            r[0] += 1
+            r[1] += dur
+            r[2] += by
+    tot_by = sum(r[2] for r in roles.values()) / n
+    out += ["", f"## HBM fraction per kernel role (B = {a.rows}, {a.pos} KV positions)", "",
+            "Algorithmic bytes per launch: the weights a GEMV streams (IQ4_XS rows of the 27B matrices) plus its",
+            "activation digits in and fp32 outputs (or K-split partial planes) out; a preparation's fp32 rows in",
+            "(residual + partial planes, gate and up, ...) and its fp32 rows and digit planes out; GDN: the state",
+            "read, B state snapshots written, conv state and inputs/outputs; attention: the K and V rows of every",
+            "position.  GB/s = bytes / average duration; fraction of 8000 GB/s.",
+            "", "| role | kernel | launches per step | avg us | MB per launch | GB/s | fraction | % of step time |",
+            "|---|---|---:|---:|---:|---:|---:|---:|"]
+    for (role, k), (cnt, dur, by) in sorted(roles.items(), key=lambda kv: -kv[1][1]):
+        if dur / n / 1e3 < a.min_us:
+            continue
+        gbs = by / dur if dur else 0.0          # bytes / ns = GB/s
+        out.append(f"| {role} | `{k}` | {cnt / n:.1f} | {dur / cnt / 1e3:.2f} | {by / cnt / 1e6:.2f} | {gbs:.0f} | "
+                   f"{gbs / 8000:.3f} | {100 * dur / n / busy:.1f} |")
+    out += ["", f"Whole step: {tot_by / 1e9:.2f} GB algorithmic in {busy / 1e3:.1f} us of kernel time = "
+                f"{tot_by / busy:.0f} GB/s ({tot_by / busy / 8000:.3f} of 8 TB/s)."]
     print("\n".join(out))
 
 
@@ -232,8 +364,14 @@ def main():
     st.add_argument("--rows", type=int, default=4)
     st.add_argument("--title", default=None)
     st.add_argument("--min-us", type=float, default=1.0, help="omit kernels below this many us per step")
+    st.add_argument("--pos", type=int, default=640, help="KV positions of the verify steps (bytes of attention)")
+    cn = sub.add_parser("counters")
+    cn.add_argument("dbs", nargs="+")
+    cn.add_argument("--bench-json", required=True)
+    cn.add_argument("--cmd", required=True, help="the commands, separated by ' ;; '")
     a = ap.parse_args()
-    {"stats": cmd_stats, "traffic": cmd_traffic, "sweep": cmd_sweep, "steps": cmd_steps}[a.cmd_name](a)
+    {"stats": cmd_stats, "traffic": cmd_traffic, "sweep": cmd_sweep, "steps": cmd_steps,
+     "counters": cmd_counters}[a.cmd_name](a)
 
 
 if __name__ == "__main__":

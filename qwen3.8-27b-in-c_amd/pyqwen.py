@@ -271,6 +271,7 @@ class GpuLib:
                             ctypes.c_uint32, ctypes.POINTER(u64), U32P],
             "qgpu_gemv_prepare": [F32P, u64, i32, u64], "qgpu_gemv_prepared": [vp, i32, F32P, u64, i32],
             "qgpu_copy": [vp, vp, ctypes.c_size_t],
+            "qgpu_checksum": [vp, ctypes.c_size_t, U32P, i32], "qgpu_tensor_checksum": [vp, U32P, i32],
             "qgpu_gdn_conv": [F32P, u64, i32, i32, F32P, F32P, u64, i32, ctypes.POINTER(i32), F32P, u64],
             "qgpu_gdn_recurrence": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, u64, i32, ctypes.POINTER(i32),
                                     i32, i32, i32, i32, f32, F32P, u64],
@@ -303,6 +304,8 @@ class GpuLib:
         L.qgpu_strerror.restype = ctypes.c_char_p
         L.qgpu_tensor_bytes.argtypes = [vp]
         L.qgpu_tensor_bytes.restype = u64
+        L.qgpu_tensor_device_bytes.argtypes = [vp]
+        L.qgpu_tensor_device_bytes.restype = u64
         self.ok(L.qgpu_init(device))
 
     def ok(self, rc):
@@ -391,6 +394,7 @@ def _model_lib():
     L.qwen_model_set_pos.argtypes = [vp, u32]
     L.qwen_model_set_host_sync.argtypes = [vp, i32]
     L.qwen_model_set_graphs.argtypes = [vp, i32]
+    L.qwen_model_set_profile.argtypes = [vp, i32]
     L.model_generate_spec.argtypes = [vp, U32P, u32, u32, u32, u32, i32, U32P, U32P, ctypes.POINTER(GenStats)]
     L.model_generate_spec.restype = u32
     L.model_spec_begin.argtypes = [vp, U32P, u32, u32]
@@ -428,6 +432,15 @@ class Model:
             raise QgpuError(f"model_init failed ({path or 'synthetic'})")
         self.V = self.L.qwen_model_get(self.h, b"vocab")
         self.E = self.L.qwen_model_get(self.h, b"n_embd")
+
+    def set_profile(self, on):
+        self.L.qwen_model_set_profile(self.h, 1 if on else 0)
+
+    def prof_counters(self):
+        """the reference's section counters (seconds) and model_forward call count"""
+        out = {k: ctypes.c_double.in_dll(self.L, f"qwen_prof_{k}").value for k in ("embed", "gdn", "attn", "head")}
+        out["calls"] = ctypes.c_uint64.in_dll(self.L, "qwen_prof_calls").value
+        return out
 
     def status(self):
         """0 = last call done, -1 = rejected on the host, -2 = device error (include/model.h)"""

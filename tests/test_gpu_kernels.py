@@ -58,6 +58,30 @@ def test_tensor_repack_roundtrip(gpu, fmt):
     assert np.array_equal(gpu.tensor_download(T), z["W"])
 
 
+@pytest.mark.parametrize("nbytes,n", [(16, 1), (16, 3), (4096, 7), (1 << 20, 2048),
+                                      ((47710208 // 16) * 16 + 16 * 999, 2048)])
+def test_checksum_is_the_xor_of_the_words(gpu, nbytes, n):
+    """qgpu_checksum: the XOR of the n per-block partials is the XOR of the 32-bit words, for
+    buffers smaller than one block, within the grid and past it (grid-stride tail)"""
+    a = np.random.default_rng(nbytes % 1000).integers(0, 2 ** 32, nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    src, part = gpu.put(a), gpu.put(np.full(n, 0xDEADBEEF, np.uint32))
+    gpu.ok(gpu.L.qgpu_checksum(ctypes.c_void_p(src.ptr), nbytes, part.u32(), n))
+    assert np.bitwise_xor.reduce(part.download(np.uint32)) == np.bitwise_xor.reduce(a)
+    assert gpu.L.qgpu_checksum(ctypes.c_void_p(src.ptr), 12, part.u32(), n) == -1      # QGPU_E_ARG
+    assert gpu.L.qgpu_checksum(ctypes.c_void_p(src.ptr), nbytes, part.u32(), 0) == -1
+
+
+def test_tensor_checksum_of_unpacked_rows(gpu):
+    """a tensor kept in GGUF rows on the device (F32) checksums to the XOR of the uploaded bytes"""
+    z = load("gemv_F32_512x64.npz")
+    T = gpu.tensor(z["W"], int(z["type"]), 512, 64)
+    part = gpu.put(np.zeros(64, np.uint32))
+    assert gpu.L.qgpu_tensor_device_bytes(T.h) == z["W"].nbytes
+    gpu.ok(gpu.L.qgpu_tensor_checksum(T.h, part.u32(), 64))
+    assert np.bitwise_xor.reduce(part.download(np.uint32)) == \
+        np.bitwise_xor.reduce(np.frombuffer(z["W"].tobytes(), np.uint32))
+
+
 @pytest.mark.parametrize("fmt", FORMATS)
 def test_dequant_rows_bitexact(gpu, fmt):
     z = load(f"gemv_{fmt}_512x64.npz")

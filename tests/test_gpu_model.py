@@ -12,6 +12,7 @@ gap of the fixtures is above 0.3, so the streams must be identical).
 import hashlib
 import os
 import tempfile
+import time
 
 import numpy as np
 import pytest
@@ -315,6 +316,36 @@ def test_model_forward_batch_and_sequential_vs_reference(gpu, tiny):
     sref = z["seq_logits"].reshape(8, V)
     for b in range(8):
         assert rel_err(seq[b], sref[b]) < 1e-3, b
+    m.close()
+
+
+def test_model_forward_section_profile(gpu, tiny):
+    """The reference's --profile counters (model.c:697-742): with profiling on, model_forward adds
+    the device time of the embedding, the GDN layers, the attention layers and the head; the
+    logits are those of the run without profiling; with it off only the call count moves."""
+    path, z = tiny
+    p = z["prompt"]
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    plain = np.array([m.forward(int(p[i]), i) for i in range(6)])
+    c0 = m.prof_counters()
+    m.reset()
+    m.set_profile(1)
+    t0 = time.perf_counter()
+    prof = np.array([m.forward(int(p[i]), i) for i in range(6)])
+    wall = time.perf_counter() - t0
+    c1 = m.prof_counters()
+    assert np.array_equal(plain, prof)
+    d = {k: c1[k] - c0[k] for k in c1}
+    print(f"  sections over 6 calls: {d}", flush=True)
+    assert d["calls"] == 6
+    for k in ("embed", "gdn", "attn", "head"):
+        assert d[k] > 0, k
+    assert d["embed"] + d["gdn"] + d["attn"] + d["head"] < wall
+    assert d["gdn"] > d["embed"]
+    m.set_profile(0)
+    m.forward(int(p[6]), 6)
+    c2 = m.prof_counters()
+    assert c2["calls"] == c1["calls"] + 1 and all(c2[k] == c1[k] for k in ("embed", "gdn", "attn", "head"))
     m.close()
 
 
