@@ -602,7 +602,27 @@ static __device__ __forceinline__ void rms_reduce(const GemvArgs &args, int wv, 
 // code, not inline asm: its input comes straight from an MFMA, and the
 // compiler inserts the MFMA-to-VALU wait states only for instructions it
 // generates itself.
-static __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+#ifndef GEMV_MAD_SEP
+#define GEMV_MAD_SEP 1
+#endif
+static __device__ __forceinline__ int mad24(int a, int b, int c)
+{
+    int r = __mul24(a, b) + c;
+#if GEMV_MAD_SEP
+    // an empty asm between the multiply-adds of a chain: the compiler otherwise
+    // turns pairs of them into two multiplies and a v_add3_u32 (3 instructions
+    // for 2 products instead of 2 v_mad_i32_i24)
+    asm("" : "+v"(r));
+#endif
+    return r;
+}
+
+// Registers 0..2 of a lane's MFMA result are digits 0..2 of its token; register 3
+// (digit slot 3) is always zero -- its A lanes load nothing -- so the scale and
+// accumulate steps stop at DIGIT_REGS.
+#ifndef DIGIT_REGS
+#define DIGIT_REGS 3
+#endif
 
 // IQ4_NL codebook split across two 8-entry v_perm_b32 tables indexed by the
 // whole nibble q: perm(XH:XL, q) + perm(YH:YL, q ^ 8) = c(q).  Selectors 8..15
@@ -697,7 +717,7 @@ static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, cons
                 aop, by, __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, bx, (v4i){0, 0, 0, 0}, 0, 0, 0), 0, 0, 0);
             // |D| < 2^19, |wsc| <= 32: exact 24-bit multiply-add
 #pragma unroll
-            for (int i = 0; i < 4; i++) acci[a][i] = mad24(D[i], wsc, acci[a][i]);
+            for (int i = 0; i < DIGIT_REGS; i++) acci[a][i] = mad24(D[i], wsc, acci[a][i]);
         }
     }
     const float d = h2f(w.hdr.x & 0xFFFFu);
@@ -705,7 +725,7 @@ static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, cons
     for (int a = 0; a < NA; a++) {
         const float xg = tok_scale(x.xt[a], g);
 #pragma unroll
-        for (int v = 0; v < 4; v++) accf[a][v] += (float)acci[a][v] * ((d * p8(v)) * xg);   // d 2^(8 v): exact
+        for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += (float)acci[a][v] * ((d * p8(v)) * xg);   // d 2^(8 v): exact
     }
 }
 
@@ -773,7 +793,7 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
 #pragma unroll
         for (int a = 0; a < NA; a++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) accs[a][i] = 0.0f;
+            for (int i = 0; i < DIGIT_REGS; i++) accs[a][i] = 0.0f;
 #pragma unroll
         for (int ib = 0; ib < 8; ib++) {
             const uint4 q = w.q[ib >> 1];
@@ -783,14 +803,14 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
             for (int a = 0; a < NA; a++) {
                 const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(kq_aop<NA>(x, a, ib), b, z4, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; i++) accs[a][i] = fmaf((float)D[i], dib, accs[a][i]);
+                for (int i = 0; i < DIGIT_REGS; i++) accs[a][i] = fmaf((float)D[i], dib, accs[a][i]);
             }
         }
 #pragma unroll
         for (int a = 0; a < NA; a++) {
             const float xg = tok_scale(x.xt[a], g);
 #pragma unroll
-            for (int v = 0; v < 4; v++) accf[a][v] += accs[a][v] * (p8(v) * xg);
+            for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += accs[a][v] * (p8(v) * xg);
         }
     } else if constexpr (FMT == T_Q6_K) {
         const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
@@ -813,7 +833,7 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
                 const v4i DB = __builtin_amdgcn_mfma_i32_16x16x32_i8(
                     aop, kq_b(0, hi), __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, kq_b(0, NEG32), z4, 0, 0, 0), 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[a][i] = mad24(DA[i], sa, mad24(DB[i], sb2, acc[a][i]));
+                for (int i = 0; i < DIGIT_REGS; i++) acc[a][i] = mad24(DA[i], sa, mad24(DB[i], sb2, acc[a][i]));
             }
         }
         const float d = h2f(w.d & 0xFFFFu);
@@ -821,7 +841,7 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
         for (int a = 0; a < NA; a++) {
             const float xg = tok_scale(x.xt[a], g);
 #pragma unroll
-            for (int v = 0; v < 4; v++) accf[a][v] += (float)acc[a][v] * ((d * p8(v)) * xg);
+            for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += (float)acc[a][v] * ((d * p8(v)) * xg);
         }
     } else {                                                   // Q4_K, Q5_K
         const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
@@ -844,7 +864,7 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
                 const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, kq_b(lo, hi), z4, 0, 0, 0);
                 acm[a] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop, kq_b(mrep, mrep), acm[a], 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; i++) acq[a][i] = mad24(D[i], sc, acq[a][i]);
+                for (int i = 0; i < DIGIT_REGS; i++) acq[a][i] = mad24(D[i], sc, acq[a][i]);
             }
         }
         const float d = h2f(w.hdr.x & 0xFFFFu), dm = h2f(w.hdr.x >> 16);
@@ -852,7 +872,7 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
         for (int a = 0; a < NA; a++) {
             const float xg = tok_scale(x.xt[a], g);
 #pragma unroll
-            for (int v = 0; v < 4; v++)
+            for (int v = 0; v < DIGIT_REGS; v++)
                 accf[a][v] += (float)acq[a][v] * ((d * p8(v)) * xg) - (float)acm[a][v] * ((dm * p8(v)) * xg);
         }
     }
@@ -933,7 +953,9 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
     if (MODE & IQ4_RMS) rms_reduce(args, wv, NW, lane, rp, rsc);
     // registers 0..3 of lane (g, n) hold digits 0..3 of token g, row n: sum them
 #pragma unroll
-    for (int a = 0; a < NA; a++) red[wv][a][g][n] = (accf[a][0] + accf[a][1]) + (accf[a][2] + accf[a][3]);
+    for (int a = 0; a < NA; a++)
+        red[wv][a][g][n] = DIGIT_REGS == 3 ? (accf[a][0] + accf[a][1]) + accf[a][2]
+                                           : (accf[a][0] + accf[a][1]) + (accf[a][2] + accf[a][3]);
     __syncthreads();
     for (int e = tid; e < NA * 64; e += NW * 64) {     // (plane, token, row) entries of the tile
         const int a = e >> 6, i = (e >> 4) & 3, nn = e & 15;
