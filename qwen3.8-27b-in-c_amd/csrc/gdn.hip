@@ -147,9 +147,10 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float *__restrict__ xq,
 // tokens, into LDS.  Conv-state snapshots are written once per channel: q/k
 // channels by the block (h < n_k, rb = 0), v channels by their own block.
 // Every global load of the block (state rows, conv windows and inputs of all
-// tokens, gates) is issued before the first use; the norms and q.k of all
-// tokens are reduced together before the (sequential) recurrence, which then
-// needs two row sums per token.
+// tokens, gates) is issued before the first use; the L2 norms and q.k of all
+// tokens are computed before the (sequential) recurrence, which then needs two
+// row sums per token.  The state is read from ring slot *cur and the state after
+// token b is written to slot (*cur + 1 + b) % nslot.
 __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, uint64_t ldx, const float *__restrict__ cw,
                                                    float *__restrict__ cring, uint64_t cstride,
                                                    const float *__restrict__ beta_raw, const float *__restrict__ alpha_raw,
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
                                                    int n_k, int n_v, float eps, float *__restrict__ out, uint64_t ldo)
 {
     __shared__ float Yq[GDN_MAXB][GDN_HK], Yk[GDN_MAXB][GDN_HK], Yv[GDN_MAXB][GDN_RB];
-    __shared__ float Gbeta[GDN_MAXB], Gdec[GDN_MAXB];
+    __shared__ float Gbeta[GDN_MAXB], Gdec[GDN_MAXB], Gkq[GDN_MAXB];
     const int h = blockIdx.x / (GDN_HK / GDN_RB);
     const int rb = blockIdx.x % (GDN_HK / GDN_RB);
     const int tid = threadIdx.x;
@@ -233,47 +234,52 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
         }
     }
     __syncthreads();
-    // ---- L2 norms (kernels.c:780-805) and q.k of every token: independent of the state
-    float qsv[GDN_MAXB], ksv[GDN_MAXB], kqv[GDN_MAXB];
-#pragma unroll
-    for (int b = 0; b < GDN_MAXB; b++) {
-        qsv[b] = ksv[b] = kqv[b] = 0.0f;
-        if (b >= B) continue;
+    // ---- L2 norms (kernels.c:780-805) and q.k of every token, off the recurrence's serial path:
+    // row group b (16 lanes) of the block handles token b, normalises its q and k in LDS and
+    // keeps k.q of the normalised vectors
+    if (r < B) {
+        const int b = r;
         const float4 q0 = *(const float4 *)&Yq[b][cc * 8], q1 = *(const float4 *)&Yq[b][cc * 8 + 4];
         const float4 k0 = *(const float4 *)&Yk[b][cc * 8], k1 = *(const float4 *)&Yk[b][cc * 8 + 4];
-        const float q[8] = { q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w };
-        const float k[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+        float q[8] = { q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w };
+        float k[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
         float qq = 0.0f, kk = 0.0f, kq = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) { qq = fmaf(q[i], q[i], qq); kk = fmaf(k[i], k[i], kk); kq = fmaf(k[i], q[i], kq); }
-        qsv[b] = rowsum16(qq);
-        ksv[b] = rowsum16(kk);
-        kqv[b] = rowsum16(kq);
+        qq = rowsum16(qq);
+        kk = rowsum16(kk);
+        kq = rowsum16(kq);
+        const float qn = sqrtf(qq), kn = sqrtf(kk);
+        const float qs = 1.0f / (qn > eps ? qn : eps), ks = 1.0f / (kn > eps ? kn : eps);
+#pragma unroll
+        for (int i = 0; i < 8; i++) { q[i] *= qs; k[i] *= ks; }
+        // every lane of the row group holds the same sums; all write the same values
+        *(float4 *)&Yq[b][cc * 8] = make_float4(q[0], q[1], q[2], q[3]);
+        *(float4 *)&Yq[b][cc * 8 + 4] = make_float4(q[4], q[5], q[6], q[7]);
+        *(float4 *)&Yk[b][cc * 8] = make_float4(k[0], k[1], k[2], k[3]);
+        *(float4 *)&Yk[b][cc * 8 + 4] = make_float4(k[4], k[5], k[6], k[7]);
+        if (cc == 0) Gkq[b] = kq * qs * ks;
     }
+    __syncthreads();
     // ---- delta-rule recurrence: o = (g S q + d (k.q)) / sqrt(128), S <- g S + d k^T (model.c:494-615)
     const float qscale = 1.0f / sqrtf((float)GDN_HK);
     float S[8] = { sa.x, sa.y, sa.z, sa.w, sbv.x, sbv.y, sbv.z, sbv.w };
 #pragma unroll
     for (int b = 0; b < GDN_MAXB; b++) {
         if (b >= B) break;
-        const float qn = sqrtf(qsv[b]), kn = sqrtf(ksv[b]);
-        const float qs = 1.0f / (qn > eps ? qn : eps), ks = 1.0f / (kn > eps ? kn : eps);
-        const float kq = kqv[b] * qs * ks;
         const float4 q0 = *(const float4 *)&Yq[b][cc * 8], q1 = *(const float4 *)&Yq[b][cc * 8 + 4];
         const float4 k0 = *(const float4 *)&Yk[b][cc * 8], k1 = *(const float4 *)&Yk[b][cc * 8 + 4];
-        float q[8] = { q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w };
-        float k[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
+        const float q[8] = { q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w };
+        const float k[8] = { k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w };
         float sk = 0.0f, sq = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            q[i] *= qs;
-            k[i] *= ks;
             sk = fmaf(S[i], k[i], sk);
             sq = fmaf(S[i], q[i], sq);
         }
         sk = rowsum16(sk);
         sq = rowsum16(sq);
-        const float beta = Gbeta[b], decay = Gdec[b];
+        const float beta = Gbeta[b], decay = Gdec[b], kq = Gkq[b];
         const float vj = Yv[b][r];
         const float dj = (vj - decay * sk) * beta;
         if (cc == 0) out[(uint64_t)b * ldo + (uint64_t)h * GDN_HK + j] = (decay * sq + dj * kq) * qscale;
@@ -368,3 +374,4 @@ extern "C" int qgpu_gdn_fused(const float *x, uint64_t ldx, int B, int conv_dim,
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }
+
