@@ -40,6 +40,12 @@ typedef struct {
     int32_t  tie_shift;                      /* 1: output.weight row v = token_embd row v-1 (mod
                                                 vocab), so the greedy next token of t is t+1
                                                 unless the layers outweigh the embedding  */
+    int32_t  tokenizer;                      /* 1: the GGUF also carries a byte-level BPE
+                                                vocabulary (tokenizer.ggml.model "gpt2",
+                                                .tokens, .merges): ids 0..255 the byte
+                                                symbols, then a few merged tokens, fillers,
+                                                and <|endoftext|>, <|im_start|>, <|im_end|>
+                                                as the last three ids (vocab >= 300)     */
 } qwen_synth_spec_t;
 
 /* The 27B hybrid: 48 GDN + 16 GQA layers + MTP, H=5120, F=17408, V=248320, all IQ4_XS. */

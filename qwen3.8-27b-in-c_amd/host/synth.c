@@ -403,15 +403,89 @@ static int w_str(FILE *f, const char *s) { uint64_t n = strlen(s); return w_u64(
 static int kv_u32(FILE *f, const char *k, uint32_t v) { return w_str(f, k) || w_u32(f, GGUF_TYPE_UINT32) || w_u32(f, v); }
 static int kv_f32(FILE *f, const char *k, float v) { return w_str(f, k) || w_u32(f, GGUF_TYPE_FLOAT32) || w_bytes(f, &v, 4); }
 
+/* The byte-level symbol of byte b (the GPT-2 byte-to-unicode map): the printable
+ * bytes '!'..'~', 0xA1..0xAC and 0xAE..0xFF stand for themselves, every other
+ * byte for code point 256 + its rank among those others; as UTF-8 in out[4]. */
+static void byte_symbol(int b, char out[4])
+{
+    int cp = b, rank = 0;
+    const int printable = (b >= '!' && b <= '~') || (b >= 0xA1 && b <= 0xAC) || (b >= 0xAE && b <= 0xFF);
+    if (!printable) {
+        for (int c = 0; c < b; c++)
+            if (!((c >= '!' && c <= '~') || (c >= 0xA1 && c <= 0xAC) || (c >= 0xAE && c <= 0xFF))) rank++;
+        cp = 256 + rank;
+    }
+    if (cp < 0x80) { out[0] = (char)cp; out[1] = 0; }
+    else { out[0] = (char)(0xC0 | (cp >> 6)); out[1] = (char)(0x80 | (cp & 0x3F)); out[2] = 0; }
+}
+
+/* merges of the synthetic vocabulary (left, right), in rank order; "\x20" is written as its symbol */
+static const char *const SYN_MERGES[][2] = {
+    { "t", "h" }, { "th", "e" }, { " ", "t" }, { "e", "r" }, { "i", "n" }, { "o", "n" },
+    { "a", "n" }, { " ", "a" }, { " t", "he" }, { "e", "s" }, { "o", "r" }, { "l", "l" },
+};
+#define N_SYN_MERGES (sizeof SYN_MERGES / sizeof SYN_MERGES[0])
+
+/* a piece of a merge as vocabulary text: every byte as its symbol */
+static void syn_text(const char *piece, char *out, size_t cap)
+{
+    size_t n = 0;
+    for (const unsigned char *c = (const unsigned char *)piece; *c && n + 3 < cap; c++) {
+        char sym[4];
+        byte_symbol(*c, sym);
+        for (const char *q = sym; *q; q++) out[n++] = *q;
+    }
+    out[n] = 0;
+}
+
+static void syn_token(const qwen_synth_spec_t *s, uint32_t id, char *out, size_t cap)
+{
+    if (id < 256) { byte_symbol((int)id, out); return; }
+    if (id < 256 + N_SYN_MERGES) {
+        char l[32], r[32];
+        syn_text(SYN_MERGES[id - 256][0], l, sizeof l);
+        syn_text(SYN_MERGES[id - 256][1], r, sizeof r);
+        snprintf(out, cap, "%s%s", l, r);
+        return;
+    }
+    if (id == s->vocab - 3) { snprintf(out, cap, "<|endoftext|>"); return; }
+    if (id == s->vocab - 2) { snprintf(out, cap, "<|im_start|>"); return; }
+    if (id == s->vocab - 1) { snprintf(out, cap, "<|im_end|>"); return; }
+    snprintf(out, cap, "<|t%u|>", id);
+}
+
+static int write_tokenizer(FILE *f, const qwen_synth_spec_t *s)
+{
+    int err = w_str(f, "tokenizer.ggml.model") | w_u32(f, GGUF_TYPE_STRING) | w_str(f, "gpt2");
+    err |= w_str(f, "tokenizer.ggml.tokens") | w_u32(f, GGUF_TYPE_ARRAY) | w_u32(f, GGUF_TYPE_STRING) |
+           w_u64(f, s->vocab);
+    for (uint32_t id = 0; id < s->vocab; id++) {
+        char t[64];
+        syn_token(s, id, t, sizeof t);
+        err |= w_str(f, t);
+    }
+    err |= w_str(f, "tokenizer.ggml.merges") | w_u32(f, GGUF_TYPE_ARRAY) | w_u32(f, GGUF_TYPE_STRING) |
+           w_u64(f, N_SYN_MERGES);
+    for (size_t m = 0; m < N_SYN_MERGES; m++) {
+        char l[32], r[32], t[72];
+        syn_text(SYN_MERGES[m][0], l, sizeof l);
+        syn_text(SYN_MERGES[m][1], r, sizeof r);
+        snprintf(t, sizeof t, "%s %s", l, r);
+        err |= w_str(f, t);
+    }
+    return err;
+}
+
 int qwen_synth_write_gguf(const qwen_synth_spec_t *s, const char *path)
 {
     const char *A = "qwen35";
     const uint32_t nt = qwen_synth_count(s);
+    if (s->tokenizer && s->vocab < 256 + N_SYN_MERGES + 3) return -1;
     FILE *f = fopen(path, "wb");
     if (!f) return -1;
     char k[128];
     int err = 0;
-    const uint32_t n_kv = 20;
+    const uint32_t n_kv = 20 + (s->tokenizer ? 3 : 0);
     err |= w_u32(f, GGUF_MAGIC) | w_u32(f, 3) | w_u64(f, nt) | w_u64(f, n_kv);
     err |= w_str(f, "general.architecture") | w_u32(f, GGUF_TYPE_STRING) | w_str(f, A);
     err |= kv_u32(f, "general.alignment", 32);
@@ -440,6 +514,7 @@ int qwen_synth_write_gguf(const qwen_synth_spec_t *s, const char *path)
         err |= w_str(f, k) | w_u32(f, GGUF_TYPE_ARRAY) | w_u32(f, GGUF_TYPE_UINT32) | w_u64(f, 4);
         err |= w_bytes(f, secs, sizeof secs);
     }
+    if (s->tokenizer) err |= write_tokenizer(f, s);
 #undef KU
 #undef KF
     uint64_t off = 0;

@@ -51,7 +51,7 @@ class SynthSpec(ctypes.Structure):
         + [(n, ctypes.c_int32) for n in "type_default type_embd type_output type_qkv type_eh_proj".split()]
         + [("gain_output", ctypes.c_float), ("seed", ctypes.c_uint64)]
         + [("gain_embd", ctypes.c_float), ("gain_resid", ctypes.c_float), ("mtp_diag", ctypes.c_int32),
-           ("norm_sigma", ctypes.c_float), ("tie_shift", ctypes.c_int32)])
+           ("norm_sigma", ctypes.c_float), ("tie_shift", ctypes.c_int32), ("tokenizer", ctypes.c_int32)])
 
 
 class SynthTensor(ctypes.Structure):
@@ -116,8 +116,10 @@ class HostLib:
         if self.L.qwen_synth_write_gguf(ctypes.byref(spec), path.encode()):
             raise OSError(f"writing {path} failed")
 
-    def write_tiny_gguf(self, path, seed, mixed=0):
-        self.write_gguf(self.spec_tiny(seed, mixed), path)
+    def write_tiny_gguf(self, path, seed, mixed=0, tokenizer=0):
+        spec = self.spec_tiny(seed, mixed)
+        spec.tokenizer = tokenizer
+        self.write_gguf(spec, path)
 
     def tensors(self, spec):
         n = self.L.qwen_synth_count(ctypes.byref(spec))

@@ -64,3 +64,25 @@ def test_reference_program_builds_against_libqwen(tmp_path, name):
     defined = subprocess.run(["nm", "--defined-only", exe], check=True, capture_output=True, text=True).stdout
     for sym in ("model_init", "gemv_batch", "gguf_open", "dequant_row"):
         assert f" T {sym}\n" not in defined, sym
+
+
+def test_reference_tokenizer_test_runs_on_libqwen(tmp_path):
+    """The reference's test_tokenizer, linked with libqwen.so (its gguf_open and the
+    mapped file it leaves in gguf_context_t feed the reference tokenizer), prints the
+    same encodings as the same program on the reference engine, for a GGUF that
+    carries a byte-level BPE vocabulary; every prompt decodes back to itself."""
+    from qwen_pkg import host_lib
+    ref_exe = os.path.join(ROOT, "oracle", "_ref", "test_tokenizer_cpu")
+    if not os.path.exists(ref_exe):
+        pytest.skip("oracle/_ref/test_tokenizer_cpu not built")
+    exe = compile_program("test_tokenizer", str(tmp_path))
+    gguf = str(tmp_path / "tok.gguf")
+    host_lib().write_tiny_gguf(gguf, 1234, 2, tokenizer=1)
+    ours = subprocess.run([exe, gguf], capture_output=True, text=True, timeout=60)
+    ref = subprocess.run([ref_exe, gguf], capture_output=True, text=True, timeout=60)
+    assert ours.returncode == 0 and ref.returncode == 0, ours.stderr + ref.stderr
+    assert ours.stdout == ref.stdout
+    assert "vocab_size = 1024, n_merges = 12" in ours.stdout
+    prompts = [ln.split('"', 1)[1].rsplit('"', 1)[0] for ln in ours.stdout.splitlines() if ln.startswith("Prompt [")]
+    decoded = [ln.split('"', 1)[1].rsplit('"', 1)[0] for ln in ours.stdout.splitlines() if ln.startswith("Decoded:")]
+    assert len(prompts) == 5 and decoded == prompts
