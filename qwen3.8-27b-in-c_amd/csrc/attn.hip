@@ -88,11 +88,18 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
 // The number of spans follows the live context: ntl tiles hold positions
 // 0..pos+B-1; nsl = ceil(ntl / tps) spans of tps tiles, for at most nspan
 // spans (the launch size); blocks past nsl exit and the combine skips them.
-// partials: pml [n_kv][nspan][ATT_MAXQ][2] (m, l), po [n_kv][nspan][ATT_MAXQ][ATT_HD]
+// partials: pml [n_kv][nspan][ATT_MAXQ][2] (m, l), po [n_kv][nspan][ATT_MAXQ][ATT_HD]; m is the
+// running maximum of the scores in log2 units (q.k / sqrt(hd) * log2 e), l = sum of exp2(s - m)
 #define ATT_TP    16          // positions per tile
 #define ATT_MAXB  8           // new positions per fused call
 #ifndef ATT_NSPAN
 #define ATT_NSPAN 64          // spans per kv head at most
+#endif
+#ifndef ATT_PF
+#define ATT_PF 1              // tiles whose K/V loads are in flight while one is computed
+#endif
+#ifndef ATT_NW3
+#define ATT_NW3 8             // waves of the three-row-tile span kernel
 #endif
 #ifndef ATT_MINTPS
 #define ATT_MINTPS 1          // tiles per span at least
@@ -126,6 +133,30 @@ static __device__ __forceinline__ void span_split(int pos0, int B, int nspan, in
     nsl = (ntl + tps - 1) / tps;
 }
 
+// 16-lane row reductions with DPP moves; each step combines a value with its mirror
+// image, so every lane of a row ends with the same bits
+template <int CTRL>
+static __device__ __forceinline__ float dpp_mov(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+static __device__ __forceinline__ float rowsum16(float v)
+{
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);   // row_half_mirror
+    v += dpp_mov<0x140>(v);   // row_mirror
+    return v;
+}
+static __device__ __forceinline__ float rowmax16(float v)
+{
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return v;
+}
+
 static __device__ __forceinline__ float wsum64(float v)
 {
 #pragma unroll
@@ -147,7 +178,10 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     constexpr int SXF = 2 * ATT_NWV * NRT * 64 * 4;               // floats of the score exchange
     __shared__ float lds[FUSED && NRT * 16 * ATT_HD > SXF ? NRT * 16 * ATT_HD : SXF];   // q rows (FUSED), then the score exchange
     __shared__ float Kn[FUSED ? ATT_MAXB : 1][ATT_HD];   // new k rows, normalised and rotated
+    __shared__ float Vn[FUSED ? ATT_MAXB : 1][ATT_HD];   // new v rows
     __shared__ float Rc[FUSED ? ATT_MAXB * ATT_HD / 2 : 1], Rs[FUSED ? ATT_MAXB * ATT_HD / 2 : 1];   // RoPE tables
+    __shared__ __attribute__((aligned(16))) float Pl[2 * NRT * 256];   // probabilities [buf][rt][gq][n][v]
+    __shared__ __attribute__((aligned(16))) float Al[2 * NRT * 16];    // rescale factors [buf][row]
     const int g = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, gq = lane >> 4;
@@ -160,7 +194,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     // rows and the norm weights
     constexpr int QV = FUSED ? NRT * 16 * 64 / (ATT_NWV * 64) : 1;   // float4 of q rows per thread
     constexpr int KV = FUSED ? ATT_MAXB * 64 / (ATT_NWV * 64) : 1;
-    float4 qv[QV], knv[KV], qw = make_float4(0.0f, 0.0f, 0.0f, 0.0f), kw = qw;
+    float4 qv[QV], knv[KV], vnv[KV], qw = make_float4(0.0f, 0.0f, 0.0f, 0.0f), kw = qw;
     v4f qop[NRT][ATT_NQ];
     if (FUSED) {
 #pragma unroll
@@ -175,8 +209,11 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 #pragma unroll
         for (int u = 0; u < KV; u++) {
             const int e = tid + u * ATT_NWV * 64, b = e >> 6, d4 = e & 63;
-            knv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (b < p.B) knv[u] = *(const float4 *)(p.k + (uint64_t)b * p.ldkv + hoff + 4 * d4);
+            knv[u] = vnv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (b < p.B) {
+                knv[u] = *(const float4 *)(p.k + (uint64_t)b * p.ldkv + hoff + 4 * d4);
+                vnv[u] = *(const float4 *)(p.v + (uint64_t)b * p.ldkv + hoff + 4 * d4);
+            }
         }
         qw = *(const float4 *)(p.qw + 4 * lane);
         kw = *(const float4 *)(p.kw + 4 * lane);
@@ -198,40 +235,51 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     const int tile0 = s * tps, tile1 = min(tile0 + tps, ntl);
     const int posA = tile0 * ATT_TP, posB = min(tile1 * ATT_TP, tmax + 1);   // positions of this span
 
-    // ---- operand loads of tile t (positions beyond the live end read as zeros).  K rows of
-    // the new positions (FUSED) come from Kn once the prologue has prepared them:
-    // load_k(t, kr, 0) loads the cached rows only, load_k(t, kr, 1) then fills the new ones.
-    auto load_k = [&](int t, v4f *kr, int new_rows) {
-        const int pp = t * ATT_TP + n;
-        if (FUSED && new_rows) {
-            if (pp >= pos0 && pp <= tmax)
+    // ---- operand loads of tile tt into a ring slot: the cached K and V rows through buffer loads
+    // at 32-bit offsets from this kv head's row 0.  Rows past the live end read row tmax instead
+    // (the mask gives them probability 0, and the row is finite).  FUSED: the rows of positions
+    // pos0.. (not in the caches before this launch) are replaced from Kn and Vn when the tile is
+    // used.  Every lane loads every tile, so the loads are straight-line code and the wait for a
+    // slot counts exactly the loads issued after it.
+    const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void *)(p.kc + hoff), 0, 0x7FFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void *)(p.vc + hoff), 0, 0x7FFFFFFF, 0x00020000);
+    const uint32_t rowb = (uint32_t)kvrow * 4u;
+    // a tile whose rows are all live: lane offsets of the tile's first row (computed once) plus the
+    // tile's row offset in a scalar register; the last tile of the live context: clamped rows
+    const uint32_t kofs = (uint32_t)n * rowb + (uint32_t)(d0 + 4 * gq) * 4u;
+    uint32_t vofs[4];
 #pragma unroll
-                for (int q = 0; q < ATT_NQ; q++) kr[q] = *(const v4f *)&Kn[pp - pos0][d0 + 16 * q + 4 * gq];
-            return;
+    for (int v = 0; v < 4; v++) vofs[v] = (uint32_t)(4 * gq + v) * rowb + (uint32_t)(d0 + ATT_NQ * n) * 4u;
+    auto load_kv = [&](int tt, v4f *kr_, vqf *vr_) {
+        const int p0 = tt * ATT_TP;
+        uint32_t ko = kofs, vo[4] = { vofs[0], vofs[1], vofs[2], vofs[3] }, so = (uint32_t)p0 * rowb;
+        if (p0 + ATT_TP - 1 > tmax) {             // wave-uniform
+            ko = (uint32_t)min(p0 + n, tmax) * rowb + (uint32_t)(d0 + 4 * gq) * 4u;
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                vo[v] = (uint32_t)min(p0 + 4 * gq + v, tmax) * rowb + (uint32_t)(d0 + ATT_NQ * n) * 4u;
+            so = 0;
         }
 #pragma unroll
-        for (int q = 0; q < ATT_NQ; q++) kr[q] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        if (pp <= tmax && (!FUSED || pp < pos0))
-#pragma unroll
-            for (int q = 0; q < ATT_NQ; q++)
-                kr[q] = *(const v4f *)(p.kc + (uint64_t)pp * kvrow + hoff + d0 + 16 * q + 4 * gq);
-    };
-    auto load_v = [&](int t, vqf *vr) {
+        for (int q = 0; q < ATT_NQ; q++)
+            kr_[q] = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rsK, ko + 64u * q, so, 0));
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int pp = t * ATT_TP + 4 * gq + v;
-            vr[v] = vqf{};
-            if (pp <= tmax) {
-                if (FUSED && pp >= pos0) vr[v] = *(const vqf *)(p.v + (uint64_t)(pp - pos0) * p.ldkv + hoff + d0 + ATT_NQ * n);
-                else vr[v] = *(const vqf *)(p.vc + (uint64_t)pp * kvrow + hoff + d0 + ATT_NQ * n);
-            }
+            if constexpr (ATT_NQ == 4)
+                vr_[v] = __builtin_bit_cast(vqf, __builtin_amdgcn_raw_buffer_load_b128(rsV, vo[v], so, 0));
+            else
+                vr_[v] = __builtin_bit_cast(vqf, __builtin_amdgcn_raw_buffer_load_b64(rsV, vo[v], so, 0));
         }
     };
-    // the first tile's operands are in flight during the q preparation
-    v4f kr[ATT_NQ];
-    vqf vr[4];
-    load_k(tile0, kr, 0);
-    load_v(tile0, vr);
+    // a ring of ATT_PF + 1 operand slots: tile t sits in slot (t - tile0) % (ATT_PF + 1), and the
+    // loads of tiles t + 1 .. t + ATT_PF are in flight while tile t is computed.  The first
+    // ATT_PF tiles' loads are issued before the q preparation.
+    constexpr int NSL = ATT_PF + 1;
+    v4f kr[NSL][ATT_NQ];
+    vqf vr[NSL][4];
+#pragma unroll
+    for (int u = 0; u < ATT_PF; u++)
+        if (tile0 + u < tile1) load_kv(tile0 + u, kr[u], vr[u]);
 
     if (FUSED) {
         float (*Qs)[ATT_HD] = (float (*)[ATT_HD])lds;
@@ -255,6 +303,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         for (int u = 0; u < KV; u++) {
             const int e = tid + u * ATT_NWV * 64;
             *(float4 *)&Kn[e >> 6][4 * (e & 63)] = knv[u];
+            *(float4 *)&Vn[e >> 6][4 * (e & 63)] = vnv[u];
         }
 #pragma unroll
         for (int u = 0; u < ATT_MAXB * ATT_HD / 2 / (ATT_NWV * 64); u++) {
@@ -297,7 +346,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 if (t < posA || t >= posB) continue;
                 const uint64_t row = (uint64_t)t * kvrow + hoff + 4 * d4;
                 st_stream4(p.kc + row, *(const float4 *)&Kn[b][4 * d4]);
-                st_stream4(p.vc + row, *(const float4 *)(p.v + (uint64_t)b * p.ldkv + hoff + 4 * d4));
+                st_stream4(p.vc + row, *(const float4 *)&Vn[b][4 * d4]);
             }
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++)
@@ -307,28 +356,44 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     }
 
     v4f oacc[NRT][ATT_NQ];
-    float mrow[NRT], lrow[NRT];
-    int lim[NRT];                                 // last position row rt*16 + n may see (-1: padding row)
 #pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        mrow[rt] = -INFINITY;
-        lrow[rt] = 0.0f;
-        const int r = rt * 16 + n;
-        lim[rt] = r < QH ? pos0 + r / per : -1;
+    for (int rt = 0; rt < NRT; rt++)
 #pragma unroll
         for (int c = 0; c < ATT_NQ; c++) oacc[rt][c] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    const float scale = 1.0f / sqrtf((float)ATT_HD);
+    // scores in log2 units: q.k / sqrt(hd) * log2(e), so probabilities are exp2 of differences
+    const float scale = 1.4426950408889634f / sqrtf((float)ATT_HD);
     v4f *Sx = (v4f *)lds;                         // [2][ATT_NWV][NRT][64]
-    if (FUSED) load_k(tile0, kr, 1);
-    for (int t = tile0; t < tile1; t++) {
+    const float *Sf = (const float *)lds;
+    constexpr int SM_UPW = (NRT * 4 + ATT_NWV - 1) / ATT_NWV;    // softmax units per wave
+    float sm[SM_UPW], sl[SM_UPW];
+    int slim[SM_UPW];
+#pragma unroll
+    for (int j = 0; j < SM_UPW; j++) {
+        const int R = 4 * (wv + j * ATT_NWV) + (lane >> 4);
+        sm[j] = -INFINITY;
+        sl[j] = 0.0f;
+        slim[j] = R < QH ? pos0 + R / per : -1;
+    }
+    for (int t0 = tile0; t0 < tile1; t0 += NSL)
+#pragma unroll
+    for (int u = 0; u < NSL; u++) {
+        const int t = t0 + u;
+        if (t >= tile1) break;
         const int buf = (t - tile0) & 1;
-        v4f kn[ATT_NQ];
-        vqf vn[4];
-        if (t + 1 < tile1) {
-            load_k(t + 1, kn, 0);
-            if (FUSED) load_k(t + 1, kn, 1);
-            load_v(t + 1, vn);
+        if (t + ATT_PF < tile1) load_kv(t + ATT_PF, kr[(u + ATT_PF) % NSL], vr[(u + ATT_PF) % NSL]);
+        if (FUSED && t * ATT_TP + ATT_TP - 1 >= pos0) {   // rows of new positions, prepared in Kn, Vn
+            const int pp = t * ATT_TP + n, b = min(max(pp - pos0, 0), p.B - 1);
+#pragma unroll
+            for (int q = 0; q < ATT_NQ; q++) {
+                const v4f kn = *(const v4f *)&Kn[b][d0 + 16 * q + 4 * gq];
+                if (pp >= pos0) kr[u][q] = kn;
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int pv_ = t * ATT_TP + 4 * gq + v, bv = min(max(pv_ - pos0, 0), p.B - 1);
+                const vqf vn = *(const vqf *)&Vn[bv][d0 + ATT_NQ * n];
+                if (pv_ >= pos0) vr[u][v] = vn;
+            }
         }
         // partial score tiles over this wave's dims
 #pragma unroll
@@ -337,65 +402,61 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 #pragma unroll
             for (int q = 0; q < ATT_NQ; q++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) sp = mfma4(kr[q][j], qop[rt][q][j], sp);
+                for (int j = 0; j < 4; j++) sp = mfma4(kr[u][q][j], qop[rt][q][j], sp);
             Sx[((buf * ATT_NWV + wv) * NRT + rt) * 64 + lane] = sp;
+        }
+        __syncthreads();
+        // softmax: unit su (rows 4 su .. 4 su + 3 of the block, 16 positions: one value per lane)
+        // is owned by wave su % NWV, which keeps the running max / sum of its rows
+#pragma unroll
+        for (int j = 0; j < SM_UPW; j++) {
+            const int su = wv + j * ATT_NWV;
+            if (su < NRT * 4) {
+                const int R = 4 * su + (lane >> 4), pq = lane & 15, rt = R >> 4, nr = R & 15;
+                const int li = ((pq >> 2) * 16 + nr) * 4 + (pq & 3);     // float of lane (pq/4, nr), register pq%4
+                float sc = Sf[((buf * ATT_NWV + 0) * NRT + rt) * 256 + li];
+#pragma unroll
+                for (int w = 1; w < ATT_NWV; w++) sc += Sf[((buf * ATT_NWV + w) * NRT + rt) * 256 + li];
+                const int pp = t * ATT_TP + pq;
+                const float sv = pp <= slim[j] ? sc * scale : -INFINITY;
+                const float mnew = fmaxf(sm[j], rowmax16(sv));
+                const float alpha = mnew > -INFINITY ? __builtin_amdgcn_exp2f(sm[j] - mnew) : 1.0f;   // 0 for the first live tile
+                const float pv = sv > -INFINITY ? __builtin_amdgcn_exp2f(sv - mnew) : 0.0f;
+                sl[j] = sl[j] * alpha + rowsum16(pv);
+                sm[j] = mnew;
+                Pl[(((buf * NRT + rt) * 4 + (pq >> 2)) * 16 + nr) * 4 + (pq & 3)] = pv;
+                if (pq == 0) Al[buf * NRT * 16 + R] = alpha;
+            }
         }
         __syncthreads();
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
-            v4f st = Sx[((buf * ATT_NWV + 0) * NRT + rt) * 64 + lane];
+            const v4f pv = *(const v4f *)&Pl[(((buf * NRT + rt) * 4 + gq) * 16 + n) * 4];
+            const v4f al = *(const v4f *)&Al[buf * NRT * 16 + rt * 16 + 4 * gq];
+            // rescale the O rows 4gq + w by their rows' factor
 #pragma unroll
-            for (int w = 1; w < ATT_NWV; w++) st += Sx[((buf * ATT_NWV + w) * NRT + rt) * 64 + lane];
-            float sv[4];
-            float mx = -INFINITY;
+            for (int w = 0; w < 4; w++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int pp = t * ATT_TP + 4 * gq + v;
-                sv[v] = pp <= lim[rt] ? st[v] * scale : -INFINITY;
-                mx = fmaxf(mx, sv[v]);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mnew = fmaxf(mrow[rt], mx);
-            float alpha = 1.0f, pv[4], ps = 0.0f;
-            if (mnew > -INFINITY) alpha = expf(mrow[rt] - mnew);     // exp(-inf) = 0 for the first live tile
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                pv[v] = sv[v] > -INFINITY ? expf(sv[v] - mnew) : 0.0f;
-                ps += pv[v];
-            }
-            ps += __shfl_xor(ps, 16);
-            ps += __shfl_xor(ps, 32);
-            lrow[rt] = lrow[rt] * alpha + ps;
-            mrow[rt] = mnew;
-            // rescale the O rows 4gq + w by their rows' factor (held by lane 4gq + w)
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const float aw = __shfl(alpha, 4 * gq + w);
-#pragma unroll
-                for (int c = 0; c < ATT_NQ; c++) oacc[rt][c][w] *= aw;
-            }
+                for (int c = 0; c < ATT_NQ; c++) oacc[rt][c][w] *= al[w];
 #pragma unroll
             for (int v = 0; v < 4; v++)
 #pragma unroll
-                for (int c = 0; c < ATT_NQ; c++) oacc[rt][c] = mfma4(pv[v], vr[v][c], oacc[rt][c]);
-        }
-        if (t + 1 < tile1) {
-#pragma unroll
-            for (int q = 0; q < ATT_NQ; q++) kr[q] = kn[q];
-#pragma unroll
-            for (int v = 0; v < 4; v++) vr[v] = vn[v];
+                for (int c = 0; c < ATT_NQ; c++) oacc[rt][c] = mfma4(pv[v], vr[u][v][c], oacc[rt][c]);
         }
     }
     // ---- partials of this span
     float *ml = p.pml + ((uint64_t)g * p.nspan + s) * ATT_MAXQ * 2;
     float *o = p.po + ((uint64_t)g * p.nspan + s) * ATT_MAXQ * ATT_HD;
 #pragma unroll
-    for (int rt = 0; rt < NRT; rt++) {
-        if (wv == 0 && gq == 0 && rt * 16 + n < QH) {
-            ml[2 * (rt * 16 + n)] = mrow[rt];
-            ml[2 * (rt * 16 + n) + 1] = lrow[rt];
+    for (int j = 0; j < SM_UPW; j++) {
+        const int R = 4 * (wv + j * ATT_NWV) + (lane >> 4);
+        if ((lane & 15) == 0 && wv + j * ATT_NWV < NRT * 4 && R < QH) {
+            ml[2 * R] = sm[j];
+            ml[2 * R + 1] = sl[j];
         }
+    }
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++) {
 #pragma unroll
         for (int w = 0; w < 4; w++) {
             const int r = rt * 16 + 4 * gq + w;
@@ -423,6 +484,16 @@ static __device__ __forceinline__ float combine_one(const float *q, uint64_t ldq
     const float *mlg = pml + (uint64_t)g * nspan * ATT_MAXQ * 2 + 2 * qi;
     const float *pog = po + (uint64_t)g * nspan * ATT_MAXQ * ATT_HD + (uint64_t)qi * ATT_HD + d;
     const float gate = q[(uint64_t)b * ldq + (uint64_t)h * 2 * ATT_HD + ATT_HD + d];
+    // every o load of the call first, 16 spans at a step: they do not depend on the (m, l)
+    // reduction, so the call waits for one memory latency.  Past nc a load repeats span nc - 1
+    // (finite) and that span's weight f is 0 below, so the padding terms add 0.
+    float ov[ATT_NSPAN];
+#pragma unroll
+    for (int c0 = 0; c0 < ATT_NSPAN; c0 += 16)
+        if (c0 < nc)
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                ov[c0 + j] = pog[(uint64_t)(c0 + j < nc ? c0 + j : nc - 1) * ATT_MAXQ * ATT_HD];
     float mc[ATT_SPL], lc[ATT_SPL], f[ATT_SPL];
     float m = -INFINITY;
 #pragma unroll
@@ -441,27 +512,23 @@ static __device__ __forceinline__ float combine_one(const float *q, uint64_t ldq
     float l = 0.0f;
 #pragma unroll
     for (int u = 0; u < ATT_SPL; u++) {
-        f[u] = mc[u] > -INFINITY ? expf(mc[u] - m) : 0.0f;
+        f[u] = mc[u] > -INFINITY ? __builtin_amdgcn_exp2f(mc[u] - m) : 0.0f;      // maxima in log2 units
         l += lc[u] * f[u];
     }
 #pragma unroll
     for (int o = 32; o; o >>= 1) l += __shfl_xor(l, o);
-    // 16 spans per step: their o loads are issued together.  Past nc the load repeats span
-    // nc - 1 (finite) and the lane holding span c0 + j has f = 0, so the padding terms add 0.
+    // sum over spans in order, 16 at a step (the o loads were all issued above)
     float acc = 0.0f;
-    for (int c0 = 0; c0 < nc; c0 += 16) {
-        float fu = f[0];                          // spans c0 .. c0 + 15 sit in f[c0 / 64]
 #pragma unroll
-        for (int u = 1; u < ATT_SPL; u++)
-            if ((c0 >> 6) == u) fu = f[u];
-        float ov[16];
+    for (int c0 = 0; c0 < ATT_NSPAN; c0 += 16)
+        if (c0 < nc) {
+            const float fu = f[c0 >> 6];          // spans c0 .. c0 + 15 sit in f[c0 / 64]
 #pragma unroll
-        for (int j = 0; j < 16; j++) ov[j] = pog[(uint64_t)(c0 + j < nc ? c0 + j : nc - 1) * ATT_MAXQ * ATT_HD];
-#pragma unroll
-        for (int j = 0; j < 16; j++)
-            acc = fmaf(ov[j], __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fu), (c0 + j) & 63)),
-                       acc);
-    }
+            for (int j = 0; j < 16; j++)
+                acc = fmaf(ov[c0 + j],
+                           __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fu), (c0 + j) & 63)),
+                           acc);
+        }
     return (acc / l) * (1.0f / (1.0f + expf(-gate)));
 }
 
@@ -566,8 +633,8 @@ static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out,
     // 8 waves of 32 dims for one or two row tiles, 4 waves of 64 dims for three (same-box A/B: each
     // the faster one by ~0.5%)
     const dim3 grid(a.n_kv, a.nspan);
-#define ATT_GO(F_, R_) hipLaunchKernelGGL((k_attn_span<F_, R_, (R_ < 3 ? 8 : 4)>), grid, dim3((R_ < 3 ? 8 : 4) * 64), 0, \
-                                          qg::stream, a)
+#define ATT_GO(F_, R_) hipLaunchKernelGGL((k_attn_span<F_, R_, (R_ < 3 ? 8 : ATT_NW3)>), grid, \
+                                          dim3((R_ < 3 ? 8 : ATT_NW3) * 64), 0, qg::stream, a)
 #define ATT_RTS(F_) do { switch (nrt) { case 1: ATT_GO(F_, 1); break; case 2: ATT_GO(F_, 2); break; \
                          default: ATT_GO(F_, 3); break; } } while (0)
     if (fused) ATT_RTS(1); else ATT_RTS(0);
