@@ -95,9 +95,9 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
 #ifndef ATT_NSPAN
 #define ATT_NSPAN 64          // spans per kv head at most
 #endif
-#ifndef ATT_PF
-#define ATT_PF 1              // tiles whose K/V loads are in flight while one is computed
-#endif
+#define ATT_RECORDS 0x7FFFFFFFu   // bytes the K/V buffer resources cover (offsets are < 2^31)
+#define ATT_OOB 0x80000000u       // an offset at or past ATT_RECORDS: the load reads zeros, fetches nothing
+static_assert(ATT_OOB >= ATT_RECORDS, "dead K/V loads must fall outside the buffer resource");
 #ifndef ATT_NW3
 #define ATT_NW3 8             // waves of the three-row-tile span kernel
 #endif
@@ -241,8 +241,8 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     // pos0.. (not in the caches before this launch) are replaced from Kn and Vn when the tile is
     // used.  Every lane loads every tile, so the loads are straight-line code and the wait for a
     // slot counts exactly the loads issued after it.
-    const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void *)(p.kc + hoff), 0, 0x7FFFFFFF, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void *)(p.vc + hoff), 0, 0x7FFFFFFF, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc((void *)(p.kc + hoff), 0, (int)ATT_RECORDS, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc((void *)(p.vc + hoff), 0, (int)ATT_RECORDS, 0x00020000);
     const uint32_t rowb = (uint32_t)kvrow * 4u;
     // a tile whose rows are all live: lane offsets of the tile's first row (computed once) plus the
     // tile's row offset in a scalar register; the last tile of the live context: clamped rows
@@ -250,10 +250,17 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     uint32_t vofs[4];
 #pragma unroll
     for (int v = 0; v < 4; v++) vofs[v] = (uint32_t)(4 * gq + v) * rowb + (uint32_t)(d0 + ATT_NQ * n) * 4u;
-    auto load_kv = [&](int tt, v4f *kr_, vqf *vr_) {
+    // live = 0: the loads are issued (so every path issues the same loads) at an offset past the
+    // buffer's end: they read zeros and fetch nothing
+    auto load_kv = [&](int tt, v4f *kr_, vqf *vr_, bool live) {
         const int p0 = tt * ATT_TP;
         uint32_t ko = kofs, vo[4] = { vofs[0], vofs[1], vofs[2], vofs[3] }, so = (uint32_t)p0 * rowb;
-        if (p0 + ATT_TP - 1 > tmax) {             // wave-uniform
+        if (!live) {                               // wave-uniform
+            ko = ATT_OOB;
+#pragma unroll
+            for (int v = 0; v < 4; v++) vo[v] = ATT_OOB;
+            so = 0;
+        } else if (p0 + ATT_TP - 1 > tmax) {      // wave-uniform
             ko = (uint32_t)min(p0 + n, tmax) * rowb + (uint32_t)(d0 + 4 * gq) * 4u;
 #pragma unroll
             for (int v = 0; v < 4; v++)
@@ -271,15 +278,16 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 vr_[v] = __builtin_bit_cast(vqf, __builtin_amdgcn_raw_buffer_load_b64(rsV, vo[v], so, 0));
         }
     };
-    // a ring of ATT_PF + 1 operand slots: tile t sits in slot (t - tile0) % (ATT_PF + 1), and the
-    // loads of tiles t + 1 .. t + ATT_PF are in flight while tile t is computed.  The first
-    // ATT_PF tiles' loads are issued before the q preparation.
-    constexpr int NSL = ATT_PF + 1;
+    // a ring of three operand slots: tile t sits in slot (t - tile0) % 3.  Its K is used one
+    // step before its V (scores run a tile ahead of P.V), and its loads are issued two steps
+    // before its V is used.  The first two tiles' loads are issued before the q preparation.
+    constexpr int NSL = 3;
     v4f kr[NSL][ATT_NQ];
     vqf vr[NSL][4];
-#pragma unroll
-    for (int u = 0; u < ATT_PF; u++)
-        if (tile0 + u < tile1) load_kv(tile0 + u, kr[u], vr[u]);
+    // (loads are issued for every step, past the span's last tile too, as loads that fetch
+    // nothing: every path then issues the same loads and the waits count them exactly)
+    load_kv(tile0, kr[0], vr[0], true);
+    load_kv(tile0 + 1, kr[1], vr[1], tile0 + 1 < tile1);
 
     if (FUSED) {
         float (*Qs)[ATT_HD] = (float (*)[ATT_HD])lds;
@@ -374,38 +382,42 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         sl[j] = 0.0f;
         slim[j] = R < QH ? pos0 + R / per : -1;
     }
-    for (int t0 = tile0; t0 < tile1; t0 += NSL)
-#pragma unroll
-    for (int u = 0; u < NSL; u++) {
-        const int t = t0 + u;
-        if (t >= tile1) break;
-        const int buf = (t - tile0) & 1;
-        if (t + ATT_PF < tile1) load_kv(t + ATT_PF, kr[(u + ATT_PF) % NSL], vr[(u + ATT_PF) % NSL]);
-        if (FUSED && t * ATT_TP + ATT_TP - 1 >= pos0) {   // rows of new positions, prepared in Kn, Vn
-            const int pp = t * ATT_TP + n, b = min(max(pp - pos0, 0), p.B - 1);
+    // K rows of new positions (FUSED: prepared in Kn, not in the caches yet) into slot kr_
+    auto new_k = [&](int tt, v4f *kr_) {
+        if (FUSED && tt * ATT_TP + ATT_TP - 1 >= pos0) {      // wave-uniform
+            const int pp = tt * ATT_TP + n, b = min(max(pp - pos0, 0), p.B - 1);
 #pragma unroll
             for (int q = 0; q < ATT_NQ; q++) {
                 const v4f kn = *(const v4f *)&Kn[b][d0 + 16 * q + 4 * gq];
-                if (pp >= pos0) kr[u][q] = kn;
-            }
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int pv_ = t * ATT_TP + 4 * gq + v, bv = min(max(pv_ - pos0, 0), p.B - 1);
-                const vqf vn = *(const vqf *)&Vn[bv][d0 + ATT_NQ * n];
-                if (pv_ >= pos0) vr[u][v] = vn;
+                if (pp >= pos0) kr_[q] = kn;
             }
         }
-        // partial score tiles over this wave's dims
+    };
+    // partial score tiles of tile tt over this wave's dims, into exchange buffer bf
+    auto scores = [&](const v4f *kr_, int bf) {
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
             v4f sp = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int q = 0; q < ATT_NQ; q++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) sp = mfma4(kr[u][q][j], qop[rt][q][j], sp);
-            Sx[((buf * ATT_NWV + wv) * NRT + rt) * 64 + lane] = sp;
+                for (int j = 0; j < 4; j++) sp = mfma4(kr_[q][j], qop[rt][q][j], sp);
+            Sx[((bf * ATT_NWV + wv) * NRT + rt) * 64 + lane] = sp;
         }
-        __syncthreads();
+    };
+    new_k(tile0, kr[0]);
+    scores(kr[0], 0);
+    __syncthreads();
+    // step t: loads of tile t + 2; the softmax of tile t (vector ALU), which reads the exchange
+    // buffer the previous step filled, beside the scores of tile t + 1 (matrix cores) into the
+    // other buffer; one barrier; then P.V of tile t.
+    for (int t0 = tile0; t0 < tile1; t0 += NSL)
+#pragma unroll
+    for (int u = 0; u < NSL; u++) {
+        const int t = t0 + u;
+        if (t >= tile1) break;
+        const int buf = (t - tile0) & 1;
+        load_kv(t + 2, kr[(u + 2) % NSL], vr[(u + 2) % NSL], t + 2 < tile1);
         // softmax: unit su (rows 4 su .. 4 su + 3 of the block, 16 positions: one value per lane)
         // is owned by wave su % NWV, which keeps the running max / sum of its rows
 #pragma unroll
@@ -428,7 +440,19 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 if (pq == 0) Al[buf * NRT * 16 + R] = alpha;
             }
         }
+        if (t + 1 < tile1) {
+            new_k(t + 1, kr[(u + 1) % NSL]);
+            scores(kr[(u + 1) % NSL], buf ^ 1);
+        }
         __syncthreads();
+        if (FUSED && t * ATT_TP + ATT_TP - 1 >= pos0) {      // V rows of new positions, prepared in Vn
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int pv_ = t * ATT_TP + 4 * gq + v, bv = min(max(pv_ - pos0, 0), p.B - 1);
+                const vqf vn = *(const vqf *)&Vn[bv][d0 + ATT_NQ * n];
+                if (pv_ >= pos0) vr[u][v] = vn;
+            }
+        }
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
             const v4f pv = *(const v4f *)&Pl[(((buf * NRT + rt) * 4 + gq) * 16 + n) * 4];
