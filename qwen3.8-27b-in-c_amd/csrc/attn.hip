@@ -157,11 +157,27 @@ static __device__ __forceinline__ float rowmax16(float v)
     return v;
 }
 
-static __device__ __forceinline__ float wsum64(float v)
+// sum over the wave: 16-lane rows by DPP, then the four row sums in a fixed order (every lane
+// gets the same bits)
+static __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v = rowsum16(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (a + b) + (c + d);
+}
+
+// maximum over the wave (16-lane rows by DPP, then the four row maxima)
+static __device__ __forceinline__ float wave_max(float v)
+{
+    v = rowmax16(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 static __device__ __forceinline__ v4f mfma4(float a, float b, v4f c)
@@ -320,30 +336,25 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
             Rs[e] = sv[u];
         }
         __syncthreads();
-        // per-head RMSNorm: one wave per row, 4 dims per lane
+        // per-head RMSNorm, then NeoX RoPE on (i, i + half) at position pos0 + b: one wave per row,
+        // 4 dims per lane for the norm, then pair i per lane for the rotation (the wave's own LDS
+        // writes are in order before its reads, so no barrier between the two)
         {
             const int nrow = QH + (has_new ? p.B : 0);
             for (int r = wv; r < nrow; r += ATT_NWV) {
                 float *x = r < QH ? Qs[r] : Kn[r - QH];
                 const float4 w = r < QH ? qw : kw;
                 float4 v = *(const float4 *)(x + 4 * lane);
-                const float sc = 1.0f / sqrtf(wsum64(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w) / (float)ATT_HD + p.eps);
+                const float sc = 1.0f / sqrtf(wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w) / (float)ATT_HD + p.eps);
                 v = make_float4((v.x * sc) * w.x, (v.y * sc) * w.y, (v.z * sc) * w.z, (v.w * sc) * w.w);
                 *(float4 *)(x + 4 * lane) = v;
-            }
-        }
-        __syncthreads();
-        // NeoX RoPE on (i, i + half) at position pos0 + b (tables of the B positions in LDS)
-        {
-            const int nrow = QH + (has_new ? p.B : 0);
-            for (int e = tid; e < nrow * p.half; e += ATT_NWV * 64) {
-                const int r = e / p.half, i = e % p.half;
-                float *x = r < QH ? Qs[r] : Kn[r - QH];
                 const int b = r < QH ? r / per : r - QH;
-                const float cs = Rc[b * p.half + i], sn = Rs[b * p.half + i];
-                const float v0 = x[i], v1 = x[i + p.half];
-                x[i] = v0 * cs - v1 * sn;
-                x[i + p.half] = v0 * sn + v1 * cs;
+                for (int i = lane; i < p.half; i += 64) {
+                    const float cs = Rc[b * p.half + i], sn = Rs[b * p.half + i];
+                    const float v0 = x[i], v1 = x[i + p.half];
+                    x[i] = v0 * cs - v1 * sn;
+                    x[i + p.half] = v0 * sn + v1 * cs;
+                }
             }
         }
         __syncthreads();
@@ -596,9 +607,7 @@ __global__ __launch_bounds__(4 * ATT_HD) void k_attn_combine_act(const float *q,
     for (int t = 0; t < 4; t++) { v[t] = vb[t][d]; m[t] = fabsf(v[t]); }
     if (active)
 #pragma unroll
-        for (int o = 32; o; o >>= 1)
-#pragma unroll
-            for (int t = 0; t < 4; t++) m[t] = fmaxf(m[t], __shfl_xor(m[t], o));
+        for (int t = 0; t < 4; t++) m[t] = wave_max(m[t]);
     act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)h * DIGIT_TILE,
                xs + (uint64_t)a * XS_FLOATS + (uint64_t)h * 16, active);
 }
