@@ -693,10 +693,15 @@ static __device__ __forceinline__ void iq4_load_a(IQ4A<NA> &x, const uint8_t *Ab
 // 2^(8 v): the weight of digit v
 static __device__ __forceinline__ float p8(int v) { return __builtin_bit_cast(float, (uint32_t)(127 + 8 * v) << 23); }
 // scale of token g (this lane group's) from the four token scales
-static __device__ __forceinline__ float tok_scale(float4 xt, int g) { return g == 0 ? xt.x : g == 1 ? xt.y : g == 2 ? xt.z : xt.w; }
+// (oh: the one-hot of the lane group, so the choice is four exact multiply-adds with the
+// scales as scalar operands, not a branch per lane group)
+static __device__ __forceinline__ float tok_scale(float4 xt, const float4 &oh)
+{
+    return fmaf(xt.w, oh.w, fmaf(xt.z, oh.z, fmaf(xt.y, oh.y, xt.x * oh.x)));
+}
 
 template <int NA>
-static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, const IQ4A<NA> &x, int g, float (&accf)[NA][4])
+static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, const IQ4A<NA> &x, const float4 &g, float (&accf)[NA][4])
 {
     const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
     v4i acci[NA];
@@ -723,9 +728,9 @@ static __device__ __forceinline__ void iq4_compute(const WRec<T_IQ4_XS> &w, cons
     const float d = h2f(w.hdr.x & 0xFFFFu);
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        const float xg = tok_scale(x.xt[a], g);
+        const float dx = d * tok_scale(x.xt[a], g);     // digit v's weight 2^(8 v) is applied at the end
 #pragma unroll
-        for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += (float)acci[a][v] * ((d * p8(v)) * xg);   // d 2^(8 v): exact
+        for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += (float)acci[a][v] * dx;
     }
 }
 
@@ -785,7 +790,7 @@ static __device__ __forceinline__ long kq_aop(const IQ4A<NA> &x, int a, int ib)
 static __device__ __forceinline__ long kq_b(uint32_t lo, uint32_t hi) { return (long)(((uint64_t)hi << 32) | lo); }
 
 template <int FMT, int NA>
-static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A<NA> &x, int g, float (&accf)[NA][4])
+static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A<NA> &x, const float4 &g, float (&accf)[NA][4])
 {
     const v4i z4 = (v4i){0, 0, 0, 0};
     if constexpr (FMT == T_Q8_0) {
@@ -810,7 +815,7 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
         for (int a = 0; a < NA; a++) {
             const float xg = tok_scale(x.xt[a], g);
 #pragma unroll
-            for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += accs[a][v] * (p8(v) * xg);
+            for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += accs[a][v] * xg;
         }
     } else if constexpr (FMT == T_Q6_K) {
         const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
@@ -839,9 +844,9 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
         const float d = h2f(w.d & 0xFFFFu);
 #pragma unroll
         for (int a = 0; a < NA; a++) {
-            const float xg = tok_scale(x.xt[a], g);
+            const float dx = d * tok_scale(x.xt[a], g);
 #pragma unroll
-            for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += (float)acc[a][v] * ((d * p8(v)) * xg);
+            for (int v = 0; v < DIGIT_REGS; v++) accf[a][v] += (float)acc[a][v] * dx;
         }
     } else {                                                   // Q4_K, Q5_K
         const uint32_t qd[8] = { w.qa.x, w.qa.y, w.qa.z, w.qa.w, w.qb.x, w.qb.y, w.qb.z, w.qb.w };
@@ -870,10 +875,10 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
         const float d = h2f(w.hdr.x & 0xFFFFu), dm = h2f(w.hdr.x >> 16);
 #pragma unroll
         for (int a = 0; a < NA; a++) {
-            const float xg = tok_scale(x.xt[a], g);
+            const float xg = tok_scale(x.xt[a], g), dx = d * xg, dmx = dm * xg;
 #pragma unroll
             for (int v = 0; v < DIGIT_REGS; v++)
-                accf[a][v] += (float)acq[a][v] * ((d * p8(v)) * xg) - (float)acm[a][v] * ((dm * p8(v)) * xg);
+                accf[a][v] += (float)acq[a][v] * dx - (float)acm[a][v] * dmx;
         }
     }
 }
@@ -900,6 +905,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
     __shared__ float red[NW][NA][4][16];
     __shared__ float rsc[QGPU_MAX_B];
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    const float4 oh = make_float4(g == 0, g == 1, g == 2, g == 3);   // token g of this lane group
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar loop control
     const uint32_t tile = (MODE & IQ4_SPLIT) ? blockIdx.x / args.ks : blockIdx.x;
     const int kq = (MODE & IQ4_SPLIT) ? blockIdx.x % args.ks : 0;   // K range of this block (split GEMV)
@@ -943,19 +949,20 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
                 const int pw = sb + d + IQ4_WDEPTH - 1, pa = sb + d + IQ4_ADEPTH - 1;
                 if (pa < sb1) LOAD_A((d + IQ4_ADEPTH - 1) % IQ4_ADEPTH, pa);
                 if (pw < sb1) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
-                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], g, accf);
-                else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], g, accf);
+                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], oh, accf);
+                else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], oh, accf);
             }
         }
     }
 #undef LOAD_W
 #undef LOAD_A
     if (MODE & IQ4_RMS) rms_reduce(args, wv, NW, lane, rp, rsc);
-    // registers 0..3 of lane (g, n) hold digits 0..3 of token g, row n: sum them
+    // registers 0..3 of lane (g, n) hold digits 0..3 of token g, row n: sum them with their weights
+    // 2^(8 v) (a power of two: the same bits as weighting every super-block's term)
 #pragma unroll
     for (int a = 0; a < NA; a++)
-        red[wv][a][g][n] = DIGIT_REGS == 3 ? (accf[a][0] + accf[a][1]) + accf[a][2]
-                                           : (accf[a][0] + accf[a][1]) + (accf[a][2] + accf[a][3]);
+        red[wv][a][g][n] = DIGIT_REGS == 3 ? (accf[a][0] + accf[a][1] * p8(1)) + accf[a][2] * p8(2)
+                                           : (accf[a][0] + accf[a][1] * p8(1)) + (accf[a][2] * p8(2) + accf[a][3] * p8(3));
     __syncthreads();
     for (int e = tid; e < NA * 64; e += NW * 64) {     // (plane, token, row) entries of the tile
         const int a = e >> 6, i = (e >> 4) & 3, nn = e & 15;
