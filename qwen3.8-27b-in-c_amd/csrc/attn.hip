@@ -63,27 +63,30 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
 
 // Span kernel (flash decoding on the matrix cores).  Block (g, s): kv head g,
 // span s of 16-position tiles, NW waves; wave w owns head dims [DW w, DW w + DW),
-// DW = 256 / NW (the comments below take NW = 4, DW = 64).
+// DW = 256 / NW (NW = 8, DW = 32 in every launch).
 // It serves every query row of the group, r = b * per + (h - g*per) < QH =
 // per * B, as NRT row tiles of 16.
 //   * Scores, per tile and row tile: S^T (16 positions x 16 rows) = K Q^T with
 //     v_mfma_f32_16x16x4_f32, lane l supplying K[pos l%16][d] and Q[row l%16][d]
-//     for d = 64w + 16q + 4(l/16) + j (q, j < 4: any order of the d sum is the
-//     same dot product).  Each wave sums its 64 dims; the four partial tiles meet
-//     in LDS and every wave adds them in the same order.
-//   * The score tile's accumulator layout (lane l, register v: position
-//     4(l/16) + v, row l%16) is the A operand of P.V as it stands: MFMA step v
-//     takes positions {v, 4+v, 8+v, 12+v}; lane l supplies V[that position][64w +
-//     4(l%16) + c] for output tile c, so one float4 per step feeds four MFMAs.
-//   * Online softmax per row (running max and sum); rows of a tile meet over
-//     the four 16-lane groups.  O accumulates in fp32 registers (lane l, register
-//     w: row 4(l/16) + w, dim 64w' + 4(l%16) + c).
-//   * The K and V operands of the next tile are loaded while this tile runs.
+//     for d = DW w + 16q + 4(l/16) + j (any order of the d sum is the same dot
+//     product).  Each wave writes its partial tile to LDS.
+//   * Softmax: the rows are cut into units of 4 (16 positions each: one value per
+//     lane); the wave that owns a unit sums the NW partial scores in wave order,
+//     keeps the running max and sum of its rows (scores in log2 units, exp2), and
+//     writes the probabilities and the rows' rescale factors to LDS.
+//   * P.V: the probabilities come back in the score accumulator's layout (lane l,
+//     register v: position 4(l/16) + v, row l%16), the A operand of P.V: MFMA step
+//     v takes positions {v, 4+v, 8+v, 12+v}; lane l supplies V[that position][DW w
+//     + NQ (l%16) + c] for output tile c.  O accumulates in fp32 registers (lane l,
+//     register r: row 4(l/16) + r).
+//   * Step t: loads of tile t + 2, the softmax of tile t beside the scores of tile
+//     t + 1, one barrier, P.V of tile t (a ring of three K/V register slots).
 //   FUSED = 1: the block also applies the per-head q/k RMSNorm and RoPE
 //              (reference model.c:318-406) in LDS: q rows, and the new k rows
-//              of positions pos..pos+B-1 when the span reaches them; the block
-//              whose span holds a new position writes its k/v rows to the caches
-//              (no block reads new rows from the caches in this launch).
+//              of positions pos..pos+B-1; the new k and v rows replace the
+//              cached rows of those positions when a tile is used, and the block
+//              whose span holds a new position writes them to the caches (no
+//              block reads new rows from the caches in this launch).
 //   FUSED = 0: q rows already prepared, caches already hold every position.
 // The number of spans follows the live context: ntl tiles hold positions
 // 0..pos+B-1; nsl = ceil(ntl / tps) spans of tps tiles, for at most nspan
@@ -131,53 +134,6 @@ static __device__ __forceinline__ void span_split(int pos0, int B, int nspan, in
     tps = (ntl + ns - 1) / ns;
     if (tps < ATT_MINTPS) tps = ATT_MINTPS;
     nsl = (ntl + tps - 1) / tps;
-}
-
-// 16-lane row reductions with DPP moves; each step combines a value with its mirror
-// image, so every lane of a row ends with the same bits
-template <int CTRL>
-static __device__ __forceinline__ float dpp_mov(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-static __device__ __forceinline__ float rowsum16(float v)
-{
-    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
-    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
-    v += dpp_mov<0x141>(v);   // row_half_mirror
-    v += dpp_mov<0x140>(v);   // row_mirror
-    return v;
-}
-static __device__ __forceinline__ float rowmax16(float v)
-{
-    v = fmaxf(v, dpp_mov<0xB1>(v));
-    v = fmaxf(v, dpp_mov<0x4E>(v));
-    v = fmaxf(v, dpp_mov<0x141>(v));
-    v = fmaxf(v, dpp_mov<0x140>(v));
-    return v;
-}
-
-// sum over the wave: 16-lane rows by DPP, then the four row sums in a fixed order (every lane
-// gets the same bits)
-static __device__ __forceinline__ float wave_sum(float v)
-{
-    v = rowsum16(v);
-    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return (a + b) + (c + d);
-}
-
-// maximum over the wave (16-lane rows by DPP, then the four row maxima)
-static __device__ __forceinline__ float wave_max(float v)
-{
-    v = rowmax16(v);
-    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 static __device__ __forceinline__ v4f mfma4(float a, float b, v4f c)
@@ -345,7 +301,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 float *x = r < QH ? Qs[r] : Kn[r - QH];
                 const float4 w = r < QH ? qw : kw;
                 float4 v = *(const float4 *)(x + 4 * lane);
-                const float sc = 1.0f / sqrtf(wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w) / (float)ATT_HD + p.eps);
+                const float sc = 1.0f / sqrtf(wave_sum64(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w) / (float)ATT_HD + p.eps);
                 v = make_float4((v.x * sc) * w.x, (v.y * sc) * w.y, (v.z * sc) * w.z, (v.w * sc) * w.w);
                 *(float4 *)(x + 4 * lane) = v;
                 const int b = r < QH ? r / per : r - QH;
@@ -542,16 +498,14 @@ static __device__ __forceinline__ float combine_one(const float *q, uint64_t ldq
         }
         m = fmaxf(m, mc[u]);
     }
-#pragma unroll
-    for (int o = 32; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = wave_max64(m);
     float l = 0.0f;
 #pragma unroll
     for (int u = 0; u < ATT_SPL; u++) {
         f[u] = mc[u] > -INFINITY ? __builtin_amdgcn_exp2f(mc[u] - m) : 0.0f;      // maxima in log2 units
         l += lc[u] * f[u];
     }
-#pragma unroll
-    for (int o = 32; o; o >>= 1) l += __shfl_xor(l, o);
+    l = wave_sum64(l);
     // sum over spans in order, 16 at a step (the o loads were all issued above)
     float acc = 0.0f;
 #pragma unroll
@@ -607,7 +561,7 @@ __global__ __launch_bounds__(4 * ATT_HD) void k_attn_combine_act(const float *q,
     for (int t = 0; t < 4; t++) { v[t] = vb[t][d]; m[t] = fabsf(v[t]); }
     if (active)
 #pragma unroll
-        for (int t = 0; t < 4; t++) m[t] = wave_max(m[t]);
+        for (int t = 0; t < 4; t++) m[t] = wave_max64(m[t]);
     act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)h * DIGIT_TILE,
                xs + (uint64_t)a * XS_FLOATS + (uint64_t)h * 16, active);
 }

@@ -55,23 +55,7 @@ static __device__ __forceinline__ float sum16(float v)
     return v;
 }
 
-// The same row sum with DPP lane moves (VALU, no LDS round trip): lane ^ 1,
-// lane ^ 2 (quad_perm), the other quad of the half row (row_half_mirror), the
-// other half row (row_mirror).  Each step adds a value to its mirror image, so
-// every lane of the row ends with the same bits.
-template <int CTRL>
-static __device__ __forceinline__ float dpp_mov(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-static __device__ __forceinline__ float rowsum16(float v)
-{
-    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
-    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
-    v += dpp_mov<0x141>(v);   // row_half_mirror
-    v += dpp_mov<0x140>(v);   // row_mirror
-    return v;
-}
+// (rowsum16: the same row sum with DPP lane moves, qgpu_internal.h)
 
 // block = 16 state rows of one v-head; thread (row r = tid/16, column chunk cc = tid%16, 8 columns)
 __global__ __launch_bounds__(256) void k_gdn_recur(const float *__restrict__ xq, uint64_t ldq,

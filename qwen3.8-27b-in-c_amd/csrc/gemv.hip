@@ -371,12 +371,6 @@ struct ActDev {
 
 static __device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + expf(-v)); }
 
-static __device__ __forceinline__ float wave_sum(float v)
-{
-#pragma unroll
-    for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
 
 // One block = one 256-element super-block (blockIdx.x) of the 4 tokens of
 // plane blockIdx.y.  The activation transform KIND (QGPU_ACT_*) is applied
@@ -430,12 +424,10 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
             m[i] = fabsf(v[i]);
         }
 #pragma unroll
-        for (int o = 32; o; o >>= 1)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                ss[i] += __shfl_xor(ss[i], o);
-                m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
-            }
+        for (int i = 0; i < 4; i++) {
+            ss[i] = wave_sum64(ss[i]);
+            m[i] = wave_max64(m[i]);
+        }
         if (lane == 0)
 #pragma unroll
             for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
@@ -471,9 +463,7 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
                 }
         }
 #pragma unroll
-        for (int o = 32; o; o >>= 1)
-#pragma unroll
-            for (int i = 0; i < 4; i++) ss[i] += __shfl_xor(ss[i], o);
+        for (int i = 0; i < 4; i++) ss[i] = wave_sum64(ss[i]);
         if (lane == 0)
 #pragma unroll
             for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
@@ -498,9 +488,7 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
 #pragma unroll
         for (int i = 0; i < 4; i++) ss[i] = raw[i] * raw[i];
 #pragma unroll
-        for (int o = 32; o; o >>= 1)
-#pragma unroll
-            for (int i = 0; i < 4; i++) ss[i] += __shfl_xor(ss[i], o);
+        for (int i = 0; i < 4; i++) ss[i] = wave_sum64(ss[i]);
         if (lane == 0)
 #pragma unroll
             for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
@@ -540,9 +528,7 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
 #pragma unroll
         for (int i = 0; i < 4; i++) m[i] = fabsf(v[i]);
 #pragma unroll
-        for (int o = 32; o; o >>= 1)
-#pragma unroll
-            for (int i = 0; i < 4; i++) m[i] = fmaxf(m[i], __shfl_xor(m[i], o));
+        for (int i = 0; i < 4; i++) m[i] = wave_max64(m[i]);
     }
     act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * DIGIT_TILE, xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16);
     if (KIND == ACT_RMS_DEFER && e < nt)     // red[] was written before the barriers of act_digits
@@ -591,9 +577,7 @@ static __device__ __forceinline__ void rms_reduce(const GemvArgs &args, int wv, 
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int t = wv + u * nw;
-        float s = rp.v[u];
-#pragma unroll
-        for (int o = 32; o; o >>= 1) s += __shfl_xor(s, o);
+        const float s = wave_sum64(rp.v[u]);
         if (lane == 0 && t < args.ntok) rsc[t] = 1.0f / sqrtf(s * args.rss_inv_n + args.eps);
     }
 }

@@ -77,6 +77,47 @@ static __device__ __forceinline__ void st_stream4(float *p, float4 v) { st_strea
 // 2^(8 dgt - s_t) converts the integer result of A row t*4 + dgt.  Every thread of the block calls it (two
 // barriers); in blocks of more than 256 threads, threads 0..255 pass active =
 // true and the others false (they only take part in the barriers).
+// Lane reductions with DPP moves (VALU, no LDS round trip).  A 16-lane row: lane ^ 1, lane ^ 2
+// (quad_perm), the other quad of the half row (row_half_mirror), the other half row
+// (row_mirror); each step combines a value with its mirror image, so every lane of the row ends
+// with the same bits.  A wave: the four row results read from lanes 0, 16, 32, 48, combined in a
+// fixed order (every lane of the wave gets the same bits).  All 64 lanes must be active.
+template <int CTRL>
+static __device__ __forceinline__ float dpp_mov(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+static __device__ __forceinline__ float rowsum16(float v)
+{
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mov<0x141>(v);   // row_half_mirror
+    v += dpp_mov<0x140>(v);   // row_mirror
+    return v;
+}
+static __device__ __forceinline__ float rowmax16(float v)
+{
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return v;
+}
+static __device__ __forceinline__ float lane_value(float v, int l)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+static __device__ __forceinline__ float wave_sum64(float v)
+{
+    v = rowsum16(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+static __device__ __forceinline__ float wave_max64(float v)
+{
+    v = rowmax16(v);
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
 struct ActDigitLds {
     uint8_t stage[DIGIT_TILE];
     float mx[4][4];          // [token][wave]
