@@ -372,13 +372,12 @@ struct ActDev {
 static __device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + expf(-v)); }
 
 
-// One block = one 256-element super-block (blockIdx.x) of the 4 tokens of
-// plane blockIdx.y.  The activation transform KIND (QGPU_ACT_*) is applied
-// first; v may also be stored in fp32 (xout).  Every global load a thread
-// needs (4 tokens; partial planes; gate and weight rows) is issued before the
-// first use, so a block waits for one memory latency, not one per token.
-template <int KIND>
-__global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict__ A, float *__restrict__ xs)
+// Row RMSNorm over a whole row or over each of its two segments (the MTP input
+// concat(enorm(e), hnorm(h))).  One block = one 256-element super-block
+// (blockIdx.x) of the 4 tokens of plane blockIdx.y; each block recomputes the row
+// RMS of its segment in the same order, so every block gets the same value.  The
+// four tokens' loads are issued before their first use.
+__global__ __launch_bounds__(256) void k_prep_rms(ActDev p, uint8_t *__restrict__ A, float *__restrict__ xs)
 {
     __shared__ ActDigitLds dl;
     __shared__ float red[4][4];          // sums of squares [token][wave]
@@ -389,150 +388,158 @@ __global__ __launch_bounds__(256) void k_prep_act(ActDev p, uint8_t *__restrict_
     int tr[4];                                                     // row of token i (clamped: always loadable)
 #pragma unroll
     for (int i = 0; i < 4; i++) tr[i] = 4 * a + (i < nt ? i : 0);
-    float v[4];
-    bool have_max = false;                                         // m[] already holds the per-wave max |v|
-    float m[4];
-    if (KIND == ACT_RMS_DEFER) {
-        // v = x_eff * w, x_eff = x + (p_0 + p_1 + ...) over the n_part partial planes; the row factor
-        // 1/sqrt(mean(x_eff^2) + eps) multiplies the GEMV output (W (x s w) = s W (x w)), from the
-        // per-super-block sums of squares written here
-        float xr[4], pr[8][4];
+    float v[4], m[4];
+    const uint64_t segl = p.seg;
+    const int part = (uint64_t)sb * 256 >= segl ? 1 : 0;
+    const float *src = part ? p.y : p.x;
+    const float *w = part ? p.w2 : p.w;
+    const uint64_t ld = part ? p.ldy : p.ldx, kk = k - (part ? segl : 0);
+    float own[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) xr[i] = p.x[(uint64_t)tr[i] * p.ldx + k];
+    for (int i = 0; i < 4; i++) own[i] = src[(uint64_t)tr[i] * ld + kk];
+    const float wk = w[kk];
+    float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint64_t j0 = e; j0 < segl / 4; j0 += 5 * 256) {
+        float4 q[5][4];
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const uint64_t qo = (uint64_t)(q < p.n_part ? q : 0) * p.pstride;
+        for (int u = 0; u < 5; u++) {
+            const uint64_t j = j0 + (uint64_t)u * 256;
 #pragma unroll
-            for (int i = 0; i < 4; i++) pr[q][i] = p.n_part ? p.part[qo + (uint64_t)tr[i] * p.ldp + k] : 0.0f;
+            for (int i = 0; i < 4; i++)
+                q[u][i] = (i < nt && j < segl / 4) ? ((const float4 *)(src + (uint64_t)(4 * a + i) * ld))[j]
+                                                  : make_float4(0, 0, 0, 0);
         }
-        const float wk = p.w[k];
-        float ss[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float xe = xr[i];
-            if (p.n_part) {
-                float ps = pr[0][i];
+        for (int u = 0; u < 5; u++)
 #pragma unroll
-                for (int q = 1; q < 8; q++)
-                    if (q < p.n_part) ps += pr[q][i];
-                xe += ps;
+            for (int i = 0; i < 4; i++) {
+                ss[i] = fmaf(q[u][i].x, q[u][i].x, ss[i]); ss[i] = fmaf(q[u][i].y, q[u][i].y, ss[i]);
+                ss[i] = fmaf(q[u][i].z, q[u][i].z, ss[i]); ss[i] = fmaf(q[u][i].w, q[u][i].w, ss[i]);
             }
-            if (i >= nt) xe = 0.0f;
-            else if (p.xnew) p.xnew[(uint64_t)(4 * a + i) * p.ldxn + k] = xe;
-            v[i] = xe * wk;
-            ss[i] = xe * xe;
-            m[i] = fabsf(v[i]);
-        }
+    }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            ss[i] = wave_sum64(ss[i]);
-            m[i] = wave_max64(m[i]);
-        }
-        if (lane == 0)
+    for (int i = 0; i < 4; i++) ss[i] = wave_sum64(ss[i]);
+    if (lane == 0)
 #pragma unroll
-            for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
-        have_max = true;
-    } else if (KIND == QGPU_ACT_RMSNORM) {
-        // row RMS over the segment holding this super-block (each block recomputes it: same order, same value)
-        const uint64_t segl = p.seg;
-        const int part = (uint64_t)sb * 256 >= segl ? 1 : 0;
-        const float *src = part ? p.y : p.x;
-        const float *w = part ? p.w2 : p.w;
-        const uint64_t ld = part ? p.ldy : p.ldx, kk = k - (part ? segl : 0);
-        float own[4];
+        for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
+    __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 4; i++) own[i] = src[(uint64_t)tr[i] * ld + kk];
-        const float wk = w[kk];
-        float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint64_t j0 = e; j0 < segl / 4; j0 += 5 * 256) {
-            float4 q[5][4];
-#pragma unroll
-            for (int u = 0; u < 5; u++) {
-                const uint64_t j = j0 + (uint64_t)u * 256;
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    q[u][i] = (i < nt && j < segl / 4) ? ((const float4 *)(src + (uint64_t)(4 * a + i) * ld))[j]
-                                                      : make_float4(0, 0, 0, 0);
-            }
-#pragma unroll
-            for (int u = 0; u < 5; u++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    ss[i] = fmaf(q[u][i].x, q[u][i].x, ss[i]); ss[i] = fmaf(q[u][i].y, q[u][i].y, ss[i]);
-                    ss[i] = fmaf(q[u][i].z, q[u][i].z, ss[i]); ss[i] = fmaf(q[u][i].w, q[u][i].w, ss[i]);
-                }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) ss[i] = wave_sum64(ss[i]);
-        if (lane == 0)
-#pragma unroll
-            for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float tot = (red[i][0] + red[i][1]) + (red[i][2] + red[i][3]);
-            const float sc = 1.0f / sqrtf(tot / (float)segl + p.eps);
-            v[i] = i < nt ? (own[i] * sc) * wk : 0.0f;
-        }
-    } else if (KIND == QGPU_ACT_GATED_NORM) {
-        // heads of seg = 64 * hw elements: waves [h0, h0 + hw) of this block hold one head
-        const int hw = (int)(p.seg >> 6), h0 = (wv / hw) * hw;
-        float raw[4], gy[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            raw[i] = p.x[(uint64_t)tr[i] * p.ldx + k];
-            gy[i] = p.y[(uint64_t)tr[i] * p.ldy + k];
-        }
-        const float wk = p.w[k & (p.seg - 1)];
-        float ss[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) ss[i] = raw[i] * raw[i];
-#pragma unroll
-        for (int i = 0; i < 4; i++) ss[i] = wave_sum64(ss[i]);
-        if (lane == 0)
-#pragma unroll
-            for (int i = 0; i < 4; i++) red[i][wv] = ss[i];
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float tot = red[i][h0];
-            for (int q = 1; q < hw; q++) tot += red[i][h0 + q];
-            const float sc = 1.0f / sqrtf(tot / (float)p.seg + p.eps);
-            v[i] = i < nt ? ((raw[i] * sc) * wk) * silu_dev(gy[i]) : 0.0f;
-        }
-    } else {
-        float xv[4], yv[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            xv[i] = p.x[(uint64_t)tr[i] * p.ldx + k];
-            yv[i] = KIND == QGPU_ACT_SILU_MUL ? p.y[(uint64_t)tr[i] * p.ldy + k] : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            v[i] = i >= nt ? 0.0f : KIND == QGPU_ACT_SILU_MUL ? silu_dev(xv[i]) * yv[i] : xv[i];
+    for (int i = 0; i < 4; i++) {
+        const float tot = (red[i][0] + red[i][1]) + (red[i][2] + red[i][3]);
+        const float sc = 1.0f / sqrtf(tot / (float)segl + p.eps);
+        v[i] = i < nt ? (own[i] * sc) * wk : 0.0f;
     }
     if (p.xout) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
             if (i < nt) p.xout[(uint64_t)(4 * a + i) * p.ldxo + k] = v[i];
     }
-    if (!p.digits) {                  // fp32 rows only (VALU formats); the deferred norm still needs its sums
-        if (KIND == ACT_RMS_DEFER) {
-            __syncthreads();
-            if (e < nt)
-                p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[e][0] + red[e][1]) + (red[e][2] + red[e][3]);
-        }
-        return;
-    }
-    if (!have_max) {
+    if (!p.digits) return;               // fp32 rows only (VALU formats)
 #pragma unroll
-        for (int i = 0; i < 4; i++) m[i] = fabsf(v[i]);
-#pragma unroll
-        for (int i = 0; i < 4; i++) m[i] = wave_max64(m[i]);
-    }
+    for (int i = 0; i < 4; i++) m[i] = wave_max64(fabsf(v[i]));
     act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * DIGIT_TILE, xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16);
-    if (KIND == ACT_RMS_DEFER && e < nt)     // red[] was written before the barriers of act_digits
-        p.rss[(uint64_t)(4 * a + e) * p.nsb + sb] = (red[e][0] + red[e][1]) + (red[e][2] + red[e][3]);
+}
+
+// One token per block: the deferred RMSNorm (with the residual's pending partial
+// planes), SiLU(x)·y, the per-head gated norm, and the plain copy.  Block (sb, t),
+// 256 threads: thread e holds element e of super-block sb of token t, so a thread
+// issues 1 + NP + 1 loads (deferred RMSNorm with NP partial planes), 2 or 3 (the
+// others), with no branch around them.  Wave r holds elements 64r..64r+63, which
+// are token t's whole 192-byte run of sub-block pair r in the digit tile (layout
+// above act_digits): lane l = 16h + 4gg + c holds element 64r + 16h + 4gg + c,
+// whose digit dg is byte r*768 + t*192 + gg*48 + dg*16 + 4h + c.  The four lanes
+// of a quad hold the four bytes of one dword per digit; a byte transpose inside
+// the quad (DPP broadcasts and two v_perm_b32) gives lane c the dword of digit c,
+// and lanes c < 3 store it -- no staging through LDS.  One barrier exchanges the
+// per-wave sums of squares and maxima (the gated norm takes two: its maximum
+// follows the head scale).  The per-element arithmetic and the reduction orders
+// are those of the 4-token form (wave sums, then (w0 + w1) + (w2 + w3)), so
+// digits, scales, sums of squares and residual rows do not depend on the grid.
+template <int KIND, int NP>
+__global__ __launch_bounds__(256) void k_prep_tok(ActDev p, uint8_t *__restrict__ A, float *__restrict__ xs)
+{
+    __shared__ float ssw[4], mxw[4];
+    const int e = threadIdx.x, lane = e & 63, wv = e >> 6;
+    const int sb = blockIdx.x, t = blockIdx.y, a = t >> 2, i = t & 3;
+    const uint32_t k = (uint32_t)sb * 256 + e;
+    float v, ss = 0.0f;
+    if (KIND == ACT_RMS_DEFER) {
+        // x_eff = x + (p_0 + p_1 + ...) over the NP partial planes, written back to xnew;
+        // v = x_eff * w, and the super-block's sum of x_eff^2 for the GEMV's row factor
+        const float xr = (p.x + (uint64_t)t * p.ldx)[k];
+        float pr[NP > 0 ? NP : 1];
+#pragma unroll
+        for (int q = 0; q < NP; q++) pr[q] = (p.part + (uint64_t)q * p.pstride + (uint64_t)t * p.ldp)[k];
+        const float wk = p.w[k];
+        float xe = xr;
+        if (NP > 0) {
+            float ps = pr[0];
+#pragma unroll
+            for (int q = 1; q < NP; q++) ps += pr[q];
+            xe += ps;
+        }
+        if (p.xnew) (p.xnew + (uint64_t)t * p.ldxn)[k] = xe;
+        v = xe * wk;
+        ss = wave_sum64(xe * xe);
+    } else if (KIND == QGPU_ACT_GATED_NORM) {
+        // heads of seg = 64 * hw elements: waves [h0, h0 + hw) of this block hold one head
+        const int hw = (int)(p.seg >> 6), h0 = (wv / hw) * hw;
+        const float raw = (p.x + (uint64_t)t * p.ldx)[k];
+        const float gy = (p.y + (uint64_t)t * p.ldy)[k];
+        const float wk = p.w[k & (uint32_t)(p.seg - 1)];
+        const float sw = wave_sum64(raw * raw);
+        if (lane == 0) ssw[wv] = sw;
+        __syncthreads();
+        float tot = ssw[h0];
+        for (int q = 1; q < hw; q++) tot += ssw[h0 + q];
+        const float sc = 1.0f / sqrtf(tot / (float)p.seg + p.eps);
+        v = ((raw * sc) * wk) * silu_dev(gy);
+    } else if (KIND == QGPU_ACT_SILU_MUL) {
+        const float xv = (p.x + (uint64_t)t * p.ldx)[k];
+        const float yv = (p.y + (uint64_t)t * p.ldy)[k];
+        v = silu_dev(xv) * yv;
+    } else {
+        v = (p.x + (uint64_t)t * p.ldx)[k];
+    }
+    if (p.xout) (p.xout + (uint64_t)t * p.ldxo)[k] = v;
+    const float mw = wave_max64(fabsf(v));
+    if (lane == 0) {
+        mxw[wv] = mw;
+        if (KIND == ACT_RMS_DEFER) ssw[wv] = ss;
+    }
+    __syncthreads();
+    if (KIND == ACT_RMS_DEFER && e == 0) p.rss[(uint64_t)t * p.nsb + sb] = (ssw[0] + ssw[1]) + (ssw[2] + ssw[3]);
+    if (!p.digits) return;                                       // fp32 rows only (VALU formats)
+    // shift puts the super-block maximum just under 2^22 (0 for an all-zero or non-finite maximum)
+    const float mx = fmaxf(fmaxf(mxw[0], mxw[1]), fmaxf(mxw[2], mxw[3]));
+    int shift = 0;
+    if (mx > 0.0f && isfinite(mx)) {
+        int E;
+        frexpf(mx, &E);
+        shift = 22 - E;
+    }
+    // three balanced base-256 digits of X = rint(v 2^shift), packed in bytes 0..2 of P
+    const float sv = ldexpf(v, shift);
+    int X = isfinite(sv) ? (int)rintf(sv) : 0;
+    uint32_t P = 0;
+#pragma unroll
+    for (int dg = 0; dg < 3; dg++) {
+        const int d = (dg < 2) ? (int)(int8_t)(X & 0xFF) : X;
+        X = (X - d) >> 8;
+        P |= ((uint32_t)d & 0xFFu) << (8 * dg);
+    }
+    // quad byte transpose: lane c gets byte c of P from each lane of its quad, in lane order
+    const uint32_t c = (uint32_t)lane & 3u;
+    const uint32_t P0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x00, 0xF, 0xF, false);
+    const uint32_t P1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x55, 0xF, 0xF, false);
+    const uint32_t P2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0xAA, 0xF, 0xF, false);
+    const uint32_t P3 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0xFF, 0xF, 0xF, false);
+    // v_perm_b32 selectors: 0..3 bytes of the second operand, 4..7 of the first, 12 the constant 0
+    const uint32_t W = __builtin_amdgcn_perm(P1, P0, c | ((c + 4u) << 8) | 0x0C0C0000u) |
+                       __builtin_amdgcn_perm(P3, P2, 0x00000C0Cu | (c << 16) | ((c + 4u) << 24));
+    uint8_t *tile = A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * DIGIT_TILE + wv * DIGIT_SUB + i * 192;
+    if (c < 3) *(uint32_t *)(tile + ((lane >> 2) & 3) * 48 + c * 16 + (lane >> 4) * 4) = W;
+    if (e < 4) xs[(uint64_t)a * XS_FLOATS + (uint64_t)sb * 16 + 4 * e + i] = ldexpf(1.0f, 8 * e - shift);
 }
 
 // ---------------------------------------------------------------- IQ4_XS MFMA GEMV
@@ -1140,9 +1147,14 @@ static int prep_act(const GemvExec &ex, const qgpu_act *act, int n, uint64_t ne0
         if (!act->w || (rows && act->ldx < ne0) || (act->xout && rows && act->ldxo < ne0)) return QGPU_E_ARG;
         d.part = act->part; d.ldp = act->ldp; d.pstride = (uint64_t)n * act->ldp; d.n_part = act->n_part;
         d.xnew = act->xnew; d.ldxn = act->ldxn; d.rss = ws_rss(ex); d.nsb = (int)(ne0 / 256);
-        const dim3 grid((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1));
-        hipLaunchKernelGGL(k_prep_act<ACT_RMS_DEFER>, grid, dim3(256), 0, ex.st, d, ex.ws,
-                           (float *)(ex.ws + 2 * PLANE_BYTES));
+        const dim3 grid((unsigned)(ne0 / 256), (unsigned)n);
+        uint8_t *A = ex.ws;
+        float *xs = (float *)(ex.ws + 2 * PLANE_BYTES);
+#define PT_NP(NP_) case NP_: hipLaunchKernelGGL((k_prep_tok<ACT_RMS_DEFER, NP_>), grid, dim3(256), 0, ex.st, d, A, xs); break
+        switch (act->n_part) {
+        PT_NP(0); PT_NP(1); PT_NP(2); PT_NP(3); PT_NP(4); PT_NP(5); PT_NP(6); PT_NP(7); default: PT_NP(8);
+        }
+#undef PT_NP
         QG_LAUNCH_CHECK();
         if (deferred) *deferred = true;
         return QGPU_OK;
@@ -1172,14 +1184,16 @@ static int prep_act(const GemvExec &ex, const qgpu_act *act, int n, uint64_t ne0
     default: return QGPU_E_ARG;
     }
     if (rows && act->ldx < wx) return QGPU_E_ARG;
-    const dim3 grid((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1));
+    const dim3 grid((unsigned)(ne0 / 256), (unsigned)n);                  // one token per block
     uint8_t *A = ex.ws;
     float *xs = (float *)(ex.ws + 2 * PLANE_BYTES);
     switch (act->kind) {
-    case QGPU_ACT_COPY: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_COPY>, grid, dim3(256), 0, ex.st, d, A, xs); break;
-    case QGPU_ACT_RMSNORM: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_RMSNORM>, grid, dim3(256), 0, ex.st, d, A, xs); break;
-    case QGPU_ACT_SILU_MUL: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_SILU_MUL>, grid, dim3(256), 0, ex.st, d, A, xs); break;
-    default: hipLaunchKernelGGL(k_prep_act<QGPU_ACT_GATED_NORM>, grid, dim3(256), 0, ex.st, d, A, xs); break;
+    case QGPU_ACT_COPY: hipLaunchKernelGGL((k_prep_tok<QGPU_ACT_COPY, 0>), grid, dim3(256), 0, ex.st, d, A, xs); break;
+    case QGPU_ACT_RMSNORM:                                                     // four tokens per block
+        hipLaunchKernelGGL(k_prep_rms, dim3((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1)), dim3(256), 0, ex.st, d, A, xs);
+        break;
+    case QGPU_ACT_SILU_MUL: hipLaunchKernelGGL((k_prep_tok<QGPU_ACT_SILU_MUL, 0>), grid, dim3(256), 0, ex.st, d, A, xs); break;
+    default: hipLaunchKernelGGL((k_prep_tok<QGPU_ACT_GATED_NORM, 0>), grid, dim3(256), 0, ex.st, d, A, xs); break;
     }
     QG_LAUNCH_CHECK();
     return QGPU_OK;

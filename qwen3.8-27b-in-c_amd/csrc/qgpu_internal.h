@@ -59,24 +59,6 @@ static __device__ __forceinline__ void st_stream4(float *p, float4 v) { st_strea
 #define PLANE_BYTES ((size_t)MAX_NSB * DIGIT_TILE)
 #define XS_FLOATS   ((size_t)MAX_NSB * 16)
 
-// Digit planes of one (4-token plane, 256-element super-block), written by a
-// block of 256 threads: thread e holds element e of the super-block for the 4
-// tokens (v[i]; tokens past the batch hold 0) and m[i], the largest |v[i]| of
-// its wave.  Per token t the shift s_t puts the super-block maximum just under
-// 2^22 (s_t = 22 - exponent of the max; 0 for an all-zero or non-finite max);
-// x 2^s_t rounds to an integer X split into three balanced base-256 digits (X =
-// d0 + 2^8 d1 + 2^16 d2, d0, d1 in [-128, 127], |d2| <= 64): x to 2^-23 of the
-// super-block maximum.  A tile layout (3072 bytes): lane l = g*16 + m of the
-// GEMV wave holds, for A row m = t*4 + dgt (token-major; rows with dgt = 3 are
-// zero), digit dgt of token t at the 8 elements of sub-block ib that K-slots
-// 8g..8g+7 stand for (slot 8g+c, c < 4 -> element 4g+c; slot 8g+4+c -> element
-// 16+4g+c); two sub-blocks interleave so a lane fetches 16 bytes, and each
-// token's lanes come first to last in one 192-byte run: byte
-// (ib/2)*768 + (t*12 + g*3 + dgt)*16 + (ib%2)*8 + slot%8.  A GEMV of fewer than
-// 4 tokens reads only the runs of its tokens.  xs_tile[dgt*4 + t] =
-// 2^(8 dgt - s_t) converts the integer result of A row t*4 + dgt.  Every thread of the block calls it (two
-// barriers); in blocks of more than 256 threads, threads 0..255 pass active =
-// true and the others false (they only take part in the barriers).
 // Lane reductions with DPP moves (VALU, no LDS round trip).  A 16-lane row: lane ^ 1, lane ^ 2
 // (quad_perm), the other quad of the half row (row_half_mirror), the other half row
 // (row_mirror); each step combines a value with its mirror image, so every lane of the row ends
@@ -118,6 +100,24 @@ static __device__ __forceinline__ float wave_max64(float v)
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// Digit planes of one (4-token plane, 256-element super-block), written by a
+// block of 256 threads: thread e holds element e of the super-block for the 4
+// tokens (v[i]; tokens past the batch hold 0) and m[i], the largest |v[i]| of
+// its wave.  Per token t the shift s_t puts the super-block maximum just under
+// 2^22 (s_t = 22 - exponent of the max; 0 for an all-zero or non-finite max);
+// x 2^s_t rounds to an integer X split into three balanced base-256 digits (X =
+// d0 + 2^8 d1 + 2^16 d2, d0, d1 in [-128, 127], |d2| <= 64): x to 2^-23 of the
+// super-block maximum.  A tile layout (3072 bytes): lane l = g*16 + m of the
+// GEMV wave holds, for A row m = t*4 + dgt (token-major; rows with dgt = 3 are
+// zero), digit dgt of token t at the 8 elements of sub-block ib that K-slots
+// 8g..8g+7 stand for (slot 8g+c, c < 4 -> element 4g+c; slot 8g+4+c -> element
+// 16+4g+c); two sub-blocks interleave so a lane fetches 16 bytes, and each
+// token's lanes come first to last in one 192-byte run: byte
+// (ib/2)*768 + (t*12 + g*3 + dgt)*16 + (ib%2)*8 + slot%8.  A GEMV of fewer than
+// 4 tokens reads only the runs of its tokens.  xs_tile[dgt*4 + t] =
+// 2^(8 dgt - s_t) converts the integer result of A row t*4 + dgt.  Every thread of the block calls it (two
+// barriers); in blocks of more than 256 threads, threads 0..255 pass active =
+// true and the others false (they only take part in the barriers).
 struct ActDigitLds {
     uint8_t stage[DIGIT_TILE];
     float mx[4][4];          // [token][wave]
