@@ -29,6 +29,7 @@ extern "C" {
 
 #define QGPU_MAX_B       8    /* columns per batched GEMV (reference GEMV_MAX_B, kernels.h:19) */
 #define QGPU_MAX_MULTI   8    /* matrices per grouped GEMV (reference GEMV_MULTI_MAX, kernels.c:657) */
+#define QGPU_MAX_KS     32    /* K ranges per tile of a per-matrix split (qgpu_gemv_act_batch_ks) */
 
 /* ------------------------------------------------------------ runtime */
 /* Selects the device, creates the stream and the GEMV workspace. Idempotent. */
@@ -138,6 +139,16 @@ typedef struct {
 /* qgpu_gemv_multi_batch with the input given as a transform of device rows. */
 int  qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,
                          float *const *outs, const uint64_t *ldos, int flags);
+/* qgpu_gemv_act_batch with a K split per matrix (no reference counterpart: a
+ * scheduling form of the grouped GEMV, kernels.c:657).  The tiles of matrix j
+ * are cut into ks[j] K ranges (1..QGPU_MAX_KS, at most ne0 / 256), and range q
+ * writes partial plane q: outs[j][q*n*ldos[j] + t*ldos[j] + r]; the caller sums
+ * the planes in q order (ks[j] = 1: the plain output).  Splitting the small
+ * matrices of a grouped launch spreads their bytes over many compute units
+ * instead of adding a whole tile to a few.  Packed formats for ks[j] > 1; no
+ * accumulation. */
+int  qgpu_gemv_act_batch_ks(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,
+                            float *const *outs, const uint64_t *ldos, const int *ks);
 /* Transform only: v into act->xout (required) and the IQ4_XS digit planes
  * (so qgpu_gemv_prepared may follow). */
 int  qgpu_act_prepare(const qgpu_act *act, int n, uint64_t ne0);
@@ -211,7 +222,6 @@ int  qgpu_gdn_recurrence(const float *xq, uint64_t ldq, const float *beta_raw, c
                          uint64_t ldba, const float *dt_bias, const float *ssm_a, float *ring,
                          uint64_t slot_stride, int nslot, const int *cur, int B, int n_k, int n_v,
                          int head_dim, float eps, float *out, uint64_t ldo);
-/* rows x n: out = rmsnorm(x, w) * silu(z)  (per-head gated norm, model.c:928-941) */
 /* qgpu_gdn_conv + qgpu_gdn_recurrence in one launch (same arguments, results
  * and ring slots; the conv output is not stored): conv_dim = (2 n_k + n_v) * 128,
  * x = the raw wqkv projection rows. */
@@ -219,6 +229,16 @@ int  qgpu_gdn_fused(const float *x, uint64_t ldx, int B, int conv_dim, const flo
                     uint64_t conv_stride, const float *beta_raw, const float *alpha_raw, uint64_t ldba,
                     const float *dt_bias, const float *ssm_a, float *ssm_ring, uint64_t ssm_stride, int nslot,
                     const int *cur, int n_k, int n_v, int head_dim, float eps, float *out, uint64_t ldo);
+/* qgpu_gdn_fused with beta_raw and alpha_raw given as ba_planes partial planes
+ * (plane q at beta_raw + q*ba_pstride, the same for alpha_raw; 1..QGPU_MAX_KS,
+ * ba_planes * B <= 256), summed in plane order per token and head: the outputs
+ * of qgpu_gemv_act_batch_ks. */
+int  qgpu_gdn_fused_planes(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w, float *conv_ring,
+                           uint64_t conv_stride, const float *beta_raw, const float *alpha_raw, uint64_t ldba,
+                           int ba_planes, uint64_t ba_pstride, const float *dt_bias, const float *ssm_a,
+                           float *ssm_ring, uint64_t ssm_stride, int nslot, const int *cur, int n_k, int n_v,
+                           int head_dim, float eps, float *out, uint64_t ldo);
+/* rows x n: out = rmsnorm(x, w) * silu(z)  (per-head gated norm, model.c:928-941) */
 int  qgpu_rmsnorm_gated(float *out, const float *x, const float *z, const float *w, int n, int rows,
                         uint64_t ld, float eps);
 

@@ -12,6 +12,7 @@
 #define GDN_MAXB 8
 #define GDN_HK   128          // head_k_dim = head_v_dim (= ssm state size)
 #define GDN_RB   16           // state rows per block
+#define GDN_MAXBA QGPU_MAX_KS // partial planes of the gate inputs
 
 static __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
 
@@ -138,13 +139,15 @@ __global__ __launch_bounds__(256) void k_gdn_recur(const float *__restrict__ xq,
 __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, uint64_t ldx, const float *__restrict__ cw,
                                                    float *__restrict__ cring, uint64_t cstride,
                                                    const float *__restrict__ beta_raw, const float *__restrict__ alpha_raw,
-                                                   uint64_t ldba, const float *__restrict__ dt_bias,
+                                                   uint64_t ldba, int ba_planes, uint64_t ba_pstride,
+                                                   const float *__restrict__ dt_bias,
                                                    const float *__restrict__ ssm_a, float *__restrict__ sring,
                                                    uint64_t sstride, int nslot, const int *__restrict__ cur_dev, int B,
                                                    int n_k, int n_v, float eps, float *__restrict__ out, uint64_t ldo)
 {
     __shared__ float Yq[GDN_MAXB][GDN_HK], Yk[GDN_MAXB][GDN_HK], Yv[GDN_MAXB][GDN_RB];
     __shared__ float Gbeta[GDN_MAXB], Gdec[GDN_MAXB], Gkq[GDN_MAXB];
+    __shared__ float Pb[GDN_MAXBA][GDN_MAXB], Pa[GDN_MAXBA][GDN_MAXB];   // gate planes [plane][token]
     const int h = blockIdx.x / (GDN_HK / GDN_RB);
     const int rb = blockIdx.x % (GDN_HK / GDN_RB);
     const int tid = threadIdx.x;
@@ -173,20 +176,15 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
 #pragma unroll
         for (int b = 0; b < GDN_MAXB; b++) xB[b] = x[(uint64_t)(b < B ? b : B - 1) * ldx + cB];
     }
-    // ---- loads: per-token gates of this head
-    float braw = 0.0f, araw = 0.0f;
-    if (tid < B) {
-        braw = beta_raw[(uint64_t)tid * ldba + h];
-        araw = alpha_raw[(uint64_t)tid * ldba + h];
+    // ---- loads: per-token gate inputs of this head, one (plane, token) per thread (into LDS; summed
+    // after the first barrier)
+    if (tid < ba_planes * B) {
+        const int q = tid / B, t = tid - q * B;
+        const uint64_t o = (uint64_t)q * ba_pstride + (uint64_t)t * ldba + h;
+        Pb[q][t] = beta_raw[o];
+        Pa[q][t] = alpha_raw[o];
     }
     const float ah = ssm_a[h], dtb = dt_bias[h];
-    // ---- gates: beta = sigmoid(b), decay = exp(a * softplus(alpha + dt_bias)) (model.c:572-575)
-    if (tid < B) {
-        Gbeta[tid] = 1.0f / (1.0f + expf(-braw));
-        const float av = araw + dtb;
-        const float sp = av > 30.0f ? av : log1pf(expf(av));
-        Gdec[tid] = expf(ah * sp);
-    }
     // ---- conv + SiLU, conv-state snapshots
     {
         float *dA = tid < GDN_HK ? &Yq[0][tid] : &Yk[0][tid - GDN_HK];
@@ -218,6 +216,19 @@ __global__ __launch_bounds__(256) void k_gdn_fused(const float *__restrict__ x, 
         }
     }
     __syncthreads();
+    // ---- gates: beta = sigmoid(b), decay = exp(a * softplus(alpha + dt_bias)) (model.c:572-575), the
+    // gate inputs summed over their planes in plane order
+    if (tid < B) {
+        float braw = Pb[0][tid], araw = Pa[0][tid];
+        for (int q = 1; q < ba_planes; q++) {
+            braw += Pb[q][tid];
+            araw += Pa[q][tid];
+        }
+        Gbeta[tid] = 1.0f / (1.0f + expf(-braw));
+        const float av = araw + dtb;
+        const float sp = av > 30.0f ? av : log1pf(expf(av));
+        Gdec[tid] = expf(ah * sp);
+    }
     // ---- L2 norms (kernels.c:780-805) and q.k of every token, off the recurrence's serial path:
     // row group b (16 lanes) of the block handles token b, normalises its q and k in LDS and
     // keeps k.q of the normalised vectors
@@ -337,10 +348,12 @@ extern "C" int qgpu_rmsnorm_gated(float *out, const float *x, const float *z, co
     return QGPU_OK;
 }
 
-extern "C" int qgpu_gdn_fused(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w, float *conv_ring,
-                              uint64_t conv_stride, const float *beta_raw, const float *alpha_raw, uint64_t ldba,
-                              const float *dt_bias, const float *ssm_a, float *ssm_ring, uint64_t ssm_stride, int nslot,
-                              const int *cur, int n_k, int n_v, int head_dim, float eps, float *out, uint64_t ldo)
+extern "C" int qgpu_gdn_fused_planes(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w,
+                                     float *conv_ring, uint64_t conv_stride, const float *beta_raw,
+                                     const float *alpha_raw, uint64_t ldba, int ba_planes, uint64_t ba_pstride,
+                                     const float *dt_bias, const float *ssm_a, float *ssm_ring, uint64_t ssm_stride,
+                                     int nslot, const int *cur, int n_k, int n_v, int head_dim, float eps, float *out,
+                                     uint64_t ldo)
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
@@ -350,12 +363,22 @@ extern "C" int qgpu_gdn_fused(const float *x, uint64_t ldx, int B, int conv_dim,
         conv_dim != (2 * n_k + n_v) * GDN_HK || conv_stride < (uint64_t)conv_dim * 4 ||
         ssm_stride < (uint64_t)n_v * GDN_HK * GDN_HK || ldx < (uint64_t)conv_dim || ldo < (uint64_t)n_v * GDN_HK ||
         ldba < (uint64_t)n_v || ((uintptr_t)conv_ring & 15) || ((uintptr_t)conv_w & 15) || ((uintptr_t)ssm_ring & 15) ||
-        conv_stride % 4 || ssm_stride % 4)
+        conv_stride % 4 || ssm_stride % 4 || ba_planes < 1 || ba_planes > GDN_MAXBA || ba_planes * B > 256 ||
+        (ba_planes > 1 && ba_pstride < (uint64_t)B * ldba))
         return QGPU_E_ARG;
     hipLaunchKernelGGL(k_gdn_fused, dim3(n_v * (GDN_HK / GDN_RB)), dim3(256), 0, qg::stream, x, ldx, conv_w, conv_ring,
-                       conv_stride, beta_raw, alpha_raw, ldba, dt_bias, ssm_a, ssm_ring, ssm_stride, nslot, cur, B, n_k,
-                       n_v, eps, out, ldo);
+                       conv_stride, beta_raw, alpha_raw, ldba, ba_planes, ba_pstride, dt_bias, ssm_a, ssm_ring,
+                       ssm_stride, nslot, cur, B, n_k, n_v, eps, out, ldo);
     QG_LAUNCH_CHECK();
     return QGPU_OK;
+}
+
+extern "C" int qgpu_gdn_fused(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w, float *conv_ring,
+                              uint64_t conv_stride, const float *beta_raw, const float *alpha_raw, uint64_t ldba,
+                              const float *dt_bias, const float *ssm_a, float *ssm_ring, uint64_t ssm_stride, int nslot,
+                              const int *cur, int n_k, int n_v, int head_dim, float eps, float *out, uint64_t ldo)
+{
+    return qgpu_gdn_fused_planes(x, ldx, B, conv_dim, conv_w, conv_ring, conv_stride, beta_raw, alpha_raw, ldba, 1, 0,
+                                 dt_bias, ssm_a, ssm_ring, ssm_stride, nslot, cur, n_k, n_v, head_dim, eps, out, ldo);
 }
 

@@ -549,6 +549,8 @@ struct GemvMat {
     uint64_t ldo;
     uint32_t rows, tile0, row_lo, row_hi;   // flat tile start; rows written: [row_lo, row_hi)
     uint32_t tile_first;                    // first tile of this matrix that is launched
+    uint32_t blk0, ks;                      // first block; K ranges per tile (block q of a tile writes
+    uint64_t pstride;                       // partial plane q at out + q * pstride when the launch splits)
 };
 struct GemvArgs {
     GemvMat m[QGPU_MAX_MULTI];
@@ -557,8 +559,6 @@ struct GemvArgs {
     const float *xs;
     const float *x;        // VALU path: fp32 activations
     uint64_t ldx, ne0;
-    int ks;                // K split: ks blocks per tile, block q writes partial plane q (out + q*pstride)
-    uint64_t pstride;
     const float *rss;      // deferred RMSNorm: outputs *= 1/sqrt(sum_sb rss[t*rss_nsb+sb] * rss_inv_n + eps)
     int rss_nsb;
     float rss_inv_n, eps;
@@ -898,13 +898,13 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
     const float4 oh = make_float4(g == 0, g == 1, g == 2, g == 3);   // token g of this lane group
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar loop control
-    const uint32_t tile = (MODE & IQ4_SPLIT) ? blockIdx.x / args.ks : blockIdx.x;
-    const int kq = (MODE & IQ4_SPLIT) ? blockIdx.x % args.ks : 0;   // K range of this block (split GEMV)
-    const int ks = (MODE & IQ4_SPLIT) ? args.ks : 1;
     int k = 0;
-    while (k + 1 < args.n_mat && tile >= args.m[k + 1].tile0) k++;
+    while (k + 1 < args.n_mat && blockIdx.x >= args.m[k + 1].blk0) k++;
     const GemvMat &M = args.m[k];
-    const uint32_t T = tile - M.tile0 + M.tile_first;
+    const uint32_t lb = blockIdx.x - M.blk0;                        // block within matrix k
+    const int ks = (MODE & IQ4_SPLIT) ? (int)M.ks : 1;
+    const uint32_t T = ((MODE & IQ4_SPLIT) ? lb / (uint32_t)ks : lb) + M.tile_first;
+    const int kq = (MODE & IQ4_SPLIT) ? (int)(lb % (uint32_t)ks) : 0;   // K range of this block (split GEMV)
     const int nsb = args.nsb;
     constexpr uint32_t REC = FMT == T_IQ4_XS ? IQ4_REC_BYTES : FMT == T_Q4_K ? 2304 : FMT == T_Q5_K ? 2816 : FMT == T_Q6_K ? 3360 : 4352;
     const uint8_t *rec0 = M.W + (uint64_t)T * nsb * REC;
@@ -965,7 +965,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
         if (t < args.ntok && r >= M.row_lo && r < M.row_hi) {
             if (MODE & IQ4_RMS) s *= rsc[t];
             if (MODE & IQ4_SPLIT) {
-                M.out[(uint64_t)kq * args.pstride + (uint64_t)t * M.ldo + r] = s;
+                M.out[(uint64_t)kq * M.pstride + (uint64_t)t * M.ldo + r] = s;
             } else {
                 float *o = M.out + (uint64_t)t * M.ldo + r;
                 *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + s : s;
@@ -1223,23 +1223,24 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
 #endif
 static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x,
                         uint64_t ldx, int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
-                        const uint64_t *r1s, int ks, float eps, bool deferred)
+                        const uint64_t *r1s, int ks, const int *ksm, float eps, bool deferred)
 {
     const qgpu_tensor *W0 = Ws[idx[0]];
     GemvArgs A = {};
     A.n_mat = cnt; A.ntok = n; A.flags = flags; A.x = x; A.ldx = ldx; A.ne0 = W0->ne0;
-    A.ks = ks;
-    A.pstride = (uint64_t)n * ldos[idx[0]];
     if (deferred) {
         A.rss = ws_rss(ex); A.rss_nsb = (int)(W0->ne0 / 256); A.rss_inv_n = 1.0f / (float)W0->ne0; A.eps = eps;
     }
     A.nsb = (int)(W0->ne0 / 256);
     const bool mfma = W0->packed;
     const uint32_t per = mfma ? IQ4_TILE_ROWS : 8;
-    uint32_t tiles = 0;
+    uint32_t tiles = 0, blocks = 0;
+    bool split = false;
     for (int j = 0; j < cnt; j++) {
         const qgpu_tensor *W = Ws[idx[j]];
         const uint64_t lo = r0s ? r0s[idx[j]] : 0, hi = r1s ? r1s[idx[j]] : W->ne1;
+        const uint32_t t = (uint32_t)((hi + per - 1) / per - lo / per);
+        const int kj = ksm ? ksm[idx[j]] : ks;                 // K ranges per tile of this matrix
         GemvMat &M = A.m[j];
         M.W = (const uint8_t *)W->data;
         M.out = outs[idx[j]];
@@ -1249,7 +1250,12 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         M.row_hi = (uint32_t)hi;
         M.tile_first = (uint32_t)(lo / per);
         M.tile0 = tiles;
-        tiles += (uint32_t)((hi + per - 1) / per - lo / per);
+        M.blk0 = blocks;
+        M.ks = (uint32_t)kj;
+        M.pstride = (uint64_t)n * ldos[idx[j]];
+        tiles += t;
+        blocks += t * (uint32_t)kj;
+        if (kj > 1) split = true;
     }
     if (!tiles) return QGPU_OK;
     if (mfma) {
@@ -1271,13 +1277,13 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         if (force_nw == 1 || force_nw == 2 || force_nw == 4 || force_nw == 8) nw = force_nw;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
         if (A.rss && nw < 4) nw = 4;                        // row factors: <= 2 tokens per wave
-        const int mode = (A.rss ? IQ4_RMS : 0) | (ks > 1 ? IQ4_SPLIT : 0);
+        const int mode = (A.rss ? IQ4_RMS : 0) | (split ? IQ4_SPLIT : 0);
         switch (W0->type) {
-        case T_IQ4_XS: launch_mfma<T_IQ4_XS>(ex, A, tiles * ks, na, nw, mode); break;
-        case T_Q4_K: launch_mfma<T_Q4_K>(ex, A, tiles * ks, na, nw, mode); break;
-        case T_Q5_K: launch_mfma<T_Q5_K>(ex, A, tiles * ks, na, nw, mode); break;
-        case T_Q6_K: launch_mfma<T_Q6_K>(ex, A, tiles * ks, na, nw, mode); break;
-        case T_Q8_0: launch_mfma<T_Q8_0>(ex, A, tiles * ks, na, nw, mode); break;
+        case T_IQ4_XS: launch_mfma<T_IQ4_XS>(ex, A, blocks, na, nw, mode); break;
+        case T_Q4_K: launch_mfma<T_Q4_K>(ex, A, blocks, na, nw, mode); break;
+        case T_Q5_K: launch_mfma<T_Q5_K>(ex, A, blocks, na, nw, mode); break;
+        case T_Q6_K: launch_mfma<T_Q6_K>(ex, A, blocks, na, nw, mode); break;
+        case T_Q8_0: launch_mfma<T_Q8_0>(ex, A, blocks, na, nw, mode); break;
         default: return QGPU_E_TYPE;
         }
         QG_LAUNCH_CHECK();
@@ -1308,7 +1314,7 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
 // act == NULL: packed matrices only, on the digit planes of the last prepare.
 static int gemv_multi_on(const GemvExec &ex, const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,
                          float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
-                         const uint64_t *r1s, int ks = 1)
+                         const uint64_t *r1s, int ks = 1, const int *ksm = nullptr)
 {
     int rc = QGPU_OK;
     if (!Ws || !outs || !ldos || n_mat < 1 || n_mat > QGPU_MAX_MULTI || n < 1 || n > QGPU_MAX_B || !Ws[0])
@@ -1322,6 +1328,12 @@ static int gemv_multi_on(const GemvExec &ex, const qgpu_tensor *const *Ws, int n
         if (Ws[j]->packed) any_mfma = true; else any_valu = true;
     }
     if (ks < 1 || ks > 8 || (ks > 1 && (n_mat != 1 || any_valu || r0s || (int)(ne0 / 256) < ks))) return QGPU_E_ARG;
+    if (ksm) {                                              // per-matrix K split (packed formats, plain outputs)
+        if (ks != 1 || (flags & QGPU_GEMV_ACCUM)) return QGPU_E_ARG;
+        for (int j = 0; j < n_mat; j++)
+            if (ksm[j] < 1 || ksm[j] > QGPU_MAX_KS || (int)(ne0 / 256) < ksm[j] || (ksm[j] > 1 && !Ws[j]->packed))
+                return QGPU_E_ARG;
+    }
     const float *xv = nullptr;                              // fp32 rows for the VALU kernel (unpacked formats)
     uint64_t ldxv = ne0;
     bool deferred = false;
@@ -1349,7 +1361,7 @@ static int gemv_multi_on(const GemvExec &ex, const qgpu_tensor *const *Ws, int n
         int idx[QGPU_MAX_MULTI], cnt = 0;
         for (int i = j; i < n_mat; i++)
             if (!done[i] && Ws[i]->type == Ws[j]->type) { idx[cnt++] = i; done[i] = 1; }
-        rc = launch_group(ex, Ws, idx, cnt, xv, ldxv, n, outs, ldos, flags, r0s, r1s, ks, eps, deferred);
+        rc = launch_group(ex, Ws, idx, cnt, xv, ldxv, n, outs, ldos, flags, r0s, r1s, ks, ksm, eps, deferred);
         if (rc) return rc;
     }
     return QGPU_OK;
@@ -1429,6 +1441,15 @@ extern "C" int qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, cons
 {
     if (!act) return QGPU_E_ARG;
     return gemv_multi(Ws, n_mat, act, n, outs, ldos, flags, nullptr, nullptr);
+}
+
+extern "C" int qgpu_gemv_act_batch_ks(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,
+                                      float *const *outs, const uint64_t *ldos, const int *ks)
+{
+    if (!act || !ks) return QGPU_E_ARG;
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    return gemv_multi_on(lib_exec(), Ws, n_mat, act, n, outs, ldos, 0, nullptr, nullptr, 1, ks);
 }
 
 extern "C" int qgpu_gemv_act_split(const qgpu_tensor *W, const qgpu_act *act, int n, float *part, uint64_t ldp,

@@ -387,7 +387,9 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     AL(g->d_pos, 4); AL(g->d_cur, 4); AL(g->d_tok, 64); AL(g->d_cand, 64); AL(g->d_vtok, 64); AL(g->d_acc, 64);
     AL(g->bx, MAXB * E); AL(g->bxb, MAXB * E); AL(g->bqkv, MAXB * g->SQ); AL(g->bk, MAXB * g->kvrow);
     AL(g->bv, MAXB * g->kvrow); AL(g->bz, MAXB * (uint64_t)d->d_inner);
-    AL(g->bbeta, MAXB * (uint64_t)d->n_v_heads + 4); AL(g->balpha, MAXB * (uint64_t)d->n_v_heads + 4);
+    /* gate inputs: up to QGPU_MAX_KS partial planes of MAXB rows (gdn_dev) */
+    AL(g->bbeta, QGPU_MAX_KS * MAXB * (uint64_t)d->n_v_heads + 4);
+    AL(g->balpha, QGPU_MAX_KS * MAXB * (uint64_t)d->n_v_heads + 4);
     AL(g->bffn, MAXB * F); AL(g->battn, MAXB * g->A); AL(g->xq, MAXB * (uint64_t)d->conv_dim);
     AL(g->h_save, MAXB * E); AL(g->logits_b, MAXB * V); AL(g->logits1, V); AL(g->mtp_h, E);
     AL(g->mx, MAXB * E); AL(g->cat, MAXB * 2 * E); AL(g->part, 8 * MAXB * E);
@@ -639,11 +641,23 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     const qgpu_tensor *W[4] = { D->wqkv, D->wgate, D->beta, D->alpha };
     float *outs[4] = { g->bqkv, g->bz, g->bbeta, g->balpha };
     const uint64_t ld[4] = { g->SQ, di, d->n_v_heads, d->n_v_heads };
-    K(qgpu_gemv_act_batch(W, 4, &an, (int)B, outs, ld, 0));
+    /* beta and alpha (n_v_heads rows each: a few tiles) are cut into one K range per 256-column
+     * super-block, so their bytes spread over many compute units instead of adding a whole tile to a
+     * few (with 1024 + 6 tiles, 6 compute units would stream 5 tiles and the rest 4); the GDN kernel
+     * sums the partial planes */
+    int kba = 1;
+    if (mat_packed(D->beta) && mat_packed(D->alpha)) {
+        kba = (int)(d->n_embd / 256);
+        if (kba > QGPU_MAX_KS) kba = QGPU_MAX_KS;
+        if (kba * (int)B > 256) kba = 256 / (int)B;
+    }
+    const int ks[4] = { 1, 1, kba, kba };
+    K(qgpu_gemv_act_batch_ks(W, 4, &an, (int)B, outs, ld, ks));
     /* conv1d + SiLU + L2 norms + delta rule over the B tokens, state snapshots into the ring */
-    K(qgpu_gdn_fused(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems, g->bbeta,
-                     g->balpha, d->n_v_heads, D->dt_bias, D->ssm_a, D->ssm_ring, g->ssm_elems, NSLOT, g->d_cur,
-                     (int)d->n_k_heads, (int)d->n_v_heads, (int)d->head_v_dim, eps, g->battn, di));
+    K(qgpu_gdn_fused_planes(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems,
+                            g->bbeta, g->balpha, d->n_v_heads, kba, (uint64_t)B * d->n_v_heads, D->dt_bias,
+                            D->ssm_a, D->ssm_ring, g->ssm_elems, NSLOT, g->d_cur, (int)d->n_k_heads,
+                            (int)d->n_v_heads, (int)d->head_v_dim, eps, g->battn, di));
     /* per-head gated RMSNorm (model.c:928-941) fused into the ssm_out input */
     qgpu_act gn;
     memset(&gn, 0, sizeof gn);

@@ -280,6 +280,8 @@ class GpuLib:
             "qgpu_rmsnorm_gated": [F32P, F32P, F32P, F32P, i32, i32, u64, f32],
             "qgpu_gdn_fused": [F32P, u64, i32, i32, F32P, F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, u64, i32,
                                ctypes.POINTER(i32), i32, i32, i32, f32, F32P, u64],
+            "qgpu_gdn_fused_planes": [F32P, u64, i32, i32, F32P, F32P, u64, F32P, F32P, u64, i32, u64, F32P, F32P,
+                                      F32P, u64, i32, ctypes.POINTER(i32), i32, i32, i32, f32, F32P, u64],
             "qgpu_attn_prep": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
                                ctypes.POINTER(i32), i32, i32, i32, i32, f32],
             "qgpu_attn_decode": [F32P, u64, F32P, F32P, ctypes.POINTER(i32), i32, i32, i32, i32, i32, F32P, u64],
@@ -291,6 +293,8 @@ class GpuLib:
             "qgpu_set_i32": [ctypes.POINTER(i32), i32],
             "qgpu_gemv_act_batch": [ctypes.POINTER(vp), i32, ctypes.POINTER(Act), i32, ctypes.POINTER(F32P),
                                     ctypes.POINTER(u64), i32],
+            "qgpu_gemv_act_batch_ks": [ctypes.POINTER(vp), i32, ctypes.POINTER(Act), i32, ctypes.POINTER(F32P),
+                                       ctypes.POINTER(u64), ctypes.POINTER(i32)],
             "qgpu_act_prepare": [ctypes.POINTER(Act), i32, u64],
             "qgpu_gemv_act_split": [vp, ctypes.POINTER(Act), i32, F32P, u64, i32],
             "qgpu_gemv_split_ks": [vp],

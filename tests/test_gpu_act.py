@@ -196,3 +196,59 @@ def test_rmsnorm_consumes_partials(gpu, tp, tc, B):
     a2.kind, a2.x, a2.ldx, a2.part, a2.ldp, a2.n_part = pyqwen.ACT_COPY, Rb.f32(), E, pb.f32(), E, ks
     assert gpu.L.qgpu_gemv_act_batch(Ws, 1, ctypes.byref(a2), B, outs, lds, 0) != 0
     gpu.sync()
+
+
+@pytest.mark.parametrize("B", [1, 4, 8])
+def test_act_batch_ks_planes(gpu, B):
+    """qgpu_gemv_act_batch_ks, the grouped GEMV with a K split per matrix (the GDN input projection cuts
+    its two narrow gate matrices so): matrices with ks = 1 give the outputs of qgpu_gemv_act_batch bit
+    for bit; a matrix with ks > 1 gives ks partial planes whose sum (in plane order) is the oracle GEMV of
+    the RMSNorm input within 1e-3, and qgpu_gemv_act_batch's output within 2e-5 (the deferred row factor
+    applies to every plane).  Mixed formats: one launch per format, each with its own split."""
+    print(f"\n[act-ks] B={B}", flush=True)
+    host = host_lib()
+    E = 2048
+    mats = [(23, 384, 1), (14, 256, 1), (23, 48, 8), (8, 48, 3)]       # (type, rows, K ranges)
+    Ws_h = [host.synth_matrix(t, E, r, 41 + i, t, 0.02) for i, (t, r, _) in enumerate(mats)]
+    Ts = [gpu.tensor(W, t, E, r) for W, (t, r, _) in zip(Ws_h, mats)]
+    rng = np.random.default_rng(70 + B)
+    x = (rng.standard_normal((B, E)) * 3).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(E)).astype(np.float32)
+    xb, wb = gpu.put(x), gpu.put(w)
+    a = pyqwen.Act()
+    a.kind, a.x, a.ldx, a.w, a.eps = pyqwen.ACT_RMSNORM, xb.f32(), E, wb.f32(), EPS
+    n = len(mats)
+    Ws = (ctypes.c_void_p * n)(*[T.h for T in Ts])
+    lds = (ctypes.c_uint64 * n)(*[r for _, r, _ in mats])
+    plain = [gpu.buf(B * r * 4) for _, r, _ in mats]
+    split = [gpu.buf(k * B * r * 4) for _, r, k in mats]
+    gpu.ok(gpu.L.qgpu_gemv_act_batch(Ws, n, ctypes.byref(a), B, (pyqwen.F32P * n)(*[b.f32() for b in plain]),
+                                     lds, 0))
+    ks = (ctypes.c_int * n)(*[k for _, _, k in mats])
+    gpu.ok(gpu.L.qgpu_gemv_act_batch_ks(Ws, n, ctypes.byref(a), B, (pyqwen.F32P * n)(*[b.f32() for b in split]),
+                                        lds, ks))
+    xin = np.stack([o_rmsnorm(x[b], w) for b in range(B)])
+    for j, (t, r, k) in enumerate(mats):
+        p = plain[j].download(np.float32).reshape(B, r)
+        s = split[j].download(np.float32).reshape(k, B, r)
+        if k == 1:
+            assert np.array_equal(s[0], p), j
+            continue
+        tot = s[0].copy()
+        for q in range(1, k):
+            tot = (tot + s[q]).astype(np.float32)
+        e_or = rel_err(tot, O.gemv(t, Ws_h[j], E, r, xin, B))
+        e_pl = rel_err(tot, p)
+        print(f"  matrix {j} type {t} ks={k}: vs oracle {e_or:.2e}, vs unsplit {e_pl:.2e}", flush=True)
+        assert e_or < 1e-3 and e_pl < 2e-5, (j, e_or, e_pl)
+    # rejected: a K range count of 0, above 32 or above the super-blocks of a row, a split of an fp32 matrix
+    for bad in ([1, 1, 0, 1], [1, 1, 33, 1], [1, 1, 9, 1]):
+        kb = (ctypes.c_int * n)(*bad)
+        assert gpu.L.qgpu_gemv_act_batch_ks(Ws, n, ctypes.byref(a), B,
+                                            (pyqwen.F32P * n)(*[b.f32() for b in split]), lds, kb) != 0, bad
+    Wf = host.synth_matrix(0, E, 48, 49, 0, 0.02)
+    Tf = gpu.tensor(Wf, 0, E, 48)
+    Wf_s = (ctypes.c_void_p * 1)(Tf.h)
+    assert gpu.L.qgpu_gemv_act_batch_ks(Wf_s, 1, ctypes.byref(a), B, (pyqwen.F32P * 1)(split[2].f32()),
+                                        (ctypes.c_uint64 * 1)(48), (ctypes.c_int * 1)(2)) != 0
+    gpu.sync()

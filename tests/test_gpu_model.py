@@ -104,6 +104,72 @@ def test_gdn_block_config3_vs_oracle_with_snapshots_and_rollback(gpu, fused):
     assert rel_err(ob.download(np.float32, nv * hk), o2) < 1e-3
 
 
+@pytest.mark.parametrize("planes", [1, 3, 20])
+def test_gdn_fused_gate_planes(gpu, planes):
+    """qgpu_gdn_fused_planes: the gate inputs (beta, alpha) given as partial planes, summed in plane order
+    per (token, head), give the outputs and the state/conv snapshots of qgpu_gdn_fused on the summed
+    inputs bit for bit, and the oracle's within 1e-3 (config-3 shapes, T = 4)."""
+    print(f"\n[gdn-planes] {planes} gate planes", flush=True)
+    T, nk, nv, hk = 4, 16, 48, 128
+    cd, eps = 2 * nk * hk + nv * hk, 1e-6
+    host = host_lib()
+    qkv = host.synth_normal(T * cd, 4, 1).reshape(T, cd)
+    cw = host.synth_normal(cd * 4, 4, 4, 0.0, 0.5)
+    conv0 = host.synth_normal(cd * 4, 4, 5, 0.0, 0.5)
+    ssm0 = host.synth_normal(nv * hk * hk, 4, 6, 0.0, 0.01)
+    dtb = np.full(nv, 0.1, np.float32)
+    sa = -np.ones(nv, np.float32)
+    rng = np.random.default_rng(planes)
+    bp = (rng.standard_normal((planes, T, nv)) / np.sqrt(planes)).astype(np.float32)
+    ap = (rng.standard_normal((planes, T, nv)) / np.sqrt(planes)).astype(np.float32)
+
+    def psum(p):
+        s = p[0].copy()
+        for q in range(1, len(p)):
+            s = (s + p[q]).astype(np.float32)
+        return s
+    br, ar = psum(bp), psum(ap)
+    L = O.lib()
+    oc, os_ = conv0.copy(), ssm0.copy()
+    oout = np.zeros(T * nv * hk, np.float32)
+    L.or_gdn_block(T, cd, nk, nv, hk, hk, eps, O.fptr(qkv), O.fptr(br), O.fptr(ar), O.fptr(cw), O.fptr(dtb),
+                   O.fptr(sa), O.fptr(oc), O.fptr(os_), O.fptr(oout), None, None)
+    cur0 = 2
+    cstride, sstride = cd * 4, nv * hk * hk
+    cring = gpu.put(np.zeros(NSLOT * cstride, np.float32))
+    sring = gpu.put(np.zeros(NSLOT * sstride, np.float32))
+    cring.upload(conv0, cur0 * cstride * 4)
+    sring.upload(ssm0, cur0 * sstride * 4)
+    curb = gpu.put(np.array([cur0], np.int32))
+    xb, cwb, dtbb, sab = gpu.put(qkv), gpu.put(cw), gpu.put(dtb), gpu.put(sa)
+    ob = gpu.buf(T * nv * hk * 4)
+    # summed inputs through qgpu_gdn_fused (the current slot is read, never written: both runs start there)
+    bb, ab = gpu.put(br), gpu.put(ar)
+    gpu.ok(gpu.L.qgpu_gdn_fused(xb.f32(), cd, T, cd, cwb.f32(), cring.f32(), cstride, bb.f32(), ab.f32(), nv,
+                                dtbb.f32(), sab.f32(), sring.f32(), sstride, NSLOT, curb.i32(), nk, nv, hk, eps,
+                                ob.f32(), nv * hk))
+    o1 = ob.download(np.float32)
+    c1, s1 = cring.download(np.float32), sring.download(np.float32)
+    bpb, apb = gpu.put(bp), gpu.put(ap)
+    gpu.ok(gpu.L.qgpu_gdn_fused_planes(xb.f32(), cd, T, cd, cwb.f32(), cring.f32(), cstride, bpb.f32(), apb.f32(),
+                                       nv, planes, T * nv, dtbb.f32(), sab.f32(), sring.f32(), sstride, NSLOT,
+                                       curb.i32(), nk, nv, hk, eps, ob.f32(), nv * hk))
+    o2 = ob.download(np.float32)
+    assert np.array_equal(o1, o2)
+    assert np.array_equal(c1, cring.download(np.float32)) and np.array_equal(s1, sring.download(np.float32))
+    e = rel_err(o2, oout)
+    print(f"  output vs oracle {e:.2e}", flush=True)
+    assert e < 1e-3
+    # plane counts outside 1..32, or 32 planes of 9 tokens (> 256 gate loads), are rejected
+    for npl in (0, 33):
+        assert gpu.L.qgpu_gdn_fused_planes(xb.f32(), cd, T, cd, cwb.f32(), cring.f32(), cstride, bpb.f32(),
+                                           apb.f32(), nv, npl, T * nv, dtbb.f32(), sab.f32(), sring.f32(), sstride,
+                                           NSLOT, curb.i32(), nk, nv, hk, eps, ob.f32(), nv * hk) != 0, npl
+    assert gpu.L.qgpu_gdn_fused_planes(xb.f32(), cd, T, cd, cwb.f32(), cring.f32(), cstride, bpb.f32(), apb.f32(),
+                                       nv, 2, T * nv - 1, dtbb.f32(), sab.f32(), sring.f32(), sstride, NSLOT,
+                                       curb.i32(), nk, nv, hk, eps, ob.f32(), nv * hk) != 0   # planes overlap
+    gpu.sync()
+
 def test_rmsnorm_gated(gpu):
     rng = np.random.default_rng(1)
     rows, n = 12, 128
