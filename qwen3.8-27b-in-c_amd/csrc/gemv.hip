@@ -565,24 +565,26 @@ struct GemvArgs {
 };
 
 // Row factors of the deferred RMSNorm, one per token, into rsc[]: wave w owns tokens
-// w, w + nw (<= 2 per wave for nw >= 4); the per-super-block sums of squares are
+// w, w + nw, ... (NU = ceil(8 / nw) per wave); the per-super-block sums of squares are
 // added in the same fixed order in every block.  rms_load issues the loads (before
 // the main loop, so their latency is hidden), rms_reduce finishes after it.
 // (rss_nsb <= 64: one sum per lane and token)
-struct RmsPart { float v[2]; };
-static __device__ __forceinline__ void rms_load(const GemvArgs &args, int wv, int nw, int lane, RmsPart &rp)
+template <int NU> struct RmsPart { float v[NU]; };
+template <int NU>
+static __device__ __forceinline__ void rms_load(const GemvArgs &args, int wv, int nw, int lane, RmsPart<NU> &rp)
 {
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+    for (int u = 0; u < NU; u++) {
         const int t = wv + u * nw;
         rp.v[u] = (t < args.ntok && lane < args.rss_nsb) ? args.rss[(uint64_t)t * args.rss_nsb + lane] : 0.0f;
     }
 }
-static __device__ __forceinline__ void rms_reduce(const GemvArgs &args, int wv, int nw, int lane, const RmsPart &rp,
+template <int NU>
+static __device__ __forceinline__ void rms_reduce(const GemvArgs &args, int wv, int nw, int lane, const RmsPart<NU> &rp,
                                                   float *rsc)
 {
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+    for (int u = 0; u < NU; u++) {
         const int t = wv + u * nw;
         const float s = wave_sum64(rp.v[u]);
         if (lane == 0 && t < args.ntok) rsc[t] = 1.0f / sqrtf(s * args.rss_inv_n + args.eps);
@@ -639,10 +641,12 @@ static __device__ __forceinline__ void iq4_decode8(uint32_t q, uint32_t &x_lo, u
 
 // Weight records come from HBM and activation digits from L2, so the two are
 // prefetched to different depths: weights IQ4_WDEPTH super-blocks ahead
-// (10 VGPRs each), digits IQ4_ADEPTH ahead (16 * NA + 4 * NA VGPRs each).
-// Measured on MI355X over the whole 27B step with 3-digit tiles: weights 2 ahead
-// is 0.7% faster than 3 (decode 5.55 -> 5.49 ms), 4 ahead 5% slower, digits 2
-// ahead 3% slower.
+// (10 VGPRs each), digits IQ4_ADEPTH1 / IQ4_ADEPTH2 ahead (16 * NA VGPRs each).
+// Measured on MI355X: weights 2 ahead is 0.7% faster than 3 over the 27B step
+// (decode 5.55 -> 5.49 ms), 4 ahead 5% slower.  Digits 2 ahead with one digit
+// plane: 17408x5120 B = 4 15.0 -> 14.3 us, B = 1 14.7 -> 13.2 us, decode step
+// 4.82 -> 4.70 ms, at 84 VGPRs (5 waves per SIMD instead of 7); with two planes
+// 1-11% slower (B = 8 shapes), so those keep 1.
 template <int FMT> struct WRec;                              // a lane's slice of one record
 template <> struct WRec<T_IQ4_XS> { uint2 hdr; uint4 qa, qb; };
 template <int NA>
@@ -877,21 +881,25 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
 #ifndef IQ4_WDEPTH
 #define IQ4_WDEPTH 2    // weight records in flight per wave
 #endif
-#ifndef IQ4_ADEPTH
-#define IQ4_ADEPTH 1    // digit super-blocks in flight per wave
+#ifndef IQ4_ADEPTH1
+#define IQ4_ADEPTH1 2   // digit super-blocks in flight per wave, one digit plane (B <= 4)
 #endif
-// main-loop unroll: a common multiple of the two ring depths (compile-time ring slots)
-#define IQ4_UNROLL ((IQ4_WDEPTH % IQ4_ADEPTH) == 0 ? IQ4_WDEPTH : IQ4_WDEPTH * IQ4_ADEPTH)
+#ifndef IQ4_ADEPTH2
+#define IQ4_ADEPTH2 1   // the same, two digit planes (B = 5..8: 20 more VGPRs per slot)
+#endif
 
 // MODE bit 0 (IQ4_RMS): deferred RMSNorm row factors; bit 1 (IQ4_SPLIT): K split
 // into partial planes.  Plain launches (MODE 0) compile without either.
 #define IQ4_RMS   1
 #define IQ4_SPLIT 2
 template <int FMT, int NA, int NW, int MODE>
-#ifndef IQ4_MINW
-#define IQ4_MINW 1
+#ifndef IQ4_MINW1
+#define IQ4_MINW1 1     // minimum waves per SIMD the compiler must allow (caps VGPRs), one digit plane
 #endif
-__global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs args)
+#ifndef IQ4_MINW2
+#define IQ4_MINW2 1     // the same, two digit planes
+#endif
+__global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_gemv_mfma(const GemvArgs args)
 {
     __shared__ float red[NW][NA][4][16];
     __shared__ float rsc[QGPU_MAX_B];
@@ -910,7 +918,7 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
     const uint8_t *rec0 = M.W + (uint64_t)T * nsb * REC;
     const int kb0 = kq * nsb / ks, nkb = (kq + 1) * nsb / ks - kb0;
     const int sb0 = kb0 + wv * nkb / NW, sb1 = kb0 + (wv + 1) * nkb / NW;
-    RmsPart rp;
+    RmsPart<(QGPU_MAX_B + NW - 1) / NW> rp;
     if (MODE & IQ4_RMS) rms_load(args, wv, NW, lane, rp);
 
     float accf[NA][4];
@@ -920,28 +928,31 @@ __global__ __launch_bounds__(NW * 64, IQ4_MINW) void k_gemv_mfma(const GemvArgs 
         for (int i = 0; i < 4; i++) accf[a][i] = 0.0f;
 
     // two register rings: weights of super-block sb+IQ4_WDEPTH-1 and digits of
-    // sb+IQ4_ADEPTH-1 are loading while sb is decoded and multiplied (ring
-    // indices are compile-time after unrolling by IQ4_UNROLL).  Each step
+    // sb+ADEPTH-1 are loading while sb is decoded and multiplied (ring
+    // indices are compile-time after unrolling by UNROLL).  Each step
     // issues its digit loads before its weight loads (vmcnt retires loads in
     // issue order, so a wait for the digits need not cover the newer weights).
+    constexpr int ADEPTH = NA == 1 ? IQ4_ADEPTH1 : IQ4_ADEPTH2;
+    // main-loop unroll: a common multiple of the two ring depths (compile-time ring slots)
+    constexpr int UNROLL = (IQ4_WDEPTH % ADEPTH) == 0 ? IQ4_WDEPTH : IQ4_WDEPTH * ADEPTH;
     WRec<FMT> wr[IQ4_WDEPTH];
-    IQ4A<NA> ar[IQ4_ADEPTH];
+    IQ4A<NA> ar[ADEPTH];
 #define LOAD_W(slot, sbx) kq_load_w<FMT>(wr[slot], rec0 + (uint64_t)(sbx) * REC, lane, n)
 #define LOAD_A(slot, sbx) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)(sbx) * DIGIT_TILE, args.xs + (uint64_t)(sbx) * 16, lane, args.ntok)
 #pragma unroll
-    for (int d = 0; d < IQ4_WDEPTH - 1 || d < IQ4_ADEPTH - 1; d++) {
-        if (d < IQ4_ADEPTH - 1 && sb0 + d < sb1) LOAD_A(d, sb0 + d);
+    for (int d = 0; d < IQ4_WDEPTH - 1 || d < ADEPTH - 1; d++) {
+        if (d < ADEPTH - 1 && sb0 + d < sb1) LOAD_A(d, sb0 + d);
         if (d < IQ4_WDEPTH - 1 && sb0 + d < sb1) LOAD_W(d, sb0 + d);
     }
-    for (int sb = sb0; sb < sb1; sb += IQ4_UNROLL) {
+    for (int sb = sb0; sb < sb1; sb += UNROLL) {
 #pragma unroll
-        for (int d = 0; d < IQ4_UNROLL; d++) {
+        for (int d = 0; d < UNROLL; d++) {
             if (sb + d < sb1) {
-                const int pw = sb + d + IQ4_WDEPTH - 1, pa = sb + d + IQ4_ADEPTH - 1;
-                if (pa < sb1) LOAD_A((d + IQ4_ADEPTH - 1) % IQ4_ADEPTH, pa);
+                const int pw = sb + d + IQ4_WDEPTH - 1, pa = sb + d + ADEPTH - 1;
+                if (pa < sb1) LOAD_A((d + ADEPTH - 1) % ADEPTH, pa);
                 if (pw < sb1) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
-                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], oh, accf);
-                else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % IQ4_ADEPTH], oh, accf);
+                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % ADEPTH], oh, accf);
+                else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % ADEPTH], oh, accf);
             }
         }
     }
@@ -1043,7 +1054,7 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
     __shared__ float rsc[QGPU_MAX_B];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     if (args.rss) {
-        RmsPart rp;
+        RmsPart<2> rp;
         rms_load(args, wv, 4, lane, rp);
         rms_reduce(args, wv, 4, lane, rp, rsc);
         __syncthreads();
@@ -1207,13 +1218,52 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
 {
 #define MF_GO(NA_, NW_, M_) hipLaunchKernelGGL((k_gemv_mfma<FMT, NA_, NW_, M_>), dim3(blocks), dim3(64 * NW_), 0, ex.st, A)
 #define MF_NW(NA_, M_) do { if (nw == 1) MF_GO(NA_, 1, M_); else if (nw == 2) MF_GO(NA_, 2, M_); \
-                            else if (nw == 4) MF_GO(NA_, 4, M_); else MF_GO(NA_, 8, M_); } while (0)
+                            else if (nw == 3) MF_GO(NA_, 3, M_); else if (nw == 4) MF_GO(NA_, 4, M_); \
+                            else MF_GO(NA_, 8, M_); } while (0)
 #define MF_MODE(NA_) do { if (mode == 0) MF_NW(NA_, 0); else if (mode == IQ4_RMS) MF_NW(NA_, IQ4_RMS); \
                           else if (mode == IQ4_SPLIT) MF_NW(NA_, IQ4_SPLIT); else MF_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
     if (na == 1) MF_MODE(1); else MF_MODE(2);
 #undef MF_MODE
 #undef MF_NW
 #undef MF_GO
+}
+
+// Blocks of one kernel instance that a compute unit holds at once (its VGPRs set the waves
+// per SIMD), from the runtime's occupancy calculator; cached per instance.
+template <int FMT, int NA, int NW, int M>
+static int mfma_resident()
+{
+    static int nb = -1;
+    if (nb < 0) {
+        int v = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, (const void *)k_gemv_mfma<FMT, NA, NW, M>, 64 * NW, 0) !=
+            hipSuccess)
+            v = 0;
+        nb = v;
+    }
+    return nb;
+}
+template <int FMT>
+static int mfma_resident_of(int na, int nw, int mode)
+{
+#define MR_NW(NA_, M_) (nw == 2 ? mfma_resident<FMT, NA_, 2, M_>() : nw == 3 ? mfma_resident<FMT, NA_, 3, M_>() \
+                                  : mfma_resident<FMT, NA_, 4, M_>())
+#define MR_MODE(NA_) (mode == 0 ? MR_NW(NA_, 0) : mode == IQ4_RMS ? MR_NW(NA_, IQ4_RMS) \
+                      : mode == IQ4_SPLIT ? MR_NW(NA_, IQ4_SPLIT) : MR_NW(NA_, IQ4_RMS | IQ4_SPLIT))
+    return na == 1 ? MR_MODE(1) : MR_MODE(2);
+#undef MR_MODE
+#undef MR_NW
+}
+static int mfma_resident_fmt(int type, int na, int nw, int mode)
+{
+    switch (type) {
+    case T_IQ4_XS: return mfma_resident_of<T_IQ4_XS>(na, nw, mode);
+    case T_Q4_K: return mfma_resident_of<T_Q4_K>(na, nw, mode);
+    case T_Q5_K: return mfma_resident_of<T_Q5_K>(na, nw, mode);
+    case T_Q6_K: return mfma_resident_of<T_Q6_K>(na, nw, mode);
+    case T_Q8_0: return mfma_resident_of<T_Q8_0>(na, nw, mode);
+    default: return 0;
+    }
 }
 
 #ifndef NW8_TILES
@@ -1267,17 +1317,37 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         // model's shapes with the 3/1 prefetch rings: 4 waves is best or within
         // noise everywhere except narrow outputs (<= 512 tiles, e.g. 5120 rows,
         // fewer blocks than 2 per CU), where 8 waves per tile hide more latency.
-        // QGPU_GEMV_NW=1|2|4|8 forces the split.
+        // QGPU_GEMV_NW=1|2|3|4|8 forces the split.
         static int force_nw = -1;
         if (force_nw < 0) {
             const char *e = getenv("QGPU_GEMV_NW");
             force_nw = e ? atoi(e) : 0;
         }
         int nw = (ks == 1 && tiles <= NW8_TILES) ? 8 : 4;
-        if (force_nw == 1 || force_nw == 2 || force_nw == 4 || force_nw == 8) nw = force_nw;
+        if (force_nw >= 1 && force_nw <= 4) nw = force_nw;
+        if (force_nw == 8) nw = 8;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
-        if (A.rss && nw < 4) nw = 4;                        // row factors: <= 2 tokens per wave
+        if (A.rss && nw < 3) nw = 4;                        // row factors: <= 3 tokens per wave
         const int mode = (A.rss ? IQ4_RMS : 0) | (split ? IQ4_SPLIT : 0);
+#ifndef GEMV_NW3_RESIDENT
+#define GEMV_NW3_RESIDENT 1
+#endif
+#ifndef GEMV_NW_MIN_RESIDENT
+#define GEMV_NW_MIN_RESIDENT 3   // 2 waves per tile measured slower than a second round of blocks
+#endif
+        // Residency: when the compute units cannot hold every 4-wave block at once (the kernel's
+        // VGPRs cap the waves per SIMD), the blocks left over start only as the first ones end,
+        // a second round at the end of the launch; 3 waves per tile (longer K slices) then fit
+        // them all where they can (the GDN input projection at B = 5..8: 1144 blocks against
+        // 4 x 256 resident 4-wave blocks, 5 x 256 3-wave blocks).
+        if (GEMV_NW3_RESIDENT && nw == 4 && force_nw == 0 && qg::n_cu > 0 &&
+            (long)blocks > (long)mfma_resident_fmt(W0->type, na, 4, mode) * qg::n_cu) {
+            for (int w = 3; w >= GEMV_NW_MIN_RESIDENT; w--)
+                if (A.nsb / ks >= w && (long)blocks <= (long)mfma_resident_fmt(W0->type, na, w, mode) * qg::n_cu) {
+                    nw = w;
+                    break;
+                }
+        }
         switch (W0->type) {
         case T_IQ4_XS: launch_mfma<T_IQ4_XS>(ex, A, blocks, na, nw, mode); break;
         case T_Q4_K: launch_mfma<T_Q4_K>(ex, A, blocks, na, nw, mode); break;

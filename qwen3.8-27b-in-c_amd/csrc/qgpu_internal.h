@@ -167,6 +167,8 @@ extern int initialized;
 // workspace for the GEMV activation prep (digit planes + scales)
 extern void *ws;
 extern size_t ws_bytes;
+extern int n_cu;          // compute units of the device
+
 int ensure_init();
 int check(hipError_t e);
 size_t row_bytes(int type, uint64_t ne0);

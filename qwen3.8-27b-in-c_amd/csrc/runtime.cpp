@@ -9,6 +9,7 @@ hipStream_t stream = nullptr;
 int initialized = 0;
 void *ws = nullptr;
 size_t ws_bytes = 0;
+int n_cu = 0;
 
 int check(hipError_t e) { return e == hipSuccess ? QGPU_OK : (int)e; }
 
@@ -52,6 +53,7 @@ extern "C" int qgpu_init(int device)
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return QGPU_E_INIT;
     QG_CHECK(hipSetDevice(device));
+    QG_CHECK(hipDeviceGetAttribute(&qg::n_cu, hipDeviceAttributeMultiprocessorCount, device));
     QG_CHECK(hipStreamCreateWithFlags(&qg::stream, hipStreamNonBlocking));
     qg::ws_bytes = qg_gemv_workspace_bytes();
     QG_CHECK(hipMalloc(&qg::ws, qg::ws_bytes));
