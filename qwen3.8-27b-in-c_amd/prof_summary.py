@@ -38,6 +38,7 @@ import argparse
 import glob
 import json
 import os
+import re
 import sqlite3
 import statistics
 import sys
@@ -232,30 +233,51 @@ IQ4_ROW = lambda cols: cols // 256 * 136        # bytes of one IQ4_XS row
 DIGITS = 3                                      # activation digit bytes per element (int8 x 3)
 
 
+def prep_kind(k):
+    """(transform kind, partial planes or None) of a preparation kernel name: k_prep_tok<KIND, NP>
+    (one token per block) or the older k_prep_act<KIND>; kinds 2 SiLU x up, 3 gated norm, 4 RMSNorm"""
+    m = re.match(r"k_prep_(tok|act)<(\d+)(?:, (\d+))?>", k)
+    if not m:
+        return None, None
+    return int(m.group(2)), (int(m.group(3)) if m.group(3) is not None else None)
+
+
 def step_roles(step, B, P):
     """(role, bytes) of each dispatch of one verify step, by kernel name, grid and what came before"""
     d, f4 = D27, 4
     out, prev, n_part = [], "", 0
+    gdn_in = d["CONV"] + d["VD"] + 2 * d["VH"]          # rows of the GDN input projection
     for name, _, dur, gx, wx in step:
         k, grid = short(name), gx // max(wx, 1)
+        kind, planes = prep_kind(k)
+        prev_kind, _ = prep_kind(prev)
+        split = k.startswith("k_gemv_mfma") and (k.endswith(", 2>") or k.endswith(", 3>"))
         if k.startswith("k_dequant_rows"):
             role, by = "embedding rows (dequant)", B * IQ4_ROW(d["E"]) + B * d["E"] * f4
-        elif k == "k_prep_act<4>":
+        elif kind == 4:
+            np_ = n_part if planes is None else planes
             role = "RMSNorm prep (+ residual partials)"
-            by = (1 + n_part) * B * d["E"] * f4 + d["E"] * f4 + B * d["E"] * (2 * f4 + DIGITS)
-        elif k == "k_prep_act<3>":
+            by = (1 + np_) * B * d["E"] * f4 + d["E"] * f4 + B * d["E"] * (2 * f4 + DIGITS)
+        elif kind == 3:
             role, by = "gated-norm prep (GDN out)", 2 * B * d["VD"] * f4 + B * d["VD"] * (f4 + DIGITS)
-        elif k == "k_prep_act<2>":
+        elif kind == 2:
             role, by = "SiLU x up prep", 2 * B * d["F"] * f4 + B * d["F"] * (f4 + DIGITS)
-        elif k.startswith("k_gemv_mfma") and (k.endswith(", 2>") or k.endswith(", 3>")):
+        elif split and grid > 1024 and grid < 1280 and prev_kind == 4:
+            # the GDN input projection with beta and alpha cut into one K range per super-block
+            kba = (grid - (d["CONV"] + d["VD"]) // 16) // (2 * d["VH"] // 16)
+            role = "GEMV GDN in (qkv, z; beta, alpha K-split)"
+            by = gdn_in * IQ4_ROW(d["E"]) + B * d["E"] * DIGITS + B * (d["CONV"] + d["VD"]) * f4 + \
+                kba * B * 2 * d["VH"] * f4
+            n_part = 0
+        elif split:
             ks = max(1, grid // (d["E"] // 16))
-            cols = {"k_prep_act<3>": d["VD"], "k_attn_combine_act": d["QD"], "k_prep_act<2>": d["F"]}.get(prev, 0)
-            role = {"k_prep_act<3>": "GEMV ssm_out (K-split)", "k_attn_combine_act": "GEMV attn_output (K-split)",
-                    "k_prep_act<2>": "GEMV ffn_down (K-split)"}.get(prev, "GEMV K-split (?)")
+            cols = {3: d["VD"], 2: d["F"]}.get(prev_kind, d["QD"] if prev == "k_attn_combine_act" else 0)
+            role = {3: "GEMV ssm_out (K-split)", 2: "GEMV ffn_down (K-split)"}.get(
+                prev_kind, "GEMV attn_output (K-split)" if prev == "k_attn_combine_act" else "GEMV K-split (?)")
             by = d["E"] * IQ4_ROW(cols) + B * cols * DIGITS + ks * B * d["E"] * f4
             n_part = ks
         elif k.startswith("k_gemv_mfma"):
-            rows = {1030: d["CONV"] + d["VD"] + 2 * d["VH"], 896: 2 * d["QD"] + 2 * d["KV"], 2176: 2 * d["F"],
+            rows = {1030: gdn_in, 896: 2 * d["QD"] + 2 * d["KV"], 2176: 2 * d["F"],
                     15520: d["V"]}.get(grid, grid * 16)
             role = {1030: "GEMV GDN in (qkv, z, beta, alpha)", 896: "GEMV attention q||gate, k, v",
                     2176: "GEMV ffn_gate + ffn_up", 15520: "GEMV lm_head"}.get(grid, f"GEMV {rows} rows")
