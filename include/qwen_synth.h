@@ -46,6 +46,11 @@ typedef struct {
                                                 symbols, then a few merged tokens, fillers,
                                                 and <|endoftext|>, <|im_start|>, <|im_end|>
                                                 as the last three ids (vocab >= 300)     */
+    int32_t  tie_output;                     /* 1: no output.weight tensor, so the lm_head is
+                                                token_embd (the loader's fallback, model.c:87-88);
+                                                2: output.weight is an exact copy of token_embd.
+                                                Either way output.weight is listed last, so the
+                                                other tensors of the two files are the same */
 } qwen_synth_spec_t;
 
 /* The 27B hybrid: 48 GDN + 16 GQA layers + MTP, H=5120, F=17408, V=248320, all IQ4_XS. */

@@ -242,7 +242,7 @@ static uint32_t enumerate(const qwen_synth_spec_t *s, tdesc *d)
     const float gr = s->gain_resid > 0.0f ? s->gain_resid : 0.5f;
     ADD("token_embd.weight%.0u", 0u, 2, E, V, pick(s->type_embd, T), K_MAT, ge);
     ADD("output_norm.weight%.0u", 0u, 1, E, 1, GGML_F32, K_NORM, 1.0f);
-    ADD("output.weight%.0u", 0u, 2, E, V, pick(s->type_output, T), K_MAT, s->gain_output);
+    if (!s->tie_output) ADD("output.weight%.0u", 0u, 2, E, V, pick(s->type_output, T), K_MAT, s->gain_output);
     for (uint32_t il = 0; il <= s->n_layer; il++) {
         const int mtp = il == s->n_layer;
         const int rec = !mtp && ((il + 1) % s->full_attn_interval) != 0;
@@ -276,6 +276,8 @@ static uint32_t enumerate(const qwen_synth_spec_t *s, tdesc *d)
             ADD("blk.%u.nextn.shared_head_norm.weight", il, 1, E, 1, GGML_F32, K_NORM, 1.0f);
         }
     }
+    /* a copy of token_embd (same type and bytes) as the last tensor */
+    if (s->tie_output == 2) ADD("output.weight%.0u", 0u, 2, E, V, pick(s->type_embd, T), K_MAT, ge);
 #undef ADD
     return n;
 }
@@ -374,6 +376,7 @@ int qwen_synth_fill(const qwen_synth_spec_t *s, uint32_t i, void *out)
     if (s->mtp_diag && strstr(t.name, ".nextn.eh_proj.weight"))
         return diag_eh_proj(&t, s->seed, i, out);
     if (s->tie_shift && i == 0) return tied_embd(s, out);
+    if (s->tie_output == 2 && !strcmp(t.name, "output.weight")) return qwen_synth_fill(s, 0, out);
     if (s->tie_shift && !strcmp(t.name, "output.weight")) {
         qwen_synth_tensor_t e;                    /* token_embd is tensor 0 */
         if (qwen_synth_describe(s, 0, &e) || e.type != t.type || e.nbytes != t.nbytes || e.ne[1] < 2) return -1;

@@ -51,7 +51,8 @@ class SynthSpec(ctypes.Structure):
         + [(n, ctypes.c_int32) for n in "type_default type_embd type_output type_qkv type_eh_proj".split()]
         + [("gain_output", ctypes.c_float), ("seed", ctypes.c_uint64)]
         + [("gain_embd", ctypes.c_float), ("gain_resid", ctypes.c_float), ("mtp_diag", ctypes.c_int32),
-           ("norm_sigma", ctypes.c_float), ("tie_shift", ctypes.c_int32), ("tokenizer", ctypes.c_int32)])
+           ("norm_sigma", ctypes.c_float), ("tie_shift", ctypes.c_int32), ("tokenizer", ctypes.c_int32),
+           ("tie_output", ctypes.c_int32)])
 
 
 class SynthTensor(ctypes.Structure):

@@ -385,6 +385,51 @@ def test_model_forward_batch_and_sequential_vs_reference(gpu, tiny):
     m.close()
 
 
+
+@pytest.mark.parametrize("mixed", [0, 1])
+def test_model_tied_output_vs_oracle(gpu, mixed):
+    """A model file without output.weight: model_init falls back to token_embd as the lm_head
+    (model.c:87-88) and uploads it once.  Batched, sequential and MTP logits match the oracle on the
+    same file within 1e-3 (same argmax), and equal the GPU's own logits for the file whose
+    output.weight is an explicit copy of token_embd, bit for bit."""
+    host = host_lib()
+    td = tempfile.mkdtemp()
+    p = np.random.default_rng(5).integers(0, 1024, 9).astype(np.uint32)
+    got = []
+    for tie in (1, 2):
+        spec = host.spec_tiny(31, mixed)
+        spec.tie_output = tie
+        path = os.path.join(td, f"tie{tie}.gguf")
+        host.write_gguf(spec, path)
+        m = pyqwen.Model(path, 64)
+        lb = m.forward_batch(p[:8], 0, 0)
+        m.mtp_forward_batch(p[:8], 0)
+        ml = m.mtp_forward(int(p[8]), 8)
+        m.close()
+        m = pyqwen.Model(path, 64)
+        seq = np.array([m.forward(int(p[i]), i) for i in range(4)])
+        m.close()
+        got.append((lb, ml, seq))
+        if tie == 1:
+            o = O.Model(path, 64)
+            olb = o.forward_batch(p[:8], 0, 0)
+            o.L.or_mtp_forward_batch(o.h, O.uptr(np.ascontiguousarray(p[:8])), 0, 8, 0)
+            o.L.or_mtp_forward(o.h, int(p[8]), 8, 1)
+            oml = o.arr(o.L.or_model_logits, o.V)
+            o.close()
+            o = O.Model(path, 64)
+            oseq = np.array([o.forward(int(p[i]), i) for i in range(4)])
+            o.close()
+            for b in range(8):
+                assert rel_err(lb[b], olb[b]) < 1e-3 and lb[b].argmax() == olb[b].argmax(), b
+            assert rel_err(ml, oml) < 1e-3 and ml.argmax() == oml.argmax()
+            for b in range(4):
+                assert rel_err(seq[b], oseq[b]) < 1e-3, b
+            print(f"\n[tied] mixed={mixed}: batch rel err {rel_err(lb, olb):.2e}", flush=True)
+        os.remove(path)
+    for a, b in zip(got[0], got[1]):
+        assert np.array_equal(a, b)
+
 def test_model_forward_section_profile(gpu, tiny):
     """The reference's --profile counters (model.c:697-742): with profiling on, model_forward adds
     the device time of the embedding, the GDN layers, the attention layers and the head; the

@@ -255,6 +255,46 @@ def test_oracle_model_forward_bitexact(tiny_model):
     assert np.array_equal(m.arr(m.L.or_model_mtp_h, m.E), z["mtp_h"])
 
 
+
+def _tied_pair(mixed):
+    """two tiny GGUFs that differ only in output.weight: absent (the lm_head falls back to
+    token_embd, model.c:87-88) or present as an exact copy of token_embd"""
+    host = host_lib()
+    td = tempfile.mkdtemp()
+    paths = []
+    for tie in (1, 2):
+        spec = host.spec_tiny(31, mixed)
+        spec.tie_output = tie
+        path = os.path.join(td, f"tie{tie}.gguf")
+        host.write_gguf(spec, path)
+        paths.append(path)
+    return paths
+
+
+@pytest.mark.parametrize("mixed", [0, 1])
+def test_oracle_tied_output_equals_explicit_copy(mixed):
+    """A model file without output.weight (model.c:87-88: the lm_head is token_embd) gives, bit for bit,
+    the logits of the same model whose output.weight is an explicit copy of token_embd: batched and
+    sequential forwards and the MTP draft logits.  (mixed: a Q4_K token_embd as the lm_head.)"""
+    paths = _tied_pair(mixed)
+    p = np.random.default_rng(5).integers(0, 1024, 9).astype(np.uint32)
+    res = []
+    for path in paths:
+        m = O.Model(path, 64)
+        lb = m.forward_batch(p[:8], 0, 0)
+        m.L.or_mtp_forward_batch(m.h, O.uptr(np.ascontiguousarray(p[:8])), 0, 8, 0)
+        m.L.or_mtp_forward(m.h, int(p[8]), 8, 1)
+        ml = m.arr(m.L.or_model_logits, m.V)
+        m.close()
+        m = O.Model(path, 64)
+        seq = np.array([m.forward(int(p[i]), i) for i in range(4)])
+        m.close()
+        res.append((lb, ml, seq))
+    for a, b in zip(res[0], res[1]):
+        assert np.array_equal(a, b)
+    for path in paths:
+        os.remove(path)
+
 def test_oracle_rollback_bitexact(tiny_model):
     path, z = tiny_model
     p = z["prompt"]
