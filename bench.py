@@ -71,7 +71,16 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 HBM_PEAK_GBS = 8000.0
 IQ4 = 23
 METRIC = "accepted tok/s, 27B IQ4_XS MTP k=3 on 1 GPU; gemv_batch HBM GB/s (% peak)"
-ROOF_KERNEL = "k_gemv_mfma<23, 1, 4, 0>"
+ROOF_TILES = 17408 // 16   # 16-row tiles of the roofline GEMV
+
+
+def roof_kernel(ncu):
+    """the kernel instance the roofline GEMV launches on a device of ncu compute units: IQ4_XS, one
+    digit plane, 4 waves per tile; mode 4 (pair split) when its tiles are a little over a multiple of
+    the compute units (1088 = 4 x 256 + 64 on MI355X), else mode 0"""
+    r = ROOF_TILES % ncu if ncu else 0
+    pair = ncu and ROOF_TILES > ncu and 0 < r <= ncu // 2 and r <= 256
+    return f"k_gemv_mfma<23, 1, 4, {4 if pair else 0}>"
 READ_BLOCKS = 8192      # plain-read floor launch: 8192 blocks x 256 threads (best of 1024..8192 at 47.7 MB)
 
 
@@ -80,13 +89,15 @@ def log(*a):
 
 
 def traffic_for(kernel):
-    """HBM bytes per launch measured with rocprofv3 PMC counters (profiles/traffic.json)."""
+    """HBM bytes per launch measured with rocprofv3 PMC counters (profiles/traffic.json), when they were
+    measured on this kernel instance"""
     p = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(p) as f:
-            return json.load(f).get(kernel, {}).get("bytes_per_launch")
+            d = json.load(f).get(kernel.split("<")[0], {})
     except (OSError, ValueError):
         return None
+    return d.get("bytes_per_launch") if d.get("kernel") == kernel else None
 
 
 def host_info():
@@ -234,6 +245,7 @@ def graph_ms(gpu, calls, e0, e1):
 def gemv_roofline(gpu, host, steps, warmup):
     """config-1 GEMV: gemv_batch calls, then the GEMV kernel alone (roofline)."""
     ne0, ne1, B = 5120, 17408, 4
+    rk = roof_kernel(gpu.device_info()[1])
     W = host.synth_matrix(IQ4, ne0, ne1, 1, 0, 0.02)
     x = host.synth_normal(B * ne0, 1, 1).reshape(B, ne0)
     R = 12
@@ -269,8 +281,8 @@ def gemv_roofline(gpu, host, steps, warmup):
         T.close()
     achieved = algo / (ms_kernel * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(ROOF_KERNEL.split("<")[0]),
-            "kernel": ROOF_KERNEL, "workload": "IQ4_XS 17408x5120, B=4", "kernel_us": round(ms_kernel * 1e3, 3),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(rk),
+            "kernel": rk, "workload": "IQ4_XS 17408x5120, B=4", "kernel_us": round(ms_kernel * 1e3, 3),
             "algo_bytes": algo,
             # the same weight bytes read by a plain XOR-reduction kernel (k_checksum), same rotation
             "read_floor_us": round(ms_read * 1e3, 3), "read_floor_gbs": round(dev_bytes / (ms_read * 1e-3) / 1e9, 1),
@@ -554,7 +566,7 @@ def main():
     log(f"device {name}, {ncu} CUs; mode {args.mode}")
     gs, gw = (args.steps, args.warmup) if args.mode == "gemv" else (args.gemv_steps, args.gemv_warmup)
     roof, gemv_gbs, ms_call, wx = gemv_roofline(gpu, host, gs, gw)
-    log(f"roofline {ROOF_KERNEL}: {roof['kernel_us']} us/launch, {roof['achieved']} GB/s "
+    log(f"roofline {roof['kernel']}: {roof['kernel_us']} us/launch, {roof['achieved']} GB/s "
         f"({100 * roof['frac']:.1f}% of peak); gemv_batch call {gemv_gbs:.1f} GB/s")
     if args.copy_calib:
         nb = 256 << 20

@@ -87,7 +87,7 @@ int  qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ldx, int n,
  * arguments and results as qgpu_gemv_batch (bit-identical), plus the HIP stream
  * to launch on (NULL: the default stream); it neither initialises the library
  * nor allocates: the activation workspace is a static device array of
- * 1,613,824 bytes per GPU (ne0 <= 65536, else QGPU_E_RANGE).  Calls that
+ * 1,875,968 bytes per GPU (ne0 <= 65536, else QGPU_E_RANGE).  Calls that
  * overlap on one GPU share that array and race. */
 int  qgpu_gemv_batch_noalloc(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
                              uint64_t ldo, int flags, void *stream);

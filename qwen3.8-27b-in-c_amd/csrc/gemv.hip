@@ -27,7 +27,14 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 #define RSS_FLOATS  ((size_t)QGPU_MAX_B * MAX_NSB)
 #define ACT_RMS_DEFER 4      // internal prep kind: RMSNORM with the 1/rms factor applied by the GEMV
 
-#define GEMV_WS_BYTES (2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float) + RSS_FLOATS * sizeof(float))
+// Pair split (tail balance): when a launch's tiles are a little over a multiple of the compute
+// units, the remainder tiles run as two half-K blocks each, whose results meet in 64-bit exchange
+// slots (PAIR_SLOTS per tile).  The slots hold 0 between launches.
+#define PAIR_MAX_TILES 256
+#define PAIR_SLOTS     (QGPU_MAX_B / 4 * 64)          // (plane, token, row) entries of one tile
+#define XCHG_BYTES     ((size_t)PAIR_MAX_TILES * PAIR_SLOTS * sizeof(unsigned long long))
+#define GEMV_WS_XCHG   (2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float) + RSS_FLOATS * sizeof(float))
+#define GEMV_WS_BYTES  (GEMV_WS_XCHG + XCHG_BYTES)
 size_t qg_gemv_workspace_bytes() { return GEMV_WS_BYTES; }
 
 // Where a GEMV runs: its stream and its activation workspace (two digit planes,
@@ -37,8 +44,10 @@ size_t qg_gemv_workspace_bytes() { return GEMV_WS_BYTES; }
 struct GemvExec {
     hipStream_t st;
     uint8_t *ws;
+    int n_cu;            // compute units of the device (0: no pair split)
 };
-static GemvExec lib_exec() { return GemvExec{ qg::stream, (uint8_t *)qg::ws }; }
+static GemvExec lib_exec() { return GemvExec{ qg::stream, (uint8_t *)qg::ws, qg::n_cu }; }
+static unsigned long long *ws_xchg(const GemvExec &ex) { return (unsigned long long *)(ex.ws + GEMV_WS_XCHG); }
 static float *ws_rss(const GemvExec &ex) { return (float *)(ex.ws + 2 * PLANE_BYTES + 2 * XS_FLOATS * sizeof(float)); }
 
 static __device__ __forceinline__ float h2f(uint32_t h16) { return (float)__builtin_bit_cast(_Float16, (unsigned short)h16); }
@@ -555,6 +564,8 @@ struct GemvMat {
 struct GemvArgs {
     GemvMat m[QGPU_MAX_MULTI];
     int n_mat, nsb, ntok, flags;
+    uint32_t pair0;                // IQ4_PAIR: flat tiles from pair0 on run as two half-K blocks each
+    unsigned long long *xchg;      // IQ4_PAIR: their exchange slots, (tile - pair0) * PAIR_SLOTS + entry
     const uint8_t *A;
     const float *xs;
     const float *x;        // VALU path: fp32 activations
@@ -892,6 +903,7 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
 // into partial planes.  Plain launches (MODE 0) compile without either.
 #define IQ4_RMS   1
 #define IQ4_SPLIT 2
+#define IQ4_PAIR  4     // tail balance: the last tiles of the launch in two K halves (never with IQ4_SPLIT)
 template <int FMT, int NA, int NW, int MODE>
 #ifndef IQ4_MINW1
 #define IQ4_MINW1 1     // minimum waves per SIMD the compiler must allow (caps VGPRs), one digit plane
@@ -907,12 +919,22 @@ __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_ge
     const float4 oh = make_float4(g == 0, g == 1, g == 2, g == 3);   // token g of this lane group
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar loop control
     int k = 0;
-    while (k + 1 < args.n_mat && blockIdx.x >= args.m[k + 1].blk0) k++;
+    uint32_t T;                    // row tile of this block within its matrix
+    int ks = 1, kq = 0;            // K ranges of the tile, and this block's
+    uint32_t pflat = 0;            // IQ4_PAIR: flat tile index
+    if (MODE & IQ4_PAIR) {
+        const uint32_t u = blockIdx.x >= args.pair0 ? blockIdx.x - args.pair0 : 0;
+        pflat = blockIdx.x < args.pair0 ? blockIdx.x : args.pair0 + (u >> 1);
+        if (blockIdx.x >= args.pair0) { ks = 2; kq = (int)(u & 1); }
+        while (k + 1 < args.n_mat && pflat >= args.m[k + 1].tile0) k++;
+        T = pflat - args.m[k].tile0 + args.m[k].tile_first;
+    } else {
+        while (k + 1 < args.n_mat && blockIdx.x >= args.m[k + 1].blk0) k++;
+        const uint32_t lb = blockIdx.x - args.m[k].blk0;            // block within matrix k
+        if (MODE & IQ4_SPLIT) { ks = (int)args.m[k].ks; kq = (int)(lb % (uint32_t)ks); }
+        T = ((MODE & IQ4_SPLIT) ? lb / (uint32_t)ks : lb) + args.m[k].tile_first;
+    }
     const GemvMat &M = args.m[k];
-    const uint32_t lb = blockIdx.x - M.blk0;                        // block within matrix k
-    const int ks = (MODE & IQ4_SPLIT) ? (int)M.ks : 1;
-    const uint32_t T = ((MODE & IQ4_SPLIT) ? lb / (uint32_t)ks : lb) + M.tile_first;
-    const int kq = (MODE & IQ4_SPLIT) ? (int)(lb % (uint32_t)ks) : 0;   // K range of this block (split GEMV)
     const int nsb = args.nsb;
     constexpr uint32_t REC = FMT == T_IQ4_XS ? IQ4_REC_BYTES : FMT == T_Q4_K ? 2304 : FMT == T_Q5_K ? 2816 : FMT == T_Q6_K ? 3360 : 4352;
     const uint8_t *rec0 = M.W + (uint64_t)T * nsb * REC;
@@ -975,7 +997,20 @@ __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_ge
         const uint32_t r = T * IQ4_TILE_ROWS + nn;
         if (t < args.ntok && r >= M.row_lo && r < M.row_hi) {
             if (MODE & IQ4_RMS) s *= rsc[t];
-            if (MODE & IQ4_SPLIT) {
+            if ((MODE & IQ4_PAIR) && ks == 2) {
+                // two contributors per entry: the first leaves its half in the slot, the second
+                // takes it (the exchange itself carries the value, so no fence), writes the sum and
+                // clears the slot.  a + b and b + a are the same bits, whichever half comes first.
+                unsigned long long *slot = args.xchg + (uint64_t)(pflat - args.pair0) * PAIR_SLOTS + e;
+                const unsigned long long old =
+                    atomicExch(slot, (1ull << 32) | (unsigned long long)__float_as_uint(s));
+                if (old >> 32) {
+                    s = __uint_as_float((uint32_t)old) + s;
+                    atomicExch(slot, 0ull);
+                    float *o = M.out + (uint64_t)t * M.ldo + r;
+                    *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + s : s;
+                }
+            } else if (MODE & IQ4_SPLIT) {
                 M.out[(uint64_t)kq * M.pstride + (uint64_t)t * M.ldo + r] = s;
             } else {
                 float *o = M.out + (uint64_t)t * M.ldo + r;
@@ -1221,7 +1256,10 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
                             else if (nw == 3) MF_GO(NA_, 3, M_); else if (nw == 4) MF_GO(NA_, 4, M_); \
                             else MF_GO(NA_, 8, M_); } while (0)
 #define MF_MODE(NA_) do { if (mode == 0) MF_NW(NA_, 0); else if (mode == IQ4_RMS) MF_NW(NA_, IQ4_RMS); \
-                          else if (mode == IQ4_SPLIT) MF_NW(NA_, IQ4_SPLIT); else MF_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
+                          else if (mode == IQ4_SPLIT) MF_NW(NA_, IQ4_SPLIT); \
+                          else if (mode == IQ4_PAIR) MF_NW(NA_, IQ4_PAIR); \
+                          else if (mode == (IQ4_RMS | IQ4_PAIR)) MF_NW(NA_, IQ4_RMS | IQ4_PAIR); \
+                          else MF_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
     if (na == 1) MF_MODE(1); else MF_MODE(2);
 #undef MF_MODE
 #undef MF_NW
@@ -1249,7 +1287,8 @@ static int mfma_resident_of(int na, int nw, int mode)
 #define MR_NW(NA_, M_) (nw == 2 ? mfma_resident<FMT, NA_, 2, M_>() : nw == 3 ? mfma_resident<FMT, NA_, 3, M_>() \
                                   : mfma_resident<FMT, NA_, 4, M_>())
 #define MR_MODE(NA_) (mode == 0 ? MR_NW(NA_, 0) : mode == IQ4_RMS ? MR_NW(NA_, IQ4_RMS) \
-                      : mode == IQ4_SPLIT ? MR_NW(NA_, IQ4_SPLIT) : MR_NW(NA_, IQ4_RMS | IQ4_SPLIT))
+                      : mode == IQ4_SPLIT ? MR_NW(NA_, IQ4_SPLIT) : mode == IQ4_PAIR ? MR_NW(NA_, IQ4_PAIR) \
+                      : mode == (IQ4_RMS | IQ4_PAIR) ? MR_NW(NA_, IQ4_RMS | IQ4_PAIR) : MR_NW(NA_, IQ4_RMS | IQ4_SPLIT))
     return na == 1 ? MR_MODE(1) : MR_MODE(2);
 #undef MR_MODE
 #undef MR_NW
@@ -1308,8 +1347,26 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         if (kj > 1) split = true;
     }
     if (!tiles) return QGPU_OK;
+    A.pair0 = tiles;
     if (mfma) {
         if (W0->ne0 > MAX_K) return QGPU_E_RANGE;
+#ifndef GEMV_PAIR_SPLIT
+#define GEMV_PAIR_SPLIT 1
+#endif
+        // Tail balance: with every block resident, a launch ends when the compute units holding
+        // one tile more than the others finish.  When the tiles are r > 0 over a multiple of the
+        // compute units (r at most half of them), the last r tiles run as two half-K blocks each,
+        // so those units stream half a tile more instead of a whole one (17408 x 5120: 1024 + 64
+        // tiles).  Not with a K split of the caller's (partial planes) or per-matrix splits.
+        const uint32_t ncu = ex.n_cu > 0 ? (uint32_t)ex.n_cu : 0;
+        if (GEMV_PAIR_SPLIT && ncu && !split && ks == 1 && A.nsb >= 2 && tiles > ncu) {
+            const uint32_t r = tiles % ncu;
+            if (r && r <= ncu / 2 && r <= PAIR_MAX_TILES) {
+                A.pair0 = tiles - r;
+                A.xchg = ws_xchg(ex);
+                blocks = tiles + r;
+            }
+        }
         const int na = n > 4 ? 2 : 1;
         A.A = ex.ws;
         A.xs = (const float *)(ex.ws + 2 * PLANE_BYTES);
@@ -1328,7 +1385,7 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         if (force_nw == 8) nw = 8;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
         if (A.rss && nw < 3) nw = 4;                        // row factors: <= 3 tokens per wave
-        const int mode = (A.rss ? IQ4_RMS : 0) | (split ? IQ4_SPLIT : 0);
+        const int mode = (A.rss ? IQ4_RMS : 0) | (split ? IQ4_SPLIT : 0) | (A.pair0 < tiles ? IQ4_PAIR : 0);
 #ifndef GEMV_NW3_RESIDENT
 #define GEMV_NW3_RESIDENT 1
 #endif
@@ -1340,10 +1397,10 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         // a second round at the end of the launch; 3 waves per tile (longer K slices) then fit
         // them all where they can (the GDN input projection at B = 5..8: 1144 blocks against
         // 4 x 256 resident 4-wave blocks, 5 x 256 3-wave blocks).
-        if (GEMV_NW3_RESIDENT && nw == 4 && force_nw == 0 && qg::n_cu > 0 &&
-            (long)blocks > (long)mfma_resident_fmt(W0->type, na, 4, mode) * qg::n_cu) {
+        if (GEMV_NW3_RESIDENT && nw == 4 && force_nw == 0 && ex.n_cu > 0 &&
+            (long)blocks > (long)mfma_resident_fmt(W0->type, na, 4, mode) * ex.n_cu) {
             for (int w = 3; w >= GEMV_NW_MIN_RESIDENT; w--)
-                if (A.nsb / ks >= w && (long)blocks <= (long)mfma_resident_fmt(W0->type, na, w, mode) * qg::n_cu) {
+                if (A.nsb / ks >= w && (long)blocks <= (long)mfma_resident_fmt(W0->type, na, w, mode) * ex.n_cu) {
                     nw = w;
                     break;
                 }
@@ -1467,16 +1524,19 @@ extern "C" int qgpu_gemv_batch(const qgpu_tensor *W, const float *x, uint64_t ld
 // For callers that cannot allocate device memory (code under HIP graph capture,
 // tight serving loops, harnesses that forbid hipMalloc): the workspace of the
 // batched GEMV (two 4-token digit planes for up to MAX_K = 65536 columns, their
-// conversion factors and the deferred-RMSNorm sums: 1,613,824 bytes) lives in
-// this file-scope device array, one copy per GPU, held until the process ends.
-// Its device address is looked up once per device with hipGetSymbolAddress; the
-// host-side name is never passed to a kernel.  Every call on a GPU shares that
-// GPU's copy, so calls that overlap on one GPU (two streams, two threads) race.
-// Nothing in it has to start at zero: each call writes the digit tiles and
-// factors of every super-block it reads before the GEMV reads them.
+// conversion factors, the deferred-RMSNorm sums and the exchange slots of the
+// pair-split tiles: 1,875,968 bytes) lives in this file-scope device array, one
+// copy per GPU, held until the process ends.  Its device address is looked up
+// once per device with hipGetSymbolAddress; the host-side name is never passed
+// to a kernel.  Every call on a GPU shares that GPU's copy, so calls that
+// overlap on one GPU (two streams, two threads) race.  Each call writes the
+// digit tiles and factors of every super-block it reads before the GEMV reads
+// them; the exchange slots start at zero (static storage) and every launch
+// leaves them at zero.
 static __device__ __align__(256) uint8_t scratch[GEMV_WS_BYTES];
 #define SCRATCH_MAX_DEV 64
 static uint8_t *scratch_ptr[SCRATCH_MAX_DEV];
+static int scratch_ncu[SCRATCH_MAX_DEV];
 
 extern "C" int qgpu_gemv_batch_noalloc(const qgpu_tensor *W, const float *x, uint64_t ldx, int n, float *out,
                                        uint64_t ldo, int flags, void *stream)
@@ -1489,11 +1549,14 @@ extern "C" int qgpu_gemv_batch_noalloc(const qgpu_tensor *W, const float *x, uin
     if (dev < 0 || dev >= SCRATCH_MAX_DEV) return QGPU_E_RANGE;
     if (!scratch_ptr[dev]) {                              // first call on this device: its copy's address
         void *p = nullptr;
+        int ncu = 0;
         QG_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        QG_CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
         if (!p) return QGPU_E_INIT;
+        scratch_ncu[dev] = ncu;
         scratch_ptr[dev] = (uint8_t *)p;
     }
-    const GemvExec ex{ (hipStream_t)stream, scratch_ptr[dev] };
+    const GemvExec ex{ (hipStream_t)stream, scratch_ptr[dev], scratch_ncu[dev] };
     const qgpu_act a = copy_act(x, ldx);
     return gemv_multi_on(ex, &W, 1, &a, n, &out, &ldo, flags, nullptr, nullptr);
 }

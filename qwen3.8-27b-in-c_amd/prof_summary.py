@@ -242,6 +242,19 @@ def prep_kind(k):
     return int(m.group(2)), (int(m.group(3)) if m.group(3) is not None else None)
 
 
+def gemv_tiles(k, grid, ncu=256):
+    """row tiles of a k_gemv_mfma launch of grid blocks: a pair-split launch (mode bit 4) runs its last
+    r = tiles mod ncu tiles as two blocks each (r <= ncu / 2), so grid = tiles + r"""
+    m = re.match(r"k_gemv_mfma<\d+, \d+, \d+, (\d+)>", k)
+    if not m or not int(m.group(1)) & 4:
+        return grid
+    for t in range(grid // 2, grid + 1):
+        r = t % ncu
+        if t > ncu and 0 < r <= ncu // 2 and t + r == grid:
+            return t
+    return grid
+
+
 def step_roles(step, B, P):
     """(role, bytes) of each dispatch of one verify step, by kernel name, grid and what came before"""
     d, f4 = D27, 4
@@ -277,6 +290,7 @@ def step_roles(step, B, P):
             by = d["E"] * IQ4_ROW(cols) + B * cols * DIGITS + ks * B * d["E"] * f4
             n_part = ks
         elif k.startswith("k_gemv_mfma"):
+            grid = gemv_tiles(k, grid)
             rows = {1030: gdn_in, 896: 2 * d["QD"] + 2 * d["KV"], 2176: 2 * d["F"],
                     15520: d["V"]}.get(grid, grid * 16)
             role = {1030: "GEMV GDN in (qkv, z, beta, alpha)", 896: "GEMV attention q||gate, k, v",

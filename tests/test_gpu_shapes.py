@@ -145,3 +145,51 @@ def test_gemv_outlier_activations(gpu, fmt, spike):
         exact = x[:n].astype(np.float64) @ O.dequant_rows(t, W, ne0, ne1).astype(np.float64).T
         assert np.all(np.abs(got - exact) <= bound[:n]), (fmt, spike, n)
     T.close()
+
+
+@pytest.mark.parametrize("fmt", ["IQ4_XS", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("shape", [(5120, 17408), (17408, 5120)])
+def test_gemv_pair_split_tail(gpu, fmt, shape):
+    """Tail balance: a launch a little over a multiple of the compute units (17408 rows: 1024 + 64 tiles,
+    5120 rows: 256 + 64 tiles on 256 CUs) runs its last tiles as two half-K blocks whose partial results
+    meet in exchange slots.  Every output is written (the buffer starts as NaN), the oracle agrees within
+    1e-3 at B = 1, 4, 8, a second call gives the same bits (the slots are left empty), the ACCUM flag adds
+    onto the previous contents exactly, and a captured graph of three calls replays to the same bits."""
+    ne0, ne1 = shape
+    t = FORMATS[fmt]
+    ncu = gpu.device_info()[1]
+    tiles = (ne1 + 15) // 16
+    print(f"\n[pair] {fmt} {ne0}->{ne1}: {tiles} tiles on {ncu} CUs (remainder {tiles % ncu})", flush=True)
+    W, T = matrix(gpu, t, ne0, ne1)
+    x = host_lib().synth_normal(8 * ne0, 79, t).reshape(8, ne0)
+    ref = O.gemv(t, W, ne0, ne1, x, 8, threads=16)
+    xb = gpu.put(np.ascontiguousarray(x))
+    nan = np.full(8 * ne1, np.nan, np.float32)
+    for n in (1, 4, 8):
+        ob = gpu.put(nan[:n * ne1])
+        gpu.ok(gpu.L.qgpu_gemv_batch(T.h, xb.f32(), ne0, n, ob.f32(), ne1, 0))
+        got = ob.download(np.float32).reshape(n, ne1)
+        assert not np.isnan(got).any(), (fmt, shape, n)
+        e = rel_err(got, ref[:n])
+        print(f"  B={n}: rel err {e:.2e}", flush=True)
+        assert e < 1e-3, (fmt, shape, n, e)
+        gpu.ok(gpu.L.qgpu_gemv_batch(T.h, xb.f32(), ne0, n, ob.f32(), ne1, 0))
+        again = ob.download(np.float32).reshape(n, ne1)
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), (fmt, shape, n)
+        gpu.ok(gpu.L.qgpu_gemv_batch(T.h, xb.f32(), ne0, n, ob.f32(), ne1, 1))      # QGPU_GEMV_ACCUM
+        acc = ob.download(np.float32).reshape(n, ne1)
+        assert np.array_equal(acc.view(np.uint32), (got + got).view(np.uint32)), (fmt, shape, n)
+    n = 4
+    ob = gpu.put(nan[:n * ne1])
+    gpu.sync()
+    gpu.ok(gpu.L.qgpu_graph_begin())
+    for _ in range(3):
+        gpu.ok(gpu.L.qgpu_gemv_batch(T.h, xb.f32(), ne0, n, ob.f32(), ne1, 0))
+    g = ctypes.c_void_p()
+    gpu.ok(gpu.L.qgpu_graph_end(ctypes.byref(g)))
+    eager = run(gpu, T, x, n, ne1)
+    for _ in range(2):
+        gpu.ok(gpu.L.qgpu_graph_launch(g))
+        gpu.sync()
+        assert np.array_equal(ob.download(np.float32).reshape(n, ne1).view(np.uint32), eager.view(np.uint32))
+    gpu.ok(gpu.L.qgpu_graph_destroy(g))

@@ -1,7 +1,9 @@
 """qgpu_gemv_batch_noalloc (the allocation-free gemv_batch, static device
 scratch) against qgpu_gemv_batch through the C-ABI: bit-identical outputs on two
 calls in a row, the second with a smaller input (fewer tokens, fewer columns and
-rows), for every weight format; arguments past the scratch's limits rejected."""
+rows), then a third whose 272 tiles run their last 16 as half-K pairs on 256
+compute units (the exchange slots in the scratch), for every weight format;
+arguments past the scratch's limits rejected."""
 import ctypes
 
 import numpy as np
@@ -38,8 +40,8 @@ def run_pair(gpu, T, x, n, ne0, ne1):
 def test_noalloc_gemv_matches_gemv_batch(gpu, fmt):
     t = FORMATS[fmt]
     host = host_lib()
-    print(f"\n[noalloc] {fmt}: 5120x1040 B=8, then 1024x272 B=3", flush=True)
-    for (ne0, ne1, n, seed) in ((5120, 1040, 8, 31), (1024, 272, 3, 32)):
+    print(f"\n[noalloc] {fmt}: 5120x1040 B=8, then 1024x272 B=3, then 5120x4352 B=4 (pair-split tail)", flush=True)
+    for (ne0, ne1, n, seed) in ((5120, 1040, 8, 31), (1024, 272, 3, 32), (5120, 4352, 4, 33)):
         W = host.synth_matrix(t, ne0, ne1, seed, 200 + t, 0.02 if t else 1.0)
         T = gpu.tensor(W, t, ne0, ne1)
         x = host.synth_normal(8 * ne0, seed, 9).reshape(8, ne0)
