@@ -222,24 +222,30 @@ def cpu_baseline_sample(path, prompt, cfg, seconds, gpu_prompt):
 
 
 # ---------------------------------------------------------------------------------- roofline microbench
-def graph_ms(gpu, calls, e0, e1):
-    """Captures the stream work of calls() in a HIP graph, replays it once untimed and once
-    between HIP events; returns the timed replay's milliseconds.  The replay issues the
-    captured kernels back to back, so the host's per-call cost is not in the figure."""
+ROOF_UNTIMED, ROOF_TIMED = 2, 5     # graph replays of the roofline series: untimed, then timed
+
+
+def graph_ms(gpu, calls, e0, e1, timed=1, untimed=1):
+    """Captures the stream work of calls() in a HIP graph, replays it `untimed` times, then
+    `timed` times each between HIP events; returns the timed replays' milliseconds.  A replay
+    issues the captured kernels back to back, so the host's per-call cost is not in the figure."""
     L = gpu.L
     gpu.sync()
     gpu.ok(L.qgpu_graph_begin())
     calls()
     gexec = ctypes.c_void_p()
     gpu.ok(L.qgpu_graph_end(ctypes.byref(gexec)))
-    gpu.ok(L.qgpu_graph_launch(gexec))
-    gpu.record(e0)
-    gpu.ok(L.qgpu_graph_launch(gexec))
-    gpu.record(e1)
-    ms = gpu.elapsed_ms(e0, e1)
-    gpu.sync()
+    for _ in range(untimed):
+        gpu.ok(L.qgpu_graph_launch(gexec))
+    out = []
+    for _ in range(timed):
+        gpu.record(e0)
+        gpu.ok(L.qgpu_graph_launch(gexec))
+        gpu.record(e1)
+        gpu.sync()
+        out.append(gpu.elapsed_ms(e0, e1))
     gpu.ok(L.qgpu_graph_destroy(gexec))
-    return ms
+    return out if timed > 1 else out[0]
 
 
 def gemv_roofline(gpu, host, steps, warmup):
@@ -268,7 +274,11 @@ def gemv_roofline(gpu, host, steps, warmup):
     def kernel_calls():
         for i in range(steps):
             gpu.ok(L.qgpu_gemv_prepared(Ts[i % R].h, B, ob.f32(), ne1, 0))
-    ms_kernel = graph_ms(gpu, kernel_calls, e0, e1) / steps
+    # several timed replays: the launch time moves by several percent between replays (clocks), so
+    # the line reports the median replay and the range
+    reps = [ms / steps for ms in graph_ms(gpu, kernel_calls, e0, e1, ROOF_TIMED, ROOF_UNTIMED)]
+    med = sorted(range(ROOF_TIMED), key=lambda i: reps[i])[ROOF_TIMED // 2]
+    ms_kernel = reps[med]
     # plain-read floor over the same device bytes: k_checksum over each rotating copy's records
     dev_bytes = int(L.qgpu_tensor_device_bytes(Ts[0].h))
     cs = gpu.buf(READ_BLOCKS * 4)
@@ -276,19 +286,22 @@ def gemv_roofline(gpu, host, steps, warmup):
     def read_calls():
         for i in range(steps):
             gpu.ok(L.qgpu_tensor_checksum(Ts[i % R].h, cs.u32(), READ_BLOCKS))
-    ms_read = graph_ms(gpu, read_calls, e0, e1) / steps
+    ms_read = sorted(ms / steps for ms in graph_ms(gpu, read_calls, e0, e1, ROOF_TIMED, ROOF_UNTIMED))[ROOF_TIMED // 2]
     for T in Ts:
         T.close()
     achieved = algo / (ms_kernel * 1e-3) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(rk),
             "kernel": rk, "workload": "IQ4_XS 17408x5120, B=4", "kernel_us": round(ms_kernel * 1e3, 3),
+            "kernel_us_range": [round(min(reps) * 1e3, 3), round(max(reps) * 1e3, 3)],
             "algo_bytes": algo,
             # the same weight bytes read by a plain XOR-reduction kernel (k_checksum), same rotation
             "read_floor_us": round(ms_read * 1e3, 3), "read_floor_gbs": round(dev_bytes / (ms_read * 1e-3) / 1e9, 1),
             "kernel_over_read_floor": round(ms_kernel / ms_read, 3),
-            # dispatch ordinals of this kernel (0-based, in launch order) that the events bracket
-            "dispatches": {"first": warmup + 3 * steps, "count": steps}}
+            # dispatch ordinals of this kernel (0-based, in launch order) that the events of the
+            # median replay bracket: warm-up calls, the gemv_batch series (2 replays), the untimed
+            # replays, then the timed ones
+            "dispatches": {"first": warmup + (2 + ROOF_UNTIMED + med) * steps, "count": steps}}
     gemv_call_gbs = algo / (ms_call * 1e-3) / 1e9
     return roof, gemv_call_gbs, ms_call, (W, x, ne0, ne1, B)
 
