@@ -303,6 +303,12 @@ int  qgpu_set_i32(int *dst, int value);
  * `vtok` are the argmax tokens of the B = k+1 verify rows (qgpu_argmax). */
 int  qgpu_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int *pos, int *cur,
                       int nslot, uint32_t *out);
+/* qgpu_spec_accept with the incoming position and ring slot given as values (pos0 >= 0,
+ * 0 <= cur0 < nslot) instead of read from *pos / *cur: *cur = (cur0 + 1 + j) % nslot,
+ * *pos = pos0 + j + 1.  Same acceptance (main.c:191-217); the caller needs no launch to
+ * set them first. */
+int  qgpu_spec_accept_at(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int pos0, int cur0,
+                         int *pos, int *cur, int nslot, uint32_t *out);
 
 #ifdef __cplusplus
 }

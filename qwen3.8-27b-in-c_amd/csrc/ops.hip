@@ -202,8 +202,10 @@ __global__ __launch_bounds__(256) void k_checksum(const uint4 *__restrict__ s, u
     if (threadIdx.x == 0) part[blockIdx.x] = wsum[0] ^ wsum[1] ^ wsum[2] ^ wsum[3];
 }
 
-__global__ void k_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int *pos, int *cur,
-                              int nslot, uint32_t *out)
+// pos0 / cur0 >= 0: the incoming position and ring slot as values (no launch to set them first);
+// otherwise they are read from *pos / *cur
+__global__ void k_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int pos0, int cur0,
+                              int *pos, int *cur, int nslot, uint32_t *out)
 {
     int j = k;
     if (force_j >= 0)
@@ -214,8 +216,9 @@ __global__ void k_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k,
     out[0] = (uint32_t)j;
     for (int i = 0; i <= j; i++) out[1 + i] = cand[i];
     out[j + 2] = vtok[j];
-    *cur = (*cur + 1 + j) % nslot;
-    *pos = *pos + j + 1;
+    const int c = cur0 >= 0 ? cur0 : *cur, p = pos0 >= 0 ? pos0 : *pos;
+    *cur = (c + 1 + j) % nslot;
+    *pos = p + j + 1;
 }
 
 // ---------------------------------------------------------------- C-ABI
@@ -235,8 +238,22 @@ extern "C" int qgpu_spec_accept(const uint32_t *cand, const uint32_t *vtok, int 
     int rc = qg::ensure_init();
     if (rc) return rc;
     if (!cand || !vtok || !pos || !cur || !out || k < 0 || k > 15 || nslot < k + 2) return QGPU_E_ARG;
-    hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(1), 0, qg::stream, cand, vtok, k, force_j, pos, cur, nslot,
-                       out);
+    hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(1), 0, qg::stream, cand, vtok, k, force_j, -1, -1, pos, cur,
+                       nslot, out);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_spec_accept_at(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int pos0,
+                                   int cur0, int *pos, int *cur, int nslot, uint32_t *out)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!cand || !vtok || !pos || !cur || !out || k < 0 || k > 15 || nslot < k + 2 || pos0 < 0 || cur0 < 0 ||
+        cur0 >= nslot)
+        return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(1), 0, qg::stream, cand, vtok, k, force_j, pos0, cur0, pos, cur,
+                       nslot, out);
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }

@@ -42,6 +42,11 @@ struct qwen_gpu {
     qgpu_tensor *tok_embd, *output, *eh_proj;
     float *out_norm, *enorm, *hnorm, *shnorm, *rope_cos, *rope_sin;
     int *d_pos, *d_cur;
+    /* where the kernels of the next forward read the position and the ring slot: constant
+     * tables d_posv[p] = p, d_curv[c] = c at host-chosen offsets for eager launches (no launch
+     * sets them), or d_pos / d_cur, set before each captured-graph replay (see at()) */
+    int *d_posv, *d_curv;
+    const int *pos_ptr, *cur_ptr;
     uint32_t *d_tok, *d_cand, *d_vtok, *d_acc;
     float *bx, *bxb, *bqkv, *bk, *bv, *bz, *bbeta, *balpha, *bffn, *battn, *xq, *h_save, *logits_b, *logits1,
           *mtp_h, *mx, *cat;
@@ -384,7 +389,7 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
         }
     }
 #define AL(p, n) do { if (!((p) = dalloc(g, (n) * sizeof(*(p))))) return -1; } while (0)
-    AL(g->d_pos, 4); AL(g->d_cur, 4); AL(g->d_tok, 64); AL(g->d_cand, 64); AL(g->d_vtok, 64); AL(g->d_acc, 64);
+    AL(g->d_pos, 4); AL(g->d_cur, 4); AL(g->d_posv, (uint64_t)n_ctx + MAXB); AL(g->d_curv, NSLOT); AL(g->d_tok, 64); AL(g->d_cand, 64); AL(g->d_vtok, 64); AL(g->d_acc, 64);
     AL(g->bx, MAXB * E); AL(g->bxb, MAXB * E); AL(g->bqkv, MAXB * g->SQ); AL(g->bk, MAXB * g->kvrow);
     AL(g->bv, MAXB * g->kvrow); AL(g->bz, MAXB * (uint64_t)d->d_inner);
     /* gate inputs: up to QGPU_MAX_KS partial planes of MAXB rows (gdn_dev) */
@@ -394,6 +399,18 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     AL(g->h_save, MAXB * E); AL(g->logits_b, MAXB * V); AL(g->logits1, V); AL(g->mtp_h, E);
     AL(g->mx, MAXB * E); AL(g->cat, MAXB * 2 * E); AL(g->part, 8 * MAXB * E);
 #undef AL
+    {   /* position and ring-slot tables: entry i holds i */
+        const uint64_t np = (uint64_t)n_ctx + MAXB;
+        int *tab = malloc(np * sizeof(int));
+        if (!tab) return -1;
+        for (uint64_t i = 0; i < np; i++) tab[i] = (int)i;
+        const int bad = qgpu_memcpy_h2d(g->d_posv, tab, np * sizeof(int)) ||
+                        qgpu_memcpy_h2d(g->d_curv, tab, NSLOT * sizeof(int));
+        free(tab);
+        if (bad) return -1;
+    }
+    g->pos_ptr = g->d_pos;
+    g->cur_ptr = g->d_cur;
     /* RoPE tables with the reference's own expressions (model.c:186-201) */
     const uint32_t half = c->rope_dim_count / 2;
     float *cs = malloc((size_t)n_ctx * half * sizeof(float)), *sn = malloc((size_t)n_ctx * half * sizeof(float));
@@ -614,11 +631,11 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     K(qgpu_gemv_act_batch(W, 3, &an, (int)B, outs, ld, 0));
     /* q/k norm + RoPE + cache write + attention in one kernel, then the span merge, which also
      * prepares the o-projection input when the matrix runs on the matrix cores */
-    (void)pos;   /* positions come from g->d_pos; the grid covers n_ctx (spans past the live end exit) */
+    (void)pos;   /* positions come from g->pos_ptr (at()); the grid covers n_ctx (spans past the live end exit) */
     const int prep = mat_packed(D->o);
     K((prep ? qgpu_attn_fused_act : qgpu_attn_fused)(
         g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos, g->rope_sin,
-        (int)m->cfg.rope_dim_count, g->d_pos, (int)m->n_ctx, (int)B, (int)d->n_head, (int)d->n_kv_head,
+        (int)m->cfg.rope_dim_count, g->pos_ptr, (int)m->n_ctx, (int)B, (int)d->n_head, (int)d->n_kv_head,
         (int)d->head_dim, eps, g->battn, g->A));
     if (prep) {
         residual_gemv_prepared(m, D->o, B, R);
@@ -656,7 +673,7 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     /* conv1d + SiLU + L2 norms + delta rule over the B tokens, state snapshots into the ring */
     K(qgpu_gdn_fused_planes(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems,
                             g->bbeta, g->balpha, d->n_v_heads, kba, (uint64_t)B * d->n_v_heads, D->dt_bias,
-                            D->ssm_a, D->ssm_ring, g->ssm_elems, NSLOT, g->d_cur, (int)d->n_k_heads,
+                            D->ssm_a, D->ssm_ring, g->ssm_elems, NSLOT, g->cur_ptr, (int)d->n_k_heads,
                             (int)d->n_v_heads, (int)d->head_v_dim, eps, g->battn, di));
     /* per-head gated RMSNorm (model.c:928-941) fused into the ssm_out input */
     qgpu_act gn;
@@ -759,17 +776,34 @@ static void forward_body(qwen_model_t *m, const uint32_t *d_tokens, const float 
     if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
 }
 
+/* Where the kernels of the next launch sequence read the position and the ring slot.
+ * Eager launches read the constant tables at the host's values (d_posv + pos, d_curv +
+ * cur), so no kernel sets them; a captured graph reads d_pos / d_cur, which are set
+ * before each replay (with_cur: the sequence has GDN layers). */
+static void at(qwen_model_t *m, uint32_t pos, int with_cur)
+{
+    qwen_gpu_t *g = m->gpu;
+    if (g->use_graphs && !g->prof_active) {
+        K(qgpu_set_i32(g->d_pos, (int)pos));
+        if (with_cur) K(qgpu_set_i32(g->d_cur, g->cur));
+        g->pos_ptr = g->d_pos;
+        g->cur_ptr = g->d_cur;
+    } else {
+        g->pos_ptr = g->d_posv + pos;
+        g->cur_ptr = g->d_curv + g->cur;
+    }
+}
+
 /* tokens on the device; logits of every token into d_logits ([B][V]); hidden
  * states into h_save when save_h.  GDN states advance by B (ring index). */
 static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, uint32_t pos, float *d_logits,
                         int save_h)
 {
     qwen_gpu_t *g = m->gpu;
-    K(qgpu_set_i32(g->d_pos, (int)pos));
+    at(m, pos, 1);
     run_body(m, G_FWD, forward_body, d_tokens, NULL, B, d_logits, save_h);
     g->cur_base = g->cur;
     g->cur = (g->cur + (int)B) % NSLOT;
-    K(qgpu_set_i32(g->d_cur, g->cur));
 }
 
 static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, uint32_t B, float *d_logits,
@@ -780,7 +814,7 @@ static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, 
 static void mtp_dev(qwen_model_t *m, const uint32_t *d_tokens, const float *h, uint32_t B, uint32_t pos,
                     float *d_logits)
 {
-    K(qgpu_set_i32(m->gpu->d_pos, (int)pos));
+    at(m, pos, 0);
     run_body(m, G_MTP, mtp_body, d_tokens, h, B, d_logits, 0);
 }
 
@@ -881,8 +915,7 @@ void model_rollback_to(qwen_model_t *m, uint32_t b)
     if (call_begin(m)) return;
     if (b >= SPEC_MAX_B) { reject(m, "model_rollback_to", b, 1); return; }
     qwen_gpu_t *g = m->gpu;
-    g->cur = (g->cur_base + 1 + (int)b) % NSLOT;
-    K(qgpu_set_i32(g->d_cur, g->cur));
+    g->cur = (g->cur_base + 1 + (int)b) % NSLOT;   /* the next forward reads it through at() */
     call_end(m);
 }
 
@@ -939,7 +972,7 @@ void attention_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool, uint32_t po
     qwen_gpu_t *g = m->gpu;
     glayer_t *D = (L == &m->mtp_layer) ? &g->mtp : &g->L[L - m->layers];
     K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
-    K(qgpu_set_i32(g->d_pos, (int)pos));
+    at(m, pos, 0);
     attn_dev(m, D, g->bx, 1, pos);
     materialize(m);
     K(qgpu_memcpy_d2h(m->x, g->bx, m->dims.n_embd * sizeof(float)));
@@ -957,6 +990,7 @@ void gdn_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool)
     qwen_gpu_t *g = m->gpu;
     K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
     glayer_t *D = &g->L[L - m->layers];
+    at(m, m->pos, 1);
     gdn_dev(m, D, 1);
     materialize(m);
     /* the reference updates this layer's state in place (model.c:640-661): copy
@@ -1035,10 +1069,9 @@ uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_acc
         forward_dev(m, g->d_cand, kk + 1, P + 1, g->logits_b, 1);
         K(qgpu_argmax(g->logits_b, V, V, (int)(kk + 1), g->d_vtok));
         /* acceptance + GDN rollback on the device (main.c:191-217) */
-        K(qgpu_set_i32(g->d_pos, (int)(P + 1)));
-        K(qgpu_set_i32(g->d_cur, g->cur_base));
         const int force_j = force_accept == 1 ? (int)kk : force_accept == 2 ? (int)(s.n_cycles % (kk + 1)) : -1;
-        K(qgpu_spec_accept(g->d_cand, g->d_vtok, (int)kk, force_j, g->d_pos, g->d_cur, NSLOT, g->d_acc));
+        K(qgpu_spec_accept_at(g->d_cand, g->d_vtok, (int)kk, force_j, (int)(P + 1), g->cur_base, g->d_pos,
+                              g->d_cur, NSLOT, g->d_acc));
         K(qgpu_memcpy_d2h(acc, g->d_acc, (kk + 3) * sizeof(uint32_t)));
         if (qwen_dev_err) break;
         j = acc[0] <= kk ? acc[0] : kk;
@@ -1186,12 +1219,12 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
     K(qgpu_event_create(&e1));
     /* verify: B tokens at pos (states are restored to the ring index after each rep) */
     forward_dev(m, g->d_cand, B, pos, g->logits_b, 1);
-    g->cur = cur0; g->cur_base = base0; K(qgpu_set_i32(g->d_cur, cur0));
+    g->cur = cur0; g->cur_base = base0;
     K(qgpu_event_record(e0));
     for (int r = 0; r < reps; r++) {
         forward_dev(m, g->d_cand, B, pos, g->logits_b, 1);
         K(qgpu_argmax(g->logits_b, m->cfg.vocab_size, m->cfg.vocab_size, (int)B, g->d_vtok));
-        g->cur = cur0; g->cur_base = base0; K(qgpu_set_i32(g->d_cur, cur0));
+        g->cur = cur0; g->cur_base = base0;
     }
     K(qgpu_event_record(e1));
     K(qgpu_event_elapsed_ms(e0, e1, ms_verify));
@@ -1200,7 +1233,7 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
     for (int r = 0; r < reps; r++) {
         forward_dev(m, g->d_cand, 1, pos, g->logits1, 0);
         K(qgpu_argmax(g->logits1, m->cfg.vocab_size, m->cfg.vocab_size, 1, g->d_vtok));
-        g->cur = cur0; g->cur_base = base0; K(qgpu_set_i32(g->d_cur, cur0));
+        g->cur = cur0; g->cur_base = base0;
     }
     K(qgpu_event_record(e1));
     K(qgpu_event_elapsed_ms(e0, e1, ms_decode));
@@ -1220,7 +1253,6 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
         K(qgpu_memcpy_h2d(g->mtp_h, keep, eb));
         free(keep);
     }
-    K(qgpu_set_i32(g->d_pos, (int)pos));
     K(qgpu_sync());
     qgpu_event_destroy(e0);
     qgpu_event_destroy(e1);

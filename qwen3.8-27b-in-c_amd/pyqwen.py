@@ -302,6 +302,8 @@ class GpuLib:
             "qgpu_gemv_prepared_split": [vp, i32, F32P, u64, i32],
             "qgpu_add_partials": [F32P, u64, F32P, u64, F32P, u64, i32, u64, i32],
             "qgpu_spec_accept": [U32P, U32P, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), i32, U32P],
+            "qgpu_spec_accept_at": [U32P, U32P, i32, i32, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), i32,
+                                    U32P],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)

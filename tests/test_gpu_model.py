@@ -346,6 +346,17 @@ def test_spec_accept_kernel(gpu):
         o = out.download(np.uint32)
         assert o[0] == j and list(o[1:j + 2]) == [7, 3, 9, 4][:j + 1] and o[j + 2] == vt[j]
         assert pos.download(np.int32)[0] == 100 + j + 1 and cur.download(np.int32)[0] == (7 + 1 + j) % NSLOT
+        # the same with the incoming position and slot as values (the outputs start as other values)
+        pos2, cur2, out2 = gpu.put(np.array([-5], np.int32)), gpu.put(np.array([3], np.int32)), gpu.buf(16 * 4)
+        gpu.ok(gpu.L.qgpu_spec_accept_at(cand.u32(), vb.u32(), k, fj, 100, 7, pos2.i32(), cur2.i32(), NSLOT,
+                                         out2.u32()))
+        assert np.array_equal(out2.download(np.uint32)[:j + 3], o[:j + 3])     # out[0 .. j+2] are written
+        assert pos2.download(np.int32)[0] == 100 + j + 1 and cur2.download(np.int32)[0] == (7 + 1 + j) % NSLOT
+    ob = gpu.buf(16 * 4)
+    p_, c_ = gpu.put(np.array([0], np.int32)), gpu.put(np.array([0], np.int32))
+    for p0, c0 in ((-1, 0), (5, -1), (5, NSLOT)):                  # rejected: no valid incoming position / slot
+        assert gpu.L.qgpu_spec_accept_at(cand.u32(), cand.u32(), 1, -1, p0, c0, p_.i32(), c_.i32(), NSLOT,
+                                         ob.u32()) != 0
 
 
 # ---------------------------------------------------------------- tiny hybrid model
