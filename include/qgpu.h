@@ -43,6 +43,10 @@ int  qgpu_free(void *ptr);
 int  qgpu_memcpy_h2d(void *dst, const void *src, size_t bytes);     /* synchronous */
 int  qgpu_memcpy_d2h(void *dst, const void *src, size_t bytes);     /* synchronous */
 int  qgpu_memcpy_d2d(void *dst, const void *src, size_t bytes);     /* stream-ordered */
+/* Pinned host memory that kernels can write (hipHostMalloc, coherent): the host sees
+ * their stores without a copy.  qgpu_host_free waits for the library stream first. */
+int  qgpu_host_malloc(void **p, size_t bytes);
+int  qgpu_host_free(void *p);
 int  qgpu_memset(void *dst, int value, size_t bytes);               /* stream-ordered */
 /* Timing on the library stream (HIP events). */
 int  qgpu_event_create(void **ev);
@@ -309,6 +313,17 @@ int  qgpu_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int for
  * set them first. */
 int  qgpu_spec_accept_at(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int pos0, int cur0,
                          int *pos, int *cur, int nslot, uint32_t *out);
+/* qgpu_spec_accept_at that also hands the next MTP forward its inputs on the device, so
+ * the caller can enqueue that forward before it reads j (main.c:219-221, the re-anchor):
+ * *tok_out = cand[j] and row_out[0..n) = rows[j*ld .. j*ld+n) (h_save[j]) when non-NULL,
+ * and *cand0_out = vtok[j] (the next cycle's cand[0]) when non-NULL, written after every
+ * read of cand, so it may point at cand[0].  With pos0 = P, the position of the token
+ * before the verified ones, *pos = P + j + 1 is the re-anchor's position.  `out` may be
+ * qgpu_host_malloc memory: out[0] (j) is stored last, after a system-scope fence, so a
+ * host that sees out[0] change can read out[1 .. j+2] without waiting for the stream. */
+int  qgpu_spec_accept_anchor(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int pos0, int cur0,
+                             int *pos, int *cur, int nslot, uint32_t *out, const float *rows, uint64_t ld, int n,
+                             float *row_out, uint32_t *tok_out, uint32_t *cand0_out);
 
 #ifdef __cplusplus
 }

@@ -204,21 +204,39 @@ __global__ __launch_bounds__(256) void k_checksum(const uint4 *__restrict__ s, u
 
 // pos0 / cur0 >= 0: the incoming position and ring slot as values (no launch to set them first);
 // otherwise they are read from *pos / *cur
+// Acceptance (thread 0); with row_out, the block then copies row j of `rows` (the
+// re-anchor's hidden state).  tok_out / cand0_out are written after every read of
+// cand, so cand0_out may point into cand; out[0] is written last, after a system-scope
+// fence (out may be host memory that the host polls).
 __global__ void k_spec_accept(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int pos0, int cur0,
-                              int *pos, int *cur, int nslot, uint32_t *out)
+                              int *pos, int *cur, int nslot, uint32_t *out, const float *rows, uint64_t ld, int n,
+                              float *row_out, uint32_t *tok_out, uint32_t *cand0_out)
 {
-    int j = k;
-    if (force_j >= 0)
-        j = force_j < k ? force_j : k;
-    else
-        for (int i = 0; i < k; i++)
-            if (vtok[i] != cand[i + 1]) { j = i; break; }
-    out[0] = (uint32_t)j;
-    for (int i = 0; i <= j; i++) out[1 + i] = cand[i];
-    out[j + 2] = vtok[j];
-    const int c = cur0 >= 0 ? cur0 : *cur, p = pos0 >= 0 ? pos0 : *pos;
-    *cur = (c + 1 + j) % nslot;
-    *pos = p + j + 1;
+    __shared__ int sj;
+    if (threadIdx.x == 0) {
+        int j = k;
+        if (force_j >= 0)
+            j = force_j < k ? force_j : k;
+        else
+            for (int i = 0; i < k; i++)
+                if (vtok[i] != cand[i + 1]) { j = i; break; }
+        for (int i = 0; i <= j; i++) out[1 + i] = cand[i];
+        const uint32_t next = vtok[j], anchor = cand[j];
+        out[j + 2] = next;
+        if (tok_out) *tok_out = anchor;
+        if (cand0_out) *cand0_out = next;
+        const int c = cur0 >= 0 ? cur0 : *cur, p = pos0 >= 0 ? pos0 : *pos;
+        *cur = (c + 1 + j) % nslot;
+        *pos = p + j + 1;
+        sj = j;
+        // j last: a host polling out[0] in host memory then finds out[1 .. j+2] written
+        __threadfence_system();
+        out[0] = (uint32_t)j;
+    }
+    if (!row_out) return;
+    __syncthreads();
+    const float *src = rows + (uint64_t)sj * ld;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) row_out[i] = src[i];
 }
 
 // ---------------------------------------------------------------- C-ABI
@@ -239,7 +257,7 @@ extern "C" int qgpu_spec_accept(const uint32_t *cand, const uint32_t *vtok, int 
     if (rc) return rc;
     if (!cand || !vtok || !pos || !cur || !out || k < 0 || k > 15 || nslot < k + 2) return QGPU_E_ARG;
     hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(1), 0, qg::stream, cand, vtok, k, force_j, -1, -1, pos, cur,
-                       nslot, out);
+                       nslot, out, nullptr, 0, 0, nullptr, nullptr, nullptr);
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }
@@ -253,7 +271,23 @@ extern "C" int qgpu_spec_accept_at(const uint32_t *cand, const uint32_t *vtok, i
         cur0 >= nslot)
         return QGPU_E_ARG;
     hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(1), 0, qg::stream, cand, vtok, k, force_j, pos0, cur0, pos, cur,
-                       nslot, out);
+                       nslot, out, nullptr, 0, 0, nullptr, nullptr, nullptr);
+    QG_LAUNCH_CHECK();
+    return QGPU_OK;
+}
+
+extern "C" int qgpu_spec_accept_anchor(const uint32_t *cand, const uint32_t *vtok, int k, int force_j, int pos0,
+                                       int cur0, int *pos, int *cur, int nslot, uint32_t *out, const float *rows,
+                                       uint64_t ld, int n, float *row_out, uint32_t *tok_out, uint32_t *cand0_out)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!cand || !vtok || !pos || !cur || !out || k < 0 || k > 15 || nslot < k + 2 || pos0 < 0 || cur0 < 0 ||
+        cur0 >= nslot)
+        return QGPU_E_ARG;
+    if (row_out && (!rows || n < 1 || ld < (uint64_t)n)) return QGPU_E_ARG;
+    hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(row_out ? 256 : 1), 0, qg::stream, cand, vtok, k, force_j, pos0,
+                       cur0, pos, cur, nslot, out, rows, ld, row_out ? n : 0, row_out, tok_out, cand0_out);
     QG_LAUNCH_CHECK();
     return QGPU_OK;
 }

@@ -128,6 +128,24 @@ extern "C" int qgpu_memcpy_d2h(void *d, const void *s, size_t n)
     return qg::check(hipStreamSynchronize(qg::stream));
 }
 
+// Pinned, coherent host memory: kernels store to it through the fabric, and the host
+// sees those stores without a copy or a stream synchronisation.
+extern "C" int qgpu_host_malloc(void **p, size_t bytes)
+{
+    int rc = qg::ensure_init();
+    if (rc) return rc;
+    if (!p || !bytes) return QGPU_E_ARG;
+    *p = nullptr;
+    return qg::check(hipHostMalloc(p, bytes, hipHostMallocDefault));
+}
+
+extern "C" int qgpu_host_free(void *p)
+{
+    if (!p) return QGPU_OK;
+    if (qg::stream) QG_CHECK(hipStreamSynchronize(qg::stream));
+    return qg::check(hipHostFree(p));
+}
+
 extern "C" int qgpu_memcpy_d2d(void *d, const void *s, size_t n)
 {
     int rc = qg::ensure_init();

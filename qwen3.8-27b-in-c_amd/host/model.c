@@ -48,6 +48,11 @@ struct qwen_gpu {
     int *d_posv, *d_curv;
     const int *pos_ptr, *cur_ptr;
     uint32_t *d_tok, *d_cand, *d_vtok, *d_acc;
+    /* the MTP re-anchor's token and hidden state, written by the acceptance kernel */
+    uint32_t *anchor_tok;
+    float *anchor_h;
+    /* the acceptance result in pinned host memory (the kernel writes it, the host polls it) */
+    uint32_t *h_acc;
     float *bx, *bxb, *bqkv, *bk, *bv, *bz, *bbeta, *balpha, *bffn, *battn, *xq, *h_save, *logits_b, *logits1,
           *mtp_h, *mx, *cat;
     uint64_t SQ, A, conv_elems, ssm_elems, kvrow;
@@ -143,6 +148,7 @@ static void gpu_free(qwen_gpu_t *g)
     }
     for (size_t i = 0; i < g->n_tensors; i++) qgpu_tensor_free(g->tensors[i]);
     for (size_t i = 0; i < g->n_allocs; i++) qgpu_free(g->allocs[i]);
+    qgpu_host_free(g->h_acc);
     free(g->tensors);
     free(g->allocs);
     free(g->L);
@@ -390,6 +396,8 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     }
 #define AL(p, n) do { if (!((p) = dalloc(g, (n) * sizeof(*(p))))) return -1; } while (0)
     AL(g->d_pos, 4); AL(g->d_cur, 4); AL(g->d_posv, (uint64_t)n_ctx + MAXB); AL(g->d_curv, NSLOT); AL(g->d_tok, 64); AL(g->d_cand, 64); AL(g->d_vtok, 64); AL(g->d_acc, 64);
+    AL(g->anchor_tok, 64); AL(g->anchor_h, E);
+    if (qgpu_host_malloc((void **)&g->h_acc, 64 * sizeof(uint32_t))) return -1;
     AL(g->bx, MAXB * E); AL(g->bxb, MAXB * E); AL(g->bqkv, MAXB * g->SQ); AL(g->bk, MAXB * g->kvrow);
     AL(g->bv, MAXB * g->kvrow); AL(g->bz, MAXB * (uint64_t)d->d_inner);
     /* gate inputs: up to QGPU_MAX_KS partial planes of MAXB rows (gdn_dev) */
@@ -818,6 +826,16 @@ static void mtp_dev(qwen_model_t *m, const uint32_t *d_tokens, const float *h, u
     run_body(m, G_MTP, mtp_body, d_tokens, h, B, d_logits, 0);
 }
 
+/* MTP re-anchor of the speculative loop (main.c:219-221) on the token, hidden state and
+ * position the acceptance kernel left on the device (anchor_tok, anchor_h, d_pos), so it
+ * is enqueued before the host knows j; no logits */
+static void mtp_anchor_dev(qwen_model_t *m)
+{
+    qwen_gpu_t *g = m->gpu;
+    g->pos_ptr = g->d_pos;
+    run_body(m, G_MTP, mtp_body, g->anchor_tok, g->anchor_h, 1, NULL, 0);
+}
+
 static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, uint32_t B, float *d_logits,
                      int unused)
 {
@@ -1039,6 +1057,27 @@ int model_spec_begin(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt,
     return m->gpu->status;
 }
 
+#define ACC_PENDING 0xFFFFFFFFu
+
+/* Waits for the acceptance kernel's result in pinned host memory: h_acc[0] leaves ACC_PENDING
+ * once the rest is written.  After ~0.5 s of polling the stream is drained instead (a slow or
+ * failed device; the error is recorded and the loop stops). */
+static int wait_acc(qwen_model_t *m, uint32_t *acc, uint32_t n)
+{
+    qwen_gpu_t *g = m->gpu;
+    if (qwen_dev_err) return -1;
+    const double t0 = now_s();
+    for (uint64_t spin = 1; __atomic_load_n(&g->h_acc[0], __ATOMIC_ACQUIRE) == ACC_PENDING; spin++)
+        if (!(spin & 4095) && now_s() - t0 > 0.5) {
+            K(qgpu_sync());
+            if (qwen_dev_err) return -1;
+            if (__atomic_load_n(&g->h_acc[0], __ATOMIC_ACQUIRE) == ACC_PENDING) { fail_rc("wait_acc", -1); return -1; }
+            break;
+        }
+    for (uint32_t i = 0; i < n; i++) acc[i] = __atomic_load_n(&g->h_acc[i], __ATOMIC_ACQUIRE);
+    return 0;
+}
+
 uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_accept, uint32_t max_cycles,
                         uint32_t max_tokens, uint32_t *out, uint32_t *cycle_j, qwen_gen_stats_t *st)
 {
@@ -1070,10 +1109,19 @@ uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_acc
         K(qgpu_argmax(g->logits_b, V, V, (int)(kk + 1), g->d_vtok));
         /* acceptance + GDN rollback on the device (main.c:191-217) */
         const int force_j = force_accept == 1 ? (int)kk : force_accept == 2 ? (int)(s.n_cycles % (kk + 1)) : -1;
-        K(qgpu_spec_accept_at(g->d_cand, g->d_vtok, (int)kk, force_j, (int)(P + 1), g->cur_base, g->d_pos,
-                              g->d_cur, NSLOT, g->d_acc));
-        K(qgpu_memcpy_d2h(acc, g->d_acc, (kk + 3) * sizeof(uint32_t)));
-        if (qwen_dev_err) break;
+        /* the verify left the position at P+kk+2: the reference stops there once it reaches the
+         * context end, before any rollback or re-anchor (main.c:210) */
+        const int ctx_end = P + kk + 2 >= m->n_ctx, anchor = !ctx_end && k > 0;
+        /* the result goes to pinned host memory, j (h_acc[0]) last; d_pos = P+j+1 (pos0 = P), the
+         * re-anchor's position; the next cand[0] = argmax logits_b[j] goes to d_cand[0] */
+        __atomic_store_n(&g->h_acc[0], ACC_PENDING, __ATOMIC_RELEASE);
+        K(qgpu_spec_accept_anchor(g->d_cand, g->d_vtok, (int)kk, force_j, (int)P, g->cur_base, g->d_pos,
+                                  g->d_cur, NSLOT, g->h_acc, g->h_save, E, (int)E, anchor ? g->anchor_h : NULL,
+                                  anchor ? g->anchor_tok : NULL, ctx_end ? NULL : g->d_cand));
+        /* the re-anchor (MTP on the backbone hidden state of the last accepted token, main.c:220-222)
+         * is enqueued before the host waits for j */
+        if (anchor) mtp_anchor_dev(m);
+        if (wait_acc(m, acc, kk + 3)) break;
         j = acc[0] <= kk ? acc[0] : kk;
         g->cur = (g->cur_base + 1 + (int)j) % NSLOT;
         if (cycle_j) cycle_j[s.n_cycles] = j;
@@ -1081,13 +1129,8 @@ uint32_t model_spec_run(qwen_model_t *m, uint32_t k, uint32_t eos, int force_acc
         s.n_accepted += j;
         s.n_drafts += kk;
         s.n_cycles++;
-        /* the verify left the position at P+kk+2: the reference stops there once it
-         * reaches the context end, before any rollback (main.c:210) */
-        if (P + kk + 2 >= m->n_ctx) { m->pos = P + kk + 2; break; }
+        if (ctx_end) { m->pos = P + kk + 2; break; }
         m->pos = P + j + 2;
-        /* MTP re-anchor on the backbone hidden state of the last accepted token (main.c:220-222) */
-        if (k > 0) mtp_dev(m, g->d_cand + j, g->h_save + (size_t)j * E, 1, P + j + 1, NULL);
-        K(qgpu_memcpy_d2d(g->d_cand, g->d_acc + j + 2, sizeof(uint32_t)));   /* next cand[0] = argmax logits_b[j] */
         next0 = acc[j + 2];
     }
     K(qgpu_sync());

@@ -304,6 +304,9 @@ class GpuLib:
             "qgpu_spec_accept": [U32P, U32P, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), i32, U32P],
             "qgpu_spec_accept_at": [U32P, U32P, i32, i32, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32), i32,
                                     U32P],
+            "qgpu_spec_accept_anchor": [U32P, U32P, i32, i32, i32, i32, ctypes.POINTER(i32), ctypes.POINTER(i32),
+                                        i32, U32P, F32P, u64, i32, F32P, U32P, U32P],
+            "qgpu_host_malloc": [ctypes.POINTER(vp), ctypes.c_size_t], "qgpu_host_free": [vp],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)

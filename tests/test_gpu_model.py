@@ -9,6 +9,7 @@ Bars: GEMV/GDN outputs within 1e-3 relative (normwise, max|d|/max|ref|);
 greedy token streams identical wherever the reference top-2 gap > 1e-2 (every
 gap of the fixtures is above 0.3, so the streams must be identical).
 """
+import ctypes
 import hashlib
 import os
 import tempfile
@@ -352,11 +353,50 @@ def test_spec_accept_kernel(gpu):
                                          out2.u32()))
         assert np.array_equal(out2.download(np.uint32)[:j + 3], o[:j + 3])     # out[0 .. j+2] are written
         assert pos2.download(np.int32)[0] == 100 + j + 1 and cur2.download(np.int32)[0] == (7 + 1 + j) % NSLOT
+        # the same, handing the re-anchor its inputs: hidden row j, token cand[j], and the next
+        # cand[0] = vtok[j] written into the candidate buffer itself
+        rows = np.random.default_rng(j).standard_normal((8, 48)).astype(np.float32)
+        rb, hb, tb = gpu.put(rows), gpu.put(np.full(40, np.nan, np.float32)), gpu.put(np.zeros(4, np.uint32))
+        c3 = gpu.put(np.array([7, 3, 9, 4, 0, 0, 0, 0], np.uint32))
+        pos3, cur3, out3 = gpu.put(np.array([-5], np.int32)), gpu.put(np.array([3], np.int32)), gpu.buf(16 * 4)
+        gpu.ok(gpu.L.qgpu_spec_accept_anchor(c3.u32(), vb.u32(), k, fj, 99, 7, pos3.i32(), cur3.i32(), NSLOT,
+                                             out3.u32(), rb.f32(), 48, 40, hb.f32(), tb.u32(), c3.u32()))
+        assert np.array_equal(out3.download(np.uint32)[:j + 3], o[:j + 3])
+        assert pos3.download(np.int32)[0] == 99 + j + 1 and cur3.download(np.int32)[0] == (7 + 1 + j) % NSLOT
+        assert np.array_equal(hb.download(np.float32), rows[j, :40])
+        assert tb.download(np.uint32)[0] == [7, 3, 9, 4][j]
+        assert list(c3.download(np.uint32)) == [vt[j], 3, 9, 4, 0, 0, 0, 0]
     ob = gpu.buf(16 * 4)
     p_, c_ = gpu.put(np.array([0], np.int32)), gpu.put(np.array([0], np.int32))
+    assert gpu.L.qgpu_spec_accept_anchor(cand.u32(), cand.u32(), 1, -1, 5, 0, p_.i32(), c_.i32(), NSLOT, ob.u32(),
+                                         None, 8, 8, ob.f32(), None, None) != 0   # a row copy without rows
     for p0, c0 in ((-1, 0), (5, -1), (5, NSLOT)):                  # rejected: no valid incoming position / slot
         assert gpu.L.qgpu_spec_accept_at(cand.u32(), cand.u32(), 1, -1, p0, c0, p_.i32(), c_.i32(), NSLOT,
                                          ob.u32()) != 0
+
+
+def test_spec_accept_into_host_memory(gpu):
+    """The acceptance result written by the kernel straight into qgpu_host_malloc memory:
+    out[0] (j) leaves the host's sentinel once the rest is there, read without a copy."""
+    p = ctypes.c_void_p()
+    gpu.ok(gpu.L.qgpu_host_malloc(ctypes.byref(p), 64 * 4))
+    try:
+        h = np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint32)), (64,))
+        cand = gpu.put(np.array([7, 3, 9, 4, 0, 0, 0, 0], np.uint32))
+        vb = gpu.put(np.array([3, 8, 4, 11, 0, 0, 0, 0], np.uint32))          # first mismatch at 1
+        pos, cur = gpu.put(np.array([0], np.int32)), gpu.put(np.array([0], np.int32))
+        h[:] = 0xFFFFFFFF
+        gpu.ok(gpu.L.qgpu_spec_accept_anchor(cand.u32(), vb.u32(), 3, -1, 50, 2, pos.i32(), cur.i32(), NSLOT,
+                                             ctypes.cast(p, ctypes.POINTER(ctypes.c_uint32)), None, 0, 0, None,
+                                             None, None))
+        t0 = time.time()
+        while h[0] == 0xFFFFFFFF and time.time() - t0 < 10:
+            pass
+        gpu.sync()
+        assert list(h[:4]) == [1, 7, 3, 8] and h[4] == 0xFFFFFFFF
+        assert pos.download(np.int32)[0] == 52 and cur.download(np.int32)[0] == 4
+    finally:
+        gpu.ok(gpu.L.qgpu_host_free(p))
 
 
 # ---------------------------------------------------------------- tiny hybrid model
