@@ -123,7 +123,13 @@ int  qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, i
  * so xout then holds x * w (the row factor is not in it).
  * Pending K-split partial sums (qgpu_gemv_act_split): with n_part > 0 the
  * RMSNORM input is x_eff = x + sum_{q < n_part} part[q*n*ldp + t*ldp + i];
- * xnew (ldxn; may equal x) receives x_eff.  Single-segment RMSNORM only. */
+ * xnew (ldxn; may equal x) receives x_eff.  Single-segment RMSNORM only.
+ * Embedding gather: with embd (a packed IQ4_XS matrix) and tok (n device token ids),
+ * QGPU_ACT_RMSNORM reads row t of x (of its first segment in the two-segment form) as
+ * row tok[t] of embd, dequantised as qgpu_dequant_rows does (bit-identical; ids past the
+ * last row give zero rows); x is unused, embd's ne0 is the segment length, n_part is 0,
+ * and the single-segment form writes the rows to xnew when set.  (The reference's
+ * embedding lookups, model.c:721,982,1045,1079, in the first preparation of a forward.) */
 #define QGPU_ACT_COPY        0
 #define QGPU_ACT_RMSNORM     1
 #define QGPU_ACT_SILU_MUL    2
@@ -139,6 +145,7 @@ typedef struct {
     float       *xout; uint64_t ldxo;
     const float *part; uint64_t ldp; int n_part;
     float       *xnew; uint64_t ldxn;
+    const qgpu_tensor *embd; const uint32_t *tok;
 } qgpu_act;
 /* qgpu_gemv_multi_batch with the input given as a transform of device rows. */
 int  qgpu_gemv_act_batch(const qgpu_tensor *const *Ws, int n_mat, const qgpu_act *act, int n,

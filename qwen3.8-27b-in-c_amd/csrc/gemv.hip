@@ -26,6 +26,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 #define RSS_FLOATS  ((size_t)QGPU_MAX_B * MAX_NSB)
 #define ACT_RMS_DEFER 4      // internal prep kind: RMSNORM with the 1/rms factor applied by the GEMV
+#define ACT_RMS_EMBD 5       // ACT_RMS_DEFER on rows gathered from the embedding matrix
 
 // Pair split (tail balance): when a launch's tiles are a little over a multiple of the compute
 // units, the remainder tiles run as two half-K blocks each, whose results meet in 64-bit exchange
@@ -376,7 +377,43 @@ struct ActDev {
     uint64_t ldp, pstride, ldxn;
     int n_part, nsb;
     float *xnew, *rss;
+    // x (the first segment of the two-segment RMSNORM) gathered from rows tok[t] of a packed
+    // IQ4_XS matrix of embd_ne1 rows instead of read from x
+    const uint8_t *embd;
+    const uint32_t *tok;
+    uint64_t embd_ne1;
 };
+
+// Elements k..k+3 (k % 4 == 0) of row r of a packed IQ4_XS matrix with ne0 columns, as
+// k_dequant_rows computes them (zeros for r >= ne1): the four share one dword of
+// nibbles and one sub-block scale.
+static __device__ __forceinline__ float4 embd_iq4x4(const uint8_t *W, uint64_t ne0, uint64_t ne1, uint32_t r,
+                                                    uint64_t k)
+{
+    if (r >= ne1) return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const uint32_t nsb = (uint32_t)(ne0 / 256), sb = (uint32_t)(k >> 8), ib = (uint32_t)(k >> 5) & 7;
+    const uint32_t j = (uint32_t)k & 31, n = r % IQ4_TILE_ROWS;
+    const uint8_t *rec = W + ((uint64_t)(r / IQ4_TILE_ROWS) * nsb + sb) * IQ4_REC_BYTES;
+    const uint2 hdr = *(const uint2 *)(rec + n * 8);
+    const float dl = __fmul_rn(h2f(hdr.x & 0xFFFFu), (float)hdr_scale(hdr, (int)ib));
+    const uint32_t nib = (*(const uint32_t *)(rec + IQ4_HDR_BYTES + ((ib / 4) * 64 + ((j & 15) >> 2) * 16 + n) * 16 +
+                                              (ib % 4) * 4) >> (j >= 16 ? 4 : 0)) & 0x0F0F0F0Fu;
+    // the codebook (-127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113) as int8 bytes:
+    // one byte permute per half, the half picked by bit 3 of each nibble
+    const uint32_t sel = nib & 0x07070707u, hm = ((nib >> 3) & 0x01010101u) * 0xFFu;
+    const uint32_t lo = __builtin_amdgcn_perm(0xF6EADDCFu, 0xBFAD9881u, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(0x71594535u, 0x26190D01u, sel);
+    const uint32_t b = (lo & ~hm) | (hi & hm);
+    return make_float4(__fmul_rn(dl, (float)(int8_t)(b & 0xFFu)), __fmul_rn(dl, (float)(int8_t)((b >> 8) & 0xFFu)),
+                       __fmul_rn(dl, (float)(int8_t)((b >> 16) & 0xFFu)), __fmul_rn(dl, (float)(int8_t)(b >> 24)));
+}
+
+static __device__ __forceinline__ float embd_iq4(const uint8_t *W, uint64_t ne0, uint64_t ne1, uint32_t r, uint64_t k)
+{
+    const float4 v = embd_iq4x4(W, ne0, ne1, r, k & ~(uint64_t)3);
+    const uint32_t c = (uint32_t)k & 3;
+    return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w;
+}
 
 static __device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + expf(-v)); }
 
@@ -386,6 +423,7 @@ static __device__ __forceinline__ float silu_dev(float v) { return v / (1.0f + e
 // (blockIdx.x) of the 4 tokens of plane blockIdx.y; each block recomputes the row
 // RMS of its segment in the same order, so every block gets the same value.  The
 // four tokens' loads are issued before their first use.
+template <bool GATH>
 __global__ __launch_bounds__(256) void k_prep_rms(ActDev p, uint8_t *__restrict__ A, float *__restrict__ xs)
 {
     __shared__ ActDigitLds dl;
@@ -403,9 +441,14 @@ __global__ __launch_bounds__(256) void k_prep_rms(ActDev p, uint8_t *__restrict_
     const float *src = part ? p.y : p.x;
     const float *w = part ? p.w2 : p.w;
     const uint64_t ld = part ? p.ldy : p.ldx, kk = k - (part ? segl : 0);
+    const bool gath = GATH && !part;                                // x rows from the embedding matrix
+    uint32_t er[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) er[i] = gath ? p.tok[tr[i]] : 0u;
     float own[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) own[i] = src[(uint64_t)tr[i] * ld + kk];
+    for (int i = 0; i < 4; i++)
+        own[i] = gath ? embd_iq4(p.embd, segl, p.embd_ne1, er[i], kk) : src[(uint64_t)tr[i] * ld + kk];
     const float wk = w[kk];
     float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (uint64_t j0 = e; j0 < segl / 4; j0 += 5 * 256) {
@@ -415,8 +458,10 @@ __global__ __launch_bounds__(256) void k_prep_rms(ActDev p, uint8_t *__restrict_
             const uint64_t j = j0 + (uint64_t)u * 256;
 #pragma unroll
             for (int i = 0; i < 4; i++)
-                q[u][i] = (i < nt && j < segl / 4) ? ((const float4 *)(src + (uint64_t)(4 * a + i) * ld))[j]
-                                                  : make_float4(0, 0, 0, 0);
+                q[u][i] = (i < nt && j < segl / 4)
+                              ? (gath ? embd_iq4x4(p.embd, segl, p.embd_ne1, er[i], 4 * j)
+                                      : ((const float4 *)(src + (uint64_t)(4 * a + i) * ld))[j])
+                              : make_float4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int u = 0; u < 5; u++)
@@ -472,10 +517,12 @@ __global__ __launch_bounds__(256) void k_prep_tok(ActDev p, uint8_t *__restrict_
     const int sb = blockIdx.x, t = blockIdx.y, a = t >> 2, i = t & 3;
     const uint32_t k = (uint32_t)sb * 256 + e;
     float v, ss = 0.0f;
-    if (KIND == ACT_RMS_DEFER) {
+    constexpr bool RMS = KIND == ACT_RMS_DEFER || KIND == ACT_RMS_EMBD;
+    if (RMS) {
         // x_eff = x + (p_0 + p_1 + ...) over the NP partial planes, written back to xnew;
         // v = x_eff * w, and the super-block's sum of x_eff^2 for the GEMV's row factor
-        const float xr = (p.x + (uint64_t)t * p.ldx)[k];
+        const float xr = KIND == ACT_RMS_EMBD ? embd_iq4(p.embd, (uint64_t)p.nsb * 256, p.embd_ne1, p.tok[t], k)
+                                              : (p.x + (uint64_t)t * p.ldx)[k];
         float pr[NP > 0 ? NP : 1];
 #pragma unroll
         for (int q = 0; q < NP; q++) pr[q] = (p.part + (uint64_t)q * p.pstride + (uint64_t)t * p.ldp)[k];
@@ -514,10 +561,10 @@ __global__ __launch_bounds__(256) void k_prep_tok(ActDev p, uint8_t *__restrict_
     const float mw = wave_max64(fabsf(v));
     if (lane == 0) {
         mxw[wv] = mw;
-        if (KIND == ACT_RMS_DEFER) ssw[wv] = ss;
+        if (RMS) ssw[wv] = ss;
     }
     __syncthreads();
-    if (KIND == ACT_RMS_DEFER && e == 0) p.rss[(uint64_t)t * p.nsb + sb] = (ssw[0] + ssw[1]) + (ssw[2] + ssw[3]);
+    if (RMS && e == 0) p.rss[(uint64_t)t * p.nsb + sb] = (ssw[0] + ssw[1]) + (ssw[2] + ssw[3]);
     if (!p.digits) return;                                       // fp32 rows only (VALU formats)
     // shift puts the super-block maximum just under 2^22 (0 for an all-zero or non-finite maximum)
     const float mx = fmaxf(fmaxf(mxw[0], mxw[1]), fmaxf(mxw[2], mxw[3]));
@@ -1178,26 +1225,35 @@ static int prep_act(const GemvExec &ex, const qgpu_act *act, int n, uint64_t ne0
                     bool *deferred = nullptr)
 {
     if (deferred) *deferred = false;
-    if (!act || !act->x || n < 1 || n > QGPU_MAX_B) return QGPU_E_ARG;
+    if (!act || (!act->x && !act->embd) || n < 1 || n > QGPU_MAX_B) return QGPU_E_ARG;
     if (ne0 % 256 || (digits && ne0 > MAX_K)) return QGPU_E_RANGE;
     ActDev d = {};
     d.x = act->x; d.y = act->y; d.w = act->w; d.w2 = act->w2; d.xout = act->xout;
     d.ldx = act->ldx; d.ldy = act->ldy; d.ldxo = act->ldxo; d.eps = act->eps; d.ntok = n; d.digits = digits;
     const bool rows = n > 1;
     const bool single = act->kind == QGPU_ACT_RMSNORM && (!act->seg || act->seg == ne0);
+    const bool gath = act->embd != nullptr;
+    if (gath) {                          // x gathered from embedding rows (RMSNORM, the first segment)
+        const qgpu_tensor *Em = act->embd;
+        if (act->kind != QGPU_ACT_RMSNORM || !act->tok || Em->type != T_IQ4_XS || !Em->packed || act->n_part ||
+            Em->ne0 != (single ? ne0 : act->seg))
+            return QGPU_E_ARG;
+        d.embd = (const uint8_t *)Em->data; d.tok = act->tok; d.embd_ne1 = Em->ne1;
+    }
     if (act->n_part < 0 || act->n_part > 8) return QGPU_E_ARG;
     if ((act->n_part || act->xnew) && !(single && defer)) return QGPU_E_ARG;   // deferred RMSNORM only
     if (act->n_part && (!act->part || (rows && act->ldp < ne0))) return QGPU_E_ARG;
     if (act->xnew && rows && act->ldxn < ne0) return QGPU_E_ARG;
     if (single && defer) {
-        if (!act->w || (rows && act->ldx < ne0) || (act->xout && rows && act->ldxo < ne0)) return QGPU_E_ARG;
+        if (!act->w || (!gath && rows && act->ldx < ne0) || (act->xout && rows && act->ldxo < ne0)) return QGPU_E_ARG;
         d.part = act->part; d.ldp = act->ldp; d.pstride = (uint64_t)n * act->ldp; d.n_part = act->n_part;
         d.xnew = act->xnew; d.ldxn = act->ldxn; d.rss = ws_rss(ex); d.nsb = (int)(ne0 / 256);
         const dim3 grid((unsigned)(ne0 / 256), (unsigned)n);
         uint8_t *A = ex.ws;
         float *xs = (float *)(ex.ws + 2 * PLANE_BYTES);
 #define PT_NP(NP_) case NP_: hipLaunchKernelGGL((k_prep_tok<ACT_RMS_DEFER, NP_>), grid, dim3(256), 0, ex.st, d, A, xs); break
-        switch (act->n_part) {
+        if (gath) hipLaunchKernelGGL((k_prep_tok<ACT_RMS_EMBD, 0>), grid, dim3(256), 0, ex.st, d, A, xs);
+        else switch (act->n_part) {
         PT_NP(0); PT_NP(1); PT_NP(2); PT_NP(3); PT_NP(4); PT_NP(5); PT_NP(6); PT_NP(7); default: PT_NP(8);
         }
 #undef PT_NP
@@ -1215,7 +1271,7 @@ static int prep_act(const GemvExec &ex, const qgpu_act *act, int n, uint64_t ne0
         if (d.seg != ne0 && (!act->y || !act->w2 || (rows && act->ldy < d.seg) || act->ldy % 4 ||
                              ((uintptr_t)act->y & 15)))
             return QGPU_E_ARG;
-        if (act->ldx % 4 || ((uintptr_t)act->x & 15)) return QGPU_E_ARG;   // float4 row sums
+        if (!gath && (act->ldx % 4 || ((uintptr_t)act->x & 15))) return QGPU_E_ARG;   // float4 row sums
         wx = d.seg;
         break;
     }
@@ -1229,14 +1285,17 @@ static int prep_act(const GemvExec &ex, const qgpu_act *act, int n, uint64_t ne0
         break;
     default: return QGPU_E_ARG;
     }
-    if (rows && act->ldx < wx) return QGPU_E_ARG;
+    if (!gath && rows && act->ldx < wx) return QGPU_E_ARG;
     const dim3 grid((unsigned)(ne0 / 256), (unsigned)n);                  // one token per block
     uint8_t *A = ex.ws;
     float *xs = (float *)(ex.ws + 2 * PLANE_BYTES);
     switch (act->kind) {
     case QGPU_ACT_COPY: hipLaunchKernelGGL((k_prep_tok<QGPU_ACT_COPY, 0>), grid, dim3(256), 0, ex.st, d, A, xs); break;
     case QGPU_ACT_RMSNORM:                                                     // four tokens per block
-        hipLaunchKernelGGL(k_prep_rms, dim3((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1)), dim3(256), 0, ex.st, d, A, xs);
+        if (gath)
+            hipLaunchKernelGGL(k_prep_rms<true>, dim3((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1)), dim3(256), 0, ex.st, d, A, xs);
+        else
+            hipLaunchKernelGGL(k_prep_rms<false>, dim3((unsigned)(ne0 / 256), (unsigned)(n > 4 ? 2 : 1)), dim3(256), 0, ex.st, d, A, xs);
         break;
     case QGPU_ACT_SILU_MUL: hipLaunchKernelGGL((k_prep_tok<QGPU_ACT_SILU_MUL, 0>), grid, dim3(256), 0, ex.st, d, A, xs); break;
     default: hipLaunchKernelGGL((k_prep_tok<QGPU_ACT_GATED_NORM, 0>), grid, dim3(256), 0, ex.st, d, A, xs); break;

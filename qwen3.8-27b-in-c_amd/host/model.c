@@ -42,6 +42,11 @@ struct qwen_gpu {
     qgpu_tensor *tok_embd, *output, *eh_proj;
     float *out_norm, *enorm, *hnorm, *shnorm, *rope_cos, *rope_sin;
     int *d_pos, *d_cur;
+    /* embedding rows not yet in bx: the first preparation of the forward gathers them from
+     * tok_embd (embd_fuse: packed IQ4_XS, n_embd % 256 == 0) */
+    const uint32_t *pend_tok;
+    uint32_t pend_tok_B;
+    int embd_fuse;
     /* where the kernels of the next forward read the position and the ring slot: constant
      * tables d_posv[p] = p, d_curv[c] = c at host-chosen offsets for eager launches (no launch
      * sets them), or d_pos / d_cur, set before each captured-graph replay (see at()) */
@@ -365,6 +370,13 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
         if (upload_layer(g, src, &m->layers[il], &g->L[il])) return -1;
     if (upload_layer(g, src, &m->mtp_layer, &g->mtp)) return -1;
     if (!(g->tok_embd = up_matrix(g, src, m->tok_embd))) return -1;
+    {   /* the first preparation of a forward gathers the embedding rows itself (packed IQ4_XS) */
+        int t;
+        uint64_t ne0, ne1;
+        const char *ef = getenv("QWEN_EMBD_FUSE");   /* "0": a separate dequant launch, as for other formats */
+        g->embd_fuse = !(ef && ef[0] == '0') && !qgpu_tensor_shape(g->tok_embd, &t, &ne0, &ne1) &&
+                       t == GGML_IQ4_XS && ne0 % 256 == 0 && ne0 <= 64 * 256;
+    }
     g->output = (m->output == m->tok_embd) ? g->tok_embd : up_matrix(g, src, m->output);
     if (!g->output || !(g->eh_proj = up_matrix(g, src, m->mtp_eh_proj)) ||
         !(g->out_norm = up_f32(g, src, m->output_norm)) || !(g->enorm = up_f32(g, src, m->mtp_enorm)) ||
@@ -544,8 +556,12 @@ static qgpu_act act_norm(const float *x, uint64_t ldx, const float *w, float eps
 static void materialize(qwen_model_t *m)
 {
     qwen_gpu_t *g = m->gpu;
-    if (!g->pend_ks) return;
     const uint64_t E = m->dims.n_embd;
+    if (g->pend_tok) {
+        K(qgpu_dequant_rows(g->tok_embd, g->pend_tok, (int)g->pend_tok_B, g->bx, E));
+        g->pend_tok = NULL;
+    }
+    if (!g->pend_ks) return;
     K(qgpu_add_partials(g->pend, E, g->pend, E, g->part, E, g->pend_ks, E, (int)g->pend_B));
     g->pend_ks = 0;
     g->pend = NULL;
@@ -557,8 +573,12 @@ static qgpu_act act_norm_res(qwen_model_t *m, float *R, const float *w, float *x
 {
     qwen_gpu_t *g = m->gpu;
     const uint64_t E = m->dims.n_embd;
-    if (g->pend_ks && g->pend != R) materialize(m);
+    if ((g->pend_ks && g->pend != R) || (g->pend_tok && R != g->bx)) materialize(m);
     qgpu_act a = act_norm(R, E, w, m->cfg.rms_norm_eps, xout, E);
+    if (g->pend_tok) {   /* the embedding rows: gathered by this preparation, which writes them to R */
+        a.x = NULL; a.embd = g->tok_embd; a.tok = g->pend_tok; a.xnew = R; a.ldxn = E;
+        g->pend_tok = NULL;
+    }
     if (g->pend_ks) {
         a.part = g->part; a.ldp = E; a.n_part = g->pend_ks; a.xnew = R; a.ldxn = E;
         g->pend_ks = 0;
@@ -771,17 +791,23 @@ static void forward_body(qwen_model_t *m, const uint32_t *d_tokens, const float 
     const qwen_dims_t *d = &m->dims;
     const uint64_t E = d->n_embd, V = m->cfg.vocab_size;
     prof_mark(g, 0);
-    K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bx, E));
+    if (g->embd_fuse) { g->pend_tok = d_tokens; g->pend_tok_B = B; }    /* the first preparation reads them */
+    else K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bx, E));
     prof_mark(g, 1);
     for (uint32_t il = 0; il < d->n_layer; il++) {
         if (g->L[il].rec) gdn_dev(m, &g->L[il], B);
         else attn_dev(m, &g->L[il], g->bx, B, 0);
         prof_mark(g, 2 + il);
     }
-    const qgpu_act an = act_norm_res(m, g->bx, g->out_norm, g->bxb);
+    qgpu_act an = act_norm_res(m, g->bx, g->out_norm, g->bxb);
+    /* when the last residual add is still pending (partial planes), its preparation writes the
+     * final hidden states straight into h_save; bx then lacks those planes, and nothing reads
+     * it before the next forward's embedding overwrites it */
+    const int direct = save_h && an.n_part;
+    if (direct) an.xnew = g->h_save;
     K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
     prof_mark(g, 2 + d->n_layer);
-    if (save_h) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
+    if (save_h && !direct) K(qgpu_copy(g->h_save, g->bx, B * E * sizeof(float)));
 }
 
 /* Where the kernels of the next launch sequence read the position and the ring slot.
@@ -843,10 +869,12 @@ static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, 
     qwen_gpu_t *g = m->gpu;
     const uint64_t E = m->dims.n_embd, V = m->cfg.vocab_size;
     const float eps = m->cfg.rms_norm_eps;
-    K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bxb, E));
-    /* eh_proj(concat(enorm(e), hnorm(h))) (model.c:1044-1052): both norms in the input preparation */
+    /* eh_proj(concat(enorm(e), hnorm(h))) (model.c:1044-1052): both norms in the input preparation,
+     * which also gathers the embedding rows when it can */
+    if (!g->embd_fuse) K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bxb, E));
     qgpu_act cat = act_norm(g->bxb, E, g->enorm, eps, g->cat, 2 * E);
     cat.y = h; cat.ldy = E; cat.w2 = g->hnorm; cat.seg = E;
+    if (g->embd_fuse) { cat.x = NULL; cat.embd = g->tok_embd; cat.tok = d_tokens; }
     K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->eh_proj, 1, &cat, (int)B, &g->mx, &E, 0));
     attn_dev(m, &g->mtp, g->mx, B, 0);
     if (d_logits) {

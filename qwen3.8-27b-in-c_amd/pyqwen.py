@@ -37,7 +37,8 @@ class Act(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_int), ("x", F32P), ("ldx", ctypes.c_uint64), ("y", F32P), ("ldy", ctypes.c_uint64),
                 ("w", F32P), ("w2", F32P), ("seg", ctypes.c_uint64), ("eps", ctypes.c_float), ("xout", F32P),
                 ("ldxo", ctypes.c_uint64), ("part", F32P), ("ldp", ctypes.c_uint64), ("n_part", ctypes.c_int),
-                ("xnew", F32P), ("ldxn", ctypes.c_uint64)]
+                ("xnew", F32P), ("ldxn", ctypes.c_uint64), ("embd", ctypes.c_void_p),
+                ("tok", ctypes.POINTER(ctypes.c_uint32))]
 
 
 ACT_COPY, ACT_RMSNORM, ACT_SILU_MUL, ACT_GATED_NORM = 0, 1, 2, 3

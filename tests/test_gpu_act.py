@@ -252,3 +252,62 @@ def test_act_batch_ks_planes(gpu, B):
     assert gpu.L.qgpu_gemv_act_batch_ks(Wf_s, 1, ctypes.byref(a), B, (pyqwen.F32P * 1)(split[2].f32()),
                                         (ctypes.c_uint64 * 1)(48), (ctypes.c_int * 1)(2)) != 0
     gpu.sync()
+
+
+@pytest.mark.parametrize("form", ["single", "two_segment"])
+@pytest.mark.parametrize("B", [1, 4, 8])
+def test_rmsnorm_embedding_gather(gpu, form, B):
+    """RMSNorm whose rows are gathered from a packed IQ4_XS embedding (embd, tok) gives the bits of
+    qgpu_dequant_rows followed by the same transform: GEMV outputs, xout, and (single segment, the
+    first preparation of a forward) the rows written to xnew; an id past the last row is a zero row."""
+    print(f"\n[embd-gather] {form} B={B}", flush=True)
+    host = host_lib()
+    E, V, n_out = 1024, 300, 384
+    Te = gpu.tensor(host.synth_matrix(23, E, V, 41, 7, 0.5), 23, E, V)
+    ne0 = E if form == "single" else 2 * E
+    Tn = gpu.tensor(host.synth_matrix(23, ne0, n_out, 42, 8, 0.02), 23, ne0, n_out)
+    rng = np.random.default_rng(B)
+    tok = rng.integers(0, V, B).astype(np.uint32)
+    if B > 1:
+        tok[-1] = V + 5
+    tb = gpu.put(tok)
+    xr = gpu.buf(B * E * 4)
+    gpu.ok(gpu.L.qgpu_dequant_rows(Te.h, tb.u32(), B, xr.f32(), E))
+    w = (1 + 0.1 * rng.standard_normal(E)).astype(np.float32)
+    w2 = (1 + 0.1 * rng.standard_normal(E)).astype(np.float32)
+    h = rng.standard_normal((B, E)).astype(np.float32)
+    wb, w2b, hb = gpu.put(w), gpu.put(w2), gpu.put(h)
+
+    def call(gather):
+        a = pyqwen.Act()
+        a.kind, a.ldx, a.w, a.eps = pyqwen.ACT_RMSNORM, E, wb.f32(), EPS
+        if gather:
+            a.embd, a.tok = Te.h, tb.u32()
+        else:
+            a.x = xr.f32()
+        if form == "two_segment":
+            a.y, a.ldy, a.w2, a.seg = hb.f32(), E, w2b.f32(), E
+        xo, ob = gpu.buf(B * ne0 * 4), gpu.buf(B * n_out * 4)
+        a.xout, a.ldxo = xo.f32(), ne0
+        xn = gpu.buf(B * E * 4)
+        if form == "single":
+            a.xnew, a.ldxn = xn.f32(), E
+        gpu.ok(gpu.L.qgpu_gemv_act_batch((ctypes.c_void_p * 1)(Tn.h), 1, ctypes.byref(a), B,
+                                         (pyqwen.F32P * 1)(ob.f32()), (ctypes.c_uint64 * 1)(n_out), 0))
+        return ob.download(np.float32), xo.download(np.float32), xn.download(np.float32)
+
+    plain, gath = call(False), call(True)
+    assert np.array_equal(gath[0], plain[0]) and np.array_equal(gath[1], plain[1])
+    rows = xr.download(np.float32).reshape(B, E)
+    if form == "single":
+        assert np.array_equal(gath[2].reshape(B, E), rows)
+    if B > 1:
+        assert not rows[-1].any()
+    assert np.isfinite(plain[0]).all() and np.abs(plain[0]).max() > 0
+    if form == "two_segment":        # an embedding narrower than the single-segment row: rejected
+        a = pyqwen.Act()
+        a.kind, a.w, a.eps, a.embd, a.tok = pyqwen.ACT_RMSNORM, wb.f32(), EPS, Te.h, tb.u32()
+        assert gpu.L.qgpu_gemv_act_batch((ctypes.c_void_p * 1)(Tn.h), 1, ctypes.byref(a), B,
+                                         (pyqwen.F32P * 1)(gpu.buf(B * n_out * 4).f32()),
+                                         (ctypes.c_uint64 * 1)(n_out), 0) != 0
+    gpu.sync()
