@@ -235,7 +235,8 @@ DIGITS = 3                                      # activation digit bytes per ele
 
 def prep_kind(k):
     """(transform kind, partial planes or None) of a preparation kernel name: k_prep_tok<KIND, NP>
-    (one token per block) or the older k_prep_act<KIND>; kinds 2 SiLU x up, 3 gated norm, 4 RMSNorm"""
+    (one token per block) or the older k_prep_act<KIND>; kinds 2 SiLU x up, 3 gated norm, 4 RMSNorm,
+    5 RMSNorm on gathered embedding rows"""
     m = re.match(r"k_prep_(tok|act)<(\d+)(?:, (\d+))?>", k)
     if not m:
         return None, None
@@ -267,6 +268,9 @@ def step_roles(step, B, P):
         split = k.startswith("k_gemv_mfma") and (k.endswith(", 2>") or k.endswith(", 3>"))
         if k.startswith("k_dequant_rows"):
             role, by = "embedding rows (dequant)", B * IQ4_ROW(d["E"]) + B * d["E"] * f4
+        elif kind == 5:   # the first RMSNorm of a forward on embedding rows it gathers itself
+            role = "RMSNorm prep (embedding rows gathered)"
+            by = B * IQ4_ROW(d["E"]) + d["E"] * f4 + B * d["E"] * (2 * f4 + DIGITS)
         elif kind == 4:
             np_ = n_part if planes is None else planes
             role = "RMSNorm prep (+ residual partials)"
