@@ -609,7 +609,7 @@ def main():
             "metric": METRIC, "value": pick["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(pick["us"] / 1e3, 5), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None,
-            "dtype": "fp32 (IQ4_XS: int8-MFMA digit GEMV; K-quants / Q8_0: fp32 VALU GEMV)",
+            "dtype": "fp32 (IQ4_XS, Q4_K, Q5_K, Q6_K, Q8_0 weights; int8-MFMA digit GEMV, fp32 accumulate)",
             "data": "synthetic (seeded random super-blocks per format, x ~ N(0,1))",
             "config": {"workload": "gemv_batch sweep: 5 formats x 3 shapes x B in {1,2,4,8}", "device": name,
                        "cus": ncu},

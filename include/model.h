@@ -135,7 +135,8 @@ void model_forward_batch(qwen_model_t *m, pool_t *pool, const uint32_t *tokens, 
 int  model_snapshot_states(qwen_model_t *m);             /* no-op, as the reference (model.c:1004) */
 void model_rollback_states(qwen_model_t *m);             /* no-op (model.c:1009) */
 /* recurrent states = state after token b of the last batched forward (model.c:1015-1031);
- * the caller sets m->pos. */
+ * the caller sets m->pos.  b must be below that forward's B (and below 8): otherwise the
+ * call is ignored with a message and qwen_model_status() reports -1. */
 void model_rollback_to(qwen_model_t *m, uint32_t b);
 
 /* Start a new sequence on a loaded model (no reference counterpart: the

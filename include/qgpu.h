@@ -284,8 +284,15 @@ int  qgpu_attn_fused_act(const float *q, uint64_t ldq, const float *k, const flo
                          const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
                          const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
                          int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out, uint64_t ldo);
-/* allocates the attention workspace for ctx_bound positions now (no allocation later) */
+/* allocates the attention workspace for ctx_bound positions now (no allocation later);
+ * QGPU_E_RANGE when the KV cache does not fit the kernels' offsets (qgpu_attn_cache_fits) */
 int  qgpu_attn_reserve(int ctx_bound, int n_kv);
+/* 1 when a KV cache of ctx_bound positions x n_kv heads (head_dim 256, fp32) lies within the
+ * attention kernels' 32-bit buffer offsets (ctx_bound * n_kv * 1024 bytes <= 2^31 - 1), else 0.
+ * The attention calls and qgpu_attn_reserve return QGPU_E_RANGE beyond it; model_init refuses
+ * such an n_ctx.  Arithmetic only: no device work, callable without a GPU.  (No reference
+ * counterpart: the reference's KV cache is host memory with 64-bit indexing.) */
+int  qgpu_attn_cache_fits(int ctx_bound, int n_kv);
 
 /* ------------------------------------------------------------ sampling (sampler.c:62-162) */
 /* sampler_sample on device data: logits[vocab] (the repeat penalty is applied in

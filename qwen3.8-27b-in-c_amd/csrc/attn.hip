@@ -570,11 +570,23 @@ __global__ __launch_bounds__(4 * ATT_HD) void k_attn_combine_act(const float *q,
 // one reservation serves every later context length of that head count.  A
 // larger head count (another model) takes a new buffer; the old one is kept,
 // not freed, because HIP graphs captured earlier hold its address.
+static bool attn_cache_fits(int ctx_bound, int n_kv)
+{
+    return (uint64_t)ctx_bound * (uint64_t)n_kv * ATT_HD * sizeof(float) <= ATT_RECORDS;
+}
+extern "C" int qgpu_attn_cache_fits(int ctx_bound, int n_kv)
+{
+    return ctx_bound >= 1 && n_kv >= 1 && attn_cache_fits(ctx_bound, n_kv);
+}
+
 static void *ws_attn_retired[16];
 static int n_ws_attn_retired = 0;
 
 static int attn_ws(int ctx_bound, int n_kv, int *nspan)
 {
+    // the K/V rows are read through buffer resources at 32-bit offsets from a kv head's row 0,
+    // which reach ctx_bound * n_kv * ATT_HD floats: a cache beyond the resource is rejected
+    if (!attn_cache_fits(ctx_bound, n_kv)) return QGPU_E_RANGE;
     const int nt = (ctx_bound + ATT_TP - 1) / ATT_TP;
     *nspan = nt < ATT_NSPAN ? nt : ATT_NSPAN;
     const size_t need = (size_t)n_kv * ATT_NSPAN * ATT_MAXQ * (2 + ATT_HD) * sizeof(float);

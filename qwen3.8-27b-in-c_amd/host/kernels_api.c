@@ -108,7 +108,12 @@ void gemv_rows_batch(const gguf_tensor_info_t *W, const float *x, uint64_t ldx, 
 {
     const uint64_t rows = W && W->n_dims >= 2 ? W->ne[1] : 1;
     if (!W || r1 <= r0 || n < 1) return;
-    if (n > GEMV_MAX_B || r1 > rows) { fail("gemv (batch above 8 or rows past the matrix)", QGPU_E_ARG); return; }
+    if (n > GEMV_MAX_B || r1 > rows) {
+        /* the rows and tokens the caller's buffer holds within the request are zeroed */
+        fail("gemv (batch above 8 or rows past the matrix)", QGPU_E_ARG);
+        if (out && r0 < rows) zero_out(out, ldo, n < GEMV_MAX_B ? n : GEMV_MAX_B, r0, r1 < rows ? r1 : rows);
+        return;
+    }
     qgpu_tensor *T = weight(W);
     if (!T) { zero_out(out, ldo, n, r0, r1); return; }
     uint64_t ld = 0;
@@ -155,11 +160,11 @@ static void run_rows(int op, float *out, const float *x, const float *w, uint64_
 {
     if (!n) return;
     float *d = dev_buf(2, n * sizeof(float) * 2);
-    if (!d) return;
+    if (!d) { memset(out, 0, n * sizeof(float)); return; }
     float *dw = d + n;
     int rc = qgpu_memcpy_h2d(d, x, n * sizeof(float));
     if (!rc && w) rc = qgpu_memcpy_h2d(dw, w, n * sizeof(float));
-    if (rc) { fail("copy to device", rc); return; }
+    if (rc) { fail("copy to device", rc); memset(out, 0, n * sizeof(float)); return; }
     switch (op) {
     case 0: rc = qgpu_rmsnorm(d, n, d, n, w ? dw : NULL, n, 1, eps); break;
     case 1: rc = qgpu_l2norm(d, n, d, n, n, 1, eps); break;
@@ -168,9 +173,9 @@ static void run_rows(int op, float *out, const float *x, const float *w, uint64_
     case 4: rc = qgpu_softplus(d, n); break;
     default: rc = qgpu_softmax(d, n, n, 1); break;
     }
-    if (rc) { fail("op", rc); return; }
+    if (rc) { fail("op", rc); memset(out, 0, n * sizeof(float)); return; }
     rc = qgpu_memcpy_d2h(out, d, n * sizeof(float));
-    if (rc) fail("copy to host", rc);
+    if (rc) { fail("copy to host", rc); memset(out, 0, n * sizeof(float)); }
 }
 
 void rmsnorm(float *out, const float *x, const float *weight, uint64_t n, float eps) { run_rows(0, out, x, weight, n, eps); }

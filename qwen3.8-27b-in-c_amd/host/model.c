@@ -62,6 +62,7 @@ struct qwen_gpu {
           *mtp_h, *mx, *cat;
     uint64_t SQ, A, conv_elems, ssm_elems, kvrow;
     int cur, cur_base;
+    int last_B;                 /* tokens of the last backbone forward: the states model_rollback_to may select */
     /* K-split residual GEMVs leave partial planes (part, [ks][B][n_embd]) that the
      * next RMSNorm of that residual adds in (or materialize() when none follows) */
     float *part, *pend;
@@ -349,6 +350,11 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
             return -1;
     }
     if (n_ctx < 2) { fprintf(stderr, "model_init: n_ctx must be at least 2\n"); return -1; }
+    if (n_ctx > 0x7FFFFFFFu || !qgpu_attn_cache_fits((int)n_ctx, (int)d->n_kv_head)) {
+        fprintf(stderr, "model_init: n_ctx %u: a KV cache of %u heads is beyond what the attention kernels address "
+                "(%u x %u x 1 KiB > 2 GiB)\n", n_ctx, d->n_kv_head, n_ctx, d->n_kv_head);
+        return -1;
+    }
     m->n_ctx = n_ctx;
     m->pos = 0;
 
@@ -791,7 +797,9 @@ static void forward_body(qwen_model_t *m, const uint32_t *d_tokens, const float 
     const qwen_dims_t *d = &m->dims;
     const uint64_t E = d->n_embd, V = m->cfg.vocab_size;
     prof_mark(g, 0);
-    if (g->embd_fuse) { g->pend_tok = d_tokens; g->pend_tok_B = B; }    /* the first preparation reads them */
+    /* the first preparation gathers the rows itself; a profiled forward keeps the lookup a launch of
+     * its own, so the embedding section times it (the two are bit-identical) */
+    if (g->embd_fuse && !g->prof_active) { g->pend_tok = d_tokens; g->pend_tok_B = B; }
     else K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bx, E));
     prof_mark(g, 1);
     for (uint32_t il = 0; il < d->n_layer; il++) {
@@ -838,6 +846,7 @@ static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, u
     run_body(m, G_FWD, forward_body, d_tokens, NULL, B, d_logits, save_h);
     g->cur_base = g->cur;
     g->cur = (g->cur + (int)B) % NSLOT;
+    g->last_B = (int)B;
 }
 
 static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, uint32_t B, float *d_logits,
@@ -944,6 +953,7 @@ void model_reset(qwen_model_t *m)
         K(qgpu_memset(D->ssm_ring, 0, NSLOT * g->ssm_elems * sizeof(float)));
     }
     g->cur = g->cur_base = 0;
+    g->last_B = 0;
     g->pend_ks = 0;
     g->pend = NULL;
     K(qgpu_set_i32(g->d_cur, 0));
@@ -959,8 +969,14 @@ void model_rollback_states(qwen_model_t *m) { (void)m; }
 void model_rollback_to(qwen_model_t *m, uint32_t b)
 {
     if (call_begin(m)) return;
-    if (b >= SPEC_MAX_B) { reject(m, "model_rollback_to", b, 1); return; }
     qwen_gpu_t *g = m->gpu;
+    /* the ring holds the states after tokens 0..B-1 of the last batch only */
+    if (b >= SPEC_MAX_B || b >= (uint32_t)g->last_B) {
+        fprintf(stderr, "model_rollback_to: state after token %u requested, the last batch had %d token(s); call ignored\n",
+                b, g->last_B);
+        g->status = -1;
+        return;
+    }
     g->cur = (g->cur_base + 1 + (int)b) % NSLOT;   /* the next forward reads it through at() */
     call_end(m);
 }
@@ -1283,19 +1299,19 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
     if (call_begin(m)) return -1;
     if (bad_span(m, m->pos, B) || reps < 1 || !ms_verify || !ms_decode) return reject(m, "model_time_steps", m->pos, B);
     qwen_gpu_t *g = m->gpu;
-    const int cur0 = g->cur, base0 = g->cur_base;
+    const int cur0 = g->cur, base0 = g->cur_base, lastB0 = g->last_B;
     const uint32_t pos = m->pos;
     void *e0, *e1;
     K(qgpu_event_create(&e0));
     K(qgpu_event_create(&e1));
     /* verify: B tokens at pos (states are restored to the ring index after each rep) */
     forward_dev(m, g->d_cand, B, pos, g->logits_b, 1);
-    g->cur = cur0; g->cur_base = base0;
+    g->cur = cur0; g->cur_base = base0; g->last_B = lastB0;
     K(qgpu_event_record(e0));
     for (int r = 0; r < reps; r++) {
         forward_dev(m, g->d_cand, B, pos, g->logits_b, 1);
         K(qgpu_argmax(g->logits_b, m->cfg.vocab_size, m->cfg.vocab_size, (int)B, g->d_vtok));
-        g->cur = cur0; g->cur_base = base0;
+        g->cur = cur0; g->cur_base = base0; g->last_B = lastB0;
     }
     K(qgpu_event_record(e1));
     K(qgpu_event_elapsed_ms(e0, e1, ms_verify));
@@ -1304,7 +1320,7 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
     for (int r = 0; r < reps; r++) {
         forward_dev(m, g->d_cand, 1, pos, g->logits1, 0);
         K(qgpu_argmax(g->logits1, m->cfg.vocab_size, m->cfg.vocab_size, 1, g->d_vtok));
-        g->cur = cur0; g->cur_base = base0;
+        g->cur = cur0; g->cur_base = base0; g->last_B = lastB0;
     }
     K(qgpu_event_record(e1));
     K(qgpu_event_elapsed_ms(e0, e1, ms_decode));
@@ -1327,6 +1343,7 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
     K(qgpu_sync());
     qgpu_event_destroy(e0);
     qgpu_event_destroy(e1);
+    g->last_B = lastB0;
     call_end(m);
     return m->gpu->status;
 }

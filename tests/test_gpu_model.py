@@ -526,6 +526,37 @@ def test_model_rollback_vs_reference(gpu, tiny):
         assert rel_err(lb[b], ref[b]) < 1e-3 and lb[b].argmax() == ref[b].argmax(), b
 
 
+def test_model_rollback_rejects_states_not_written(gpu, tiny):
+    """model_rollback_to(b) selects the state after token b of the last batch: b at or past that
+    batch's B is refused on the host (status -1, ring index unchanged), and a valid rollback after
+    it still gives the reference's logits."""
+    path, z = tiny
+    p = z["prompt"]
+    m = pyqwen.Model(path, int(z["n_ctx"]))
+    for i in range(5):
+        m.forward(int(p[i]), i)
+    m.forward_batch(p[10:13], 5)
+    for b in (3, 7, 8):
+        m.rollback_to(b)
+        assert m.status() == -1, b
+    m.rollback_to(1)
+    assert m.status() == 0
+    m.pos = 8
+    lb = m.forward_batch(p[13:16], 7)
+    ref = z["rollback_logits"].reshape(3, -1)
+    for b in range(3):
+        assert rel_err(lb[b], ref[b]) < 1e-3 and lb[b].argmax() == ref[b].argmax(), b
+    m.forward(int(p[0]), 10)                         # a decode step writes one state
+    m.rollback_to(1)
+    assert m.status() == -1
+    m.rollback_to(0)
+    assert m.status() == 0
+    m.reset()
+    m.rollback_to(0)                                 # nothing written since the reset
+    assert m.status() == -1
+    m.close()
+
+
 @pytest.mark.parametrize("k", [1, 2, 3, 5, 7])
 def test_model_spec_stream_vs_reference(gpu, tiny, k):
     """On-device greedy MTP speculative decode == the reference's spec stream == greedy stream."""
