@@ -72,6 +72,7 @@ HBM_PEAK_GBS = 8000.0
 IQ4 = 23
 METRIC = "accepted tok/s, 27B IQ4_XS MTP k=3 on 1 GPU; gemv_batch HBM GB/s (% peak)"
 ROOF_TILES = 17408 // 16   # 16-row tiles of the roofline GEMV
+MIX_NOTE = "the real checkpoint's format mix: token_embd Q4_K, attn_qkv Q5_K, output Q6_K, nextn.eh_proj Q8_0, the rest IQ4_XS"
 
 
 def roof_kernel(ncu):
@@ -345,9 +346,15 @@ def bench_sweep(gpu, host, steps, warmup):
 
 
 # ---------------------------------------------------------------------------------- model workloads
-def model_file(host, seed, keep_dir=None):
+def spec_27b(host, seed, weights="iq4"):
+    """the seeded 27B hybrid: every 2-D weight IQ4_XS, or (weights "mix") the real checkpoint's
+    format mix: token_embd Q4_K, attn_qkv Q5_K, output Q6_K, nextn.eh_proj Q8_0, the rest IQ4_XS"""
+    return host.spec_27b_mix(seed) if weights == "mix" else host.spec_27b(seed)
+
+
+def model_file(host, seed, keep_dir=None, weights="iq4"):
     """Writes the seeded random-init 27B model as a GGUF file (tmpfs when it fits)."""
-    spec = host.spec_27b(seed)
+    spec = spec_27b(host, seed, weights)
     need = sum(t.nbytes for t in host.tensors(spec)) + (64 << 20)
     for d in ([keep_dir] if keep_dir else []) + ["/dev/shm", tempfile.gettempdir()]:
         try:
@@ -384,9 +391,9 @@ def bench_model(args, gpu, host, roof, gemv_call_gbs):
     K, W, F = args.steps, args.warmup, args.forced_cycles
     path = None
     if not args.no_cpu:
-        path, spec = model_file(host, args.seed)
+        path, spec = model_file(host, args.seed, weights=args.weights)
     else:
-        spec = host.spec_27b(args.seed)
+        spec = spec_27b(host, args.seed, args.weights)
     n_ctx = ((n_prompt + (k + 1) * (W + K + F) + 64 + 255) // 256) * 256
     t = time.time()
     m = pyqwen.Model(path, n_ctx) if path else pyqwen.Model(spec=spec, n_ctx=n_ctx)
@@ -425,9 +432,11 @@ def bench_model(args, gpu, host, roof, gemv_call_gbs):
         "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
         "ms_per_step": round(t_dec / K * 1e3, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32 (IQ4_XS weights; int8-MFMA digit GEMV, fp32 accumulate)",
-        "data": "synthetic: seeded random-init 27B hybrid (IQ4_XS), seeded random-id prompt",
+        "data": "synthetic: seeded random-init 27B hybrid (" + (MIX_NOTE if args.weights == "mix" else "IQ4_XS")
+                + "), seeded random-id prompt",
         "config": {"workload": f"27B hybrid greedy MTP speculative decode, k={k}, {n_prompt}-token prompt, "
                                f"{K} cycles", "k": k, "prompt_tokens": n_prompt, "n_ctx": n_ctx,
+                   "weights": MIX_NOTE if args.weights == "mix" else "every 2-D weight IQ4_XS",
                    "layers": "48 GDN + 16 GQA + MTP", "device": gpu.device_info()[0]},
         "tokens": int(len(toks)), "drafts_accepted": int(st.n_accepted), "drafts": int(st.n_drafts),
         # accepted drafts per timed cycle: j_hist[j] = cycles that accepted j of the k drafts
@@ -488,9 +497,9 @@ def bench_sample(args, gpu, host, roof, gemv_call_gbs):
     K, W, n_prompt = args.steps, args.warmup, args.prompt
     path = None
     if not args.no_cpu:
-        path, spec = model_file(host, args.seed)
+        path, spec = model_file(host, args.seed, weights=args.weights)
     else:
-        spec = host.spec_27b(args.seed)
+        spec = spec_27b(host, args.seed, args.weights)
     n_ctx = ((n_prompt + max(K, W) + 64 + 255) // 256) * 256
     m = pyqwen.Model(path, n_ctx) if path else pyqwen.Model(spec=spec, n_ctx=n_ctx)
     V = m.V
@@ -555,6 +564,9 @@ def main():
     ap.add_argument("--seed", type=int, default=27)
     ap.add_argument("--gemv-steps", type=int, default=200)
     ap.add_argument("--gemv-warmup", type=int, default=20)
+    ap.add_argument("--weights", choices=["iq4", "mix"], default="iq4",
+                    help="model mode: every 2-D weight IQ4_XS (the headline workload) or the real checkpoint's "
+                         "format mix (Q4_K embedding, Q5_K attn_qkv, Q6_K output, Q8_0 eh_proj)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=None)
     ap.add_argument("--copy-calib", action="store_true",

@@ -114,6 +114,14 @@ class HostLib:
         self.L.qwen_synth_spec_27b(ctypes.byref(s), seed)
         return s
 
+    def spec_27b_mix(self, seed):
+        """the 27B hybrid with the real checkpoint's format mix (reference test_batch.c:16-20,
+        test_kernels.c:120-126): token_embd Q4_K, attn_qkv Q5_K, output Q6_K, nextn.eh_proj Q8_0,
+        every other 2-D weight IQ4_XS"""
+        s = self.spec_27b(seed)
+        s.type_embd, s.type_qkv, s.type_output, s.type_eh_proj = 12, 13, 14, 8
+        return s
+
     def write_gguf(self, spec, path):
         if self.L.qwen_synth_write_gguf(ctypes.byref(spec), path.encode()):
             raise OSError(f"writing {path} failed")

@@ -24,6 +24,11 @@ to the inputs and the reference outputs:
                                state after each call, penalised logits
   model_27b.npz              : full-size 27B greedy stream of 256 tokens + top-2 gaps
                                (`python tests/golden/make_golden.py 27b`, ~10 min)
+  model_27b_mix.npz          : the same for the 27B model with the real checkpoint's format mix
+                               (token_embd Q4_K, attn_qkv Q5_K, output Q6_K, eh_proj Q8_0; `... 27bmix`)
+  dropin_27b.npz             : what two of the reference's own programs print on the reference engine
+                               (oracle/_ref/test_forward_cpu, debug_spec2_cpu, test_quant_cpu) for that format-mix 27B
+                               file with the generator's byte-level vocabulary (`... dropin27b`, ~2 min)
 """
 import ctypes
 import hashlib
@@ -263,15 +268,16 @@ SEED_27B = 27            # the benchmark's model seed
 PROMPT_SEED_27B = 20251201
 
 
-def model27b_fixture(host, n_prompt=512, n_gen=256, n_ctx=1024):
+def model27b_fixture(host, n_prompt=512, n_gen=256, n_ctx=1024, mix=False):
     """Full-size random-init 27B: reference greedy stream after a seeded
     random-id prompt, with the top-2 gap of every step (the streams must agree
-    wherever the gap exceeds 1e-2), plus the prefill logits."""
+    wherever the gap exceeds 1e-2), plus the prefill logits.  mix: the real
+    checkpoint's format mix (model_27b_mix.npz)."""
     with tempfile.TemporaryDirectory(dir=os.environ.get("GOLDEN_TMP", None)) as td:
         exe = os.path.join(td, "ref_harness")
         subprocess.check_call(["gcc", "-O2", "-std=c11", f"-I{REF_INC}", os.path.join(HERE, "ref_harness.c"),
                                REF_LIB, f"-Wl,-rpath,{os.path.dirname(REF_LIB)}", "-lm", "-lpthread", "-o", exe])
-        spec = host.spec_27b(SEED_27B)
+        spec = host.spec_27b_mix(SEED_27B) if mix else host.spec_27b(SEED_27B)
         path = os.path.join(td, "m27.gguf")
         host.write_gguf(spec, path)
         V = spec.vocab
@@ -282,18 +288,57 @@ def model27b_fixture(host, n_prompt=512, n_gen=256, n_ctx=1024):
         os.makedirs(outd)
         subprocess.check_call([exe, path, outd, str(n_ctx), "greedy", pf, str(n_gen)])
         # fingerprint of the generated weights: sha256 of a few tensors' bytes
-        names = [b"blk.0.attn_qkv.weight", b"blk.3.attn_q.weight", b"blk.63.ffn_down.weight", b"output.weight"]
+        names = [b"blk.0.attn_qkv.weight", b"blk.3.attn_q.weight", b"blk.63.ffn_down.weight", b"output.weight",
+                 b"token_embd.weight", b"blk.64.nextn.eh_proj.weight"] if mix else \
+            [b"blk.0.attn_qkv.weight", b"blk.3.attn_q.weight", b"blk.63.ffn_down.weight", b"output.weight"]
         ts = host.tensors(spec)
         fp = {}
         for i, t in enumerate(ts):
             if t.name in names:
                 fp[t.name.decode()] = hashlib.sha256(host.fill(spec, i, t.nbytes).tobytes()).hexdigest()
-        np.savez(os.path.join(HERE, "model_27b.npz"), seed=np.uint64(SEED_27B), prompt=prompt,
+        np.savez(os.path.join(HERE, "model_27b_mix.npz" if mix else "model_27b.npz"), seed=np.uint64(SEED_27B),
+                 prompt=prompt,
                  n_ctx=np.int32(n_ctx), stream=np.fromfile(os.path.join(outd, "stream.u32"), np.uint32),
                  gap=np.fromfile(os.path.join(outd, "gap.f32"), np.float32),
                  prefill_logits=np.fromfile(os.path.join(outd, "prefill_logits.f32"), np.float32),
                  fingerprint=np.array(json.dumps(fp)))
         print("27b fixture", fp)
+
+
+def file_digest(path, span=32 << 20):
+    """sha256 of a file's first and last `span` bytes (the GGUF header, metadata and vocabulary
+    lie at the start; a full hash of 14.5 GB would take longer than the programs it checks)"""
+    h = hashlib.sha256()
+    size = os.path.getsize(path)
+    with open(path, "rb") as f:
+        h.update(f.read(span))
+        f.seek(max(0, size - span))
+        h.update(f.read(span))
+    h.update(str(size).encode())
+    return h.hexdigest()
+
+
+def dropin27b_fixture(host):
+    """The reference's test_forward.c and debug_spec2.c, compiled on the reference engine, on the
+    seeded 27B file carrying the generator's byte-level vocabulary: their printed output is what
+    the same programs linked with libqwen.so must print on the GPU."""
+    with tempfile.TemporaryDirectory(dir=os.environ.get("GOLDEN_TMP", None)) as td:
+        spec = host.spec_27b_mix(SEED_27B)
+        spec.tokenizer = 1
+        path = os.path.join(td, "m27_mix_tok.gguf")
+        host.write_gguf(spec, path)
+        out = {}
+        for prog in ("test_forward", "debug_spec2", "test_quant"):
+            exe = os.path.join(ROOT, "oracle", "_ref", f"{prog}_cpu")
+            # (test_quant exits 1 on this file: its plausibility rule |mean| < 0.5 does not hold for the
+            # generator's ssm_a; the output is what is compared)
+            out[prog] = subprocess.run([exe, path], capture_output=True, text=True, check=prog != "test_quant",
+                                       cwd=td).stdout
+        np.savez(os.path.join(HERE, "dropin_27b.npz"), seed=np.uint64(SEED_27B), digest=np.array(file_digest(path)),
+                 test_forward=np.array(out["test_forward"]), debug_spec2=np.array(out["debug_spec2"]),
+                 test_quant=np.array(out["test_quant"]))
+        print(out["test_forward"])
+        print(out["debug_spec2"])
 
 
 def main():
@@ -316,6 +361,10 @@ def main():
         long_fixtures(host)
     if "27b" in which:
         model27b_fixture(host)
+    if "27bmix" in which:
+        model27b_fixture(host, mix=True)
+    if "dropin27b" in which:
+        dropin27b_fixture(host)
 
 
 if __name__ == "__main__":

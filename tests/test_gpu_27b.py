@@ -1,7 +1,9 @@
-"""Full-size parity: the seeded random-init 27B hybrid (64 layers + MTP, all
-IQ4_XS, generated on the box from the same seed as the fixture) against the
-reference engine's own run on the same weights (tests/golden/model_27b.npz,
-made by make_golden.py from the compiled reference):
+"""Full-size parity: the seeded random-init 27B hybrid (64 layers + MTP,
+generated on the box from the same seed as the fixture) against the reference
+engine's own run on the same weights, in two weight layouts: all IQ4_XS
+(tests/golden/model_27b.npz) and the real checkpoint's format mix, token_embd
+Q4_K, attn_qkv Q5_K, output Q6_K, nextn.eh_proj Q8_0 (model_27b_mix.npz); both
+made by make_golden.py from the compiled reference:
   * the logits of the last prompt token after a 512-token prefill, within 1e-3;
   * the 256-token greedy stream (device greedy decode, and the device MTP
     speculative loop at k = 3) identical to the reference's wherever the
@@ -19,23 +21,23 @@ from gpu_util import gpu, rel_err  # noqa: F401
 from qwen_pkg import host_lib, pyqwen
 
 pytestmark = pytest.mark.gpu
-FIX = os.path.join(O.GOLDEN, "model_27b.npz")
 
 
-@pytest.fixture(scope="module")
-def m27():
-    if not os.path.exists(FIX):
-        pytest.skip("model_27b.npz fixture absent")
-    z = np.load(FIX, allow_pickle=False)
+@pytest.fixture(scope="module", params=["model_27b.npz", "model_27b_mix.npz"])
+def m27(request):
+    fix = os.path.join(O.GOLDEN, request.param)
+    if not os.path.exists(fix):
+        pytest.skip(f"{request.param} fixture absent")
+    z = np.load(fix, allow_pickle=False)
     host = host_lib()
-    spec = host.spec_27b(int(z["seed"]))
+    spec = (host.spec_27b_mix if "mix" in request.param else host.spec_27b)(int(z["seed"]))
     # the generator must reproduce the fixture's weights byte for byte
     fp = json.loads(str(z["fingerprint"]))
     for i, t in enumerate(host.tensors(spec)):
         name = t.name.decode()
         if name in fp:
             assert hashlib.sha256(host.fill(spec, i, t.nbytes).tobytes()).hexdigest() == fp[name], name
-    print("\n[27b] building the model on the GPU", flush=True)
+    print(f"\n[27b] building the model of {request.param} on the GPU", flush=True)
     m = pyqwen.Model(spec=spec, n_ctx=int(z["n_ctx"]))
     yield m, z
     m.close()

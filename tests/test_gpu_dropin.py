@@ -2,9 +2,10 @@
 was compiled unchanged from the reference's src/ against include/ (oracle's
 Makefile, into oracle/_ref/dropin/), so what it checks is this library behind
 the reference's API.  The programs a small model can drive run here; the ones
-that need the full vocabulary or tensor names of the 27B file (test_forward,
-test_forward_batch, test_quant, test_kernels) and the tokenizer tools only
-build (tests/test_dropin_build.py).
+that need the 27B file's vocabulary size or tensor names (test_forward,
+test_forward_batch, test_quant, test_kernels, debug_rollback, debug_spec2) run
+on a full-size file in tests/test_gpu_dropin_27b.py; every program builds in
+tests/test_dropin_build.py.
   * test_ops: the reference's known-answer and dimension checks of rmsnorm,
     l2norm, silu, sigmoid, softplus and softmax (kernels.h on host buffers);
   * test_batch: gemv_batch(n) bit-identical to n single-token gemv calls, on
