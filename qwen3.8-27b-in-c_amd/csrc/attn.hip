@@ -66,19 +66,21 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_prep(float *q, uint64_t ldq, co
 // DW = 256 / NW (NW = 8, DW = 32 in every launch).
 // It serves every query row of the group, r = b * per + (h - g*per) < QH =
 // per * B, as NRT row tiles of 16.
-//   * Scores, per tile and row tile: S^T (16 positions x 16 rows) = K Q^T with
-//     v_mfma_f32_16x16x4_f32, lane l supplying K[pos l%16][d] and Q[row l%16][d]
-//     for d = DW w + 16q + 4(l/16) + j (any order of the d sum is the same dot
-//     product).  Each wave writes its partial tile to LDS.
+//   * Scores, per tile and row tile: S^T (16 positions x 16 rows) = K Q^T as three
+//     fp16 split products (hi hi + hi lo + lo hi, v_mfma_f32_16x16x32_f16), lane l
+//     supplying K[pos l%16][d] and Q[row l%16][d] for its 8 dims d = DW w + 16q +
+//     4(l/16) + j, q < 2, j < 4 (any order of the d sum is the same dot product).
+//     Each wave writes its partial tile to LDS.
 //   * Softmax: the rows are cut into units of 4 (16 positions each: one value per
 //     lane); the wave that owns a unit sums the NW partial scores in wave order,
 //     keeps the running max and sum of its rows (scores in log2 units, exp2), and
 //     writes the probabilities and the rows' rescale factors to LDS.
-//   * P.V: the probabilities come back in the score accumulator's layout (lane l,
-//     register v: position 4(l/16) + v, row l%16), the A operand of P.V: MFMA step
-//     v takes positions {v, 4+v, 8+v, 12+v}; lane l supplies V[that position][DW w
-//     + NQ (l%16) + c] for output tile c.  O accumulates in fp32 registers (lane l,
-//     register r: row 4(l/16) + r).
+//   * P.V: the probabilities come back as bf16 hi and lo parts in the score
+//     accumulator's layout (lane l: positions 4(l/16) .. 4(l/16) + 3, row l%16), the
+//     A operand of a 16-position product (three bf16 split products,
+//     v_mfma_f32_16x16x16_bf16); lane l supplies V[those positions][DW w + NQ (l%16)
+//     + c] for output tile c.  O accumulates in fp32 registers (lane l, register r:
+//     row 4(l/16) + r).
 //   * Step t: loads of tile t + 2, the softmax of tile t beside the scores of tile
 //     t + 1, one barrier, P.V of tile t (a ring of three K/V register slots).
 //   FUSED = 1: the block also applies the per-head q/k RMSNorm and RoPE
@@ -105,7 +107,8 @@ static_assert(ATT_OOB >= ATT_RECORDS, "dead K/V loads must fall outside the buff
 #define ATT_NW3 8             // waves of the three-row-tile span kernel
 #endif
 #ifndef ATT_MINTPS
-#define ATT_MINTPS 1          // tiles per span at least
+#define ATT_MINTPS 2          // tiles per span at least (800 positions, B = 4 / 8: 15.4 / 20.2 -> 14.4 / 17.8 us
+                              // per call against 1; 4: 15.2 / 18.7 us)
 #endif
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -136,9 +139,74 @@ static __device__ __forceinline__ void span_split(int pos0, int B, int nspan, in
     nsl = (ntl + tps - 1) / tps;
 }
 
-static __device__ __forceinline__ v4f mfma4(float a, float b, v4f c)
+// Split-precision products on the half-precision matrix cores.  An fp32 operand x is held as
+// hi + lo, hi = x rounded to the narrow type, lo = (x - hi) rounded (x - hi is exact in fp32);
+// a product a b is summed as a_hi b_hi + a_hi b_lo + a_lo b_hi in fp32 accumulators (the
+// dropped a_lo b_lo and the two roundings are below 2^-2p relative for a p-bit significand).
+//   fp16 (p = 11): |x - hi - lo| <= 2^-22 |x|, range |x| < 65504: the q and k rows, which are
+//                  RMS-normalised (|x| <= sqrt(head_dim) * |norm weight|);
+//   bf16 (p = 8):  2^-16 |x|, the fp32 range: the probabilities and the v rows (unbounded).
+// v_mfma_f32_16x16x32_f16 does 16 x 16 x 32 multiply-adds in 16 cycles and
+// v_mfma_f32_16x16x16_bf16 16 x 16 x 16 in 8, against 16 x 16 x 4 in 32 for the fp32 form: the
+// three products cost 5.3x fewer matrix-core cycles than one fp32 product.
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __bf16 v4b __attribute__((ext_vector_type(4)));
+struct SplitH { v8h hi, lo; };
+struct SplitB { v4s hi, lo; };
+// two values: one packed convert for hi, its two halves widened back exactly, one packed convert
+// of the differences for lo: 6 instructions per pair
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+static __device__ __forceinline__ void split_h2(float x0, float x1, v2h &hi, v2h &lo)
 {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    hi = __builtin_convertvector((v2f{x0, x1}), v2h);
+    const v2f w = __builtin_convertvector(hi, v2f);
+    lo = __builtin_convertvector((v2f{x0 - w[0], x1 - w[1]}), v2h);
+}
+static __device__ __forceinline__ SplitH split_h8(v4f x0, v4f x1)
+{
+    SplitH r;
+    v2h h[4], l[4];
+    split_h2(x0[0], x0[1], h[0], l[0]);
+    split_h2(x0[2], x0[3], h[1], l[1]);
+    split_h2(x1[0], x1[1], h[2], l[2]);
+    split_h2(x1[2], x1[3], h[3], l[3]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        r.hi[2 * i] = h[i][0]; r.hi[2 * i + 1] = h[i][1];
+        r.lo[2 * i] = l[i][0]; r.lo[2 * i + 1] = l[i][1];
+    }
+    return r;
+}
+// two values: hi = the pair rounded to bf16 (one packed convert), widened back exactly by a shift
+// and a mask, lo = the rounded differences (one packed convert): 6 instructions per pair
+typedef __bf16 v2b __attribute__((ext_vector_type(2)));
+static __device__ __forceinline__ void split_b2(float x0, float x1, uint32_t &hi, uint32_t &lo)
+{
+    v2f x = {x0, x1};
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(x, v2b));
+    const float d0 = x0 - __builtin_bit_cast(float, hi << 16), d1 = x1 - __builtin_bit_cast(float, hi & 0xFFFF0000u);
+    v2f d = {d0, d1};
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(d, v2b));
+}
+static __device__ __forceinline__ SplitB split_b4(float x0, float x1, float x2, float x3)
+{
+    uint32_t h0, l0, h1, l1;
+    split_b2(x0, x1, h0, l0);
+    split_b2(x2, x3, h1, l1);
+    return SplitB{ __builtin_bit_cast(v4s, make_uint2(h0, h1)), __builtin_bit_cast(v4s, make_uint2(l0, l1)) };
+}
+static __device__ __forceinline__ v4f mfma_split_h(const SplitH &a, const SplitH &b, v4f c)
+{
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.lo, b.hi, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.hi, b.lo, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a.hi, b.hi, c, 0, 0, 0);
+}
+static __device__ __forceinline__ v4f mfma_split_b(const SplitB &a, const SplitB &b, v4f c)
+{
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.lo, b.hi, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.hi, b.lo, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.hi, b.hi, c, 0, 0, 0);
 }
 
 template <int FUSED, int NRT, int ATT_NWV>
@@ -147,12 +215,17 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     constexpr int ATT_DW = ATT_HD / ATT_NWV;      // head dims per wave
     constexpr int ATT_NQ = ATT_DW / 16;           // float4 operand loads per row and 16-dim output tiles per wave
     typedef typename VSlice<ATT_NQ>::T vqf;
-    constexpr int SXF = 2 * ATT_NWV * NRT * 64 * 4;               // floats of the score exchange
+    // score exchange: per (buffer, wave, row tile) the 64 lanes' v4f, one 16-byte pad after every 16
+    // lanes (68 slots), so the 16 lanes of a softmax row (4 lane groups, same n) read distinct banks
+    constexpr int SXS = 68;                                        // v4f slots per (buffer, wave, row tile)
+    constexpr int SXF = 2 * ATT_NWV * NRT * SXS * 4;               // floats of the score exchange
     __shared__ float lds[FUSED && NRT * 16 * ATT_HD > SXF ? NRT * 16 * ATT_HD : SXF];   // q rows (FUSED), then the score exchange
     __shared__ float Kn[FUSED ? ATT_MAXB : 1][ATT_HD];   // new k rows, normalised and rotated
     __shared__ float Vn[FUSED ? ATT_MAXB : 1][ATT_HD];   // new v rows
     __shared__ float Rc[FUSED ? ATT_MAXB * ATT_HD / 2 : 1], Rs[FUSED ? ATT_MAXB * ATT_HD / 2 : 1];   // RoPE tables
-    __shared__ __attribute__((aligned(16))) float Pl[2 * NRT * 256];   // probabilities [buf][rt][gq][n][v]
+    // probabilities [buf][rt][gq][n][v] as bf16 hi and lo parts: the softmax owner splits each once; the
+    // P.V lanes read their four positions' parts with one 8-byte load each
+    __shared__ __attribute__((aligned(16))) uint16_t Ph[2 * NRT * 256], Plo[2 * NRT * 256];
     __shared__ __attribute__((aligned(16))) float Al[2 * NRT * 16];    // rescale factors [buf][row]
     const int g = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -361,15 +434,24 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         }
     };
     // partial score tiles of tile tt over this wave's dims, into exchange buffer bf
+    // the K-index 8 gq + i of one 32-dim product stands for the dim d0 + 16 (i / 4) + 4 gq + i % 4 (pair
+    // h of the wave's dims: h = q / 2), in the K operand (lane: position n) and the Q operand (lane: row
+    // n) alike, so each product is a dot product over the wave's dims
+    SplitH qsp[NRT][ATT_NQ / 2];
+#pragma unroll
+    for (int rt = 0; rt < NRT; rt++)
+#pragma unroll
+        for (int h = 0; h < ATT_NQ / 2; h++) qsp[rt][h] = split_h8(qop[rt][2 * h], qop[rt][2 * h + 1]);
     auto scores = [&](const v4f *kr_, int bf) {
+        SplitH ksp[ATT_NQ / 2];
+#pragma unroll
+        for (int h = 0; h < ATT_NQ / 2; h++) ksp[h] = split_h8(kr_[2 * h], kr_[2 * h + 1]);
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
             v4f sp = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int q = 0; q < ATT_NQ; q++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) sp = mfma4(kr_[q][j], qop[rt][q][j], sp);
-            Sx[((bf * ATT_NWV + wv) * NRT + rt) * 64 + lane] = sp;
+            for (int h = 0; h < ATT_NQ / 2; h++) sp = mfma_split_h(ksp[h], qsp[rt][h], sp);
+            Sx[((bf * ATT_NWV + wv) * NRT + rt) * SXS + lane + (lane >> 4)] = sp;
         }
     };
     new_k(tile0, kr[0]);
@@ -392,10 +474,10 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
             const int su = wv + j * ATT_NWV;
             if (su < NRT * 4) {
                 const int R = 4 * su + (lane >> 4), pq = lane & 15, rt = R >> 4, nr = R & 15;
-                const int li = ((pq >> 2) * 16 + nr) * 4 + (pq & 3);     // float of lane (pq/4, nr), register pq%4
-                float sc = Sf[((buf * ATT_NWV + 0) * NRT + rt) * 256 + li];
+                const int li = ((pq >> 2) * 17 + nr) * 4 + (pq & 3);     // float of lane (pq/4, nr), register pq%4 (padded)
+                float sc = Sf[((buf * ATT_NWV + 0) * NRT + rt) * SXS * 4 + li];
 #pragma unroll
-                for (int w = 1; w < ATT_NWV; w++) sc += Sf[((buf * ATT_NWV + w) * NRT + rt) * 256 + li];
+                for (int w = 1; w < ATT_NWV; w++) sc += Sf[((buf * ATT_NWV + w) * NRT + rt) * SXS * 4 + li];
                 const int pp = t * ATT_TP + pq;
                 const float sv = pp <= slim[j] ? sc * scale : -INFINITY;
                 const float mnew = fmaxf(sm[j], rowmax16(sv));
@@ -403,7 +485,10 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 const float pv = sv > -INFINITY ? __builtin_amdgcn_exp2f(sv - mnew) : 0.0f;
                 sl[j] = sl[j] * alpha + rowsum16(pv);
                 sm[j] = mnew;
-                Pl[(((buf * NRT + rt) * 4 + (pq >> 2)) * 16 + nr) * 4 + (pq & 3)] = pv;
+                const int pi = (((buf * NRT + rt) * 4 + (pq >> 2)) * 16 + nr) * 4 + (pq & 3);
+                const __bf16 ph = (__bf16)pv;
+                Ph[pi] = __builtin_bit_cast(uint16_t, ph);
+                Plo[pi] = __builtin_bit_cast(uint16_t, (__bf16)(pv - (float)ph));
                 if (pq == 0) Al[buf * NRT * 16 + R] = alpha;
             }
         }
@@ -420,19 +505,23 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 if (pv_ >= pos0) vr[u][v] = vn;
             }
         }
+        // one 16-position product per output tile c, the K-index 4 gq + j standing for position 4 gq + j:
+        // the lane's P operand is its four probabilities, its V operand the four v rows it loaded
+        SplitB vsp[ATT_NQ];
+#pragma unroll
+        for (int c = 0; c < ATT_NQ; c++) vsp[c] = split_b4(vr[u][0][c], vr[u][1][c], vr[u][2][c], vr[u][3][c]);
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
-            const v4f pv = *(const v4f *)&Pl[(((buf * NRT + rt) * 4 + gq) * 16 + n) * 4];
+            const int pi = (((buf * NRT + rt) * 4 + gq) * 16 + n) * 4;
             const v4f al = *(const v4f *)&Al[buf * NRT * 16 + rt * 16 + 4 * gq];
             // rescale the O rows 4gq + w by their rows' factor
 #pragma unroll
             for (int w = 0; w < 4; w++)
 #pragma unroll
                 for (int c = 0; c < ATT_NQ; c++) oacc[rt][c][w] *= al[w];
+            const SplitB psp = { *(const v4s *)&Ph[pi], *(const v4s *)&Plo[pi] };
 #pragma unroll
-            for (int v = 0; v < 4; v++)
-#pragma unroll
-                for (int c = 0; c < ATT_NQ; c++) oacc[rt][c] = mfma4(pv[v], vr[u][v][c], oacc[rt][c]);
+            for (int c = 0; c < ATT_NQ; c++) oacc[rt][c] = mfma_split_b(psp, vsp[c], oacc[rt][c]);
         }
     }
     // ---- partials of this span
