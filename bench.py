@@ -492,6 +492,48 @@ def bench_longctx(args, gpu, host, roof, gemv_call_gbs):
 SAMPLE_CFG = (0.8, 0.9, 40, 1.1, 7)        # temp, top_p, top_k, repeat penalty, seed
 
 
+ATTN_CASES = [(800, 4), (800, 8), (8392, 4), (8392, 6), (8392, 8)]     # (KV positions before the call, B)
+
+
+def bench_attn(args, gpu):
+    """The model's attention call alone at the 27B shapes (24 query / 4 KV heads, head_dim 256, RoPE on 64
+    dims): qgpu_attn_fused_act (span kernel + combine with the o-projection digits) at several context
+    lengths and batch sizes, random caches; per case K calls captured in a HIP graph, the median of five
+    timed replays.  Bytes per call: the K and V rows of every position plus q, k, v in and out."""
+    L = gpu.L
+    nh, nkv, hd, rope_dim, eps, n_ctx = 24, 4, 256, 64, 1e-6, 8448
+    rng = np.random.default_rng(args.seed)
+    kc = gpu.put(rng.standard_normal((n_ctx, nkv, hd)).astype(np.float32))
+    vc = gpu.put(rng.standard_normal((n_ctx, nkv, hd)).astype(np.float32))
+    half = rope_dim // 2
+    ang = np.arange(n_ctx, dtype=np.float32)[:, None] * \
+        np.power(np.float32(1e7), (-2.0 * np.arange(half) / rope_dim).astype(np.float32))[None]
+    rc, rs = gpu.put(np.cos(ang).astype(np.float32)), gpu.put(np.sin(ang).astype(np.float32))
+    qw = gpu.put((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    kw = gpu.put((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))
+    e0, e1 = gpu.event(), gpu.event()
+    rows = []
+    for pos, B in ATTN_CASES:
+        q = gpu.put(rng.standard_normal((B, nh * 2 * hd)).astype(np.float32))
+        k = gpu.put(rng.standard_normal((B, nkv * hd)).astype(np.float32))
+        v = gpu.put(rng.standard_normal((B, nkv * hd)).astype(np.float32))
+        out, posb = gpu.buf(B * nh * hd * 4), gpu.put(np.array([pos], np.int32))
+
+        def calls():
+            for _ in range(args.steps):
+                gpu.ok(L.qgpu_attn_fused_act(q.f32(), nh * 2 * hd, k.f32(), v.f32(), nkv * hd, qw.f32(), kw.f32(),
+                                             kc.f32(), vc.f32(), rc.f32(), rs.f32(), rope_dim, posb.i32(), n_ctx, B,
+                                             nh, nkv, hd, eps, out.f32(), nh * hd))
+        for _ in range(args.warmup):
+            calls()
+        reps = sorted(ms / args.steps * 1e3 for ms in graph_ms(gpu, calls, e0, e1, ROOF_TIMED, ROOF_UNTIMED))
+        by = (pos + B) * 2 * nkv * hd * 4 + B * (nh * 2 * hd + 2 * nkv * hd + nh * hd) * 4
+        rows.append({"pos": pos, "B": B, "us": round(reps[ROOF_TIMED // 2], 3), "us_range": [round(reps[0], 3),
+                     round(reps[-1], 3)], "bytes": by, "gbs": round(by / (reps[ROOF_TIMED // 2] * 1e-6) / 1e9, 1)})
+        log(f"attention pos {pos} B {B}: {rows[-1]['us']} us per call, {rows[-1]['gbs']} GB/s")
+    return rows
+
+
 def bench_sample(args, gpu, host, roof, gemv_call_gbs):
     from qwen_pkg import pyqwen
     K, W, n_prompt = args.steps, args.warmup, args.prompt
@@ -557,7 +599,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (model: cycles; gemv: calls)")
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--mode", choices=["model", "gemv", "longctx", "sweep", "sample"], default="model")
+    ap.add_argument("--mode", choices=["model", "gemv", "longctx", "sweep", "sample", "attn"], default="model")
     ap.add_argument("--k", type=int, default=3, help="drafts per speculative cycle (model mode)")
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (model 512, longctx 8192)")
     ap.add_argument("--forced-cycles", type=int, default=None)
@@ -577,7 +619,7 @@ def main():
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     dflt = {"model": (256, 8, 512, 64, 15.0), "gemv": (200, 20, 0, 0, 5.0), "longctx": (0, 0, 8192, 16, 0.0),
-            "sweep": (40, 5, 0, 0, 0.0), "sample": (128, 8, 512, 0, 15.0)}
+            "sweep": (40, 5, 0, 0, 0.0), "sample": (128, 8, 512, 0, 15.0), "attn": (100, 5, 0, 0, 0.0)}
     s, w, p, f, c = dflt[args.mode]
     args.steps = s if args.steps is None else args.steps
     args.warmup = w if args.warmup is None else args.warmup
@@ -626,6 +668,20 @@ def main():
             "config": {"workload": "gemv_batch sweep: 5 formats x 3 shapes x B in {1,2,4,8}", "device": name,
                        "cus": ncu},
             "sweep": sweep, "roofline": roof, "cpu_baseline": None,
+        }
+    elif args.mode == "attn":
+        att = bench_attn(args, gpu)
+        pick = next(r for r in att if r["pos"] == 8392 and r["B"] == 8)
+        res = {
+            "metric": "attention call latency, 27B shapes (span kernel + combine), 8392 KV positions, B=8",
+            "value": pick["us"], "unit": "us per attention call", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(pick["us"] / 1e3, 5), "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp32 (q.k as fp16 hi/lo and p.v as bf16 hi/lo split products, fp32 accumulate)",
+            "data": "synthetic (random caches, q, k, v ~ N(0,1))",
+            "config": {"workload": "27B attention call (24 / 4 heads, head_dim 256): span kernel + combine, "
+                                   "8392 KV positions, B = 8", "device": name, "cus": ncu},
+            "attn": att, "roofline": roof, "cpu_baseline": None,
         }
     elif args.mode == "model":
         res = bench_model(args, gpu, host, roof, gemv_gbs)

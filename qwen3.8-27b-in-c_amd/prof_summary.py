@@ -279,7 +279,7 @@ def step_roles(step, B, P):
             role, by = "gated-norm prep (GDN out)", 2 * B * d["VD"] * f4 + B * d["VD"] * (f4 + DIGITS)
         elif kind == 2:
             role, by = "SiLU x up prep", 2 * B * d["F"] * f4 + B * d["F"] * (f4 + DIGITS)
-        elif split and grid > 1024 and grid < 1280 and prev_kind == 4:
+        elif split and grid > 1024 and grid < 1280 and prev_kind in (4, 5):
             # the GDN input projection with beta and alpha cut into one K range per super-block
             kba = (grid - (d["CONV"] + d["VD"]) // 16) // (2 * d["VH"] // 16)
             role = "GEMV GDN in (qkv, z; beta, alpha K-split)"
