@@ -499,7 +499,8 @@ def bench_attn(args, gpu):
     """The model's attention call alone at the 27B shapes (24 query / 4 KV heads, head_dim 256, RoPE on 64
     dims): qgpu_attn_fused_act (span kernel + combine with the o-projection digits) at several context
     lengths and batch sizes, random caches; per case K calls captured in a HIP graph, the median of five
-    timed replays.  Bytes per call: the K and V rows of every position plus q, k, v in and out."""
+    timed replays (--eager: K calls launched from the host, five timed series).  Bytes per call: the K and
+    V rows of every position plus q, k, v in and out."""
     L = gpu.L
     nh, nkv, hd, rope_dim, eps, n_ctx = 24, 4, 256, 64, 1e-6, 8448
     rng = np.random.default_rng(args.seed)
@@ -526,7 +527,17 @@ def bench_attn(args, gpu):
                                              nh, nkv, hd, eps, out.f32(), nh * hd))
         for _ in range(args.warmup):
             calls()
-        reps = sorted(ms / args.steps * 1e3 for ms in graph_ms(gpu, calls, e0, e1, ROOF_TIMED, ROOF_UNTIMED))
+        if args.eager:                  # no graph: K calls launched from the host between two events
+            reps = []
+            for _ in range(ROOF_TIMED):
+                gpu.record(e0)
+                calls()
+                gpu.record(e1)
+                gpu.sync()
+                reps.append(gpu.elapsed_ms(e0, e1) / args.steps * 1e3)
+            reps.sort()
+        else:
+            reps = sorted(ms / args.steps * 1e3 for ms in graph_ms(gpu, calls, e0, e1, ROOF_TIMED, ROOF_UNTIMED))
         by = (pos + B) * 2 * nkv * hd * 4 + B * (nh * 2 * hd + 2 * nkv * hd + nh * hd) * 4
         rows.append({"pos": pos, "B": B, "us": round(reps[ROOF_TIMED // 2], 3), "us_range": [round(reps[0], 3),
                      round(reps[-1], 3)], "bytes": by, "gbs": round(by / (reps[ROOF_TIMED // 2] * 1e-6) / 1e9, 1)})
@@ -611,6 +622,8 @@ def main():
                          "format mix (Q4_K embedding, Q5_K attn_qkv, Q6_K output, Q8_0 eh_proj)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=None)
+    ap.add_argument("--eager", action="store_true",
+                    help="attn mode: launch the timed calls from the host instead of replaying a HIP graph")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run the k_copy kernel on 256 MiB x 5 (reference point for PMC byte counters)")
     args = ap.parse_args()

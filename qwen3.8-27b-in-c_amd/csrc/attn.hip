@@ -231,6 +231,10 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, gq = lane >> 4;
     const int per = p.n_head / p.n_kv, QH = per * p.B;
+    // r / per for the row indices 0 <= r < 64 of this kernel: (r * ceil(2^16 / per)) >> 16 is exact there
+    // (the rounding up adds less than r / 2^16 < 1 / per to r / per)
+    const uint32_t inv_per = (65536u + (uint32_t)per - 1u) / (uint32_t)per;
+    auto divp = [&](int r) { return (int)(((uint32_t)r * inv_per) >> 16); };
     const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD, hoff = (uint64_t)g * ATT_HD;
     const int d0 = ATT_DW * wv;
 
@@ -247,7 +251,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
             const int e = tid + u * ATT_NWV * 64, r = e >> 6, d4 = e & 63;
             qv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             if (r < QH) {
-                const int b = r / per, h = g * per + r % per;
+                const int b = divp(r), h = g * per + (r - b * per);
                 qv[u] = *(const float4 *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + 4 * d4);
             }
         }
@@ -266,7 +270,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
             const int r = rt * 16 + n;
-            const int b = r / per, h = g * per + r % per;
+            const int b = divp(r), h = g * per + (r - b * per);
 #pragma unroll
             for (int q = 0; q < ATT_NQ; q++)
                 qop[rt][q] = r < QH ? *(const v4f *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + d0 + 16 * q + 4 * gq)
@@ -377,7 +381,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 const float sc = 1.0f / sqrtf(wave_sum64(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w) / (float)ATT_HD + p.eps);
                 v = make_float4((v.x * sc) * w.x, (v.y * sc) * w.y, (v.z * sc) * w.z, (v.w * sc) * w.w);
                 *(float4 *)(x + 4 * lane) = v;
-                const int b = r < QH ? r / per : r - QH;
+                const int b = r < QH ? divp(r) : r - QH;
                 for (int i = lane; i < p.half; i += 64) {
                     const float cs = Rc[b * p.half + i], sn = Rs[b * p.half + i];
                     const float v0 = x[i], v1 = x[i + p.half];
@@ -420,7 +424,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         const int R = 4 * (wv + j * ATT_NWV) + (lane >> 4);
         sm[j] = -INFINITY;
         sl[j] = 0.0f;
-        slim[j] = R < QH ? pos0 + R / per : -1;
+        slim[j] = R < QH ? pos0 + divp(R) : -1;
     }
     // K rows of new positions (FUSED: prepared in Kn, not in the caches yet) into slot kr_
     auto new_k = [&](int tt, v4f *kr_) {
@@ -622,37 +626,28 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_combine(const float *q, uint64_
 }
 
 // The combine with the output rows also written as the GEMV input digit planes
-// (what the COPY preparation would write from them): block (h, a), 4 x 256
-// threads, merges head h of tokens 4a..4a+3 (thread 256i + d: token 4a+i, dim d),
-// whose 256 outputs are super-block h of each row.
-__global__ __launch_bounds__(4 * ATT_HD) void k_attn_combine_act(const float *q, uint64_t ldq, const float *pml,
-                                                                 const float *po, const int *pos_dev, int B,
-                                                                 int n_head, int n_kv, int nspan, float *out,
-                                                                 uint64_t ldo, uint8_t *A, float *xs)
+// (what the COPY preparation writes from them): block (h, b), thread = dim, merges
+// head h of token b, whose 256 outputs are super-block h of the row; the block's
+// maximum (one barrier) gives the token's shift, and tok_digits writes its digits.
+// One token per block spreads the span partials' reads over n_head x B compute units.
+__global__ __launch_bounds__(ATT_HD) void k_attn_combine_act(const float *q, uint64_t ldq, const float *pml,
+                                                             const float *po, const int *pos_dev, int B,
+                                                             int n_head, int n_kv, int nspan, float *out,
+                                                             uint64_t ldo, uint8_t *A, float *xs)
 {
-    __shared__ ActDigitLds dl;
-    __shared__ float vb[4][ATT_HD];
-    const int h = blockIdx.x, a = blockIdx.y, i = threadIdx.x >> 8, d = threadIdx.x & (ATT_HD - 1);
-    const int b = 4 * a + i;
+    __shared__ float mxw[ATT_HD / 64];
+    const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x, lane = d & 63;
     int ntl, tps, nc;
     span_split(*pos_dev, B, nspan, ntl, tps, nc);
-    float val = 0.0f;
-    if (b < B) {                                  // wave-uniform
-        val = combine_one(q, ldq, pml, po, nspan, nc, n_head / n_kv, h, b, d);
-        out[(uint64_t)b * ldo + (uint64_t)h * ATT_HD + d] = val;
-    }
-    vb[i][d] = val;
+    const float val = combine_one(q, ldq, pml, po, nspan, nc, n_head / n_kv, h, b, d);
+    out[(uint64_t)b * ldo + (uint64_t)h * ATT_HD + d] = val;
+    const float mw = wave_max64(fabsf(val));
+    if (lane == 0) mxw[d >> 6] = mw;
     __syncthreads();
-    // the digit stage runs on threads 0..255 (the others take part in its barriers)
-    const bool active = threadIdx.x < ATT_HD;     // wave-uniform
-    float v[4], m[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) { v[t] = vb[t][d]; m[t] = fabsf(v[t]); }
-    if (active)
-#pragma unroll
-        for (int t = 0; t < 4; t++) m[t] = wave_max64(m[t]);
-    act_digits(v, m, dl, A + (uint64_t)a * PLANE_BYTES + (uint64_t)h * DIGIT_TILE,
-               xs + (uint64_t)a * XS_FLOATS + (uint64_t)h * 16, active);
+    const float mx = fmaxf(fmaxf(mxw[0], mxw[1]), fmaxf(mxw[2], mxw[3]));
+    const int a = b >> 2;
+    tok_digits(val, mx, b & 3, A + (uint64_t)a * PLANE_BYTES + (uint64_t)h * DIGIT_TILE,
+               xs + (uint64_t)a * XS_FLOATS + (uint64_t)h * 16);
 }
 
 // The span-partial workspace is sized for the largest span count (ATT_NSPAN), so
@@ -730,7 +725,7 @@ static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out,
 #undef ATT_GO
     QG_LAUNCH_CHECK();
     if (act)
-        hipLaunchKernelGGL(k_attn_combine_act, dim3(a.n_head, (a.B + 3) / 4), dim3(4 * ATT_HD), 0, qg::stream, a.q,
+        hipLaunchKernelGGL(k_attn_combine_act, dim3(a.n_head, a.B), dim3(ATT_HD), 0, qg::stream, a.q,
                            a.ldq, a.pml, a.po, a.pos_dev, a.B, a.n_head, a.n_kv, a.nspan, out, ldo, (uint8_t *)qg::ws,
                            (float *)((uint8_t *)qg::ws + 2 * PLANE_BYTES));
     else

@@ -498,13 +498,8 @@ __global__ __launch_bounds__(256) void k_prep_rms(ActDev p, uint8_t *__restrict_
 // planes), SiLU(x)·y, the per-head gated norm, and the plain copy.  Block (sb, t),
 // 256 threads: thread e holds element e of super-block sb of token t, so a thread
 // issues 1 + NP + 1 loads (deferred RMSNorm with NP partial planes), 2 or 3 (the
-// others), with no branch around them.  Wave r holds elements 64r..64r+63, which
-// are token t's whole 192-byte run of sub-block pair r in the digit tile (layout
-// above act_digits): lane l = 16h + 4gg + c holds element 64r + 16h + 4gg + c,
-// whose digit dg is byte r*768 + t*192 + gg*48 + dg*16 + 4h + c.  The four lanes
-// of a quad hold the four bytes of one dword per digit; a byte transpose inside
-// the quad (DPP broadcasts and two v_perm_b32) gives lane c the dword of digit c,
-// and lanes c < 3 store it -- no staging through LDS.  One barrier exchanges the
+// others), with no branch around them; tok_digits writes token t's digits of the
+// super-block straight from registers.  One barrier exchanges the
 // per-wave sums of squares and maxima (the gated norm takes two: its maximum
 // follows the head scale).  The per-element arithmetic and the reduction orders
 // are those of the 4-token form (wave sums, then (w0 + w1) + (w2 + w3)), so
@@ -566,36 +561,8 @@ __global__ __launch_bounds__(256) void k_prep_tok(ActDev p, uint8_t *__restrict_
     __syncthreads();
     if (RMS && e == 0) p.rss[(uint64_t)t * p.nsb + sb] = (ssw[0] + ssw[1]) + (ssw[2] + ssw[3]);
     if (!p.digits) return;                                       // fp32 rows only (VALU formats)
-    // shift puts the super-block maximum just under 2^22 (0 for an all-zero or non-finite maximum)
     const float mx = fmaxf(fmaxf(mxw[0], mxw[1]), fmaxf(mxw[2], mxw[3]));
-    int shift = 0;
-    if (mx > 0.0f && isfinite(mx)) {
-        int E;
-        frexpf(mx, &E);
-        shift = 22 - E;
-    }
-    // three balanced base-256 digits of X = rint(v 2^shift), packed in bytes 0..2 of P
-    const float sv = ldexpf(v, shift);
-    int X = isfinite(sv) ? (int)rintf(sv) : 0;
-    uint32_t P = 0;
-#pragma unroll
-    for (int dg = 0; dg < 3; dg++) {
-        const int d = (dg < 2) ? (int)(int8_t)(X & 0xFF) : X;
-        X = (X - d) >> 8;
-        P |= ((uint32_t)d & 0xFFu) << (8 * dg);
-    }
-    // quad byte transpose: lane c gets byte c of P from each lane of its quad, in lane order
-    const uint32_t c = (uint32_t)lane & 3u;
-    const uint32_t P0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x00, 0xF, 0xF, false);
-    const uint32_t P1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x55, 0xF, 0xF, false);
-    const uint32_t P2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0xAA, 0xF, 0xF, false);
-    const uint32_t P3 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0xFF, 0xF, 0xF, false);
-    // v_perm_b32 selectors: 0..3 bytes of the second operand, 4..7 of the first, 12 the constant 0
-    const uint32_t W = __builtin_amdgcn_perm(P1, P0, c | ((c + 4u) << 8) | 0x0C0C0000u) |
-                       __builtin_amdgcn_perm(P3, P2, 0x00000C0Cu | (c << 16) | ((c + 4u) << 24));
-    uint8_t *tile = A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * DIGIT_TILE + wv * DIGIT_SUB + i * 192;
-    if (c < 3) *(uint32_t *)(tile + ((lane >> 2) & 3) * 48 + c * 16 + (lane >> 4) * 4) = W;
-    if (e < 4) xs[(uint64_t)a * XS_FLOATS + (uint64_t)sb * 16 + 4 * e + i] = ldexpf(1.0f, 8 * e - shift);
+    tok_digits(v, mx, i, A + (uint64_t)a * PLANE_BYTES + (uint64_t)sb * DIGIT_TILE, xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16);
 }
 
 // ---------------------------------------------------------------- IQ4_XS MFMA GEMV

@@ -161,6 +161,50 @@ static __device__ __forceinline__ void act_digits(const float v[4], const float 
     }
 }
 
+// Digits of one token of a super-block, written by a block of 256 threads: thread e holds element
+// e of the super-block (v) and mx, the super-block's largest |v| (the same value in every thread).
+// Wave r holds elements 64r..64r+63, which are the token's whole 192-byte run of sub-block pair r
+// in the digit tile (layout above act_digits): lane l = 16h + 4gg + c holds element 64r + 16h +
+// 4gg + c, whose digit dg is byte r*768 + i*192 + gg*48 + dg*16 + 4h + c (i: the token's slot in
+// its 4-token plane).  The four lanes of a quad hold the four bytes of one dword per digit; a byte
+// transpose inside the quad (DPP broadcasts and two v_perm_b32) gives lane c the dword of digit c,
+// and lanes c < 3 store it -- no staging through LDS.  The shift and digits are those act_digits
+// computes for the same token and maximum.
+static __device__ __forceinline__ void tok_digits(float v, float mx, int i, uint8_t *__restrict__ A_tile,
+                                                  float *__restrict__ xs_tile)
+{
+    const int e = threadIdx.x & 255, lane = e & 63, wv = e >> 6;
+    // shift puts the super-block maximum just under 2^22 (0 for an all-zero or non-finite maximum)
+    int shift = 0;
+    if (mx > 0.0f && isfinite(mx)) {
+        int E;
+        frexpf(mx, &E);
+        shift = 22 - E;
+    }
+    // three balanced base-256 digits of X = rint(v 2^shift), packed in bytes 0..2 of P
+    const float sv = ldexpf(v, shift);
+    int X = isfinite(sv) ? (int)rintf(sv) : 0;
+    uint32_t P = 0;
+#pragma unroll
+    for (int dg = 0; dg < 3; dg++) {
+        const int d = (dg < 2) ? (int)(int8_t)(X & 0xFF) : X;
+        X = (X - d) >> 8;
+        P |= ((uint32_t)d & 0xFFu) << (8 * dg);
+    }
+    // quad byte transpose: lane c gets byte c of P from each lane of its quad, in lane order
+    const uint32_t c = (uint32_t)lane & 3u;
+    const uint32_t P0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x00, 0xF, 0xF, false);
+    const uint32_t P1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0x55, 0xF, 0xF, false);
+    const uint32_t P2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0xAA, 0xF, 0xF, false);
+    const uint32_t P3 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, 0xFF, 0xF, 0xF, false);
+    // v_perm_b32 selectors: 0..3 bytes of the second operand, 4..7 of the first, 12 the constant 0
+    const uint32_t W = __builtin_amdgcn_perm(P1, P0, c | ((c + 4u) << 8) | 0x0C0C0000u) |
+                       __builtin_amdgcn_perm(P3, P2, 0x00000C0Cu | (c << 16) | ((c + 4u) << 24));
+    uint8_t *tile = A_tile + wv * DIGIT_SUB + i * 192;
+    if (c < 3) *(uint32_t *)(tile + ((lane >> 2) & 3) * 48 + c * 16 + (lane >> 4) * 4) = W;
+    if (e < 4) xs_tile[4 * e + i] = ldexpf(1.0f, 8 * e - shift);
+}
+
 namespace qg {
 extern hipStream_t stream;
 extern int initialized;

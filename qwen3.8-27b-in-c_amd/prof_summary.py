@@ -6,6 +6,7 @@
     prof_summary.py sweep   BENCH_JSON --cmd "<command that made it>"
     prof_summary.py steps   DB_OR_DIR --cmd "<command that made it>" [--rows 4] [--title T]
     prof_summary.py counters DB [DB ...] --bench-json FILE --cmd "<commands that made them>"
+    prof_summary.py kcounters DB [DB ...] --bench-json FILE [--kernel k_attn_span] --cmd "<commands>"
 
 stats   : per-kernel calls / total / average duration of a --kernel-trace run,
           and, given the benchmark's JSON line, the average duration of the
@@ -24,6 +25,9 @@ counters: every PMC counter of one or more --pmc runs of `bench.py --mode gemv`,
           and over the plain-read kernel (k_checksum) of the read floor, side
           by side: the GEMV's instruction mix and vector-memory path against a
           kernel that only reads the same bytes.
+kcounters: every PMC counter of --pmc runs of `bench.py --mode attn --eager` for one kernel
+          (name prefix), averaged per dispatch for each of the benchmark's attention cases,
+          with per-wave and per-tile instruction counts.
 steps   : per-kernel time of one verify step of a --kernel-trace run of the model
           benchmark.  The trace is cut after every k_argmax_final; a verify step
           is a piece that ends in the argmax of --rows rows (drafts and decode
@@ -194,6 +198,59 @@ def cmd_counters(a):
         out += ["", f"L2 read requests from the CUs (TCP_TCC_READ_REQ): GEMV {gv:,.0f} per launch, read kernel "
                     f"{rv:,.0f} ({gv / rv:.2f}x) for the same weight bytes; the excess is the activation digit "
                     "tiles every row tile reads again from L2."]
+    print("\n".join(out))
+
+
+def span_tiles(pos, B, nspan=64, mintps=2, tp=16):
+    """(tiles per span, spans) of the attention span kernel for a call at pos with B new positions"""
+    ntl = (pos + B + tp - 1) // tp
+    ns = min(ntl, nspan)
+    tps = max(-(-ntl // ns), mintps)
+    return tps, -(-ntl // tps)
+
+
+def cmd_kcounters(a):
+    b = bench_line(a.bench_json)
+    cases = b["attn"]
+    out = [f"# PMC counters: `{a.kernel}` per attention call (bench.py --mode attn --eager)", "",
+           "Commands (`/root/repo` is the repository root; one rocprofv3 --pmc pass per line):", "", "```",
+           *a.cmd.split(" ;; "), "```", "",
+           f"The benchmark runs the cases in order with the same number of calls each, so the kernel's dispatches "
+           f"split into {len(cases)} equal consecutive groups; each value is the average over the second half of its "
+           "group (after the warm-up calls), summed over the counter's instances of one dispatch.  Per-wave "
+           "figures divide by SQ_WAVES; per-tile figures also by the tiles each block streams.", ""]
+    vals = {}
+    for db in a.dbs:
+        c = sqlite3.connect(find_db(db))
+        acc = {}
+        for name, did, cn, v in c.execute("select kernel_name, dispatch_id, counter_name, value from "
+                                          "counters_collection order by dispatch_id").fetchall():
+            if short(name).startswith(a.kernel):
+                acc.setdefault(cn, {}).setdefault(did, 0.0)
+                acc[cn][did] += v
+        for cn, per in acc.items():
+            seq = [per[d] for d in sorted(per)]         # every instance of the kernel, in dispatch order
+            if not seq or len(seq) % len(cases):
+                continue
+            n = len(seq) // len(cases)
+            vals[cn] = [statistics.fmean(seq[i * n + n // 2:(i + 1) * n]) for i in range(len(cases))]
+    hdr = [f"{c['pos']} / B={c['B']}" for c in cases]
+    out += ["| counter | " + " | ".join(hdr) + " |", "|---|" + "---:|" * len(cases)]
+    for cn in sorted(vals):
+        out.append(f"| {cn} | " + " | ".join(f"{v:,.0f}" for v in vals[cn]) + " |")
+    if "SQ_WAVES" in vals:
+        tiles = [span_tiles(c["pos"], c["B"]) for c in cases]
+        out += ["", "| per wave | " + " | ".join(hdr) + " |", "|---|" + "---:|" * len(cases)]
+        out.append("| tiles per span, spans | " + " | ".join(f"{t}, {s}" for t, s in tiles) + " |")
+        for cn in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_INSTS_SALU", "SQ_INSTS_VMEM_RD"):
+            if cn in vals:
+                out.append(f"| {cn} per wave | " + " | ".join(
+                    f"{v / w:,.0f}" for v, w in zip(vals[cn], vals["SQ_WAVES"])) + " |")
+                out.append(f"| {cn} per wave per tile | " + " | ".join(
+                    f"{v / w / t[0]:,.1f}" for v, w, t in zip(vals[cn], vals["SQ_WAVES"], tiles)) + " |")
+    if "SQ_LDS_BANK_CONFLICT" in vals and "SQ_ACTIVE_INST_LDS" in vals:
+        out.append("| LDS bank-conflict cycles / LDS active cycles | " + " | ".join(
+            f"{c / l:.3f}" if l else "-" for c, l in zip(vals["SQ_LDS_BANK_CONFLICT"], vals["SQ_ACTIVE_INST_LDS"])) + " |")
     print("\n".join(out))
 
 
@@ -409,9 +466,14 @@ def main():
     cn.add_argument("dbs", nargs="+")
     cn.add_argument("--bench-json", required=True)
     cn.add_argument("--cmd", required=True, help="the commands, separated by ' ;; '")
+    kc = sub.add_parser("kcounters")
+    kc.add_argument("dbs", nargs="+")
+    kc.add_argument("--bench-json", required=True)
+    kc.add_argument("--kernel", default="k_attn_span")
+    kc.add_argument("--cmd", required=True, help="the commands, separated by ' ;; '")
     a = ap.parse_args()
     {"stats": cmd_stats, "traffic": cmd_traffic, "sweep": cmd_sweep, "steps": cmd_steps,
-     "counters": cmd_counters}[a.cmd_name](a)
+     "counters": cmd_counters, "kcounters": cmd_kcounters}[a.cmd_name](a)
 
 
 if __name__ == "__main__":
