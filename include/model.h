@@ -16,7 +16,11 @@
  * Differences from the reference, by design:
  *   - SPEC_MAX_B is 8 (drafts k <= 7); the reference caps k at 2.
  *   - Recurrent-state checkpoints are a ring of state slots on the device;
- *     model_rollback_to() moves the ring index (no copy).
+ *     model_rollback_to() moves the ring index (no copy).  Batches of 5..8
+ *     tokens keep the recurrent state as the batch's starting state plus one
+ *     rank-1 factor per token (one state write instead of B); the next forward
+ *     applies the factors up to the selected token first (QWEN_GDN_FACTOR_MIN_B
+ *     sets the batch size from which this form is used; 9 turns it off).
  *   - Calls whose positions run past n_ctx (pos + B > n_ctx) are rejected on
  *     the host with a message, before any device work; the reference writes
  *     past its KV arrays.  After a rejected call or a device error,
@@ -197,7 +201,9 @@ uint32_t model_generate_sample(qwen_model_t *m, const uint32_t *prompt, uint32_t
 uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_predict,
                                uint32_t eos, uint32_t *out, qwen_gen_stats_t *st);
 /* One timed verify step (B tokens at the current position) and one timed decode
- * step, on device buffers (benchmark support); the model state is restored. */
+ * step, on device buffers (benchmark support); the model state is restored.  If the
+ * last forward kept its recurrent states in factor form, the selected state is
+ * written out first, and model_rollback_to may afterwards only select it (b = 0). */
 int  model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, float *ms_decode, float *ms_draft);
 
 /* Status of the last model call: 0 = done, -1 = rejected on the host (bad

@@ -249,6 +249,34 @@ int  qgpu_gdn_fused_planes(const float *x, uint64_t ldx, int B, int conv_dim, co
                            int ba_planes, uint64_t ba_pstride, const float *dt_bias, const float *ssm_a,
                            float *ssm_ring, uint64_t ssm_stride, int nslot, const int *cur, int n_k, int n_v,
                            int head_dim, float eps, float *out, uint64_t ldo);
+/* qgpu_gdn_fused_planes with the recurrent state kept in rank-1 factor form
+ * (the same recurrence as model.c:494-615; the reference keeps snapshots,
+ * model.c:1015-1031).  The state after token b is dec_b * S_{b-1} + d_b kn_b^T
+ * per v-head (d_b: one coefficient per state row, kn_b: the normalised k of its
+ * k-head, dec_b: the decay), exactly the update the recurrence applies.
+ * factors: two buffers of 8 token records of f_tok floats each (f_tok >=
+ * (n_v + n_k) * 128 + n_v, a multiple of 4): record b = d_b of every v-head
+ * [n_v][128], then kn_b [n_k][128], then dec_b [n_v].  fstate (device, 2 ints):
+ * P, the tokens of the previous factor-form call still to be applied, and the
+ * buffer holding their factors.  The call reads the state in slot
+ * (*cur - P) % nslot and applies those P tokens first; factor_out = 0: it then
+ * writes the state after each of its B tokens to slot (*cur + 1 + b) % nslot as
+ * qgpu_gdn_fused_planes does; factor_out = 1: it writes the state after the P
+ * tokens to slot *cur and the factors of its B tokens to the other buffer, and
+ * no state snapshots.  After a factor_out = 1 call at slot c, rolling back to
+ * the state after token j is *cur = (c + 1 + j) % nslot with P = j + 1 and the
+ * buffer flipped; the conv states are snapshots in both forms.  fstate = NULL
+ * and factor_out = 0 is qgpu_gdn_fused_planes.  No reference counterpart:
+ * the verify writes one state instead of B. */
+int  qgpu_gdn_fused_factor(const float *x, uint64_t ldx, int B, int conv_dim, const float *conv_w, float *conv_ring,
+                           uint64_t conv_stride, const float *beta_raw, const float *alpha_raw, uint64_t ldba,
+                           int ba_planes, uint64_t ba_pstride, const float *dt_bias, const float *ssm_a,
+                           float *ssm_ring, uint64_t ssm_stride, int nslot, const int *cur, int n_k, int n_v,
+                           int head_dim, float eps, float *out, uint64_t ldo, float *factors, uint64_t f_tok,
+                           const int *fstate, int factor_out);
+/* the state after the P pending tokens of fstate (see qgpu_gdn_fused_factor) into slot *cur */
+int  qgpu_gdn_materialize(float *ssm_ring, uint64_t ssm_stride, int nslot, const int *cur, int n_k, int n_v,
+                          int head_dim, const float *factors, uint64_t f_tok, const int *fstate);
 /* rows x n: out = rmsnorm(x, w) * silu(z)  (per-head gated norm, model.c:928-941) */
 int  qgpu_rmsnorm_gated(float *out, const float *x, const float *z, const float *w, int n, int rows,
                         uint64_t ld, float eps);

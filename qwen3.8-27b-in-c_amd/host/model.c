@@ -35,6 +35,7 @@ typedef struct {
     float *attn_norm, *post_norm, *q_norm, *k_norm, *conv1d, *dt_bias, *ssm_a, *ssm_norm;
     float *kv_k, *kv_v;           /* attention: [n_ctx][n_kv*head_dim] */
     float *conv_ring, *ssm_ring;  /* GDN: NSLOT slots of conv (conv_dim*4) / ssm (n_v*128*128) state */
+    float *gdn_f;                 /* GDN: two buffers of MAXB rank-1 factor records (f_tok floats each) */
 } glayer_t;
 
 struct qwen_gpu {
@@ -63,6 +64,15 @@ struct qwen_gpu {
     uint64_t SQ, A, conv_elems, ssm_elems, kvrow;
     int cur, cur_base;
     int last_B;                 /* tokens of the last backbone forward: the states model_rollback_to may select */
+    /* GDN factor form (qgpu_gdn_fused_factor), for forwards of factor_min_b tokens or more: the
+     * state stays in the slot of the forward (fbase) and each token's rank-1 factors go to
+     * factor buffer fpar; the next forward applies the (cur - fbase) % NSLOT kept tokens first.
+     * fbase = -1: the states are snapshots (nothing pending).  fst_ptr: where the kernels read
+     * {pending tokens, buffer}: the constant table d_fstv (eager) or d_fst (captured graphs). */
+    int fbase, fpar, factor_min_b;
+    uint64_t f_tok;
+    int *d_fst, *d_fstv;
+    const int *fst_ptr;
     /* K-split residual GEMVs leave partial planes (part, [ks][B][n_embd]) that the
      * next RMSNorm of that residual adds in (or materialize() when none follows) */
     float *part, *pend;
@@ -370,6 +380,12 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
         g->use_graphs = ge && ge[0] == '1';
         const char *pe = getenv("QWEN_PROFILE");
         g->prof = pe && pe[0] && pe[0] != '0';
+        /* QWEN_GDN_FACTOR_MIN_B=n: forwards of n tokens or more keep the GDN state in factor form
+         * (default 5; 9 turns it off).  Measured on MI355X at the 27B shapes: a GDN layer at B = 8
+         * writes one state instead of 8 snapshots, at B <= 4 the snapshots cost about the same. */
+        const char *fe = getenv("QWEN_GDN_FACTOR_MIN_B");
+        g->factor_min_b = fe && atoi(fe) >= 1 ? atoi(fe) : 5;
+        g->fbase = -1;
     }
     g->L = calloc(d->n_layer, sizeof *g->L);
     for (uint32_t il = 0; il < d->n_layer; il++)
@@ -393,6 +409,7 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     g->kvrow = (uint64_t)d->n_kv_head * d->head_dim;
     g->conv_elems = (uint64_t)d->conv_dim * 4;
     g->ssm_elems = (uint64_t)d->n_v_heads * d->head_v_dim * d->head_k_dim;
+    g->f_tok = ((uint64_t)(d->n_v_heads + d->n_k_heads) * d->head_v_dim + d->n_v_heads + 3) & ~3ull;
     uint64_t SQ = d->conv_dim;
     if (2ull * d->n_head * d->head_dim > SQ) SQ = 2ull * d->n_head * d->head_dim;
     if (F > SQ) SQ = F;
@@ -405,7 +422,8 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
         if (D->rec) {
             D->conv_ring = dalloc(g, NSLOT * g->conv_elems * sizeof(float));
             D->ssm_ring = dalloc(g, NSLOT * g->ssm_elems * sizeof(float));
-            if (!D->conv_ring || !D->ssm_ring) return -1;
+            D->gdn_f = dalloc(g, 2 * MAXB * g->f_tok * sizeof(float));
+            if (!D->conv_ring || !D->ssm_ring || !D->gdn_f) return -1;
         } else {
             D->kv_k = dalloc(g, kvb);
             D->kv_v = dalloc(g, kvb);
@@ -413,6 +431,7 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
         }
     }
 #define AL(p, n) do { if (!((p) = dalloc(g, (n) * sizeof(*(p))))) return -1; } while (0)
+    AL(g->d_fst, 2); AL(g->d_fstv, 2 * 2 * NSLOT);
     AL(g->d_pos, 4); AL(g->d_cur, 4); AL(g->d_posv, (uint64_t)n_ctx + MAXB); AL(g->d_curv, NSLOT); AL(g->d_tok, 64); AL(g->d_cand, 64); AL(g->d_vtok, 64); AL(g->d_acc, 64);
     AL(g->anchor_tok, 64); AL(g->anchor_h, E);
     if (qgpu_host_malloc((void **)&g->h_acc, 64 * sizeof(uint32_t))) return -1;
@@ -434,7 +453,11 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
                         qgpu_memcpy_h2d(g->d_curv, tab, NSLOT * sizeof(int));
         free(tab);
         if (bad) return -1;
+        int fst[2 * 2 * NSLOT];                 /* entry 2 * P + par: {P, par} */
+        for (int i = 0; i < 2 * NSLOT; i++) { fst[2 * i] = i >> 1; fst[2 * i + 1] = i & 1; }
+        if (qgpu_memcpy_h2d(g->d_fstv, fst, sizeof fst)) return -1;
     }
+    g->fst_ptr = g->d_fst;
     g->pos_ptr = g->d_pos;
     g->cur_ptr = g->d_cur;
     /* RoPE tables with the reference's own expressions (model.c:186-201) */
@@ -705,10 +728,11 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     const int ks[4] = { 1, 1, kba, kba };
     K(qgpu_gemv_act_batch_ks(W, 4, &an, (int)B, outs, ld, ks));
     /* conv1d + SiLU + L2 norms + delta rule over the B tokens, state snapshots into the ring */
-    K(qgpu_gdn_fused_planes(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems,
+    K(qgpu_gdn_fused_factor(g->bqkv, g->SQ, (int)B, (int)d->conv_dim, D->conv1d, D->conv_ring, g->conv_elems,
                             g->bbeta, g->balpha, d->n_v_heads, kba, (uint64_t)B * d->n_v_heads, D->dt_bias,
                             D->ssm_a, D->ssm_ring, g->ssm_elems, NSLOT, g->cur_ptr, (int)d->n_k_heads,
-                            (int)d->n_v_heads, (int)d->head_v_dim, eps, g->battn, di));
+                            (int)d->n_v_heads, (int)d->head_v_dim, eps, g->battn, di, D->gdn_f, g->f_tok,
+                            g->fst_ptr, (int)B >= g->factor_min_b));
     /* per-head gated RMSNorm (model.c:928-941) fused into the ssm_out input */
     qgpu_act gn;
     memset(&gn, 0, sizeof gn);
@@ -822,17 +846,49 @@ static void forward_body(qwen_model_t *m, const uint32_t *d_tokens, const float 
  * Eager launches read the constant tables at the host's values (d_posv + pos, d_curv +
  * cur), so no kernel sets them; a captured graph reads d_pos / d_cur, which are set
  * before each replay (with_cur: the sequence has GDN layers). */
+static int gdn_pending(const qwen_gpu_t *g)
+{
+    return g->fbase >= 0 ? (g->cur - g->fbase + NSLOT) % NSLOT : 0;
+}
+
+static void at(qwen_model_t *m, uint32_t pos, int with_cur);
+
+/* Writes the state the ring index selects into slot cur of every GDN layer when it is still kept
+ * as a base state plus factors (after a factor-form forward), so that nothing is pending.  The
+ * other states of that forward are then gone: model_rollback_to may only select this one. */
+static void gdn_settle(qwen_model_t *m)
+{
+    qwen_gpu_t *g = m->gpu;
+    if (!gdn_pending(g)) return;
+    at(m, m->pos, 1);
+    for (uint32_t il = 0; il < m->dims.n_layer; il++)
+        if (g->L[il].rec)
+            K(qgpu_gdn_materialize(g->L[il].ssm_ring, g->ssm_elems, NSLOT, g->cur_ptr, (int)m->dims.n_k_heads,
+                                   (int)m->dims.n_v_heads, (int)m->dims.head_v_dim, g->L[il].gdn_f, g->f_tok,
+                                   g->fst_ptr));
+    g->fbase = -1;
+    g->cur_base = (g->cur - 1 + NSLOT) % NSLOT;
+    g->last_B = 1;
+}
+
 static void at(qwen_model_t *m, uint32_t pos, int with_cur)
 {
     qwen_gpu_t *g = m->gpu;
+    const int P = gdn_pending(g);
     if (g->use_graphs && !g->prof_active) {
         K(qgpu_set_i32(g->d_pos, (int)pos));
-        if (with_cur) K(qgpu_set_i32(g->d_cur, g->cur));
+        if (with_cur) {
+            K(qgpu_set_i32(g->d_cur, g->cur));
+            K(qgpu_set_i32(g->d_fst, P));
+            K(qgpu_set_i32(g->d_fst + 1, g->fpar));
+        }
         g->pos_ptr = g->d_pos;
         g->cur_ptr = g->d_cur;
+        g->fst_ptr = g->d_fst;
     } else {
         g->pos_ptr = g->d_posv + pos;
         g->cur_ptr = g->d_curv + g->cur;
+        g->fst_ptr = g->d_fstv + 2 * (2 * P + g->fpar);
     }
 }
 
@@ -844,6 +900,12 @@ static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, u
     qwen_gpu_t *g = m->gpu;
     at(m, pos, 1);
     run_body(m, G_FWD, forward_body, d_tokens, NULL, B, d_logits, save_h);
+    if ((int)B >= g->factor_min_b) {              /* GDN state kept in slot cur, factors in the other buffer */
+        g->fbase = g->cur;
+        g->fpar ^= 1;
+    } else {
+        g->fbase = -1;
+    }
     g->cur_base = g->cur;
     g->cur = (g->cur + (int)B) % NSLOT;
     g->last_B = (int)B;
@@ -954,6 +1016,8 @@ void model_reset(qwen_model_t *m)
     }
     g->cur = g->cur_base = 0;
     g->last_B = 0;
+    g->fbase = -1;
+    g->fpar = 0;
     g->pend_ks = 0;
     g->pend = NULL;
     K(qgpu_set_i32(g->d_cur, 0));
@@ -1052,6 +1116,7 @@ void gdn_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool)
     qwen_gpu_t *g = m->gpu;
     K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
     glayer_t *D = &g->L[L - m->layers];
+    gdn_settle(m);                        /* this call updates one layer in place: every state a snapshot first */
     at(m, m->pos, 1);
     gdn_dev(m, D, 1);
     materialize(m);
@@ -1299,19 +1364,20 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
     if (call_begin(m)) return -1;
     if (bad_span(m, m->pos, B) || reps < 1 || !ms_verify || !ms_decode) return reject(m, "model_time_steps", m->pos, B);
     qwen_gpu_t *g = m->gpu;
-    const int cur0 = g->cur, base0 = g->cur_base, lastB0 = g->last_B;
+    gdn_settle(m);                      /* every rep then starts from the same snapshot state */
+    const int cur0 = g->cur, base0 = g->cur_base, lastB0 = g->last_B, fbase0 = g->fbase, fpar0 = g->fpar;
     const uint32_t pos = m->pos;
     void *e0, *e1;
     K(qgpu_event_create(&e0));
     K(qgpu_event_create(&e1));
     /* verify: B tokens at pos (states are restored to the ring index after each rep) */
     forward_dev(m, g->d_cand, B, pos, g->logits_b, 1);
-    g->cur = cur0; g->cur_base = base0; g->last_B = lastB0;
+    g->cur = cur0; g->cur_base = base0; g->last_B = lastB0; g->fbase = fbase0; g->fpar = fpar0;
     K(qgpu_event_record(e0));
     for (int r = 0; r < reps; r++) {
         forward_dev(m, g->d_cand, B, pos, g->logits_b, 1);
         K(qgpu_argmax(g->logits_b, m->cfg.vocab_size, m->cfg.vocab_size, (int)B, g->d_vtok));
-        g->cur = cur0; g->cur_base = base0; g->last_B = lastB0;
+        g->cur = cur0; g->cur_base = base0; g->last_B = lastB0; g->fbase = fbase0; g->fpar = fpar0;
     }
     K(qgpu_event_record(e1));
     K(qgpu_event_elapsed_ms(e0, e1, ms_verify));
@@ -1320,7 +1386,7 @@ int model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, fl
     for (int r = 0; r < reps; r++) {
         forward_dev(m, g->d_cand, 1, pos, g->logits1, 0);
         K(qgpu_argmax(g->logits1, m->cfg.vocab_size, m->cfg.vocab_size, 1, g->d_vtok));
-        g->cur = cur0; g->cur_base = base0; g->last_B = lastB0;
+        g->cur = cur0; g->cur_base = base0; g->last_B = lastB0; g->fbase = fbase0; g->fpar = fpar0;
     }
     K(qgpu_event_record(e1));
     K(qgpu_event_elapsed_ms(e0, e1, ms_decode));

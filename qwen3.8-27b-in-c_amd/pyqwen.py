@@ -292,6 +292,11 @@ class GpuLib:
                                ctypes.POINTER(i32), i32, i32, i32, f32, F32P, u64],
             "qgpu_gdn_fused_planes": [F32P, u64, i32, i32, F32P, F32P, u64, F32P, F32P, u64, i32, u64, F32P, F32P,
                                       F32P, u64, i32, ctypes.POINTER(i32), i32, i32, i32, f32, F32P, u64],
+            "qgpu_gdn_fused_factor": [F32P, u64, i32, i32, F32P, F32P, u64, F32P, F32P, u64, i32, u64, F32P, F32P,
+                                      F32P, u64, i32, ctypes.POINTER(i32), i32, i32, i32, f32, F32P, u64, F32P, u64,
+                                      ctypes.POINTER(i32), i32],
+            "qgpu_gdn_materialize": [F32P, u64, i32, ctypes.POINTER(i32), i32, i32, i32, F32P, u64,
+                                     ctypes.POINTER(i32)],
             "qgpu_attn_prep": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
                                ctypes.POINTER(i32), i32, i32, i32, i32, f32],
             "qgpu_attn_decode": [F32P, u64, F32P, F32P, ctypes.POINTER(i32), i32, i32, i32, i32, i32, F32P, u64],

@@ -171,6 +171,86 @@ def test_gdn_fused_gate_planes(gpu, planes):
                                        curb.i32(), nk, nv, hk, eps, ob.f32(), nv * hk) != 0   # planes overlap
     gpu.sync()
 
+@pytest.mark.parametrize("seq", [((8, 3), (8, 7), (1, 0)), ((6, 5), (4, 0), (8, 2)), ((5, 0), (5, 4), (3, 1)),
+                                 ((8, 7), (8, 7), (8, 7))])
+def test_gdn_factor_form_equals_snapshots(gpu, seq):
+    """qgpu_gdn_fused_factor: three calls (B tokens, then a rollback to the state after token j), the first two
+    keeping the state in rank-1 factor form and the third taking snapshots, give the outputs of every call, the
+    third call's state snapshots and the conv snapshots of the snapshot-only sequence (qgpu_gdn_fused_planes)
+    bit for bit; qgpu_gdn_materialize after the second call writes the state the snapshot sequence selects.
+    Config-3 shapes (48 v-heads, 16 k-heads, 128x128 states); ring slots wrap around."""
+    print(f"\n[gdn-factor] calls (B, j): {seq}", flush=True)
+    nk, nv, hk = 16, 48, 128
+    cd, eps = 2 * nk * hk + nv * hk, 1e-6
+    host = host_lib()
+    cw = host.synth_normal(cd * 4, 5, 4, 0.0, 0.5)
+    conv0 = host.synth_normal(cd * 4, 5, 5, 0.0, 0.5)
+    ssm0 = host.synth_normal(nv * hk * hk, 5, 6, 0.0, 0.01)
+    dtb = np.full(nv, 0.1, np.float32)
+    sa = -np.ones(nv, np.float32)
+    cstride, sstride = cd * 4, nv * hk * hk
+    ftok = ((nv + nk) * hk + nv + 3) // 4 * 4
+    cwb, dtbb, sab = gpu.put(cw), gpu.put(dtb), gpu.put(sa)
+    cur0 = 6
+    rings = []
+    for _ in range(2):
+        cring = gpu.put(np.zeros(NSLOT * cstride, np.float32))
+        sring = gpu.put(np.zeros(NSLOT * sstride, np.float32))
+        cring.upload(conv0, cur0 * cstride * 4)
+        sring.upload(ssm0, cur0 * sstride * 4)
+        rings.append((cring, sring))
+    fbuf = gpu.put(np.zeros(2 * 8 * ftok, np.float32))
+    fst = gpu.put(np.zeros(2, np.int32))
+    curs = [gpu.put(np.array([cur0], np.int32)) for _ in range(2)]
+    ob = gpu.buf(8 * nv * hk * 4)
+    cur, pend, par = cur0, 0, 0
+    for call, (B, j) in enumerate(seq):
+        x = host.synth_normal(B * cd, 6, call).reshape(B, cd)
+        br = host.synth_normal(B * nv, 6, 10 + call).reshape(B, nv)
+        ar = host.synth_normal(B * nv, 6, 20 + call).reshape(B, nv)
+        xb, bb, ab = gpu.put(x), gpu.put(br), gpu.put(ar)
+        cring, sring = rings[0]
+        gpu.ok(gpu.L.qgpu_gdn_fused_planes(xb.f32(), cd, B, cd, cwb.f32(), cring.f32(), cstride, bb.f32(), ab.f32(), nv,
+                                           1, 0, dtbb.f32(), sab.f32(), sring.f32(), sstride, NSLOT, curs[0].i32(), nk,
+                                           nv, hk, eps, ob.f32(), nv * hk))
+        o_snap = ob.download(np.float32, B * nv * hk)
+        factor = call < 2
+        fst.upload(np.array([pend, par], np.int32))
+        cring, sring = rings[1]
+        gpu.ok(gpu.L.qgpu_gdn_fused_factor(xb.f32(), cd, B, cd, cwb.f32(), cring.f32(), cstride, bb.f32(), ab.f32(),
+                                           nv, 1, 0, dtbb.f32(), sab.f32(), sring.f32(), sstride, NSLOT, curs[1].i32(),
+                                           nk, nv, hk, eps, ob.f32(), nv * hk, fbuf.f32(), ftok, fst.i32(),
+                                           1 if factor else 0))
+        o_fac = ob.download(np.float32, B * nv * hk)
+        assert np.array_equal(o_snap, o_fac), f"call {call}: outputs differ"
+        # conv snapshots are written in both forms
+        ca, cb = rings[0][0].download(np.float32).reshape(NSLOT, -1), rings[1][0].download(np.float32).reshape(NSLOT, -1)
+        for b in range(B):
+            assert np.array_equal(ca[(cur + 1 + b) % NSLOT], cb[(cur + 1 + b) % NSLOT]), (call, b)
+        if factor:
+            pend, par = j + 1, par ^ 1
+        else:
+            sa_, sb_ = rings[0][1].download(np.float32).reshape(NSLOT, -1), rings[1][1].download(np.float32).reshape(NSLOT, -1)
+            for b in range(B):
+                assert np.array_equal(sa_[(cur + 1 + b) % NSLOT], sb_[(cur + 1 + b) % NSLOT]), (call, b)
+            pend = 0
+        cur = (cur + 1 + j) % NSLOT
+        for cb_ in curs:
+            gpu.ok(gpu.L.qgpu_set_i32(cb_.i32(), cur))
+        if call == 1:
+            # the state the snapshot sequence selects, written from the kept factors
+            fst.upload(np.array([pend, par], np.int32))
+            mat = gpu.put(rings[1][1].download(np.float32))
+            gpu.ok(gpu.L.qgpu_gdn_materialize(mat.f32(), sstride, NSLOT, curs[1].i32(), nk, nv, hk, fbuf.f32(), ftok,
+                                              fst.i32()))
+            want = rings[0][1].download(np.float32).reshape(NSLOT, -1)[cur]
+            assert np.array_equal(mat.download(np.float32).reshape(NSLOT, -1)[cur], want)
+            mat.close()
+        print(f"  call {call}: B={B} ({'factor' if factor else 'snapshot'} form) identical; rollback to {j}",
+              flush=True)
+    gpu.sync()
+
+
 def test_rmsnorm_gated(gpu):
     rng = np.random.default_rng(1)
     rows, n = 12, 128
