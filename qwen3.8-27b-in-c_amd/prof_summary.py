@@ -361,8 +361,14 @@ def step_roles(step, B, P):
                 n_part = 0
         elif k == "k_gdn_fused":
             state = d["VH"] * d["HS"] * d["HS"] * f4
-            role = "GDN conv + recurrence + snapshots"
-            by = (1 + B) * state + (1 + B) * d["CONV"] * 3 * f4 + B * (d["CONV"] + d["VD"] + 2 * d["VH"]) * f4
+            io = (1 + B) * d["CONV"] * 3 * f4 + B * (d["CONV"] + d["VD"] + 2 * d["VH"]) * f4
+            if B >= 5:      # rank-1 factor form (the model's default from 5 tokens): one state in, one out
+                ftok = (d["VD"] + d["KD"] + d["VH"]) * f4
+                role = "GDN conv + recurrence (factor form)"
+                by = 2 * state + 2 * B * ftok + io
+            else:
+                role = "GDN conv + recurrence + snapshots"
+                by = (1 + B) * state + io
         elif k.startswith("k_attn_span"):
             role = "attention spans (KV read)"
             by = P * 2 * d["KV"] * f4 + B * (2 * d["QD"] + 2 * d["KV"]) * f4
