@@ -203,7 +203,7 @@ uint32_t model_generate_greedy(qwen_model_t *m, const uint32_t *prompt, uint32_t
 /* One timed verify step (B tokens at the current position) and one timed decode
  * step, on device buffers (benchmark support); the model state is restored.  If the
  * last forward kept its recurrent states in factor form, the selected state is
- * written out first, and model_rollback_to may afterwards only select it (b = 0). */
+ * written out first, and model_rollback_to is refused until the next forward. */
 int  model_time_steps(qwen_model_t *m, uint32_t B, int reps, float *ms_verify, float *ms_decode, float *ms_draft);
 
 /* Status of the last model call: 0 = done, -1 = rejected on the host (bad

@@ -855,7 +855,7 @@ static void at(qwen_model_t *m, uint32_t pos, int with_cur);
 
 /* Writes the state the ring index selects into slot cur of every GDN layer when it is still kept
  * as a base state plus factors (after a factor-form forward), so that nothing is pending.  The
- * other states of that forward are then gone: model_rollback_to may only select this one. */
+ * other states of that forward are then gone: model_rollback_to is refused until the next forward. */
 static void gdn_settle(qwen_model_t *m)
 {
     qwen_gpu_t *g = m->gpu;
@@ -867,8 +867,7 @@ static void gdn_settle(qwen_model_t *m)
                                    (int)m->dims.n_v_heads, (int)m->dims.head_v_dim, g->L[il].gdn_f, g->f_tok,
                                    g->fst_ptr));
     g->fbase = -1;
-    g->cur_base = (g->cur - 1 + NSLOT) % NSLOT;
-    g->last_B = 1;
+    g->last_B = 0;
 }
 
 static void at(qwen_model_t *m, uint32_t pos, int with_cur)

@@ -606,6 +606,64 @@ def test_model_rollback_vs_reference(gpu, tiny):
         assert rel_err(lb[b], ref[b]) < 1e-3 and lb[b].argmax() == ref[b].argmax(), b
 
 
+def test_gdn_factor_form_model_matches_snapshots(gpu, tiny):
+    """The model with the GDN factor form for batches of 5..8 tokens (the default) against the same model
+    with snapshots everywhere (QWEN_GDN_FACTOR_MIN_B=9): batches of 8, 6 and 5 with rollbacks between them,
+    single-token steps after a factor-form batch (the kept tokens applied in a snapshot-form call), the step
+    timer after a factor-form batch (which writes the selected state out and then allows only b = 0), and a
+    last batch: every logit row and hidden state bit-identical."""
+    path, z = tiny
+    p = z["prompt"]
+    models = []
+    for fmin in ("9", None):
+        if fmin is None:
+            os.environ.pop("QWEN_GDN_FACTOR_MIN_B", None)
+        else:
+            os.environ["QWEN_GDN_FACTOR_MIN_B"] = fmin
+        try:
+            models.append(pyqwen.Model(path, int(z["n_ctx"])))
+        finally:
+            os.environ.pop("QWEN_GDN_FACTOR_MIN_B", None)
+    snap, fac = models
+
+    def both(fn):
+        a, b = fn(snap), fn(fac)
+        assert snap.status() == 0 and fac.status() == 0
+        return a, b
+    pos = 0
+    for i in range(3):
+        a, b = both(lambda m: m.forward(int(p[i]), i))
+        assert np.array_equal(a, b)
+    pos = 3
+    for B, j in ((8, 3), (6, 5), (5, 0), (8, 7)):
+        a, b = both(lambda m: m.forward_batch(p[pos:pos + B], pos))
+        assert np.array_equal(a, b), (B, j)
+        assert np.array_equal(snap.h_save(B), fac.h_save(B)), (B, j)
+        both(lambda m: m.rollback_to(j))
+        pos += j + 1
+        both(lambda m: setattr(m, "pos", pos))
+        print(f"  batch of {B} at {pos - j - 1}, rollback to {j}: identical", flush=True)
+    a, b = both(lambda m: m.forward(int(p[pos]), pos))      # applies the 8 kept tokens of the last batch
+    assert np.array_equal(a, b)
+    pos += 1
+    a, b = both(lambda m: m.forward_batch(p[pos:pos + 6], pos))
+    assert np.array_equal(a, b)
+    pos += 6
+    both(lambda m: m.time_steps(5, 2))                        # writes the selected state out (factor form)
+    fac.rollback_to(0)
+    assert fac.status() == -1                                 # the other states of that batch are gone
+    for m in models:
+        m.pos = pos
+    a, b = both(lambda m: m.forward_batch(p[pos:pos + 4], pos))
+    assert np.array_equal(a, b)
+    both(lambda m: m.rollback_to(1))                          # a snapshot-form batch: any b again
+    pos += 2
+    a, b = both(lambda m: m.forward(int(p[pos]), pos))
+    assert np.array_equal(a, b)
+    for m in models:
+        m.close()
+
+
 def test_model_rollback_rejects_states_not_written(gpu, tiny):
     """model_rollback_to(b) selects the state after token b of the last batch: b at or past that
     batch's B is refused on the host (status -1, ring index unchanged), and a valid rollback after
