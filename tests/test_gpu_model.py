@@ -765,18 +765,20 @@ def test_model_spec_begin_run_resumes(gpu, tiny, mode):
     assert np.array_equal(got, toks)
 
 
+@pytest.mark.parametrize("k", [3, 5])
 @pytest.mark.parametrize("mode", [0, 2])
-def test_model_graphs_match_eager(gpu, tiny, mode):
+def test_model_graphs_match_eager(gpu, tiny, mode, k):
     """Replayed launch sequences (HIP graphs) give bit-identical streams and
     logits to kernel-by-kernel launches: every cycle replays the draft, verify and
     anchor graphs at new positions and ring slots, with host reads between replays,
-    then a host-API forward runs after the device loop."""
+    then a host-API forward runs after the device loop.  k = 5 verifies 6 tokens, so its
+    GDN states are in factor form (the kept tokens and factor buffer read from device memory)."""
     path, z = tiny
     res = []
     for graphs in (False, True):
         m = pyqwen.Model(path, int(z["n_ctx"]))
         m.set_graphs(graphs)
-        toks, js, st = m.generate_spec(z["prompt"][:20], 40, 3, force_accept=mode)
+        toks, js, st = m.generate_spec(z["prompt"][:20], 40, k, force_accept=mode)
         lb = m.forward_batch(z["prompt"][20:24], m.pos, 1)
         res.append((toks.copy(), js.copy(), lb.copy()))
         m.close()
