@@ -1,6 +1,6 @@
 """Batched GEMV at the model's real shapes for every matrix-core weight format
 (the quant-format sweep: 5120->17408, 17408->5120 and the 5120->248320 lm_head,
-B = 1, 4, 8), and on outlier-heavy activations.
+B = 1, 2, 4, 8), and on outlier-heavy activations.
 
 Checker: the oracle's gemv_batch / gemv_rows_batch (bit-exact with the
 reference's AVX2 kernels).  Bar: 1e-3 normwise relative (max|d| / max|ref|).
@@ -43,11 +43,11 @@ def run(gpu, T, x, n, ne1):
 def test_gemv_sweep_shapes_vs_oracle(gpu, fmt, shape):
     ne0, ne1 = shape
     t = FORMATS[fmt]
-    print(f"\n[sweep] {fmt} {ne0}->{ne1} B=1,4,8", flush=True)
+    print(f"\n[sweep] {fmt} {ne0}->{ne1} B=1,2,4,8", flush=True)
     W, T = matrix(gpu, t, ne0, ne1)
     x = host_lib().synth_normal(8 * ne0, 78, t).reshape(8, ne0)
     ref = O.gemv(t, W, ne0, ne1, x, 8, threads=16)
-    for n in (1, 4, 8):
+    for n in (1, 2, 4, 8):
         got = run(gpu, T, x, n, ne1)
         e = rel_err(got, ref[:n])
         print(f"  B={n}: rel err {e:.2e}", flush=True)
@@ -67,7 +67,7 @@ def test_gemv_ksplit_17408_vs_oracle(gpu, fmt):
     assert ks >= 2
     x = host_lib().synth_normal(8 * ne0, 79, t).reshape(8, ne0)
     ref = O.gemv(t, W, ne0, ne1, x, 8, threads=16)
-    for n in (1, 4, 8):
+    for n in (1, 2, 4, 8):
         xb, pb = gpu.put(np.ascontiguousarray(x[:n])), gpu.buf(ks * n * ne1 * 4)
         a = pyqwen.Act()
         a.kind, a.x, a.ldx = pyqwen.ACT_COPY, xb.f32(), ne0
@@ -86,7 +86,7 @@ LM_ROWS = [(0, 512), (61_440, 61_952), (124_160, 124_672), (186_880, 187_392), (
 def test_gemv_lm_head_vs_oracle(gpu, fmt):
     ne0, ne1 = 5120, 248_320
     t = FORMATS[fmt]
-    print(f"\n[lm_head] {fmt} {ne0}->{ne1} ({ne1 // 16} tiles) B=1,4,8", flush=True)
+    print(f"\n[lm_head] {fmt} {ne0}->{ne1} ({ne1 // 16} tiles) B=1,2,4,8", flush=True)
     W, T = matrix(gpu, t, ne0, ne1)
     x = host_lib().synth_normal(8 * ne0, 80, t).reshape(8, ne0)
     L = O.lib()
@@ -96,7 +96,7 @@ def test_gemv_lm_head_vs_oracle(gpu, fmt):
         L.or_gemv_rows_batch(t, W.ctypes.data_as(ctypes.c_void_p), ne0, O.fptr(x), ne0, 8, O.fptr(o), ne1, r0, r1)
         refs.append(o[:, r0:r1].copy())
     ref = np.concatenate(refs, axis=1)
-    for n in (1, 4, 8):
+    for n in (1, 2, 4, 8):
         got = run(gpu, T, x, n, ne1)
         sel = np.concatenate([got[:, r0:r1] for r0, r1 in LM_ROWS], axis=1)
         e = rel_err(sel, ref[:n])
@@ -128,7 +128,7 @@ def test_gemv_outlier_activations(gpu, fmt, spike):
     |err_r| <= sum_sb 2^-22 max_sb sum_{i in sb} |W_ri| + fp32 accumulation (<= 1e-6 sum |W_ri x_i|)."""
     t = FORMATS[fmt]
     ne0, ne1 = 5120, 2048
-    print(f"\n[outlier] {fmt} spike {spike:g} B=1,4,8", flush=True)
+    print(f"\n[outlier] {fmt} spike {spike:g} B=1,2,4,8", flush=True)
     W = host_lib().synth_matrix(t, ne0, ne1, 81, 400 + t, 0.02)
     T = gpu.tensor(W, t, ne0, ne1)
     x = outlier_x(8, ne0, int(spike) + t, spike)
@@ -137,7 +137,7 @@ def test_gemv_outlier_activations(gpu, fmt, spike):
     mx = np.abs(x.astype(np.float64)).reshape(8, ne0 // 256, 256).max(2)       # [tok][sb]
     bound = (absW.reshape(ne1, ne0 // 256, 256).sum(2) @ mx.T).T * 2.0 ** -22   # [tok][rows]
     bound += 1e-6 * (np.abs(x.astype(np.float64)) @ absW.T)
-    for n in (1, 4, 8):
+    for n in (1, 2, 4, 8):
         got = run(gpu, T, x, n, ne1)
         e = rel_err(got, ref[:n])
         print(f"  B={n}: rel err {e:.2e}", flush=True)
@@ -165,7 +165,7 @@ def test_gemv_pair_split_tail(gpu, fmt, shape):
     ref = O.gemv(t, W, ne0, ne1, x, 8, threads=16)
     xb = gpu.put(np.ascontiguousarray(x))
     nan = np.full(8 * ne1, np.nan, np.float32)
-    for n in (1, 4, 8):
+    for n in (1, 2, 4, 8):
         ob = gpu.put(nan[:n * ne1])
         gpu.ok(gpu.L.qgpu_gemv_batch(T.h, xb.f32(), ne0, n, ob.f32(), ne1, 0))
         got = ob.download(np.float32).reshape(n, ne1)
