@@ -492,13 +492,14 @@ def bench_longctx(args, gpu, host, roof, gemv_call_gbs):
 SAMPLE_CFG = (0.8, 0.9, 40, 1.1, 7)        # temp, top_p, top_k, repeat penalty, seed
 
 
-ATTN_CASES = [(800, 4), (800, 8), (8392, 4), (8392, 6), (8392, 8)]     # (KV positions before the call, B)
+ATTN_CASES = [(800, 1), (800, 4), (800, 8), (8392, 4), (8392, 6), (8392, 8)]     # (KV positions before the call, B)
 
 
 def bench_attn(args, gpu):
     """The model's attention call alone at the 27B shapes (24 query / 4 KV heads, head_dim 256, RoPE on 64
     dims): qgpu_attn_fused_act (span kernel + combine with the o-projection digits) at several context
-    lengths and batch sizes, random caches; per case K calls captured in a HIP graph, the median of five
+    lengths and batch sizes, random caches, with the live-context bound the model passes
+    (qgpu_attn_fused_act_live); per case K calls captured in a HIP graph, the median of five
     timed replays (--eager: K calls launched from the host, five timed series).  Bytes per call: the K and
     V rows of every position plus q, k, v in and out."""
     L = gpu.L
@@ -519,12 +520,15 @@ def bench_attn(args, gpu):
         k = gpu.put(rng.standard_normal((B, nkv * hd)).astype(np.float32))
         v = gpu.put(rng.standard_normal((B, nkv * hd)).astype(np.float32))
         out, posb = gpu.buf(B * nh * hd * 4), gpu.put(np.array([pos], np.int32))
+        # the live-context bound the model gives this call (the head split while the context allows)
+        bound = L.qgpu_attn_split_bound(n_ctx, B, nh, nkv)
+        live = bound if pos + B <= bound else 0
 
         def calls():
             for _ in range(args.steps):
-                gpu.ok(L.qgpu_attn_fused_act(q.f32(), nh * 2 * hd, k.f32(), v.f32(), nkv * hd, qw.f32(), kw.f32(),
-                                             kc.f32(), vc.f32(), rc.f32(), rs.f32(), rope_dim, posb.i32(), n_ctx, B,
-                                             nh, nkv, hd, eps, out.f32(), nh * hd))
+                gpu.ok(L.qgpu_attn_fused_act_live(q.f32(), nh * 2 * hd, k.f32(), v.f32(), nkv * hd, qw.f32(),
+                                                  kw.f32(), kc.f32(), vc.f32(), rc.f32(), rs.f32(), rope_dim,
+                                                  posb.i32(), n_ctx, B, nh, nkv, hd, eps, out.f32(), nh * hd, live))
         for _ in range(args.warmup):
             calls()
         if args.eager:                  # no graph: K calls launched from the host between two events
@@ -539,7 +543,8 @@ def bench_attn(args, gpu):
         else:
             reps = sorted(ms / args.steps * 1e3 for ms in graph_ms(gpu, calls, e0, e1, ROOF_TIMED, ROOF_UNTIMED))
         by = (pos + B) * 2 * nkv * hd * 4 + B * (nh * 2 * hd + 2 * nkv * hd + nh * hd) * 4
-        rows.append({"pos": pos, "B": B, "us": round(reps[ROOF_TIMED // 2], 3), "us_range": [round(reps[0], 3),
+        rows.append({"pos": pos, "B": B, "head_split": live > 0, "us": round(reps[ROOF_TIMED // 2], 3),
+                     "us_range": [round(reps[0], 3),
                      round(reps[-1], 3)], "bytes": by, "gbs": round(by / (reps[ROOF_TIMED // 2] * 1e-6) / 1e9, 1)})
         log(f"attention pos {pos} B {B}: {rows[-1]['us']} us per call, {rows[-1]['gbs']} GB/s")
     return rows

@@ -312,6 +312,23 @@ int  qgpu_attn_fused_act(const float *q, uint64_t ldq, const float *k, const flo
                          const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
                          const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
                          int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out, uint64_t ldo);
+/* qgpu_attn_fused_act for a caller that knows a bound on the live context: live_hi >= pos + B
+ * for every position the launch will see (a captured graph's replays included).  While
+ * live_hi <= qgpu_attn_split_bound(ctx_bound, B, n_head, n_kv), the span blocks of each kv
+ * head are doubled, each serving half of its query heads; the results are bit-identical to
+ * qgpu_attn_fused_act.  live_hi = 0: no bound (qgpu_attn_fused_act); QGPU_E_ARG when
+ * 0 < live_hi < B or live_hi > ctx_bound.  (No reference counterpart: the reference's
+ * attention loops over heads on the CPU, model.c:353-406.) */
+int  qgpu_attn_fused_act_live(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                              const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                              const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,
+                              int ctx_bound, int B, int n_head, int n_kv, int head_dim, float eps, float *out,
+                              uint64_t ldo, int live_hi);
+/* The largest live context (positions, <= ctx_bound) up to which qgpu_attn_fused_act_live splits
+ * the query heads of B tokens over two blocks per span; 0 when it never does (where the split
+ * would not take fewer 16-row tiles, e.g. B = 1 or 2 with 6 query heads per kv head).
+ * Initialises the library when needed. */
+int  qgpu_attn_split_bound(int ctx_bound, int B, int n_head, int n_kv);
 /* allocates the attention workspace for ctx_bound positions now (no allocation later);
  * QGPU_E_RANGE when the KV cache does not fit the kernels' offsets (qgpu_attn_cache_fits) */
 int  qgpu_attn_reserve(int ctx_bound, int n_kv);

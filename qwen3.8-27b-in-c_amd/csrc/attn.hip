@@ -13,6 +13,7 @@
 // Positions come from device memory (*pos_dev) so the launch sequence can be
 // captured in a graph and replayed at any position.
 #include "qgpu_internal.h"
+#include <climits>
 
 #define ATT_HD   256
 #define ATT_MAXQ 64             // row stride of the span partials
@@ -130,7 +131,7 @@ struct AttnArgs {
 
 // live tiles ntl, tiles per span tps and spans with work nsl, from the device
 // position (the span kernel and the combine derive the same split)
-static __device__ __forceinline__ void span_split(int pos0, int B, int nspan, int &ntl, int &tps, int &nsl)
+static __host__ __device__ __forceinline__ void span_split(int pos0, int B, int nspan, int &ntl, int &tps, int &nsl)
 {
     ntl = (pos0 + B + ATT_TP - 1) / ATT_TP;
     const int ns = ntl < nspan ? ntl : nspan;
@@ -209,9 +210,10 @@ static __device__ __forceinline__ v4f mfma_split_b(const SplitB &a, const SplitB
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.hi, b.hi, c, 0, 0, 0);
 }
 
-template <int FUSED, int NRT, int ATT_NWV>
+template <int FUSED, int NRT, int ATT_NWV, int HS>
 __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 {
+    static_assert(HS == 1 || HS == 2, "one block or two per (kv head, span)");
     constexpr int ATT_DW = ATT_HD / ATT_NWV;      // head dims per wave
     constexpr int ATT_NQ = ATT_DW / 16;           // float4 operand loads per row and 16-dim output tiles per wave
     typedef typename VSlice<ATT_NQ>::T vqf;
@@ -227,14 +229,32 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     // P.V lanes read their four positions' parts with one 8-byte load each
     __shared__ __attribute__((aligned(16))) uint16_t Ph[2 * NRT * 256], Plo[2 * NRT * 256];
     __shared__ __attribute__((aligned(16))) float Al[2 * NRT * 16];    // rescale factors [buf][row]
-    const int g = blockIdx.x, s = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, gq = lane >> 4;
-    const int per = p.n_head / p.n_kv, QH = per * p.B;
-    // r / per for the row indices 0 <= r < 64 of this kernel: (r * ceil(2^16 / per)) >> 16 is exact there
-    // (the rounding up adds less than r / 2^16 < 1 / per to r / per)
-    const uint32_t inv_per = (65536u + (uint32_t)per - 1u) / (uint32_t)per;
+    // HS = 2: the query heads of a kv head are split between two blocks, halves hh = 0, 1, each
+    // serving per / 2 heads of every token.  Blocks L and L + 8 (one XCD under round-robin dispatch,
+    // so the second finds the K/V rows in the same L2) take the two halves of one (kv head, span)
+    // pair u, pairs in span order (the blocks of spans with work come first).
+    int g, s, hh = 0;
+    if (HS == 1) {
+        g = blockIdx.x;
+        s = blockIdx.y;
+    } else {
+        const int L = blockIdx.x, q8 = L >> 3, u = (q8 >> 1) * 8 + (L & 7);
+        hh = q8 & 1;
+        if (u >= p.n_kv * p.nspan) return;
+        g = u % p.n_kv;
+        s = u / p.n_kv;
+    }
+    const int per = p.n_head / p.n_kv, pr = per / HS, QH = pr * p.B;
+    // r / pr for the row indices 0 <= r < 64 of this kernel: (r * ceil(2^16 / pr)) >> 16 is exact there
+    // (the rounding up adds less than r / 2^16 < 1 / pr to r / pr)
+    const uint32_t inv_per = (65536u + (uint32_t)pr - 1u) / (uint32_t)pr;
     auto divp = [&](int r) { return (int)(((uint32_t)r * inv_per) >> 16); };
+    // block row r (token b = r / pr, head j = r - b pr of the block's) is row b per + hh pr + j of
+    // the kv head's partials and query head g per + hh pr + j
+    auto rfull = [&](int r) { return HS == 1 ? r : r + divp(r) * (per - pr) + hh * pr; };
     const uint64_t kvrow = (uint64_t)p.n_kv * ATT_HD, hoff = (uint64_t)g * ATT_HD;
     const int d0 = ATT_DW * wv;
 
@@ -251,7 +271,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
             const int e = tid + u * ATT_NWV * 64, r = e >> 6, d4 = e & 63;
             qv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             if (r < QH) {
-                const int b = divp(r), h = g * per + (r - b * per);
+                const int b = divp(r), h = g * per + hh * pr + (r - b * pr);
                 qv[u] = *(const float4 *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + 4 * d4);
             }
         }
@@ -270,7 +290,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
 #pragma unroll
         for (int rt = 0; rt < NRT; rt++) {
             const int r = rt * 16 + n;
-            const int b = divp(r), h = g * per + (r - b * per);
+            const int b = divp(r), h = g * per + hh * pr + (r - b * pr);
 #pragma unroll
             for (int q = 0; q < ATT_NQ; q++)
                 qop[rt][q] = r < QH ? *(const v4f *)(p.q + (uint64_t)b * p.ldq + (uint64_t)h * 2 * ATT_HD + d0 + 16 * q + 4 * gq)
@@ -392,7 +412,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
         }
         __syncthreads();
         // cache rows of the new positions this span holds (each position is in exactly one span)
-        if (has_new)
+        if (has_new && hh == 0)
             for (int e = tid; e < p.B * 64; e += ATT_NWV * 64) {
                 const int b = e >> 6, d4 = e & 63, t = pos0 + b;
                 if (t < posA || t >= posB) continue;
@@ -535,8 +555,9 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
     for (int j = 0; j < SM_UPW; j++) {
         const int R = 4 * (wv + j * ATT_NWV) + (lane >> 4);
         if ((lane & 15) == 0 && wv + j * ATT_NWV < NRT * 4 && R < QH) {
-            ml[2 * R] = sm[j];
-            ml[2 * R + 1] = sl[j];
+            const int rf = rfull(R);
+            ml[2 * rf] = sm[j];
+            ml[2 * rf + 1] = sl[j];
         }
     }
 #pragma unroll
@@ -548,7 +569,7 @@ __global__ __launch_bounds__(ATT_NWV * 64) void k_attn_span(const AttnArgs p)
                 vqf ov;
 #pragma unroll
                 for (int c = 0; c < ATT_NQ; c++) ov[c] = oacc[rt][c][w];
-                *(vqf *)(o + (uint64_t)r * ATT_HD + d0 + ATT_NQ * n) = ov;
+                *(vqf *)(o + (uint64_t)rfull(r) * ATT_HD + d0 + ATT_NQ * n) = ov;
             }
         }
     }
@@ -705,22 +726,50 @@ extern "C" int qgpu_attn_prep(float *q, uint64_t ldq, const float *k, const floa
     return QGPU_OK;
 }
 
-static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out, uint64_t ldo, int act = 0)
+// The head split: two span blocks per (kv head, span), each serving half of the kv head's query
+// heads, where that takes fewer row tiles (6 heads x 3..8 tokens: 2 -> 1 or 3 -> 2) and the live
+// context has few spans: 2 n_kv nsl <= compute units for every live context up to the bound
+// returned, in positions (0: never).  Measured at 800 positions, 6 heads per kv head: B = 4 12.7 ->
+// 11.2 us per call (span kernel + combine), B = 8 15.9 -> 14.1 us; at 8392 positions (236 span
+// blocks already) it is 4% slower, and at B = 1 (one row tile either way) 20% slower.
+#ifndef ATT_HSPLIT
+#define ATT_HSPLIT 1
+#endif
+static int att_split_bound(int nspan, int B, int n_head, int n_kv)
+{
+    const int per = n_head / n_kv;
+    if (!ATT_HSPLIT || per % 2 || (per * B + 15) / 16 <= ((per / 2) * B + 15) / 16 || qg::n_cu <= 0) return 0;
+    if (2 * n_kv * nspan <= qg::n_cu) return INT_MAX;  // every span count qualifies
+    int bound = 0;
+    for (int pos = 0;; pos += ATT_TP) {               // live contexts pos + B, one tile at a time
+        int ntl, tps, nsl;
+        span_split(pos, B, nspan, ntl, tps, nsl);
+        if (2 * n_kv * nsl > qg::n_cu) return bound;
+        bound = ntl * ATT_TP;
+    }
+}
+
+static int attn_launch(const AttnArgs &a0, int fused, int ctx_bound, float *out, uint64_t ldo, int act = 0,
+                       int live_hi = 0)
 {
     AttnArgs a = a0;
     int rc = attn_ws(ctx_bound, a.n_kv, &a.nspan);
     if (rc) return rc;
     a.pml = (float *)qg::ws_attn;
     a.po = a.pml + (size_t)a.n_kv * a.nspan * ATT_MAXQ * 2;
-    const int nrt = ((a.n_head / a.n_kv) * a.B + 15) / 16;
+    const int hs = fused && live_hi >= a.B && live_hi <= att_split_bound(a.nspan, a.B, a.n_head, a.n_kv) ? 2 : 1;
+    const int nrt = ((a.n_head / a.n_kv / hs) * a.B + 15) / 16;
     // 8 waves of 32 dims for one or two row tiles, 4 waves of 64 dims for three (same-box A/B: each
     // the faster one by ~0.5%)
-    const dim3 grid(a.n_kv, a.nspan);
-#define ATT_GO(F_, R_) hipLaunchKernelGGL((k_attn_span<F_, R_, (R_ < 3 ? 8 : ATT_NW3)>), grid, \
-                                          dim3((R_ < 3 ? 8 : ATT_NW3) * 64), 0, qg::stream, a)
-#define ATT_RTS(F_) do { switch (nrt) { case 1: ATT_GO(F_, 1); break; case 2: ATT_GO(F_, 2); break; \
-                         default: ATT_GO(F_, 3); break; } } while (0)
-    if (fused) ATT_RTS(1); else ATT_RTS(0);
+    const int units = a.n_kv * a.nspan;
+    const dim3 grid = hs == 1 ? dim3(a.n_kv, a.nspan) : dim3(16 * ((units + 7) / 8));
+#define ATT_GO(F_, R_, H_) hipLaunchKernelGGL((k_attn_span<F_, R_, (R_ < 3 ? 8 : ATT_NW3), H_>), grid, \
+                                              dim3((R_ < 3 ? 8 : ATT_NW3) * 64), 0, qg::stream, a)
+#define ATT_RTS(F_) do { switch (nrt) { case 1: ATT_GO(F_, 1, 1); break; case 2: ATT_GO(F_, 2, 1); break; \
+                         default: ATT_GO(F_, 3, 1); break; } } while (0)
+    if (hs == 2) { if (nrt == 1) ATT_GO(1, 1, 2); else ATT_GO(1, 2, 2); }
+    else if (fused) ATT_RTS(1);
+    else ATT_RTS(0);
 #undef ATT_RTS
 #undef ATT_GO
     QG_LAUNCH_CHECK();
@@ -755,7 +804,8 @@ extern "C" int qgpu_attn_decode(const float *q, uint64_t ldq, const float *kcach
 static int attn_fused(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
                       const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
                       const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev, int ctx_bound,
-                      int B, int n_head, int n_kv, int head_dim, float eps, float *out, uint64_t ldo, int act)
+                      int B, int n_head, int n_kv, int head_dim, float eps, float *out, uint64_t ldo, int act,
+                      int live_hi = 0)
 {
     int rc = qg::ensure_init();
     if (rc) return rc;
@@ -772,7 +822,8 @@ static int attn_fused(const float *q, uint64_t ldq, const float *k, const float 
     a.q = q; a.ldq = ldq; a.k = k; a.v = v; a.ldkv = ldkv; a.qw = q_norm_w; a.kw = k_norm_w;
     a.rcos = rope_cos; a.rsin = rope_sin; a.kc = kcache; a.vc = vcache; a.pos_dev = pos_dev;
     a.half = rope_dim / 2; a.B = B; a.n_head = n_head; a.n_kv = n_kv; a.eps = eps;
-    return attn_launch(a, 1, ctx_bound, out, ldo, act);
+    if (live_hi && (live_hi < B || live_hi > ctx_bound)) return QGPU_E_ARG;
+    return attn_launch(a, 1, ctx_bound, out, ldo, act, live_hi);
 }
 
 extern "C" int qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
@@ -793,6 +844,25 @@ extern "C" int qgpu_attn_fused_act(const float *q, uint64_t ldq, const float *k,
 {
     return attn_fused(q, ldq, k, v, ldkv, q_norm_w, k_norm_w, kcache, vcache, rope_cos, rope_sin, rope_dim, pos_dev,
                       ctx_bound, B, n_head, n_kv, head_dim, eps, out, ldo, 1);
+}
+
+extern "C" int qgpu_attn_fused_act_live(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
+                                        const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
+                                        const float *rope_cos, const float *rope_sin, int rope_dim,
+                                        const int *pos_dev, int ctx_bound, int B, int n_head, int n_kv, int head_dim,
+                                        float eps, float *out, uint64_t ldo, int live_hi)
+{
+    return attn_fused(q, ldq, k, v, ldkv, q_norm_w, k_norm_w, kcache, vcache, rope_cos, rope_sin, rope_dim, pos_dev,
+                      ctx_bound, B, n_head, n_kv, head_dim, eps, out, ldo, 1, live_hi);
+}
+
+extern "C" int qgpu_attn_split_bound(int ctx_bound, int B, int n_head, int n_kv)
+{
+    if (qg::ensure_init()) return 0;
+    if (ctx_bound < 1 || B < 1 || n_kv < 1 || n_head % n_kv) return 0;
+    const int nt = (ctx_bound + ATT_TP - 1) / ATT_TP, nspan = nt < ATT_NSPAN ? nt : ATT_NSPAN;
+    const int b = att_split_bound(nspan, B, n_head, n_kv);
+    return b < ctx_bound ? b : ctx_bound;
 }
 
 // Reserve the attention workspace up front (so later calls never allocate,

@@ -78,10 +78,14 @@ struct qwen_gpu {
     float *part, *pend;
     int pend_ks;
     uint32_t pend_B;
+    /* attention span blocks split a kv head's query heads while the live context of a B-token
+     * forward is at most att_split[B] positions (qgpu_attn_split_bound; 0: never); att_live is
+     * the bound the next body's attention launches are given (att_split[B] or 0) */
+    int att_split[QGPU_MAX_B + 1], att_live;
     /* replayable launch sequences (HIP graphs) of the forward / MTP bodies, one per
-     * (kind, token pointer, hidden-state pointer, logits pointer, B, flag) */
+     * (kind, token pointer, hidden-state pointer, logits pointer, B, flag, att_live) */
     int use_graphs, n_graphs;
-    struct { int kind, flag; uint32_t B; const void *tok, *h, *lg; void *exec; } graphs[48];
+    struct { int kind, flag, live; uint32_t B; const void *tok, *h, *lg; void *exec; } graphs[48];
     int status;               /* of the last call: 0, -1 rejected on the host, -2 device error */
     /* section timing of model_forward: events before the embedding, after it, after each layer
      * and after the head (n_layer + 3), recorded while prof_active */
@@ -478,6 +482,8 @@ static int model_load(qwen_model_t *m, const source_t *src, uint32_t n_ctx)
     m->rope_cos = cs;                          /* host copies (reference field names) */
     m->rope_sin = sn;
     if (rc || qgpu_attn_reserve((int)n_ctx, (int)d->n_kv_head)) return -1;
+    for (int b = 1; b <= QGPU_MAX_B; b++)
+        g->att_split[b] = qgpu_attn_split_bound((int)n_ctx, b, (int)d->n_head, (int)d->n_kv_head);
     /* host-side fields, laid out as the reference's arenas (model.c:166-230) */
     {
         const uint64_t sq = g->SQ > F ? g->SQ : F, kvs = 2ull * d->n_kv_head * d->head_dim;
@@ -690,10 +696,15 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
      * prepares the o-projection input when the matrix runs on the matrix cores */
     (void)pos;   /* positions come from g->pos_ptr (at()); the grid covers n_ctx (spans past the live end exit) */
     const int prep = mat_packed(D->o);
-    K((prep ? qgpu_attn_fused_act : qgpu_attn_fused)(
-        g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v, g->rope_cos, g->rope_sin,
-        (int)m->cfg.rope_dim_count, g->pos_ptr, (int)m->n_ctx, (int)B, (int)d->n_head, (int)d->n_kv_head,
-        (int)d->head_dim, eps, g->battn, g->A));
+    if (prep)
+        K(qgpu_attn_fused_act_live(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v,
+                                   g->rope_cos, g->rope_sin, (int)m->cfg.rope_dim_count, g->pos_ptr, (int)m->n_ctx,
+                                   (int)B, (int)d->n_head, (int)d->n_kv_head, (int)d->head_dim, eps, g->battn, g->A,
+                                   g->att_live));
+    else
+        K(qgpu_attn_fused(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v,
+                          g->rope_cos, g->rope_sin, (int)m->cfg.rope_dim_count, g->pos_ptr, (int)m->n_ctx, (int)B,
+                          (int)d->n_head, (int)d->n_kv_head, (int)d->head_dim, eps, g->battn, g->A));
     if (prep) {
         residual_gemv_prepared(m, D->o, B, R);
     } else {
@@ -798,7 +809,7 @@ static void run_body(qwen_model_t *m, int kind, body_fn fn, const uint32_t *tok,
     if (!g->use_graphs || g->prof_active) { fn(m, tok, h, B, lg, flag); return; }
     for (int i = 0; i < g->n_graphs; i++)
         if (g->graphs[i].kind == kind && g->graphs[i].tok == tok && g->graphs[i].h == h && g->graphs[i].lg == lg &&
-            g->graphs[i].B == B && g->graphs[i].flag == flag) {
+            g->graphs[i].B == B && g->graphs[i].flag == flag && g->graphs[i].live == g->att_live) {
             K(qgpu_graph_launch(g->graphs[i].exec));
             return;
         }
@@ -809,7 +820,7 @@ static void run_body(qwen_model_t *m, int kind, body_fn fn, const uint32_t *tok,
     K(qgpu_graph_end(&exec));
     const int i = g->n_graphs++;
     g->graphs[i].kind = kind; g->graphs[i].tok = tok; g->graphs[i].h = h; g->graphs[i].lg = lg;
-    g->graphs[i].B = B; g->graphs[i].flag = flag; g->graphs[i].exec = exec;
+    g->graphs[i].B = B; g->graphs[i].flag = flag; g->graphs[i].live = g->att_live; g->graphs[i].exec = exec;
     K(qgpu_graph_launch(exec));
 }
 
@@ -893,11 +904,19 @@ static void at(qwen_model_t *m, uint32_t pos, int with_cur)
 
 /* tokens on the device; logits of every token into d_logits ([B][V]); hidden
  * states into h_save when save_h.  GDN states advance by B (ring index). */
+/* the attention launches' live-context bound for B tokens at position pos */
+static void att_bound(qwen_gpu_t *g, uint32_t pos, uint32_t B)
+{
+    const int b = B <= QGPU_MAX_B ? g->att_split[B] : 0;
+    g->att_live = b && pos + B <= (uint32_t)b ? b : 0;
+}
+
 static void forward_dev(qwen_model_t *m, const uint32_t *d_tokens, uint32_t B, uint32_t pos, float *d_logits,
                         int save_h)
 {
     qwen_gpu_t *g = m->gpu;
     at(m, pos, 1);
+    att_bound(g, pos, B);
     run_body(m, G_FWD, forward_body, d_tokens, NULL, B, d_logits, save_h);
     if ((int)B >= g->factor_min_b) {              /* GDN state kept in slot cur, factors in the other buffer */
         g->fbase = g->cur;
@@ -919,6 +938,7 @@ static void mtp_dev(qwen_model_t *m, const uint32_t *d_tokens, const float *h, u
                     float *d_logits)
 {
     at(m, pos, 0);
+    att_bound(m->gpu, pos, B);
     run_body(m, G_MTP, mtp_body, d_tokens, h, B, d_logits, 0);
 }
 
@@ -929,6 +949,7 @@ static void mtp_anchor_dev(qwen_model_t *m)
 {
     qwen_gpu_t *g = m->gpu;
     g->pos_ptr = g->d_pos;
+    g->att_live = 0;              /* the position is the device's (no host bound) */
     run_body(m, G_MTP, mtp_body, g->anchor_tok, g->anchor_h, 1, NULL, 0);
 }
 
@@ -1098,6 +1119,7 @@ void attention_layer(qwen_model_t *m, qwen_layer_t *L, pool_t *pool, uint32_t po
     glayer_t *D = (L == &m->mtp_layer) ? &g->mtp : &g->L[L - m->layers];
     K(qgpu_memcpy_h2d(g->bx, m->x, m->dims.n_embd * sizeof(float)));
     at(m, pos, 0);
+    att_bound(g, pos, 1);
     attn_dev(m, D, g->bx, 1, pos);
     materialize(m);
     K(qgpu_memcpy_d2h(m->x, g->bx, m->dims.n_embd * sizeof(float)));

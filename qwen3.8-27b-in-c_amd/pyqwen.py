@@ -304,6 +304,9 @@ class GpuLib:
                                 ctypes.POINTER(i32), i32, i32, i32, i32, i32, f32, F32P, u64],
             "qgpu_attn_fused_act": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
                                     ctypes.POINTER(i32), i32, i32, i32, i32, i32, f32, F32P, u64],
+            "qgpu_attn_fused_act_live": [F32P, u64, F32P, F32P, u64, F32P, F32P, F32P, F32P, F32P, F32P, i32,
+                                         ctypes.POINTER(i32), i32, i32, i32, i32, i32, f32, F32P, u64, i32],
+            "qgpu_attn_split_bound": [i32, i32, i32, i32],
             "qgpu_attn_reserve": [i32, i32],
             "qgpu_set_i32": [ctypes.POINTER(i32), i32],
             "qgpu_gemv_act_batch": [ctypes.POINTER(vp), i32, ctypes.POINTER(Act), i32, ctypes.POINTER(F32P),

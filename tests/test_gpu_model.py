@@ -416,6 +416,83 @@ def test_attention_prepares_o_projection(gpu, t, pos, B):
     assert e < 2e-5
 
 
+def test_attention_head_split_bound(gpu):
+    """qgpu_attn_split_bound: the head split only where it takes fewer row tiles (6 query heads per kv
+    head x 3..8 tokens), and only up to the live context where the doubled span blocks still fit the
+    compute units once: 2 n_kv nsl <= CUs, with nsl spans of max(ceil(tiles / 64), 2) tiles; on 256 CUs
+    and 4 kv heads that is 64 tiles, 1024 positions."""
+    nh, nkv, n_ctx = 24, 4, 8704
+    b = {B: gpu.L.qgpu_attn_split_bound(n_ctx, B, nh, nkv) for B in range(1, 9)}
+    n_cu = gpu.device_info()[1]
+    print(f"\n[attn-split] bounds {b} on {n_cu} CUs", flush=True)
+    assert b[1] == b[2] == 0
+    # the largest tile count t such that every live context of 1..t tiles has 2 n_kv nsl <= CUs
+    t = 0
+    while t < n_ctx // 16:
+        ntl = t + 1
+        tps = max(-(-ntl // min(ntl, 64)), 2)
+        if 2 * nkv * -(-ntl // tps) > n_cu:
+            break
+        t = ntl
+    want = min(16 * t, n_ctx)
+    if n_cu == 256:
+        assert want == 1024
+    assert all(b[B] == want for B in range(3, 9))
+    assert gpu.L.qgpu_attn_split_bound(300, 4, nh, nkv) == min(300, want)   # never past the context
+    assert gpu.L.qgpu_attn_split_bound(n_ctx, 4, 20, 4) == 0                 # 5 heads per kv head: no even split
+
+
+@pytest.mark.parametrize("pos,B", [(0, 3), (37, 4), (500, 5), (801, 4), (1000, 4), (200, 1), (3000, 4),
+                                   (300, 8), (700, 6), (1010, 7), (3000, 8)])
+def test_attention_head_split_bit_identical(gpu, pos, B):
+    """qgpu_attn_fused_act_live with a live-context bound (two span blocks per kv head, half of its query
+    heads each, while the bound allows) writes the same bits as qgpu_attn_fused_act: output rows, o-projection
+    digit planes (through the prepared GEMV) and cache rows; a bound past the split's limit, or none, takes the
+    one-block path.  Bad bounds are rejected."""
+    print(f"\n[attn-split] pos={pos} B={B}", flush=True)
+    nh, nkv, hd, rope_dim, theta, eps, _ = ATT_DIMS
+    n_ctx = 4096
+    q, k, v, qw, kw, kc, vc, rc, rs = _attn_inputs(pos, B, n_ctx)
+    host = host_lib()
+    ne0, ne1 = nh * hd, 320
+    W = host.synth_matrix(23, ne0, ne1, 43, 9, 0.02)
+    T = gpu.tensor(W, 23, ne0, ne1)
+    qb, kb, vb = gpu.put(q), gpu.put(k), gpu.put(v)
+    posb = gpu.put(np.array([pos], np.int32))
+    qwb, kwb, rcb, rsb = gpu.put(qw), gpu.put(kw), gpu.put(rc), gpu.put(rs)
+    bound = gpu.L.qgpu_attn_split_bound(n_ctx, B, nh, nkv)
+
+    def run(live):
+        kcb, vcb, ob, yb = gpu.put(kc), gpu.put(vc), gpu.buf(B * ne0 * 4), gpu.buf(B * ne1 * 4)
+        args = (qb.f32(), nh * 2 * hd, kb.f32(), vb.f32(), nkv * hd, qwb.f32(), kwb.f32(), kcb.f32(), vcb.f32(),
+                rcb.f32(), rsb.f32(), rope_dim, posb.i32(), n_ctx, B, nh, nkv, hd, eps, ob.f32(), ne0)
+        if live is None:
+            gpu.ok(gpu.L.qgpu_attn_fused_act(*args))
+        else:
+            gpu.ok(gpu.L.qgpu_attn_fused_act_live(*args, live))
+        gpu.ok(gpu.L.qgpu_gemv_prepared(T.h, B, yb.f32(), ne1, 0))
+        return [x.download(np.float32) for x in (ob, yb, kcb, vcb)]
+
+    ref = run(None)
+    lives = [0, pos + B, max(bound, pos + B), n_ctx]
+    for live in lives:
+        got = run(live)
+        split = 0 < live <= bound
+        print(f"  live {live} (bound {bound}, split {split}): identical", flush=True)
+        for a, b_ in zip(got, ref):
+            assert np.array_equal(a, b_), (live, bound)
+    ob = gpu.buf(B * ne0 * 4)
+    for bad in (B - 1, n_ctx + 1):
+        if bad < 1:
+            continue
+        rc_ = gpu.L.qgpu_attn_fused_act_live(qb.f32(), nh * 2 * hd, kb.f32(), vb.f32(), nkv * hd, qwb.f32(),
+                                             kwb.f32(), gpu.put(kc).f32(), gpu.put(vc).f32(), rcb.f32(), rsb.f32(),
+                                             rope_dim, posb.i32(), n_ctx, B, nh, nkv, hd, eps, ob.f32(), ne0, bad)
+        assert rc_ == -1                       # QGPU_E_ARG
+    if B >= 3 and pos + B <= 1024:
+        assert bound > 0            # the split path ran above
+
+
 def test_spec_accept_kernel(gpu):
     cand = gpu.put(np.array([7, 3, 9, 4, 0, 0, 0, 0], np.uint32))
     for vt, k, fj, j in (([3, 9, 4, 11], 3, -1, 3), ([3, 8, 4, 11], 3, -1, 1), ([5, 9, 4, 11], 3, -1, 0),
