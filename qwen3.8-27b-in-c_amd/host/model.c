@@ -968,13 +968,23 @@ static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, 
     if (g->embd_fuse) { cat.x = NULL; cat.embd = g->tok_embd; cat.tok = d_tokens; }
     K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->eh_proj, 1, &cat, (int)B, &g->mx, &E, 0));
     attn_dev(m, &g->mtp, g->mx, B, 0);
+    /* mtp_h = the last output row.  With one row and the residual's partial planes still pending,
+     * the kernel that adds them writes the row straight into mtp_h (mx then lacks them; nothing
+     * reads mx before the next eh_proj overwrites it) */
+    int direct = 0;
     if (d_logits) {
-        const qgpu_act an = act_norm_res(m, g->mx, g->shnorm, g->bxb);
+        qgpu_act an = act_norm_res(m, g->mx, g->shnorm, g->bxb);
+        if (B == 1 && an.n_part) { an.xnew = g->mtp_h; direct = 1; }
         K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
+    } else if (B == 1 && g->pend_ks && g->pend == g->mx && g->pend_B == 1 && !g->pend_tok) {
+        K(qgpu_add_partials(g->mtp_h, E, g->mx, E, g->part, E, g->pend_ks, E, 1));
+        g->pend_ks = 0;
+        g->pend = NULL;
+        direct = 1;
     } else {
         materialize(m);
     }
-    K(qgpu_copy(g->mtp_h, g->mx + (B - 1) * E, E * sizeof(float)));
+    if (!direct) K(qgpu_copy(g->mtp_h, g->mx + (B - 1) * E, E * sizeof(float)));
 }
 
 /* ------------------------------------------------------------------ reference API */
