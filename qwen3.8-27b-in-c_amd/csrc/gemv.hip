@@ -1039,6 +1039,121 @@ __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_ge
     }
 }
 
+// ---------------------------------------------------------------- wide GEMV (activations in LDS)
+// For a matrix of many tiles and a short K (the 248,320-row lm_head: 15,520 tiles, K = 5120), the
+// kernel above re-reads the digit tile of every (tile, super-block) from L2: 3 KB per 2.2 KB weight
+// record at B = 4 (931 MB of digits against 675 MB of weights per call).  Here a block copies the
+// call's digit planes into LDS once (NA x nsb x 3 KB) and each of its waves streams whole
+// tiles (every super-block of a tile in order), tile after tile (tiles wave0, wave0 + waves of the
+// grid, ...), its weight ring running on across tile ends; the A operand comes from LDS, one
+// super-block ahead.  A wave owns its tile's outputs, so there is no cross-wave reduction.  The
+// A rows of digit slot 3 and of tokens past ntok read whatever the tile holds there: their
+// products land in result register 3 (never used) and in the lane groups of those tokens (never
+// written).  Single matrix, no K split; the deferred RMSNorm row factor as in k_gemv_mfma.
+// One block per compute unit, of as many waves as the kernel's VGPRs let each SIMD hold: one digit
+// plane 16 (IQ4_XS..Q6_K, 100-128 VGPRs) or 12 (Q8_0, 144); two planes 12 (IQ4_XS, Q4_K: 155-166)
+// or 8 (the others, which would spill at 12).  (Two blocks of 10 waves with one plane: 4 waves per
+// SIMD by the VGPR granule, so 10 per compute unit, measured 17% slower.)
+#define WIDE_BPC(NA) 1
+#define WIDE_NW(FMT, NA) ((NA) == 1 ? ((FMT) == T_Q8_0 ? 12 : 16) : ((FMT) == T_IQ4_XS || (FMT) == T_Q4_K ? 12 : 8))
+#define WIDE_NSB(NA) 20                      // super-blocks the LDS operand holds (K <= 5120): NA x 60 KB
+#ifndef WIDE_WDEPTH
+#define WIDE_WDEPTH 3       // weight records in flight per wave
+#endif
+template <int NA>
+static __device__ __forceinline__ void lds_load_a(IQ4A<NA> &x, const uint8_t *dig, uint32_t pbytes, int sb,
+                                                  const float *xs, int lane)
+{
+    const int tk = (lane & 15) >> 2, dg = lane & 3;
+    const uint32_t off = (uint32_t)sb * DIGIT_TILE + (uint32_t)(tk * 12 + (lane >> 4) * 3 + (dg < 3 ? dg : 2)) * 16;
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+#pragma unroll
+        for (int p = 0; p < 4; p++) x.av[a][p] = *(const uint4 *)(dig + (uint32_t)a * pbytes + off + p * DIGIT_SUB);
+        x.xt[a] = *(const float4 *)(xs + (uint64_t)a * XS_FLOATS + (uint64_t)sb * 16);
+    }
+}
+
+template <int FMT, int NA, int MODE>
+__global__ __launch_bounds__(WIDE_NW(FMT, NA) * 64) void k_gemv_wide(const GemvArgs args)
+{
+    constexpr int NWW = WIDE_NW(FMT, NA);
+    __shared__ __attribute__((aligned(16))) uint8_t dig[NA * WIDE_NSB(NA) * DIGIT_TILE];
+    __shared__ float rsc[QGPU_MAX_B];
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    const float4 oh = make_float4(g == 0, g == 1, g == 2, g == 3);
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const GemvMat &M = args.m[0];
+    const int nsb = args.nsb;
+    const uint32_t ntiles = args.pair0, stride = gridDim.x * NWW;           // tiles of the launch
+    constexpr uint32_t REC = FMT == T_IQ4_XS ? IQ4_REC_BYTES : FMT == T_Q4_K ? 2304 : FMT == T_Q5_K ? 2816 : FMT == T_Q6_K ? 3360 : 4352;
+    const uint32_t t0 = blockIdx.x * NWW + wv;
+    const int nst = t0 < ntiles ? (int)((ntiles - 1 - t0) / stride + 1) * nsb : 0;    // this wave's steps
+    const uint8_t *W0 = M.W + (uint64_t)M.tile_first * nsb * REC;
+    // weight cursor (tile, super-block) of the next record to load; the first records go out
+    // before the LDS copy
+    uint32_t lt = t0;
+    int lsb = 0;
+    WRec<FMT> wr[WIDE_WDEPTH];
+#define WIDE_ADV(t_, sb_) do { if (++(sb_) == nsb) { (sb_) = 0; (t_) += stride; } } while (0)
+#define WIDE_LOAD_W(slot) do { kq_load_w<FMT>(wr[slot], W0 + ((uint64_t)lt * nsb + lsb) * REC, lane, n); \
+                               WIDE_ADV(lt, lsb); } while (0)
+#pragma unroll
+    for (int d = 0; d < WIDE_WDEPTH - 1; d++)
+        if (d < nst) WIDE_LOAD_W(d);
+    RmsPart<(QGPU_MAX_B + NWW - 1) / NWW> rp;
+    if (MODE & IQ4_RMS) rms_load(args, wv, NWW, lane, rp);
+    const uint32_t pbytes = (uint32_t)nsb * DIGIT_TILE;
+    for (uint32_t i = (uint32_t)tid * 16u; i < NA * pbytes; i += NWW * 64 * 16) {
+        const uint32_t a = i >= pbytes ? 1u : 0u, o = i - a * pbytes;
+        *(uint4 *)(dig + i) = *(const uint4 *)(args.A + (uint64_t)a * PLANE_BYTES + o);
+    }
+    if (MODE & IQ4_RMS) rms_reduce(args, wv, NWW, lane, rp, rsc);
+    __syncthreads();
+
+    float accf[NA][4];
+#pragma unroll
+    for (int a = 0; a < NA; a++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) accf[a][i] = 0.0f;
+    uint32_t ct = t0;          // compute cursor
+    int csb = 0;
+    IQ4A<NA> ar[2];
+    if (nst > 0) lds_load_a<NA>(ar[0], dig, pbytes, 0, args.xs, lane);
+    // ring slots are compile-time after unrolling by a common multiple of the two depths
+    constexpr int UNROLL = WIDE_WDEPTH % 2 == 0 ? WIDE_WDEPTH : 2 * WIDE_WDEPTH;
+    for (int j = 0; j < nst; j += UNROLL) {
+#pragma unroll
+        for (int d = 0; d < UNROLL; d++) {
+            if (j + d < nst) {
+                if (j + d + WIDE_WDEPTH - 1 < nst) WIDE_LOAD_W((d + WIDE_WDEPTH - 1) % WIDE_WDEPTH);
+                if (j + d + 1 < nst) lds_load_a<NA>(ar[(d + 1) & 1], dig, pbytes, csb + 1 < nsb ? csb + 1 : 0, args.xs, lane);
+                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % WIDE_WDEPTH], ar[d & 1], oh, accf);
+                else kq_compute<FMT, NA>(wr[d % WIDE_WDEPTH], ar[d & 1], oh, accf);
+                if (csb == nsb - 1) {                      // the tile's last super-block: its outputs
+                    const uint32_t r = (M.tile_first + ct) * IQ4_TILE_ROWS + n;
+#pragma unroll
+                    for (int a = 0; a < NA; a++) {
+                        const int t = 4 * a + g;
+                        float s = DIGIT_REGS == 3 ? (accf[a][0] + accf[a][1] * p8(1)) + accf[a][2] * p8(2)
+                                                  : (accf[a][0] + accf[a][1] * p8(1)) + (accf[a][2] * p8(2) + accf[a][3] * p8(3));
+                        if (t < args.ntok && r >= M.row_lo && r < M.row_hi) {
+                            if (MODE & IQ4_RMS) s *= rsc[t];
+                            float *o = M.out + (uint64_t)t * M.ldo + r;
+                            *o = (args.flags & QGPU_GEMV_ACCUM) ? *o + s : s;
+                        }
+#pragma unroll
+                        for (int i = 0; i < 4; i++) accf[a][i] = 0.0f;
+                    }
+                }
+                WIDE_ADV(ct, csb);
+            }
+        }
+    }
+#undef WIDE_LOAD_W
+#undef WIDE_ADV
+}
+
 // ---------------------------------------------------------------- VALU GEMV (GGUF layout)
 // Decoders of one 32-element chunk to the dequantised fp32 values (bit-exact
 // with the scalar reference: explicit round-to-nearest products, no FMA).
@@ -1297,6 +1412,16 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
 #undef MF_GO
 }
 
+template <int FMT>
+static void launch_wide(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, int na, int mode)
+{
+#define WG_GO(NA_, M_) hipLaunchKernelGGL((k_gemv_wide<FMT, NA_, M_>), dim3(blocks), dim3(64 * WIDE_NW(FMT, NA_)), 0, \
+                                          ex.st, A)
+    if (na == 1) { if (mode) WG_GO(1, IQ4_RMS); else WG_GO(1, 0); }
+    else { if (mode) WG_GO(2, IQ4_RMS); else WG_GO(2, 0); }
+#undef WG_GO
+}
+
 // Blocks of one kernel instance that a compute unit holds at once (its VGPRs set the waves
 // per SIMD), from the runtime's occupancy calculator; cached per instance.
 template <int FMT, int NA, int NW, int M>
@@ -1381,6 +1506,41 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
     A.pair0 = tiles;
     if (mfma) {
         if (W0->ne0 > MAX_K) return QGPU_E_RANGE;
+#ifndef GEMV_WIDE
+#define GEMV_WIDE 1
+#endif
+#ifndef WIDE_MIN_TILES
+#define WIDE_MIN_TILES 4096   // tiles from which one matrix with its activations in LDS takes k_gemv_wide
+#endif
+        // one wide matrix, no K split, its digit planes within the LDS operand: k_gemv_wide, all its
+        // blocks resident at once (pair0 = the launch's tile count).  It pays where the per-tile
+        // kernel re-reads whole digit planes, B = 4 and 8; 248,320 x 5120 through gemv_batch (us,
+        // per-tile -> wide): IQ4_XS B = 4 143.7 -> 133.7, B = 8 192.6 -> 187.3; Q4_K 144.6 -> 138.1,
+        // 195.7 -> 188.8; Q5_K B = 8 223.4 -> 220.0; Q8_0 B = 8 275.2 -> 249.6.  Not taken: B = 1, 2
+        // (IQ4_XS 133.0 -> 139.4), B = 5, 6 (IQ4_XS 177.4 -> 191.0, plane 2 partly empty), Q5_K at B = 4
+        // (+0.5%), Q8_0 below 7 tokens, Q6_K (too few waves for its VGPRs).
+        {
+            const int na = n > 4 ? 2 : 1, t = W0->type;
+            const bool fmt_ok = n == 4 ? (t == T_IQ4_XS || t == T_Q4_K)
+                                       : n == 8 && (t == T_IQ4_XS || t == T_Q4_K || t == T_Q5_K || t == T_Q8_0);
+            if (GEMV_WIDE && fmt_ok && cnt == 1 && !split && ks == 1 && tiles >= WIDE_MIN_TILES && ex.n_cu > 0 &&
+                A.nsb <= (na == 1 ? WIDE_NSB(1) : WIDE_NSB(2))) {
+                A.A = ex.ws;
+                A.xs = (const float *)(ex.ws + 2 * PLANE_BYTES);
+                const int mode = A.rss ? IQ4_RMS : 0;
+                const uint32_t blocks = (uint32_t)ex.n_cu * WIDE_BPC(na);
+                switch (W0->type) {
+                case T_IQ4_XS: launch_wide<T_IQ4_XS>(ex, A, blocks, na, mode); break;
+                case T_Q4_K: launch_wide<T_Q4_K>(ex, A, blocks, na, mode); break;
+                case T_Q5_K: launch_wide<T_Q5_K>(ex, A, blocks, na, mode); break;
+                case T_Q6_K: launch_wide<T_Q6_K>(ex, A, blocks, na, mode); break;
+                case T_Q8_0: launch_wide<T_Q8_0>(ex, A, blocks, na, mode); break;
+                default: return QGPU_E_TYPE;
+                }
+                QG_LAUNCH_CHECK();
+                return QGPU_OK;
+            }
+        }
 #ifndef GEMV_PAIR_SPLIT
 #define GEMV_PAIR_SPLIT 1
 #endif
