@@ -120,7 +120,9 @@ int  qgpu_gemv_prepared(const qgpu_tensor *W, int n, float *out, uint64_t ldo, i
  * the call is not IQ4_XS (those kernels read fp32 rows).  ne0 % 256 == 0.
  * Single-segment QGPU_ACT_RMSNORM inside a GEMV call is computed as
  * s * (W (x w)) with s = 1/sqrt(mean(x^2) + eps) applied to the GEMV output,
- * so xout then holds x * w (the row factor is not in it).
+ * so xout then holds x * w (the row factor is not in it).  The two-segment form
+ * with no xout, before matrix-core matrices only and no K split, is computed the
+ * same way with one factor per half (the MTP input's enorm and hnorm).
  * Pending K-split partial sums (qgpu_gemv_act_split): with n_part > 0 the
  * RMSNORM input is x_eff = x + sum_{q < n_part} part[q*n*ldp + t*ldp + i];
  * xnew (ldxn; may equal x) receives x_eff.  Single-segment RMSNORM only.

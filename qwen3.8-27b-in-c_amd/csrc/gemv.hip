@@ -27,6 +27,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 #define RSS_FLOATS  ((size_t)QGPU_MAX_B * MAX_NSB)
 #define ACT_RMS_DEFER 4      // internal prep kind: RMSNORM with the 1/rms factor applied by the GEMV
 #define ACT_RMS_EMBD 5       // ACT_RMS_DEFER on rows gathered from the embedding matrix
+#define ACT_RMS_CAT 6        // the two-segment RMSNORM [x | y] with both row factors applied by the GEMV
 
 // Pair split (tail balance): when a launch's tiles are a little over a multiple of the compute
 // units, the remainder tiles run as two half-K blocks each, whose results meet in 64-bit exchange
@@ -512,8 +513,19 @@ __global__ __launch_bounds__(256) void k_prep_tok(ActDev p, uint8_t *__restrict_
     const int sb = blockIdx.x, t = blockIdx.y, a = t >> 2, i = t & 3;
     const uint32_t k = (uint32_t)sb * 256 + e;
     float v, ss = 0.0f;
-    constexpr bool RMS = KIND == ACT_RMS_DEFER || KIND == ACT_RMS_EMBD;
-    if (RMS) {
+    constexpr bool RMS = KIND == ACT_RMS_DEFER || KIND == ACT_RMS_EMBD || KIND == ACT_RMS_CAT;
+    if (KIND == ACT_RMS_CAT) {
+        // [x | y], seg elements each: v = x * w or y * w2 (its segment's row factor is the GEMV's),
+        // and the super-block's sum of squares of x or y; x from the embedding rows when embd is set
+        const uint32_t segl = (uint32_t)p.seg;
+        const bool s1 = k >= segl;
+        const uint32_t kk = s1 ? k - segl : k;
+        const float xr = s1 ? (p.y + (uint64_t)t * p.ldy)[kk]
+                            : (p.embd ? embd_iq4(p.embd, (uint64_t)segl, p.embd_ne1, p.tok[t], kk)
+                                      : (p.x + (uint64_t)t * p.ldx)[kk]);
+        v = xr * (s1 ? p.w2 : p.w)[kk];
+        ss = wave_sum64(xr * xr);
+    } else if (RMS) {
         // x_eff = x + (p_0 + p_1 + ...) over the NP partial planes, written back to xnew;
         // v = x_eff * w, and the super-block's sum of x_eff^2 for the GEMV's row factor
         const float xr = KIND == ACT_RMS_EMBD ? embd_iq4(p.embd, (uint64_t)p.nsb * 256, p.embd_ne1, p.tok[t], k)
@@ -587,6 +599,8 @@ struct GemvArgs {
     const float *rss;      // deferred RMSNorm: outputs *= 1/sqrt(sum_sb rss[t*rss_nsb+sb] * rss_inv_n + eps)
     int rss_nsb;
     float rss_inv_n, eps;
+    int rss_seg;           // two segments (IQ4_RMS2): super-blocks [0, rss_seg) and [rss_seg, rss_nsb), each
+                           // with its own factor (rss_inv_n = 1 / segment length)
 };
 
 // Row factors of the deferred RMSNorm, one per token, into rsc[]: wave w owns tokens
@@ -613,6 +627,22 @@ static __device__ __forceinline__ void rms_reduce(const GemvArgs &args, int wv, 
         const int t = wv + u * nw;
         const float s = wave_sum64(rp.v[u]);
         if (lane == 0 && t < args.ntok) rsc[t] = 1.0f / sqrtf(s * args.rss_inv_n + args.eps);
+    }
+}
+// the same for two segments: rsc[t] from the sums of super-blocks [0, rss_seg), rsc1[t] from the rest
+template <int NU>
+static __device__ __forceinline__ void rms_reduce2(const GemvArgs &args, int wv, int nw, int lane,
+                                                   const RmsPart<NU> &rp, float *rsc, float *rsc1)
+{
+#pragma unroll
+    for (int u = 0; u < NU; u++) {
+        const int t = wv + u * nw;
+        const float s0 = wave_sum64(lane < args.rss_seg ? rp.v[u] : 0.0f);
+        const float s1 = wave_sum64(lane < args.rss_seg ? 0.0f : rp.v[u]);
+        if (lane == 0 && t < args.ntok) {
+            rsc[t] = 1.0f / sqrtf(s0 * args.rss_inv_n + args.eps);
+            rsc1[t] = 1.0f / sqrtf(s1 * args.rss_inv_n + args.eps);
+        }
     }
 }
 
@@ -918,6 +948,10 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
 #define IQ4_RMS   1
 #define IQ4_SPLIT 2
 #define IQ4_PAIR  4     // tail balance: the last tiles of the launch in two K halves (never with IQ4_SPLIT)
+#define IQ4_RMS2  8     // deferred two-segment RMSNorm: each segment's super-blocks are summed apart (a wave
+                        // meets its second-segment super-blocks after all its first-segment ones, so its
+                        // sums move aside once), and each sum takes its segment's row factor (never with
+                        // IQ4_RMS or IQ4_SPLIT)
 template <int FMT, int NA, int NW, int MODE>
 #ifndef IQ4_MINW1
 #define IQ4_MINW1 1     // minimum waves per SIMD the compiler must allow (caps VGPRs), one digit plane
@@ -927,8 +961,10 @@ template <int FMT, int NA, int NW, int MODE>
 #endif
 __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_gemv_mfma(const GemvArgs args)
 {
+    constexpr bool SEG2 = (MODE & IQ4_RMS2) != 0;
     __shared__ float red[NW][NA][4][16];
-    __shared__ float rsc[QGPU_MAX_B];
+    __shared__ float red1[SEG2 ? NW : 1][NA][4][16];        // the second segment's sums
+    __shared__ float rsc[QGPU_MAX_B], rsc1[SEG2 ? QGPU_MAX_B : 1];
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
     const float4 oh = make_float4(g == 0, g == 1, g == 2, g == 3);   // token g of this lane group
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);     // wave-uniform: scalar loop control
@@ -958,14 +994,20 @@ __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_ge
     // 17408x5120 B = 4 13.78 -> 13.56 us against contiguous quarters)
     const int nsw = wv < nkb ? (nkb - wv + NW - 1) / NW : 0;
 #define SBX(j) (kb0 + wv + (j) * NW)
+    const bool seg1_last = SEG2 && nsw > 0 && SBX(nsw - 1) >= args.rss_seg;   // the wave ends in the second segment
     RmsPart<(QGPU_MAX_B + NW - 1) / NW> rp;
-    if (MODE & IQ4_RMS) rms_load(args, wv, NW, lane, rp);
+    if (MODE & (IQ4_RMS | IQ4_RMS2)) rms_load(args, wv, NW, lane, rp);
 
-    float accf[NA][4];
+    float accf[NA][4], accf0[NA][4];                     // accf0: the first segment's sums (SEG2 only)
 #pragma unroll
     for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int i = 0; i < 4; i++) accf[a][i] = 0.0f;
+    if constexpr (SEG2)
+#pragma unroll
+        for (int a = 0; a < NA; a++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) accf0[a][i] = 0.0f;
 
     // two register rings: weights of step j+IQ4_WDEPTH-1 and digits of
     // j+ADEPTH-1 are loading while step j is decoded and multiplied (ring
@@ -991,6 +1033,13 @@ __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_ge
                 const int pw = j + d + IQ4_WDEPTH - 1, pa = j + d + ADEPTH - 1;
                 if (pa < nsw) LOAD_A((d + ADEPTH - 1) % ADEPTH, pa);
                 if (pw < nsw) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
+                if (SEG2 && SBX(j + d) >= args.rss_seg && SBX(j + d) - NW < args.rss_seg) {
+                    // this wave's first super-block of the second segment (wave-uniform, once)
+#pragma unroll
+                    for (int a = 0; a < NA; a++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) { accf0[a][i] = accf[a][i]; accf[a][i] = 0.0f; }
+                }
                 if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % ADEPTH], oh, accf);
                 else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % ADEPTH], oh, accf);
             }
@@ -1000,22 +1049,46 @@ __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_ge
 #undef LOAD_A
 #undef SBX
     if (MODE & IQ4_RMS) rms_reduce(args, wv, NW, lane, rp, rsc);
-    // registers 0..3 of lane (g, n) hold digits 0..3 of token g, row n: sum them with their weights
-    // 2^(8 v) (a power of two: the same bits as weighting every super-block's term)
+    if constexpr (SEG2) {
+        rms_reduce2(args, wv, NW, lane, rp, rsc, rsc1);
+        // the wave's sums of each segment: its second-segment super-blocks, if any, came last
+        if (seg1_last) {
 #pragma unroll
-    for (int a = 0; a < NA; a++)
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) { const float f1 = accf[a][i]; accf[a][i] = accf0[a][i]; accf0[a][i] = f1; }
+        } else {
+#pragma unroll
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) accf0[a][i] = 0.0f;
+        }
+    }
+    // registers 0..3 of lane (g, n) hold digits 0..3 of token g, row n: sum them with their weights
+    // 2^(8 v) (a power of two: the same bits as weighting every super-block's term); SEG2: accf the
+    // first segment's sums, accf0 the second's
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
         red[wv][a][g][n] = DIGIT_REGS == 3 ? (accf[a][0] + accf[a][1] * p8(1)) + accf[a][2] * p8(2)
                                            : (accf[a][0] + accf[a][1] * p8(1)) + (accf[a][2] * p8(2) + accf[a][3] * p8(3));
+        if constexpr (SEG2)
+            red1[wv][a][g][n] = DIGIT_REGS == 3 ? (accf0[a][0] + accf0[a][1] * p8(1)) + accf0[a][2] * p8(2)
+                                                : (accf0[a][0] + accf0[a][1] * p8(1)) + (accf0[a][2] * p8(2) + accf0[a][3] * p8(3));
+    }
     __syncthreads();
     for (int e = tid; e < NA * 64; e += NW * 64) {     // (plane, token, row) entries of the tile
         const int a = e >> 6, i = (e >> 4) & 3, nn = e & 15;
-        float s = 0.0f;
+        float s = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; w++) s += red[w][a][i][nn];
+        if constexpr (SEG2)
+#pragma unroll
+            for (int w = 0; w < NW; w++) s1 += red1[w][a][i][nn];
         const int t = 4 * a + i;
         const uint32_t r = T * IQ4_TILE_ROWS + nn;
         if (t < args.ntok && r >= M.row_lo && r < M.row_hi) {
             if (MODE & IQ4_RMS) s *= rsc[t];
+            if constexpr (SEG2) s = s * rsc[t] + s1 * rsc1[t];
             if ((MODE & IQ4_PAIR) && ks == 2) {
                 // two contributors per entry: the first leaves its half in the slot, the second
                 // takes it (the exchange itself carries the value, so no fence), writes the sum and
@@ -1307,11 +1380,13 @@ __global__ __launch_bounds__(256) void k_gemv_valu(const GemvArgs args)
 // Validates an activation transform for n rows of ne0 and launches its prep
 // kernel: digit planes into the workspace when `digits`, fp32 rows into xout.
 // defer: single-segment RMSNORM is prepared as x*w plus per-super-block sums of
-// squares (ws_rss) for the GEMV to apply the row factor; *deferred tells the caller.
+// squares (ws_rss) for the GEMV to apply the row factor; *deferred = 1 tells the caller.
+// defer2: the two-segment RMSNORM without xout likewise, [x*w | y*w2] with one factor per
+// half (*deferred = 2; for matrix-core GEMVs with no K split only: the caller says).
 static int prep_act(const GemvExec &ex, const qgpu_act *act, int n, uint64_t ne0, int digits, bool defer = false,
-                    bool *deferred = nullptr)
+                    int *deferred = nullptr, bool defer2 = false)
 {
-    if (deferred) *deferred = false;
+    if (deferred) *deferred = 0;
     if (!act || (!act->x && !act->embd) || n < 1 || n > QGPU_MAX_B) return QGPU_E_ARG;
     if (ne0 % 256 || (digits && ne0 > MAX_K)) return QGPU_E_RANGE;
     ActDev d = {};
@@ -1345,7 +1420,18 @@ static int prep_act(const GemvExec &ex, const qgpu_act *act, int n, uint64_t ne0
         }
 #undef PT_NP
         QG_LAUNCH_CHECK();
-        if (deferred) *deferred = true;
+        if (deferred) *deferred = 1;
+        return QGPU_OK;
+    }
+    if (defer2 && digits && act->kind == QGPU_ACT_RMSNORM && act->seg && 2 * act->seg == ne0 && !act->xout &&
+        act->seg % 256 == 0) {
+        if (!act->w || !act->w2 || !act->y || (rows && act->ldy < act->seg) || (!gath && rows && act->ldx < act->seg))
+            return QGPU_E_ARG;
+        d.seg = act->seg; d.rss = ws_rss(ex); d.nsb = (int)(ne0 / 256);
+        hipLaunchKernelGGL((k_prep_tok<ACT_RMS_CAT, 0>), dim3((unsigned)(ne0 / 256), (unsigned)n), dim3(256), 0, ex.st,
+                           d, ex.ws, (float *)(ex.ws + 2 * PLANE_BYTES));
+        QG_LAUNCH_CHECK();
+        if (deferred) *deferred = 2;
         return QGPU_OK;
     }
     if (act->xout && rows && act->ldxo < ne0) return QGPU_E_ARG;
@@ -1405,6 +1491,8 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
                           else if (mode == IQ4_SPLIT) MF_NW(NA_, IQ4_SPLIT); \
                           else if (mode == IQ4_PAIR) MF_NW(NA_, IQ4_PAIR); \
                           else if (mode == (IQ4_RMS | IQ4_PAIR)) MF_NW(NA_, IQ4_RMS | IQ4_PAIR); \
+                          else if (mode == IQ4_RMS2) MF_NW(NA_, IQ4_RMS2); \
+                          else if (mode == (IQ4_RMS2 | IQ4_PAIR)) MF_NW(NA_, IQ4_RMS2 | IQ4_PAIR); \
                           else MF_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
     if (na == 1) MF_MODE(1); else MF_MODE(2);
 #undef MF_MODE
@@ -1444,7 +1532,9 @@ static int mfma_resident_of(int na, int nw, int mode)
                                   : mfma_resident<FMT, NA_, 4, M_>())
 #define MR_MODE(NA_) (mode == 0 ? MR_NW(NA_, 0) : mode == IQ4_RMS ? MR_NW(NA_, IQ4_RMS) \
                       : mode == IQ4_SPLIT ? MR_NW(NA_, IQ4_SPLIT) : mode == IQ4_PAIR ? MR_NW(NA_, IQ4_PAIR) \
-                      : mode == (IQ4_RMS | IQ4_PAIR) ? MR_NW(NA_, IQ4_RMS | IQ4_PAIR) : MR_NW(NA_, IQ4_RMS | IQ4_SPLIT))
+                      : mode == (IQ4_RMS | IQ4_PAIR) ? MR_NW(NA_, IQ4_RMS | IQ4_PAIR) \
+                      : mode == IQ4_RMS2 ? MR_NW(NA_, IQ4_RMS2) : mode == (IQ4_RMS2 | IQ4_PAIR) ? MR_NW(NA_, IQ4_RMS2 | IQ4_PAIR) \
+                      : MR_NW(NA_, IQ4_RMS | IQ4_SPLIT))
     return na == 1 ? MR_MODE(1) : MR_MODE(2);
 #undef MR_MODE
 #undef MR_NW
@@ -1468,13 +1558,15 @@ static int mfma_resident_fmt(int type, int na, int nw, int mode)
 #endif
 static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const int *idx, int cnt, const float *x,
                         uint64_t ldx, int n, float *const *outs, const uint64_t *ldos, int flags, const uint64_t *r0s,
-                        const uint64_t *r1s, int ks, const int *ksm, float eps, bool deferred)
+                        const uint64_t *r1s, int ks, const int *ksm, float eps, int deferred)
 {
     const qgpu_tensor *W0 = Ws[idx[0]];
     GemvArgs A = {};
     A.n_mat = cnt; A.ntok = n; A.flags = flags; A.x = x; A.ldx = ldx; A.ne0 = W0->ne0;
-    if (deferred) {
-        A.rss = ws_rss(ex); A.rss_nsb = (int)(W0->ne0 / 256); A.rss_inv_n = 1.0f / (float)W0->ne0; A.eps = eps;
+    if (deferred) {          // 1: one row factor; 2: one per half of the row (the two-segment RMSNORM)
+        A.rss = ws_rss(ex); A.rss_nsb = (int)(W0->ne0 / 256); A.eps = eps;
+        A.rss_seg = deferred == 2 ? A.rss_nsb / 2 : 0;
+        A.rss_inv_n = 1.0f / (float)(deferred == 2 ? W0->ne0 / 2 : W0->ne0);
     }
     A.nsb = (int)(W0->ne0 / 256);
     const bool mfma = W0->packed;
@@ -1523,7 +1615,7 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
             const int na = n > 4 ? 2 : 1, t = W0->type;
             const bool fmt_ok = n == 4 ? (t == T_IQ4_XS || t == T_Q4_K)
                                        : n == 8 && (t == T_IQ4_XS || t == T_Q4_K || t == T_Q5_K || t == T_Q8_0);
-            if (GEMV_WIDE && fmt_ok && cnt == 1 && !split && ks == 1 && tiles >= WIDE_MIN_TILES && ex.n_cu > 0 &&
+            if (GEMV_WIDE && fmt_ok && cnt == 1 && !split && ks == 1 && !A.rss_seg && tiles >= WIDE_MIN_TILES && ex.n_cu > 0 &&
                 A.nsb <= (na == 1 ? WIDE_NSB(1) : WIDE_NSB(2))) {
                 A.A = ex.ws;
                 A.xs = (const float *)(ex.ws + 2 * PLANE_BYTES);
@@ -1576,7 +1668,8 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         if (force_nw == 8) nw = 8;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
         if (A.rss && nw < 3) nw = 4;                        // row factors: <= 3 tokens per wave
-        const int mode = (A.rss ? IQ4_RMS : 0) | (split ? IQ4_SPLIT : 0) | (A.pair0 < tiles ? IQ4_PAIR : 0);
+        const int mode = (A.rss ? (A.rss_seg ? IQ4_RMS2 : IQ4_RMS) : 0) | (split ? IQ4_SPLIT : 0) |
+                         (A.pair0 < tiles ? IQ4_PAIR : 0);
 #ifndef GEMV_NW3_RESIDENT
 #define GEMV_NW3_RESIDENT 1
 #endif
@@ -1654,7 +1747,7 @@ static int gemv_multi_on(const GemvExec &ex, const qgpu_tensor *const *Ws, int n
     }
     const float *xv = nullptr;                              // fp32 rows for the VALU kernel (unpacked formats)
     uint64_t ldxv = ne0;
-    bool deferred = false;
+    int deferred = 0;
     if (!act) {
         if (any_valu) return QGPU_E_TYPE;
     } else {
@@ -1667,7 +1760,9 @@ static int gemv_multi_on(const GemvExec &ex, const qgpu_tensor *const *Ws, int n
         }
         if (any_mfma || xform) {
             if (!any_mfma && ne0 % 256) return QGPU_E_RANGE;
-            rc = prep_act(ex, act, n, ne0, any_mfma ? 1 : 0, ne0 <= 64 * 256, &deferred);   // row factors: <= 64 sums
+            // row factors: <= 64 sums; two per row only for matrix-core GEMVs with no K split
+            rc = prep_act(ex, act, n, ne0, any_mfma ? 1 : 0, ne0 <= 64 * 256, &deferred,
+                          ne0 <= 64 * 256 && !any_valu && ks == 1 && !ksm);
             if (rc) return rc;
         }
     }

@@ -963,7 +963,9 @@ static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, 
     /* eh_proj(concat(enorm(e), hnorm(h))) (model.c:1044-1052): both norms in the input preparation,
      * which also gathers the embedding rows when it can */
     if (!g->embd_fuse) K(qgpu_dequant_rows(g->tok_embd, d_tokens, (int)B, g->bxb, E));
-    qgpu_act cat = act_norm(g->bxb, E, g->enorm, eps, g->cat, 2 * E);
+    /* with eh_proj on the matrix cores, no fp32 copy of the normalised input: the preparation then
+     * leaves both row factors to the GEMV (one launch with per-element work only) */
+    qgpu_act cat = act_norm(g->bxb, E, g->enorm, eps, mat_packed(g->eh_proj) ? NULL : g->cat, 2 * E);
     cat.y = h; cat.ldy = E; cat.w2 = g->hnorm; cat.seg = E;
     if (g->embd_fuse) { cat.x = NULL; cat.embd = g->tok_embd; cat.tok = d_tokens; }
     K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->eh_proj, 1, &cat, (int)B, &g->mx, &E, 0));

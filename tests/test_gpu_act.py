@@ -95,6 +95,63 @@ def test_act_transform_gemv(gpu, t, B, kind):
     assert ex < 1e-5 and eo < 1e-3
 
 
+@pytest.mark.parametrize("t", [23, 12, 8])          # IQ4_XS, Q4_K, Q8_0 (the 27B eh_proj formats)
+@pytest.mark.parametrize("B", [1, 4, 7])
+@pytest.mark.parametrize("shape,gather", [((1024, 384), False), ((1024, 384), True), ((2048, 4352), False)])
+def test_act_two_segment_deferred(gpu, t, B, shape, gather):
+    """The MTP input concat(enorm(e), hnorm(h)) without an fp32 copy (xout NULL): the preparation writes
+    [x*w | y*w2] and per-super-block sums of squares, and the matrix-core GEMV sums each half's super-blocks
+    apart and applies each half's row factor.  Against the oracle GEMV of the normalised rows (bar 1e-3
+    normwise) and against the same call with xout (normalised digits, one factor per element): the two
+    agree to the GEMV's rounding.  4352 rows = 272 tiles: the pair-split tail, whose halves are exactly the
+    two segments.  gather: the first half from embedding rows (IQ4_XS), as the model's MTP input."""
+    print(f"\n[act2] type={t} B={B} shape={shape} gather={gather}", flush=True)
+    host = host_lib()
+    ne0, ne1 = shape
+    h = ne0 // 2
+    W = host.synth_matrix(t, ne0, ne1, 13, t, 0.02)
+    T = gpu.tensor(W, t, ne0, ne1)
+    rng = np.random.default_rng(100 * B + t)
+    ys = rng.standard_normal((B, h)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+    w2 = (1 + 0.1 * rng.standard_normal(h)).astype(np.float32)
+    yb, wb, w2b = gpu.put(ys), gpu.put(w), gpu.put(w2)
+    if gather:
+        V = 300
+        Te = gpu.tensor(host.synth_matrix(23, h, V, 41, 7, 0.5), 23, h, V)
+        tb = gpu.put(rng.integers(0, V, B).astype(np.uint32))
+        xr = gpu.buf(B * h * 4)
+        gpu.ok(gpu.L.qgpu_dequant_rows(Te.h, tb.u32(), B, xr.f32(), h))
+        xs = xr.download(np.float32).reshape(B, h)
+    else:
+        xs = (rng.standard_normal((B, h)) * 3).astype(np.float32)
+        xb = gpu.put(xs)
+    xin = np.stack([np.concatenate([o_rmsnorm(xs[b], w), o_rmsnorm(ys[b], w2)]) for b in range(B)])
+
+    def call(with_xout):
+        a = pyqwen.Act()
+        a.kind, a.w, a.w2, a.seg, a.eps = pyqwen.ACT_RMSNORM, wb.f32(), w2b.f32(), h, EPS
+        a.y, a.ldy, a.ldx = yb.f32(), h, h
+        if gather:
+            a.embd, a.tok = Te.h, tb.u32()
+        else:
+            a.x = xb.f32()
+        xo = gpu.buf(B * ne0 * 4)
+        if with_xout:
+            a.xout, a.ldxo = xo.f32(), ne0
+        ob = gpu.buf(B * ne1 * 4)
+        gpu.ok(gpu.L.qgpu_gemv_act_batch((ctypes.c_void_p * 1)(T.h), 1, ctypes.byref(a), B,
+                                         (pyqwen.F32P * 1)(ob.f32()), (ctypes.c_uint64 * 1)(ne1), 0))
+        return ob.download(np.float32).reshape(B, ne1)
+
+    got, with_xo = call(False), call(True)
+    ref = O.gemv(t, W, ne0, ne1, xin, B)
+    e, e2, d = rel_err(got, ref), rel_err(with_xo, ref), rel_err(got, with_xo)
+    print(f"  deferred {e:.2e}  with xout {e2:.2e}  between {d:.2e}", flush=True)
+    assert e < 1e-3 and e2 < 1e-3 and d < 1e-5
+    assert np.array_equal(got, call(False))            # deterministic
+
+
 def test_act_rejects_bad_args(gpu):
     host = host_lib()
     W = host.synth_matrix(23, 512, 32, 3, 3, 0.02)
