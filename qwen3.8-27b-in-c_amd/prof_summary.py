@@ -359,6 +359,9 @@ def step_roles(step, B, P):
             by = rows * IQ4_ROW(d["E"]) + B * d["E"] * DIGITS + B * rows * f4
             if grid != 15520:
                 n_part = 0
+        elif k.startswith("k_gemv_wide"):      # the lm_head with its activations in LDS
+            role = "GEMV lm_head"
+            by = d["V"] * IQ4_ROW(d["E"]) + B * d["E"] * DIGITS + B * d["V"] * f4
         elif k == "k_gdn_fused":
             state = d["VH"] * d["HS"] * d["HS"] * f4
             io = (1 + B) * d["CONV"] * 3 * f4 + B * (d["CONV"] + d["VD"] + 2 * d["VH"]) * f4
