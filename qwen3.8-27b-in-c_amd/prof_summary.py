@@ -263,7 +263,8 @@ def cmd_sweep(a):
            "HIP graph, replayed once untimed and once between HIP events on the library stream; weights rotate over",
            "enough device copies to exceed the 256 MB MALL.  GB/s = (weight bytes + B x (in + out) x 4) / time;",
            "% = of 8 TB/s.  Every format runs the int8-MFMA digit GEMV on packed 16-row tile records",
-           "(`k_gemv_mfma<format, ...>`).", ""]
+           "(`k_gemv_mfma<format, ...>`; the 248320-row lm_head at B = 4 and 8 through `k_gemv_wide`, its",
+           "activations in LDS, where that measured faster).", ""]
     bs = sorted({r["B"] for r in rows})
     out.append("| format | rows x cols | weight MB | " + " | ".join(f"B={B} us | B={B} GB/s" for B in bs) + " |")
     out.append("|---|---|---:|" + "---:|---:|" * len(bs))
