@@ -105,6 +105,37 @@ def test_gemv_lm_head_vs_oracle(gpu, fmt):
         assert np.all(np.isfinite(got))
 
 
+@pytest.mark.parametrize("fmt", ["IQ4_XS", "Q8_0"])
+def test_gemv_lm_head_row_range(gpu, fmt):
+    """qgpu_gemv_rows_batch over a range of the 248,320-row lm_head that is still wide enough for the
+    LDS-operand kernel (rows [100, 200003): 12,495 tiles, the first and last partly outside the range),
+    B = 4 and 8: the rows of the range against the oracle, and every row outside it left as it was."""
+    ne0, ne1, r0, r1 = 5120, 248_320, 100, 200_003
+    t = FORMATS[fmt]
+    W, T = matrix(gpu, t, ne0, ne1)
+    x = host_lib().synth_normal(8 * ne0, 81, t).reshape(8, ne0)
+    checks = [(r0, r0 + 400), (99_000, 99_512), (r1 - 400, r1)]
+    L = O.lib()
+    refs = []
+    for c0, c1 in checks:
+        o = np.zeros((8, ne1), np.float32)
+        L.or_gemv_rows_batch(t, W.ctypes.data_as(ctypes.c_void_p), ne0, O.fptr(x), ne0, 8, O.fptr(o), ne1, c0, c1)
+        refs.append(o[:, c0:c1].copy())
+    for n in (4, 8):
+        print(f"\n[lm_head rows] {fmt} [{r0}, {r1}) B={n}", flush=True)
+        xb = gpu.put(np.ascontiguousarray(x[:n]))
+        fill = np.full((n, ne1), 7.0, np.float32)
+        ob = gpu.put(fill)
+        gpu.ok(gpu.L.qgpu_gemv_rows_batch(T.h, xb.f32(), ne0, n, ob.f32(), ne1, r0, r1))
+        got = ob.download(np.float32).reshape(n, ne1)
+        sel = np.concatenate([got[:, c0:c1] for c0, c1 in checks], axis=1)
+        ref = np.concatenate([rr[:n] for rr in refs], axis=1)
+        e = rel_err(sel, ref)
+        print(f"  rel err {e:.2e}", flush=True)
+        assert e < 1e-3
+        assert np.all(got[:, :r0] == 7.0) and np.all(got[:, r1:] == 7.0)
+
+
 def outlier_x(n, ne0, seed, spike):
     """N(0,1) rows with one channel per 256-element super-block at `spike` times the rest, and
     super-blocks whose scale alternates over six orders of magnitude"""
