@@ -664,13 +664,22 @@ static int mat_packed(const qgpu_tensor *W)
             t == GGML_Q8_0) && ne0 % 256 == 0;
 }
 
+/* where a preparation writes its fp32 rows: only when a matrix it feeds runs on the VALU kernel,
+ * which reads them (the matrix-core GEMV reads the digit planes) */
+static float *rows_for(const qgpu_tensor *const *W, int n, float *buf)
+{
+    for (int i = 0; i < n; i++)
+        if (!mat_packed(W[i])) return buf;
+    return NULL;
+}
+
 static void ffn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B)
 {
     qwen_gpu_t *g = m->gpu;
     const uint64_t F = m->dims.n_ff;
     /* post-attention RMSNorm -> gate/up (model.c:469-476) */
-    const qgpu_act an = act_norm_res(m, R, D->post_norm, g->bxb);
     const qgpu_tensor *W[2] = { D->ffn_gate, D->ffn_up };
+    const qgpu_act an = act_norm_res(m, R, D->post_norm, rows_for(W, 2, g->bxb));
     float *outs[2] = { g->bffn, g->bqkv };
     const uint64_t ld[2] = { F, g->SQ };
     K(qgpu_gemv_act_batch(W, 2, &an, (int)B, outs, ld, 0));
@@ -678,7 +687,7 @@ static void ffn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B)
     qgpu_act sm;
     memset(&sm, 0, sizeof sm);
     sm.kind = QGPU_ACT_SILU_MUL; sm.x = g->bffn; sm.ldx = F; sm.y = g->bqkv; sm.ldy = g->SQ;
-    sm.xout = g->bffn; sm.ldxo = F;
+    if (rows_for((const qgpu_tensor *const *)&D->ffn_down, 1, g->bffn)) { sm.xout = g->bffn; sm.ldxo = F; }
     residual_gemv(m, D->ffn_down, &sm, B, R);
 }
 
@@ -687,8 +696,8 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     qwen_gpu_t *g = m->gpu;
     const qwen_dims_t *d = &m->dims;
     const float eps = m->cfg.rms_norm_eps;
-    const qgpu_act an = act_norm_res(m, R, D->attn_norm, g->bxb);
     const qgpu_tensor *W[3] = { D->q, D->k, D->v };
+    const qgpu_act an = act_norm_res(m, R, D->attn_norm, rows_for(W, 3, g->bxb));
     float *outs[3] = { g->bqkv, g->bk, g->bv };
     const uint64_t ld[3] = { g->SQ, g->kvrow, g->kvrow };
     K(qgpu_gemv_act_batch(W, 3, &an, (int)B, outs, ld, 0));
@@ -722,8 +731,8 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     const qwen_dims_t *d = &m->dims;
     const uint64_t di = d->d_inner;
     const float eps = m->cfg.rms_norm_eps;
-    const qgpu_act an = act_norm_res(m, g->bx, D->attn_norm, g->bxb);
     const qgpu_tensor *W[4] = { D->wqkv, D->wgate, D->beta, D->alpha };
+    const qgpu_act an = act_norm_res(m, g->bx, D->attn_norm, rows_for(W, 4, g->bxb));
     float *outs[4] = { g->bqkv, g->bz, g->bbeta, g->balpha };
     const uint64_t ld[4] = { g->SQ, di, d->n_v_heads, d->n_v_heads };
     /* beta and alpha (n_v_heads rows each: a few tiles) are cut into one K range per 256-column
@@ -748,7 +757,8 @@ static void gdn_dev(qwen_model_t *m, glayer_t *D, uint32_t B)
     qgpu_act gn;
     memset(&gn, 0, sizeof gn);
     gn.kind = QGPU_ACT_GATED_NORM; gn.x = g->battn; gn.ldx = di; gn.y = g->bz; gn.ldy = di; gn.w = D->ssm_norm;
-    gn.seg = d->head_v_dim; gn.eps = eps; gn.xout = g->bffn; gn.ldxo = di;
+    gn.seg = d->head_v_dim; gn.eps = eps;
+    if (rows_for((const qgpu_tensor *const *)&D->ssm_out, 1, g->bffn)) { gn.xout = g->bffn; gn.ldxo = di; }
     residual_gemv(m, D->ssm_out, &gn, B, g->bx);
     ffn_dev(m, D, g->bx, B);
 }
@@ -842,7 +852,7 @@ static void forward_body(qwen_model_t *m, const uint32_t *d_tokens, const float 
         else attn_dev(m, &g->L[il], g->bx, B, 0);
         prof_mark(g, 2 + il);
     }
-    qgpu_act an = act_norm_res(m, g->bx, g->out_norm, g->bxb);
+    qgpu_act an = act_norm_res(m, g->bx, g->out_norm, rows_for((const qgpu_tensor *const *)&g->output, 1, g->bxb));
     /* when the last residual add is still pending (partial planes), its preparation writes the
      * final hidden states straight into h_save; bx then lacks those planes, and nothing reads
      * it before the next forward's embedding overwrites it */
@@ -975,7 +985,7 @@ static void mtp_body(qwen_model_t *m, const uint32_t *d_tokens, const float *h, 
      * reads mx before the next eh_proj overwrites it) */
     int direct = 0;
     if (d_logits) {
-        qgpu_act an = act_norm_res(m, g->mx, g->shnorm, g->bxb);
+        qgpu_act an = act_norm_res(m, g->mx, g->shnorm, rows_for((const qgpu_tensor *const *)&g->output, 1, g->bxb));
         if (B == 1 && an.n_part) { an.xnew = g->mtp_h; direct = 1; }
         K(qgpu_gemv_act_batch((const qgpu_tensor *const *)&g->output, 1, &an, (int)B, &d_logits, &V, 0));
     } else if (B == 1 && g->pend_ks && g->pend == g->mx && g->pend_B == 1 && !g->pend_tok) {
