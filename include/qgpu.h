@@ -309,7 +309,8 @@ int  qgpu_attn_fused(const float *q, uint64_t ldq, const float *k, const float *
  * GEMV: the digit planes of out (n_head*head_dim columns) are written exactly as
  * qgpu_act_prepare with QGPU_ACT_COPY would write them from out, so
  * qgpu_gemv_prepared or qgpu_gemv_prepared_split may follow with no preparation
- * launch (the o-projection input, model.c:811-816). */
+ * launch (the o-projection input, model.c:811-816).  out may be NULL: then only the
+ * digit planes are written. */
 int  qgpu_attn_fused_act(const float *q, uint64_t ldq, const float *k, const float *v, uint64_t ldkv,
                          const float *q_norm_w, const float *k_norm_w, float *kcache, float *vcache,
                          const float *rope_cos, const float *rope_sin, int rope_dim, const int *pos_dev,

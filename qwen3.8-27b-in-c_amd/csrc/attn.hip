@@ -661,7 +661,7 @@ __global__ __launch_bounds__(ATT_HD) void k_attn_combine_act(const float *q, uin
     int ntl, tps, nc;
     span_split(*pos_dev, B, nspan, ntl, tps, nc);
     const float val = combine_one(q, ldq, pml, po, nspan, nc, n_head / n_kv, h, b, d);
-    out[(uint64_t)b * ldo + (uint64_t)h * ATT_HD + d] = val;
+    if (out) out[(uint64_t)b * ldo + (uint64_t)h * ATT_HD + d] = val;   // fp32 rows when asked for
     const float mw = wave_max64(fabsf(val));
     if (lane == 0) mxw[d >> 6] = mw;
     __syncthreads();
@@ -811,7 +811,7 @@ static int attn_fused(const float *q, uint64_t ldq, const float *k, const float 
     if (rc) return rc;
     if (head_dim != ATT_HD) return QGPU_E_RANGE;
     if (!q || !k || !v || !q_norm_w || !k_norm_w || !kcache || !vcache || !rope_cos || !rope_sin || !pos_dev ||
-        !out || B < 1 || n_kv < 1 || n_head % n_kv || rope_dim < 2 || rope_dim > ATT_HD || rope_dim % 2 ||
+        (!out && !act) || B < 1 || n_kv < 1 || n_head % n_kv || rope_dim < 2 || rope_dim > ATT_HD || rope_dim % 2 ||
         ctx_bound < B || ldq % 4 || ldkv % 4 || ((uintptr_t)q & 15) || ((uintptr_t)k & 15) || ((uintptr_t)v & 15) ||
         ((uintptr_t)kcache & 15) || ((uintptr_t)vcache & 15) || ((uintptr_t)q_norm_w & 15) ||
         ((uintptr_t)k_norm_w & 15))

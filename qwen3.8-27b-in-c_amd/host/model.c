@@ -708,8 +708,8 @@ static void attn_dev(qwen_model_t *m, glayer_t *D, float *R, uint32_t B, uint32_
     if (prep)
         K(qgpu_attn_fused_act_live(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v,
                                    g->rope_cos, g->rope_sin, (int)m->cfg.rope_dim_count, g->pos_ptr, (int)m->n_ctx,
-                                   (int)B, (int)d->n_head, (int)d->n_kv_head, (int)d->head_dim, eps, g->battn, g->A,
-                                   g->att_live));
+                                   (int)B, (int)d->n_head, (int)d->n_kv_head, (int)d->head_dim, eps, NULL, g->A,
+                                   g->att_live));        /* digit planes only: the o-projection reads them */
     else
         K(qgpu_attn_fused(g->bqkv, g->SQ, g->bk, g->bv, g->kvrow, D->q_norm, D->k_norm, D->kv_k, D->kv_v,
                           g->rope_cos, g->rope_sin, (int)m->cfg.rope_dim_count, g->pos_ptr, (int)m->n_ctx, (int)B,

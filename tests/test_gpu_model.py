@@ -384,10 +384,11 @@ def test_attention_prepares_o_projection(gpu, t, pos, B):
     posb = gpu.put(np.array([pos], np.int32))
     qwb, kwb, rcb, rsb = gpu.put(qw), gpu.put(kw), gpu.put(rc), gpu.put(rs)
 
-    def attn(fn):
+    def attn(fn, rows=True):
         kcb, vcb, ob = gpu.put(kc), gpu.put(vc), gpu.buf(B * ne0 * 4)
         gpu.ok(fn(qb.f32(), nh * 2 * hd, kb.f32(), vb.f32(), nkv * hd, qwb.f32(), kwb.f32(), kcb.f32(), vcb.f32(),
-                  rcb.f32(), rsb.f32(), rope_dim, posb.i32(), n_ctx, B, nh, nkv, hd, eps, ob.f32(), ne0))
+                  rcb.f32(), rsb.f32(), rope_dim, posb.i32(), n_ctx, B, nh, nkv, hd, eps,
+                  ob.f32() if rows else None, ne0))
         return ob, kcb.download(np.float32), vcb.download(np.float32)
 
     pa, pb = gpu.buf(ks * B * ne1 * 4), gpu.buf(ks * B * ne1 * 4)
@@ -405,6 +406,14 @@ def test_attention_prepares_o_projection(gpu, t, pos, B):
     gpu.ok(gpu.L.qgpu_gemv_prepared_split(T.h, B, pb.f32(), ne1, ks))
     ob2, _, _ = attn(gpu.L.qgpu_attn_fused_act)
     gpu.ok(gpu.L.qgpu_gemv_prepared(T.h, B, yb.f32(), ne1, 0))
+    # with no fp32 rows asked for (out NULL, as the model calls it): the same digit planes
+    yc = gpu.buf(B * ne1 * 4)
+    attn(gpu.L.qgpu_attn_fused_act, rows=False)
+    gpu.ok(gpu.L.qgpu_gemv_prepared(T.h, B, yc.f32(), ne1, 0))
+    assert np.array_equal(yc.download(np.float32), ya.download(np.float32))
+    assert gpu.L.qgpu_attn_fused(qb.f32(), nh * 2 * hd, kb.f32(), vb.f32(), nkv * hd, qwb.f32(), kwb.f32(),
+                                 gpu.put(kc).f32(), gpu.put(vc).f32(), rcb.f32(), rsb.f32(), rope_dim, posb.i32(),
+                                 n_ctx, B, nh, nkv, hd, eps, None, ne0) == -1      # rows required without digits
     rows = oa.download(np.float32)
     assert np.array_equal(ob1.download(np.float32), rows) and np.array_equal(ob2.download(np.float32), rows)
     assert np.array_equal(kcb1, kca) and np.array_equal(vcb1, vca)
