@@ -9,7 +9,7 @@ vocabulary (248,320 ids), so the programs that tokenize text run too.
     logit range and the greedy token printed are the reference engine's for
     the same file (tests/golden/dropin_27b.npz, from oracle/_ref/test_forward_cpu);
   * test_forward_batch (test_forward_batch.c:17-77), B = 3, 4, 8: batched
-    logits against B sequential steps, its own verdict (exit 0, no argmax
+    logits against B sequential steps, its own pass condition (exit 0, no argmax
     difference) and max_rel within 1e-3;
   * debug_rollback (debug_rollback.c:10-57): batch, model_rollback_to(1),
     batch against the sequential model, at 27B state size;

@@ -2,7 +2,7 @@
 against the reference's golden vectors (tests/golden, produced from the
 compiled reference) and the oracle.
 
-Bars (north star): dequantisation and argmax decisions bit-exact; GEMV outputs
+Bars: dequantisation and argmax decisions bit-exact; GEMV outputs
 within 1e-3 relative of the reference.  Relative error is normwise per call:
 max|got - ref| / max|ref|.  The measured error of the matrix-core IQ4_XS path
 is ~1e-7, so the tests also hold it to GEMV_TIGHT to catch partial mistakes.
