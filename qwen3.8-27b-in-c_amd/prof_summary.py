@@ -260,8 +260,10 @@ def cmd_sweep(a):
     out = ["# gemv_batch sweep over formats, shapes and batch (config 2)", "",
            "Command (`/root/repo` is the repository root):", "", "```", a.cmd, "```", "",
            "Each point: warm-up calls, then 40 `qgpu_gemv_batch` calls (activation preparation + GEMV) captured in a",
-           "HIP graph, replayed once untimed and once between HIP events on the library stream; weights rotate over",
-           "enough device copies to exceed the 256 MB MALL.  GB/s = (weight bytes + B x (in + out) x 4) / time;",
+           "HIP graph, replayed once untimed and once between HIP events on the library stream (each shape first",
+           "runs one discarded B = 1 graph of its own: the first replay after the copies are made ran 10-15% slow);",
+           "weights rotate over enough device copies to exceed the 256 MB MALL.  GB/s = (weight bytes + B x",
+           "(in + out) x 4) / time;",
            "% = of 8 TB/s.  Every format runs the int8-MFMA digit GEMV on packed 16-row tile records",
            "(`k_gemv_mfma<format, ...>`; the 248320-row lm_head at B = 4 and 8 through `k_gemv_wide`, its",
            "activations in LDS, where that measured faster).", ""]
