@@ -948,6 +948,8 @@ static __device__ __forceinline__ void kq_compute(const WRec<FMT> &w, const IQ4A
 #define IQ4_RMS   1
 #define IQ4_SPLIT 2
 #define IQ4_PAIR  4     // tail balance: the last tiles of the launch in two K halves (never with IQ4_SPLIT)
+#define IQ4_NORING 16   // no prefetch rings: each step loads its weight record and digits at the step
+                        // (IQ4_XS, one digit plane, 3 or 4 waves per tile; see launch_group)
 #define IQ4_RMS2  8     // deferred two-segment RMSNorm: each segment's super-blocks are summed apart (a wave
                         // meets its second-segment super-blocks after all its first-segment ones, so its
                         // sums move aside once), and each sum takes its segment's row factor (never with
@@ -1009,30 +1011,33 @@ __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_ge
 #pragma unroll
             for (int i = 0; i < 4; i++) accf0[a][i] = 0.0f;
 
-    // two register rings: weights of step j+IQ4_WDEPTH-1 and digits of
-    // j+ADEPTH-1 are loading while step j is decoded and multiplied (ring
-    // indices are compile-time after unrolling by UNROLL).  Each step
-    // issues its digit loads before its weight loads (vmcnt retires loads in
-    // issue order, so a wait for the digits need not cover the newer weights).
-    constexpr int ADEPTH = NA == 1 ? IQ4_ADEPTH1 : IQ4_ADEPTH2;
+    // two register rings: each step issues the loads of step j+WDEPTH-1 (weights) and
+    // j+ADEPTH-1 (digits) before step j is decoded and multiplied (ring indices are
+    // compile-time after unrolling by UNROLL); digit loads before weight loads.  The
+    // loads of the last steps are skipped by a branch, so the compiler's waits also
+    // cover the newest loads (vmcnt(1), then vmcnt(0) within the step): in effect a
+    // wave has about one step's records in flight.  IQ4_NORING: depth 1.
+    constexpr bool RING = !(MODE & IQ4_NORING);
+    constexpr int WDEPTH = RING ? IQ4_WDEPTH : 1;
+    constexpr int ADEPTH = RING ? (NA == 1 ? IQ4_ADEPTH1 : IQ4_ADEPTH2) : 1;
     // main-loop unroll: a common multiple of the two ring depths (compile-time ring slots)
-    constexpr int UNROLL = (IQ4_WDEPTH % ADEPTH) == 0 ? IQ4_WDEPTH : IQ4_WDEPTH * ADEPTH;
-    WRec<FMT> wr[IQ4_WDEPTH];
+    constexpr int UNROLL = (WDEPTH % ADEPTH) == 0 ? WDEPTH : WDEPTH * ADEPTH;
+    WRec<FMT> wr[WDEPTH];
     IQ4A<NA> ar[ADEPTH];
 #define LOAD_W(slot, j) kq_load_w<FMT>(wr[slot], rec0 + (uint64_t)SBX(j) * REC, lane, n)
 #define LOAD_A(slot, j) iq4_load_a<NA>(ar[slot], args.A + (uint64_t)SBX(j) * DIGIT_TILE, args.xs + (uint64_t)SBX(j) * 16, lane, args.ntok)
 #pragma unroll
-    for (int d = 0; d < IQ4_WDEPTH - 1 || d < ADEPTH - 1; d++) {
+    for (int d = 0; d < WDEPTH - 1 || d < ADEPTH - 1; d++) {
         if (d < ADEPTH - 1 && d < nsw) LOAD_A(d, d);
-        if (d < IQ4_WDEPTH - 1 && d < nsw) LOAD_W(d, d);
+        if (d < WDEPTH - 1 && d < nsw) LOAD_W(d, d);
     }
     for (int j = 0; j < nsw; j += UNROLL) {
 #pragma unroll
         for (int d = 0; d < UNROLL; d++) {
             if (j + d < nsw) {
-                const int pw = j + d + IQ4_WDEPTH - 1, pa = j + d + ADEPTH - 1;
+                const int pw = j + d + WDEPTH - 1, pa = j + d + ADEPTH - 1;
                 if (pa < nsw) LOAD_A((d + ADEPTH - 1) % ADEPTH, pa);
-                if (pw < nsw) LOAD_W((d + IQ4_WDEPTH - 1) % IQ4_WDEPTH, pw);
+                if (pw < nsw) LOAD_W((d + WDEPTH - 1) % WDEPTH, pw);
                 if (SEG2 && SBX(j + d) >= args.rss_seg && SBX(j + d) - NW < args.rss_seg) {
                     // this wave's first super-block of the second segment (wave-uniform, once)
 #pragma unroll
@@ -1040,8 +1045,8 @@ __global__ __launch_bounds__(NW * 64, NA == 1 ? IQ4_MINW1 : IQ4_MINW2) void k_ge
 #pragma unroll
                         for (int i = 0; i < 4; i++) { accf0[a][i] = accf[a][i]; accf[a][i] = 0.0f; }
                 }
-                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % IQ4_WDEPTH], ar[d % ADEPTH], oh, accf);
-                else kq_compute<FMT, NA>(wr[d % IQ4_WDEPTH], ar[d % ADEPTH], oh, accf);
+                if constexpr (FMT == T_IQ4_XS) iq4_compute<NA>(wr[d % WDEPTH], ar[d % ADEPTH], oh, accf);
+                else kq_compute<FMT, NA>(wr[d % WDEPTH], ar[d % ADEPTH], oh, accf);
             }
         }
     }
@@ -1494,7 +1499,19 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
                           else if (mode == IQ4_RMS2) MF_NW(NA_, IQ4_RMS2); \
                           else if (mode == (IQ4_RMS2 | IQ4_PAIR)) MF_NW(NA_, IQ4_RMS2 | IQ4_PAIR); \
                           else MF_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
-    if (na == 1) MF_MODE(1); else MF_MODE(2);
+    if (mode & IQ4_NORING) {
+        // instantiated for IQ4_XS, one plane, 3 or 4 waves per tile, K-split or pair-split launches only
+        // (launch_group asks for no other)
+        if constexpr (FMT == T_IQ4_XS) {
+            const int m = mode & ~IQ4_NORING;
+#define MF_NR(M_) do { if (nw == 3) MF_GO(1, 3, M_ | IQ4_NORING); else MF_GO(1, 4, M_ | IQ4_NORING); } while (0)
+            if (m == IQ4_SPLIT) MF_NR(IQ4_SPLIT);
+            else if (m == IQ4_PAIR) MF_NR(IQ4_PAIR);
+            else if (m == (IQ4_RMS | IQ4_PAIR)) MF_NR(IQ4_RMS | IQ4_PAIR);
+            else MF_NR(IQ4_RMS | IQ4_SPLIT);
+#undef MF_NR
+        }
+    } else if (na == 1) MF_MODE(1); else MF_MODE(2);
 #undef MF_MODE
 #undef MF_NW
 #undef MF_GO
@@ -1668,7 +1685,7 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         if (force_nw == 8) nw = 8;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
         if (A.rss && nw < 3) nw = 4;                        // row factors: <= 3 tokens per wave
-        const int mode = (A.rss ? (A.rss_seg ? IQ4_RMS2 : IQ4_RMS) : 0) | (split ? IQ4_SPLIT : 0) |
+        int mode = (A.rss ? (A.rss_seg ? IQ4_RMS2 : IQ4_RMS) : 0) | (split ? IQ4_SPLIT : 0) |
                          (A.pair0 < tiles ? IQ4_PAIR : 0);
 #ifndef GEMV_NW3_RESIDENT
 #define GEMV_NW3_RESIDENT 1
@@ -1689,6 +1706,26 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
                     break;
                 }
         }
+#ifndef GEMV_NORING_MIN_B
+#define GEMV_NORING_MIN_B 3
+#endif
+#ifndef GEMV_NORING_MAX_TPC
+#define GEMV_NORING_MAX_TPC 12
+#endif
+        // Prefetch rings off for the verify-sized launches of IQ4_XS with one digit plane and 3 or 4
+        // tokens (up to 12 tiles per compute unit: not the lm_head).  Same-box A/B of the 27B model:
+        // verify B = 4 5.19 / 5.21 -> 5.15 / 5.16 ms, spec decode 171.0 / 170.6 -> 171.8 / 171.4 tok/s,
+        // the 17408 x 5120 GEMV 13.45 -> 13.35-13.39 us; at B = 1 (decode 4.67 -> 4.69 ms, MTP draft
+        // 0.211 -> 0.215 ms) and with two digit planes (verify B = 6 and 8 +0.2-0.3%) the rings pay.
+        // (Rings whose waits let the next step's loads stay in flight through a step -- dead loads
+        // past the last step, so that every path issues the same loads -- measured slower still:
+        // 15.1-15.2 us for that GEMV.)
+        // Only the K-split and pair-split instances (the model's verify launches and the 17408 x 5120
+        // GEMV): without the rings the plain and row-factor ones take 98-102 VGPRs, 4 waves per SIMD.
+        if (W0->type == T_IQ4_XS && na == 1 && n >= GEMV_NORING_MIN_B && (nw == 3 || nw == 4) &&
+            (mode & (IQ4_SPLIT | IQ4_PAIR)) && !(mode & IQ4_RMS2) && ex.n_cu > 0 &&
+            tiles <= (uint32_t)GEMV_NORING_MAX_TPC * (uint32_t)ex.n_cu)
+            mode |= IQ4_NORING;
         switch (W0->type) {
         case T_IQ4_XS: launch_mfma<T_IQ4_XS>(ex, A, blocks, na, nw, mode); break;
         case T_Q4_K: launch_mfma<T_Q4_K>(ex, A, blocks, na, nw, mode); break;

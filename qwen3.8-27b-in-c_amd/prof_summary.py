@@ -325,7 +325,8 @@ def step_roles(step, B, P):
         k, grid = short(name), gx // max(wx, 1)
         kind, planes = prep_kind(k)
         prev_kind, _ = prep_kind(prev)
-        split = k.startswith("k_gemv_mfma") and (k.endswith(", 2>") or k.endswith(", 3>"))
+        mm = re.match(r"k_gemv_mfma<\d+, \d+, \d+, (\d+)>", k)
+        split = bool(mm) and bool(int(mm.group(1)) & 2)          # mode bit 2: K-split partial planes
         if k.startswith("k_dequant_rows"):
             role, by = "embedding rows (dequant)", B * IQ4_ROW(d["E"]) + B * d["E"] * f4
         elif kind == 5:   # the first RMSNorm of a forward on embedding rows it gathers itself
