@@ -1722,8 +1722,11 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         // 15.1-15.2 us for that GEMV.)
         // Only the K-split and pair-split instances (the model's verify launches and the 17408 x 5120
         // GEMV): without the rings the plain and row-factor ones take 98-102 VGPRs, 4 waves per SIMD.
+        // A K split over more than 32 super-blocks (ffn_down, K = 17408: 17 per block) keeps them:
+        // spec decode 171.6-171.7 -> 172.0-172.1 tok/s (same box).
         if (W0->type == T_IQ4_XS && na == 1 && n >= GEMV_NORING_MIN_B && (nw == 3 || nw == 4) &&
-            (mode & (IQ4_SPLIT | IQ4_PAIR)) && !(mode & IQ4_RMS2) && ex.n_cu > 0 &&
+            (mode & (IQ4_SPLIT | IQ4_PAIR)) && !(mode & IQ4_RMS2) && !((mode & IQ4_SPLIT) && A.nsb > 32) &&
+            ex.n_cu > 0 &&
             tiles <= (uint32_t)GEMV_NORING_MAX_TPC * (uint32_t)ex.n_cu)
             mode |= IQ4_NORING;
         switch (W0->type) {
