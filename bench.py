@@ -77,11 +77,14 @@ MIX_NOTE = "the real checkpoint's format mix: token_embd Q4_K, attn_qkv Q5_K, ou
 
 def roof_kernel(ncu):
     """the kernel instance the roofline GEMV launches on a device of ncu compute units: IQ4_XS, one
-    digit plane, 4 waves per tile; mode 20 (pair split 4, without prefetch rings 16) when its tiles are
-    a little over a multiple of the compute units (1088 = 4 x 256 + 64 on MI355X), else mode 0"""
+    digit plane; when its tiles are a little over a multiple of the compute units (1088 = 4 x 256 + 64
+    on MI355X) mode 20 (pair split 4, no prefetch rings 16) with 8 waves per tile (at most 1100 tiles),
+    else mode 0 with 4"""
     r = ROOF_TILES % ncu if ncu else 0
-    pair = ncu and ROOF_TILES > ncu and 0 < r <= ncu // 2 and r <= 256
-    return f"k_gemv_mfma<23, 1, 4, {20 if pair else 0}>"
+    pair = bool(ncu) and ROOF_TILES > ncu and 0 < r <= ncu // 2 and r <= 256
+    noring = pair and ROOF_TILES <= 12 * ncu
+    nw = 8 if ROOF_TILES <= (1100 if noring else 512) else 4
+    return f"k_gemv_mfma<23, 1, {nw}, {20 if noring else (4 if pair else 0)}>"
 READ_BLOCKS = 8192      # plain-read floor launch: 8192 blocks x 256 threads (best of 1024..8192 at 47.7 MB)
 
 

@@ -1500,11 +1500,12 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
                           else if (mode == (IQ4_RMS2 | IQ4_PAIR)) MF_NW(NA_, IQ4_RMS2 | IQ4_PAIR); \
                           else MF_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
     if (mode & IQ4_NORING) {
-        // instantiated for IQ4_XS, one plane, 3 or 4 waves per tile, K-split or pair-split launches only
+        // instantiated for IQ4_XS, one plane, 3, 4 or 8 waves per tile, K-split or pair-split launches only
         // (launch_group asks for no other)
         if constexpr (FMT == T_IQ4_XS) {
             const int m = mode & ~IQ4_NORING;
-#define MF_NR(M_) do { if (nw == 3) MF_GO(1, 3, M_ | IQ4_NORING); else MF_GO(1, 4, M_ | IQ4_NORING); } while (0)
+#define MF_NR(M_) do { if (nw == 3) MF_GO(1, 3, M_ | IQ4_NORING); else if (nw == 8) MF_GO(1, 8, M_ | IQ4_NORING); \
+                       else MF_GO(1, 4, M_ | IQ4_NORING); } while (0)
             if (m == IQ4_SPLIT) MF_NR(IQ4_SPLIT);
             else if (m == IQ4_PAIR) MF_NR(IQ4_PAIR);
             else if (m == (IQ4_RMS | IQ4_PAIR)) MF_NR(IQ4_RMS | IQ4_PAIR);
@@ -1680,7 +1681,34 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
             const char *e = getenv("QGPU_GEMV_NW");
             force_nw = e ? atoi(e) : 0;
         }
-        int nw = (ks == 1 && tiles <= NW8_TILES) ? 8 : 4;
+#ifndef GEMV_NORING_MIN_B
+#define GEMV_NORING_MIN_B 3
+#endif
+#ifndef GEMV_NORING_MAX_TPC
+#define GEMV_NORING_MAX_TPC 12
+#endif
+#ifndef NW8_TILES_NR
+#define NW8_TILES_NR 1100   // ring-less launches of at most this many tiles run 8 waves per tile
+#endif
+        // Prefetch rings off for the verify-sized launches of IQ4_XS with one digit plane and 3 or 4
+        // tokens (up to 12 tiles per compute unit: not the lm_head).  Same-box A/B of the 27B model:
+        // verify B = 4 5.19 / 5.21 -> 5.15 / 5.16 ms, spec decode 171.0 / 170.6 -> 171.8 / 171.4 tok/s,
+        // the 17408 x 5120 GEMV 13.45 -> 13.35-13.39 us; at B = 1 (decode 4.67 -> 4.69 ms, MTP draft
+        // 0.211 -> 0.215 ms) and with two digit planes (verify B = 6 and 8 +0.2-0.3%) the rings pay.
+        // (Rings whose waits let the next step's loads stay in flight through a step -- dead loads
+        // past the last step, so that every path issues the same loads -- measured slower still:
+        // 15.1-15.2 us for that GEMV.)
+        // Only the K-split and pair-split instances (the model's verify launches and the 17408 x 5120
+        // GEMV): without the rings the plain and row-factor ones take 98-102 VGPRs, 4 waves per SIMD.
+        // A K split over more than 32 super-blocks (ffn_down, K = 17408: 17 per block) keeps them:
+        // spec decode 171.6-171.7 -> 172.0-172.1 tok/s (same box).
+        const bool noring = W0->type == T_IQ4_XS && na == 1 && n >= GEMV_NORING_MIN_B && (split || A.pair0 < tiles) &&
+                            !A.rss_seg && !(split && A.nsb > 32) && ex.n_cu > 0 &&
+                            tiles <= (uint32_t)GEMV_NORING_MAX_TPC * (uint32_t)ex.n_cu;
+        // 8 waves per tile up to 1100 tiles for the ring-less launches (attention q/k/v 896, GDN input
+        // 1030, the 17408 x 5120 GEMV 1088): verify B = 4 5.14-5.16 -> 5.12-5.13 ms (same box); at B = 1
+        // the ring kernels of these grids stay at 4 (decode 4.65 -> 4.69 ms with 8)
+        int nw = (ks == 1 && tiles <= (noring ? NW8_TILES_NR : NW8_TILES)) ? 8 : 4;
         if (force_nw >= 1 && force_nw <= 4) nw = force_nw;
         if (force_nw == 8) nw = 8;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
@@ -1706,29 +1734,7 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
                     break;
                 }
         }
-#ifndef GEMV_NORING_MIN_B
-#define GEMV_NORING_MIN_B 3
-#endif
-#ifndef GEMV_NORING_MAX_TPC
-#define GEMV_NORING_MAX_TPC 12
-#endif
-        // Prefetch rings off for the verify-sized launches of IQ4_XS with one digit plane and 3 or 4
-        // tokens (up to 12 tiles per compute unit: not the lm_head).  Same-box A/B of the 27B model:
-        // verify B = 4 5.19 / 5.21 -> 5.15 / 5.16 ms, spec decode 171.0 / 170.6 -> 171.8 / 171.4 tok/s,
-        // the 17408 x 5120 GEMV 13.45 -> 13.35-13.39 us; at B = 1 (decode 4.67 -> 4.69 ms, MTP draft
-        // 0.211 -> 0.215 ms) and with two digit planes (verify B = 6 and 8 +0.2-0.3%) the rings pay.
-        // (Rings whose waits let the next step's loads stay in flight through a step -- dead loads
-        // past the last step, so that every path issues the same loads -- measured slower still:
-        // 15.1-15.2 us for that GEMV.)
-        // Only the K-split and pair-split instances (the model's verify launches and the 17408 x 5120
-        // GEMV): without the rings the plain and row-factor ones take 98-102 VGPRs, 4 waves per SIMD.
-        // A K split over more than 32 super-blocks (ffn_down, K = 17408: 17 per block) keeps them:
-        // spec decode 171.6-171.7 -> 172.0-172.1 tok/s (same box).
-        if (W0->type == T_IQ4_XS && na == 1 && n >= GEMV_NORING_MIN_B && (nw == 3 || nw == 4) &&
-            (mode & (IQ4_SPLIT | IQ4_PAIR)) && !(mode & IQ4_RMS2) && !((mode & IQ4_SPLIT) && A.nsb > 32) &&
-            ex.n_cu > 0 &&
-            tiles <= (uint32_t)GEMV_NORING_MAX_TPC * (uint32_t)ex.n_cu)
-            mode |= IQ4_NORING;
+        if (noring && (nw == 3 || nw == 4 || nw == 8)) mode |= IQ4_NORING;
         switch (W0->type) {
         case T_IQ4_XS: launch_mfma<T_IQ4_XS>(ex, A, blocks, na, nw, mode); break;
         case T_Q4_K: launch_mfma<T_Q4_K>(ex, A, blocks, na, nw, mode); break;
