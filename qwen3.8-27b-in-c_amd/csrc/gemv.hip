@@ -1688,7 +1688,7 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
 #define GEMV_NORING_MAX_TPC 12
 #endif
 #ifndef NW8_TILES_NR
-#define NW8_TILES_NR 1100   // ring-less launches of at most this many tiles run 8 waves per tile
+#define NW8_TILES_NR 2200   // ring-less launches of at most this many tiles run 8 waves per tile
 #endif
         // Prefetch rings off for the verify-sized launches of IQ4_XS with one digit plane and 3 or 4
         // tokens (up to 12 tiles per compute unit: not the lm_head).  Same-box A/B of the 27B model:
@@ -1705,9 +1705,10 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         const bool noring = W0->type == T_IQ4_XS && na == 1 && n >= GEMV_NORING_MIN_B && (split || A.pair0 < tiles) &&
                             !A.rss_seg && !(split && A.nsb > 32) && ex.n_cu > 0 &&
                             tiles <= (uint32_t)GEMV_NORING_MAX_TPC * (uint32_t)ex.n_cu;
-        // 8 waves per tile up to 1100 tiles for the ring-less launches (attention q/k/v 896, GDN input
-        // 1030, the 17408 x 5120 GEMV 1088): verify B = 4 5.14-5.16 -> 5.12-5.13 ms (same box); at B = 1
-        // the ring kernels of these grids stay at 4 (decode 4.65 -> 4.69 ms with 8)
+        // 8 waves per tile for the ring-less launches (attention q/k/v 896 tiles, GDN input 1030, the
+        // 17408 x 5120 GEMV 1088: verify B = 4 5.14-5.16 -> 5.12-5.13 ms; FFN gate+up 2176 as well:
+        // 5.115-5.120 -> 5.110-5.112 ms, same box); at B = 1 the ring kernels of these grids stay at 4
+        // (decode 4.65 -> 4.69 ms with 8)
         int nw = (ks == 1 && tiles <= (noring ? NW8_TILES_NR : NW8_TILES)) ? 8 : 4;
         if (force_nw >= 1 && force_nw <= 4) nw = force_nw;
         if (force_nw == 8) nw = 8;
