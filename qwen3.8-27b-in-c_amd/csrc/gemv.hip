@@ -1709,7 +1709,9 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         // 17408 x 5120 GEMV 1088: verify B = 4 5.14-5.16 -> 5.12-5.13 ms; FFN gate+up 2176 as well:
         // 5.115-5.120 -> 5.110-5.112 ms, same box); at B = 1 the ring kernels of these grids stay at 4
         // (decode 4.65 -> 4.69 ms with 8)
-        int nw = (ks == 1 && tiles <= (noring ? NW8_TILES_NR : NW8_TILES)) ? 8 : 4;
+        // Two digit planes (5-8 tokens) take 8 waves per tile up to 2200 tiles as well: 8192 positions,
+        // verify k = 7 6.69 -> 6.62-6.65 ms, k = 5 6.33-6.34 -> 6.31-6.32 ms (same box).
+        int nw = (ks == 1 && tiles <= (noring || na == 2 ? NW8_TILES_NR : NW8_TILES)) ? 8 : 4;
         if (force_nw >= 1 && force_nw <= 4) nw = force_nw;
         if (force_nw == 8) nw = 8;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
