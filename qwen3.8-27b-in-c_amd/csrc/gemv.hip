@@ -1687,6 +1687,9 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
 #ifndef GEMV_NORING_MAX_TPC
 #define GEMV_NORING_MAX_TPC 12
 #endif
+#ifndef NW8_TILES_NA2
+#define NW8_TILES_NA2 1100  // two-plane launches of at most this many tiles run 8 waves per tile
+#endif
 #ifndef NW8_TILES_NR
 #define NW8_TILES_NR 2200   // ring-less launches of at most this many tiles run 8 waves per tile
 #endif
@@ -1709,9 +1712,10 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         // 17408 x 5120 GEMV 1088: verify B = 4 5.14-5.16 -> 5.12-5.13 ms; FFN gate+up 2176 as well:
         // 5.115-5.120 -> 5.110-5.112 ms, same box); at B = 1 the ring kernels of these grids stay at 4
         // (decode 4.65 -> 4.69 ms with 8)
-        // Two digit planes (5-8 tokens) take 8 waves per tile up to 2200 tiles as well: 8192 positions,
-        // verify k = 7 6.69 -> 6.62-6.65 ms, k = 5 6.33-6.34 -> 6.31-6.32 ms (same box).
-        int nw = (ks == 1 && tiles <= (noring || na == 2 ? NW8_TILES_NR : NW8_TILES)) ? 8 : 4;
+        // Two digit planes (5-8 tokens) take 8 waves per tile up to 1100 tiles (attention q/k/v, GDN
+        // input): 8192 positions, verify k = 7 6.69 -> 6.62-6.65 ms (same box); the 2176-tile FFN
+        // gate+up keeps 4 (with 8: k = 5 6.31-6.33 -> 6.36-6.38 ms).
+        int nw = (ks == 1 && tiles <= (noring ? NW8_TILES_NR : na == 2 ? NW8_TILES_NA2 : NW8_TILES)) ? 8 : 4;
         if (force_nw >= 1 && force_nw <= 4) nw = force_nw;
         if (force_nw == 8) nw = 8;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
