@@ -1731,8 +1731,9 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         // Residency: when the compute units cannot hold every 4-wave block at once (the kernel's
         // VGPRs cap the waves per SIMD), the blocks left over start only as the first ones end,
         // a second round at the end of the launch; 3 waves per tile (longer K slices) then fit
-        // them all where they can (the GDN input projection at B = 5..8: 1144 blocks against
-        // 4 x 256 resident 4-wave blocks, 5 x 256 3-wave blocks).
+        // them all where they can (the GDN input projection at B = 5..8 with 4 waves per tile:
+        // 1144 blocks against 4 x 256 resident 4-wave blocks, 5 x 256 3-wave blocks; it now
+        // takes 8, above).
         if (GEMV_NW3_RESIDENT && nw == 4 && force_nw == 0 && ex.n_cu > 0 &&
             (long)blocks > (long)mfma_resident_fmt(W0->type, na, 4, mode) * ex.n_cu) {
             for (int w = 3; w >= GEMV_NW_MIN_RESIDENT; w--)
