@@ -1499,11 +1499,13 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
                           else if (mode == IQ4_RMS2) MF_NW(NA_, IQ4_RMS2); \
                           else if (mode == (IQ4_RMS2 | IQ4_PAIR)) MF_NW(NA_, IQ4_RMS2 | IQ4_PAIR); \
                           else MF_NW(NA_, IQ4_RMS | IQ4_SPLIT); } while (0)
-    if (mode & IQ4_NORING) {
-        // instantiated for IQ4_XS, one plane, 3, 4 or 8 waves per tile, K-split or pair-split launches only
-        // (launch_group asks for no other)
+    // the ring-less instances exist for IQ4_XS, one plane, 3, 4 or 8 waves per tile, K-split or
+    // pair-split launches (launch_group asks for no other); anything else runs its ring instance
+    const int m = mode & ~IQ4_NORING;
+    const bool nr = (mode & IQ4_NORING) && FMT == T_IQ4_XS && na == 1 && (nw == 3 || nw == 4 || nw == 8) &&
+                    (m == IQ4_SPLIT || m == IQ4_PAIR || m == (IQ4_RMS | IQ4_PAIR) || m == (IQ4_RMS | IQ4_SPLIT));
+    if (nr) {
         if constexpr (FMT == T_IQ4_XS) {
-            const int m = mode & ~IQ4_NORING;
 #define MF_NR(M_) do { if (nw == 3) MF_GO(1, 3, M_ | IQ4_NORING); else if (nw == 8) MF_GO(1, 8, M_ | IQ4_NORING); \
                        else MF_GO(1, 4, M_ | IQ4_NORING); } while (0)
             if (m == IQ4_SPLIT) MF_NR(IQ4_SPLIT);
@@ -1512,7 +1514,10 @@ static void launch_mfma(const GemvExec &ex, const GemvArgs &A, uint32_t blocks, 
             else MF_NR(IQ4_RMS | IQ4_SPLIT);
 #undef MF_NR
         }
-    } else if (na == 1) MF_MODE(1); else MF_MODE(2);
+    } else {
+        mode = m;
+        if (na == 1) MF_MODE(1); else MF_MODE(2);
+    }
 #undef MF_MODE
 #undef MF_NW
 #undef MF_GO
