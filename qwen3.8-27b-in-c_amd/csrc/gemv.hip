@@ -1717,10 +1717,13 @@ static int launch_group(const GemvExec &ex, const qgpu_tensor *const *Ws, const 
         // 17408 x 5120 GEMV 1088: verify B = 4 5.14-5.16 -> 5.12-5.13 ms; FFN gate+up 2176 as well:
         // 5.115-5.120 -> 5.110-5.112 ms, same box); at B = 1 the ring kernels of these grids stay at 4
         // (decode 4.65 -> 4.69 ms with 8)
-        // Two digit planes (5-8 tokens) take 8 waves per tile up to 1100 tiles (attention q/k/v, GDN
-        // input): 8192 positions, verify k = 7 6.69 -> 6.62-6.65 ms (same box); the 2176-tile FFN
-        // gate+up keeps 4 (with 8: k = 5 6.31-6.33 -> 6.36-6.38 ms).
-        int nw = (ks == 1 && tiles <= (noring ? NW8_TILES_NR : na == 2 ? NW8_TILES_NA2 : NW8_TILES)) ? 8 : 4;
+        // Two digit planes (5-8 tokens) take 8 waves per tile up to 1100 tiles with a row factor (the
+        // model's attention q/k/v and GDN input: 8192 positions, verify k = 7 6.69 -> 6.62-6.65 ms, same
+        // box; the 2176-tile FFN gate+up keeps 4, with 8 k = 5 6.31-6.33 -> 6.36-6.38 ms) and for the
+        // K-quants (gemv_batch B = 8, 17408 x 5120: Q4_K / Q5_K / Q6_K +6-10%; IQ4_XS and Q8_0 without
+        // a row factor -3% / -5%, so those keep 4).
+        const bool na2w8 = na == 2 && (A.rss || W0->type == T_Q4_K || W0->type == T_Q5_K || W0->type == T_Q6_K);
+        int nw = (ks == 1 && tiles <= (noring ? NW8_TILES_NR : na2w8 ? NW8_TILES_NA2 : NW8_TILES)) ? 8 : 4;
         if (force_nw >= 1 && force_nw <= 4) nw = force_nw;
         if (force_nw == 8) nw = 8;
         while (nw > 1 && A.nsb / ks < nw) nw >>= 1;         // no idle waves on short K ranges
